@@ -1,0 +1,203 @@
+"""CPU oracle for spanqr's orth(X) (kcholf): the checker for the MI355X library.
+
+TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, and
+only to check or time the CPU restatement; the product (spanqr_amd, orth.py) never imports it.
+
+Two restatements of candidates/kcholqr.py:92-112 live here:
+  * kcholf_oracle.c (loaded below through ctypes): the bit-exact restatement. It fixes the order of every
+    floating-point operation, and the HIP kernels follow the same order, so GPU results are compared bit for bit.
+  * torch_path.py: a vectorised pure-PyTorch CPU restatement (BLAS summation order, so it agrees with the C oracle
+    to rounding, not bitwise). It is the "pure-PyTorch CPU path" timed as a CPU baseline.
+
+Arrays are numpy, row-major, float32 unless stated.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+TB = 64
+CB = 32
+BK = 32
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_kcholf.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_vp = ctypes.c_void_p
+
+
+def build():
+    """compile the C oracle in place (gcc; no GPU needed)"""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        c_int, c_long, c_float = ctypes.c_int, ctypes.c_long, ctypes.c_float
+        L.spqo_amax.argtypes = [_f32p, c_long, c_int, c_int]
+        L.spqo_amax.restype = c_float
+        L.spqo_pow2_scale.argtypes = [c_float]
+        L.spqo_pow2_scale.restype = c_float
+        L.spqo_rsqrt.argtypes = [c_float]
+        L.spqo_rsqrt.restype = c_float
+        L.spqo_dust.argtypes = [c_int, c_int, _f32p]
+        L.spqo_gram_splits.argtypes = [c_int, c_int]
+        L.spqo_gram_splits.restype = c_int
+        L.spqo_gram.argtypes = [_f32p, c_long, c_int, c_int, c_float, c_int, c_int, c_int, _f32p, _vp]
+        L.spqo_norm.argtypes = [_f64p, c_int]
+        L.spqo_norm.restype = c_float
+        L.spqo_shift.argtypes = [_f32p, c_int, c_float, c_float, c_float]
+        L.spqo_shift.restype = c_float
+        L.spqo_diag_factor.argtypes = [_f32p, c_long, c_float, _f32p, c_long, _f32p]
+        L.spqo_chol.argtypes = [_f32p, c_int, c_float, _f32p, _f32p]
+        L.spqo_trsm.argtypes = [_f32p, c_long, c_int, c_int, c_float, c_int, _vp, c_float, _f32p, _f32p, _f32p,
+                                c_long]
+        L.spqo_ns_D.argtypes = [_f32p, c_int, _f32p]
+        L.spqo_ns_apply.argtypes = [_f32p, c_long, c_int, c_int, _f32p, _f32p, c_long]
+        L.spqo_orth.argtypes = [_f32p, c_long, c_int, c_int, c_int, c_float, c_float, c_float, c_int, _f32p, c_long,
+                                _vp, _vp, _vp, _vp, _vp]
+        _lib = L
+    return _lib
+
+
+def _c32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---- scale (kcholqr.py:29-30, :102) ----
+
+def amax(X):
+    X = _c32(X)
+    return np.float32(lib().spqo_amax(X, X.shape[1], X.shape[0], X.shape[1]))
+
+
+def pow2_scale(m):
+    return np.float32(lib().spqo_pow2_scale(float(np.float32(m))))
+
+
+def rsqrt(x):
+    return np.float32(lib().spqo_rsqrt(float(np.float32(x))))
+
+
+# ---- dust (kcholqr.py:83-89, own generator) ----
+
+def dust(K, r):
+    Z = np.empty((K, r), np.float32)
+    lib().spqo_dust(K, r, Z)
+    return Z
+
+
+# ---- Gram (tri.py:255-297, 324-375) ----
+
+def gram(A, KS, kahan, s=None):
+    """(G [r, r], norm partials [16 U] fp64); s: scale on load (None: no scale)"""
+    A = _c32(A)
+    K, r = A.shape
+    nt = r // TB
+    G = np.empty((r, r), np.float32)
+    npart = np.empty(16 * nt * (nt + 1) // 2, np.float64)
+    lib().spqo_gram(A, r, K, r, 1.0 if s is None else float(s), s is not None, int(bool(kahan)), KS, G,
+                    _ptr(npart))
+    return G, npart
+
+
+def gram_splits(K, KS):
+    return lib().spqo_gram_splits(K, KS)
+
+
+def norm(npart):
+    npart = np.ascontiguousarray(npart, np.float64)
+    return np.float32(lib().spqo_norm(npart, npart.size))
+
+
+def shift(G, nrm, alpha=1e-7, tau_rel=1e-8):
+    """returns (G + shift I, tau) -- kcholqr.py:107-109"""
+    G = _c32(G).copy()
+    tau = lib().spqo_shift(G, G.shape[0], float(nrm), float(np.float32(alpha)), float(np.float32(tau_rel)))
+    return G, np.float32(tau)
+
+
+# ---- Cholesky (chol.cu:115-271) ----
+
+def diag_factor(D, tau):
+    D = _c32(D).copy()
+    L = np.zeros((CB, CB), np.float32)
+    Li = np.zeros((CB, CB), np.float32)
+    lib().spqo_diag_factor(D, CB, float(tau), L, CB, Li)
+    return L, Li
+
+
+def chol(G, tau):
+    """(L [r, r] lower, Li [r, 32] diagonal-tile inverses) of the clamped factorisation of G (lower tiles read)"""
+    A = _c32(G).copy()
+    r = A.shape[0]
+    L = np.zeros((r, r), np.float32)
+    Li = np.zeros((r, CB), np.float32)
+    lib().spqo_chol(A, r, float(tau), L, Li)
+    return L, Li
+
+
+# ---- TRSM (tri.py:378-412) ----
+
+def trsm(A, L, Li, s=None, Z=None, eps=0.0):
+    """Y = A L^-T; with s and Z given, the operand is fmaf(eps, Z, s * A) (the pass-1 fused input)"""
+    A = _c32(A)
+    K, r = A.shape
+    Y = np.empty((K, r), np.float32)
+    pass1 = s is not None
+    Zc = _c32(Z) if pass1 else None
+    lib().spqo_trsm(A, r, K, r, float(s) if pass1 else 1.0, int(pass1), _ptr(Zc), float(np.float32(eps)),
+                    _c32(L), _c32(Li), Y, r)
+    return Y
+
+
+# ---- Newton-Schulz (kcholqr.py:16-23) ----
+
+def ns_D(G):
+    G = _c32(G)
+    D = np.empty_like(G)
+    lib().spqo_ns_D(G, G.shape[0], D)
+    return D
+
+
+def ns_apply(Y, D):
+    Y = _c32(Y)
+    K, r = Y.shape
+    Q = np.empty((K, r), np.float32)
+    lib().spqo_ns_apply(Y, r, K, r, _c32(D), Q, r)
+    return Q
+
+
+# ---- whole call (kcholqr.py:92-112) ----
+
+def orth(X, KS, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2, stages=False):
+    """Q = orth(X). KS: rows per Gram split (the plan's choice; a multiple of 32). With stages=True also returns
+    dict(G=[3,r,r] shifted Grams, L=[3,r,r], Li=[3,r,32], Y=[3,K,r], s, nrm[3], tau[3])."""
+    X = _c32(X)
+    K, r = X.shape
+    Q = np.empty((K, r), np.float32)
+    if stages:
+        Gs = np.empty((3, r, r), np.float32)
+        Ls = np.empty((3, r, r), np.float32)
+        Lis = np.empty((3, r, CB), np.float32)
+        Ys = np.empty((3, K, r), np.float32)
+        sc = np.empty(7, np.float32)
+        ptrs = [_ptr(a) for a in (Gs, Ls, Lis, Ys, sc)]
+    else:
+        ptrs = [None] * 5
+    lib().spqo_orth(X, r, K, r, KS, float(np.float32(eps)), float(np.float32(alpha)), float(np.float32(tau)), ns,
+                    Q, r, *ptrs)
+    if not stages:
+        return Q
+    return Q, dict(G=Gs, L=Ls, Li=Lis, Y=Ys, s=sc[0], nrm=sc[1::2].copy(), tau=sc[2::2].copy())

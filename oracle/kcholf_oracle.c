@@ -1,0 +1,425 @@
+/*
+ * kcholf_oracle.c -- CPU restatement of spanqr's orth(X) ("kcholf", a robust shifted Cholesky-QR).
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker for the MI355X library: only tests/, the smoke check in
+ * __graft_entry__.py and the cpu_baseline leg of bench.py may load it. The product never links or calls it.
+ *
+ * What it restates (reference file:line):
+ *   orth                        orth.py:13-20 (r <= 512 branch)
+ *   kcholqr_f                   candidates/kcholqr.py:92-112
+ *   _pow2_scale                 candidates/kcholqr.py:29-30  (with vector_norm(X, inf) at :102)
+ *   _zdust                      candidates/kcholqr.py:83-89  (own generator, see spqo_dust)
+ *   gram_f / gram_split         candidates/tri.py:324-375 / :255-297 (Kahan within a split, fp64 across splits)
+ *   Y.T @ Y (passes 2-3, NS 1)  candidates/kcholqr.py:106, :20 (restated as the plain split Gram)
+ *   matrix_norm, shift, tau     candidates/kcholqr.py:107-109
+ *   chol32 / chol_f32           candidates/kchol.py:35-44, candidates/cuk/chol.cu:115-271
+ *   trsm_f                      candidates/tri.py:378-412
+ *   _ns_mm                      candidates/kcholqr.py:16-23
+ *
+ * Arithmetic contract. Every floating-point operation is written out: fmaf() where a fused multiply-add is meant,
+ * separate operations elsewhere (built with -ffp-contract=off, no -ffast-math). Each output element is produced by
+ * one fixed sequence of IEEE operations, and the MI355X kernels produce the same sequence (an fp32 MFMA chain on
+ * gfx950 rounds exactly like a sequential fmaf chain in k order), so results are compared bit for bit.
+ * Where the reference leaves an order open (its Triton dots, cuBLAS GEMMs, tree reductions, CUDA rsqrtf) this file
+ * fixes one, documented at each function:
+ *   - dot products are fmaf chains in ascending summation index, starting from +0 (or from the value being updated);
+ *   - Gram output tiles are 64 wide, Cholesky tiles and TRSM column blocks 32 wide (as in the reference); products
+ *     with a triangular tile inverse skip the 16-column groups above the diagonal block (exact zeros);
+ *   - the pivot reciprocal square root is a software rsqrt (bit trick + 3 Newton steps) instead of CUDA's rsqrtf;
+ *   - ||G||_F sums squares in fp64 in a fixed tree order;
+ *   - the dust matrix comes from this project's own seeded counter-based generator (the reference's torch CUDA
+ *     Philox stream cannot be reproduced off an NVIDIA GPU).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <xmmintrin.h>
+
+#define TB 64   /* Gram output tile width (tri.py:362 uses bt = 64) */
+#define CB 32   /* Cholesky diagonal tile and TRSM column block width (chol.cu:15 TB = 32, tri.py:406 bs = 32) */
+#define BK 32   /* rows per Kahan chunk in the compensated Gram (tri.py:352-355 uses BK = 32) */
+
+/* keep subnormals: clear FTZ (bit 15) and DAZ (bit 6) in this thread's MXCSR */
+static void fp_env(void) { _mm_setcsr(_mm_getcsr() & ~((1u << 15) | (1u << 6))); }
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* scale: kcholqr.py:29-30, s = where(m > 0, exp2(-round(log2(clamp_min(m, 1e-38)))), 1), m = max|x|           */
+/* ------------------------------------------------------------------------------------------------------------ */
+
+/* max |x| with NaN propagation (torch.linalg.vector_norm(X, ord=inf) at kcholqr.py:102): the largest bit pattern
+ * of |x| wins, and NaN patterns sort above +inf. */
+float spqo_amax(const float* X, long ldx, int K, int r) {
+    uint32_t m = 0;
+    for (int k = 0; k < K; ++k)
+        for (int c = 0; c < r; ++c) {
+            uint32_t u = f2u(X[(size_t)k * ldx + c]) & 0x7fffffffu;
+            if (u > m) m = u;
+        }
+    return u2f(m);
+}
+
+/* Closed form of _pow2_scale. With mm = max(m, fp32(1e-38)) = 1.f * 2^e (or subnormal), round(log2 mm) is e when
+ * 1.f < sqrt(2) and e + 1 when 1.f > sqrt(2) (no fp32 mantissa equals sqrt(2); the first fp32 above it has
+ * mantissa field 0x3504F4). Subnormal mm lies in [fp32(1e-38), 2^-126), whose log2 rounds to -126. */
+float spqo_pow2_scale(float m) {
+    if (!(m > 0.0f)) return 1.0f;            /* 0 or NaN: torch.where(m > 0, ..., 1) */
+    if (isinf(m)) return 0.0f;               /* exp2(-inf) */
+    float mm = m < 1e-38f ? 1e-38f : m;
+    uint32_t b = f2u(mm);
+    int ex = (int)((b >> 23) & 0xffu);
+    int e;
+    if (ex == 0) e = -126;
+    else e = (ex - 127) + ((b & 0x7fffffu) >= 0x3504F4u ? 1 : 0);
+    return ldexpf(1.0f, -e);
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* dust: kcholqr.py:83-89 draws Z = randn(K, r) (seed 20261018) and normalises its columns.                     */
+/* This project's generator (same role, reproducible everywhere with exact integer and IEEE double arithmetic):  */
+/*   key = mix64(20261018); element (k, c) has counter n = k*r + c;                                             */
+/*   w_j = mix64(key + (6n + j + 1) * 0x9E3779B97F4A7C15) for j = 0..5 (mix64 = splitmix64's finaliser);        */
+/*   S = sum of the twelve 32-bit halves of w_0..w_5; g = (S - 6*(2^32-1)) * 2^-32 (exact; Irwin-Hall(12),      */
+/*   mean 0, variance 1); zf = fp32(g); column norm nc = sqrt(sum_k double(zf)^2) summed in ascending k;        */
+/*   Z[k][c] = fp32(double(zf) / nc).                                                                           */
+/* ------------------------------------------------------------------------------------------------------------ */
+
+static inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+#define DUST_SEED 20261018ull
+
+static float dust_raw(uint64_t key, uint64_t n) {
+    uint64_t S = 0;
+    for (uint64_t j = 0; j < 6; ++j) {
+        uint64_t w = mix64(key + (6 * n + j + 1) * 0x9E3779B97F4A7C15ull);
+        S += (w & 0xffffffffull) + (w >> 32);
+    }
+    int64_t c = (int64_t)S - (int64_t)6 * 4294967295ll;
+    return (float)ldexp((double)c, -32);
+}
+
+void spqo_dust(int K, int r, float* Z) {
+    fp_env();
+    const uint64_t key = mix64(DUST_SEED);
+    double* n2 = (double*)calloc((size_t)r, sizeof(double));
+    for (int k = 0; k < K; ++k)
+        for (int c = 0; c < r; ++c) {
+            float z = dust_raw(key, (uint64_t)k * (uint64_t)r + (uint64_t)c);
+            Z[(size_t)k * r + c] = z;
+            n2[c] += (double)z * (double)z;
+        }
+    for (int c = 0; c < r; ++c) n2[c] = sqrt(n2[c]);
+    for (int k = 0; k < K; ++k)
+        for (int c = 0; c < r; ++c) Z[(size_t)k * r + c] = (float)((double)Z[(size_t)k * r + c] / n2[c]);
+    free(n2);
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* Gram: G = A^T A over upper 64x64 tiles (tri.py:255-297, :324-375), mirrored into the lower triangle.          */
+/* Rows split into S = ceil(K / KS) contiguous splits of KS rows (KS a multiple of BK), each split in chunks of  */
+/* BK rows, rows past K read as 0. Per element (i, j) of split s:                                              */
+/*   kahan: part = fmaf chain over the chunk's rows from +0; y = part - comp; t = acc + y; comp = (t - acc) - y; */
+/*          acc = t                                             (tri.py:351-355)                               */
+/*   plain: acc = fmaf chain over all the split's rows from +0                                                  */
+/* G[i][j] = fp32(((0.0 + P_0) + P_1) + ... + P_{S-1}) in fp64    (tri.py:375 sums the splits in fp64)          */
+/* With use_s the operand is fp32(s * a) (scale on load, tri.py:345-347).                                      */
+/* ||G||_F^2 partials: for upper tile u (row-major over ti <= tj) and row quad b (rows 4b..4b+3 of the tile),    */
+/* q = double(g)^2 per element; each tile row of 64 is reduced by a shift-down tree (offsets 32..1, lane l adds  */
+/* lane l+off), the four rows are added ((w0 + w1) + w2) + w3, and off-diagonal tiles count twice.             */
+/* ------------------------------------------------------------------------------------------------------------ */
+
+static void row_tree64(double* q) {
+    for (int off = 32; off >= 1; off >>= 1)
+        for (int l = 0; l < off; ++l) q[l] = q[l] + q[l + off];
+}
+
+int spqo_gram_splits(int K, int KS) { return (K + KS - 1) / KS; }
+
+void spqo_gram(const float* A, long lda, int K, int r, float s, int use_s, int kahan, int KS, float* G,
+               double* npart) {
+    fp_env();
+    const int nt = r / TB, U = nt * (nt + 1) / 2, S = spqo_gram_splits(K, KS);
+    float* P = (float*)malloc((size_t)S * U * TB * TB * sizeof(float));
+    int* uti = (int*)malloc(U * sizeof(int));
+    int* utj = (int*)malloc(U * sizeof(int));
+    for (int ti = 0, u = 0; ti < nt; ++ti)
+        for (int tj = ti; tj < nt; ++tj, ++u) { uti[u] = ti; utj[u] = tj; }
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int task = 0; task < S * U; ++task) {
+        fp_env();
+        const int sp = task / U, u = task % U, ti = uti[u], tj = utj[u];
+        float acc[TB][TB], comp[TB][TB], part[TB][TB], ai[TB], aj[TB];
+        memset(acc, 0, sizeof acc);
+        memset(comp, 0, sizeof comp);
+        const int k0 = sp * KS, k1 = (k0 + KS < K) ? k0 + KS : K;
+        const int nchunk = (k1 - k0 + BK - 1) / BK;
+        for (int ch = 0; ch < nchunk; ++ch) {
+            if (kahan) memset(part, 0, sizeof part);
+            float (*dst)[TB] = kahan ? part : acc;
+            for (int kk = 0; kk < BK; ++kk) {
+                const int k = k0 + ch * BK + kk;
+                for (int t = 0; t < TB; ++t) {
+                    float a = (k < k1) ? A[(size_t)k * lda + ti * TB + t] : 0.0f;
+                    float b = (k < k1) ? A[(size_t)k * lda + tj * TB + t] : 0.0f;
+                    if (use_s) { a = s * a; b = s * b; }
+                    ai[t] = a; aj[t] = b;
+                }
+                for (int i = 0; i < TB; ++i)
+                    for (int j = 0; j < TB; ++j) dst[i][j] = fmaf(ai[i], aj[j], dst[i][j]);
+            }
+            if (kahan)
+                for (int i = 0; i < TB; ++i)
+                    for (int j = 0; j < TB; ++j) {
+                        float y = part[i][j] - comp[i][j];
+                        float t = acc[i][j] + y;
+                        comp[i][j] = (t - acc[i][j]) - y;
+                        acc[i][j] = t;
+                    }
+        }
+        memcpy(P + (size_t)task * TB * TB, acc, sizeof acc);
+    }
+    #pragma omp parallel for schedule(static)
+    for (int u = 0; u < U; ++u) {
+        fp_env();
+        const int ti = uti[u], tj = utj[u];
+        for (int b = 0; b < 16; ++b) {
+            double w[4];
+            for (int rr = 0; rr < 4; ++rr) {
+                double q[TB];
+                const int i = 4 * b + rr;
+                for (int j = 0; j < TB; ++j) {
+                    double sum = 0.0;
+                    for (int sp = 0; sp < S; ++sp) sum += (double)P[((size_t)sp * U + u) * TB * TB + i * TB + j];
+                    float g = (float)sum;
+                    G[(size_t)(ti * TB + i) * r + tj * TB + j] = g;
+                    G[(size_t)(tj * TB + j) * r + ti * TB + i] = g;
+                    q[j] = (double)g * (double)g;
+                }
+                row_tree64(q);
+                w[rr] = q[0];
+            }
+            double tot = ((w[0] + w[1]) + w[2]) + w[3];
+            if (npart) npart[u * 16 + b] = (ti == tj) ? tot : 2.0 * tot;
+        }
+    }
+    free(P); free(uti); free(utj);
+}
+
+/* sum of the norm partials in ascending index from 0.0, then nrm = sqrtf(fp32(sum)) (matrix_norm, kcholqr.py:107) */
+float spqo_norm(const double* npart, int n) {
+    double s = 0.0;
+    for (int p = 0; p < n; ++p) s += npart[p];
+    return sqrtf((float)s);
+}
+
+/* kcholqr.py:108-109: G_ii += fp32(alpha * nrm); tau = fp32(fp32(tau_rel * nrm) + 1e-30) */
+float spqo_shift(float* G, int r, float nrm, float alpha, float tau_rel) {
+    const float sh = alpha * nrm;
+    for (int i = 0; i < r; ++i) G[(size_t)i * r + i] = G[(size_t)i * r + i] + sh;
+    return tau_rel * nrm + 1e-30f;
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* Cholesky with pivot clamping (chol.cu:115-271; kchol.py:35-44), 32-wide diagonal tiles as in the reference.  */
+/* Products with a tile inverse Li (lower triangular) run the chain only over m < mend(b) = 16*(b/16 + 1): the  */
+/* 16-column groups above the diagonal block are exact zeros and are skipped (the MFMA kernels skip them too).   */
+/* ------------------------------------------------------------------------------------------------------------ */
+
+static inline int mend(int b) { return 16 * (b / 16 + 1); }
+
+/* reciprocal square root used for the pivots (the reference uses CUDA rsqrtf, chol.cu:45): bit-trick start
+ * 0x5f375a86 - (bits >> 1), then three Newton steps y <- y * (1.5 - (0.5x * y) * y), the bracket as one fmaf. */
+float spqo_rsqrt(float x) {
+    float y = u2f(0x5f375a86u - (f2u(x) >> 1));
+    const float h = 0.5f * x;
+    for (int it = 0; it < 3; ++it) {
+        float t = h * y;
+        t = fmaf(-t, y, 1.5f);
+        y = y * t;
+    }
+    return y;
+}
+
+/* Factor one 32x32 diagonal tile in place (chol.cu:131-142): for c = 0..31, piv = fmaxf(D[c][c], tau) (a NaN pivot
+ * also becomes tau), rd = rsqrt(piv), L[c][c] = piv * rd, L[i][c] = D[i][c] * rd (i > c), then
+ * D[i][k] = fmaf(-L[i][c], L[k][c], D[i][k]) for c < k <= i. Then the tile inverse column by column
+ * (chol.cu:151-168): x_i = 0 for i < kk; otherwise acc = [i == kk], acc = fmaf(-L[i][m], x_m, acc) for
+ * m = 0..i-1 in order, x_i = acc * rd_i. Li[i][kk] = x_i. D: 32x32 with row stride ld (lower part read and
+ * overwritten); L gets the lower factor (upper part zero), Li the inverse (row-major 32x32). */
+void spqo_diag_factor(float* D, long ld, float tau, float* L, long ldl, float* Li) {
+    float rd[CB], lc[CB];
+    for (int c = 0; c < CB; ++c) {
+        float piv = fmaxf(D[(size_t)c * ld + c], tau);
+        float q = spqo_rsqrt(piv);
+        rd[c] = q;
+        lc[c] = piv * q;
+        for (int i = c + 1; i < CB; ++i) lc[i] = D[(size_t)i * ld + c] * q;
+        for (int i = 0; i < CB; ++i) L[(size_t)i * ldl + c] = (i >= c) ? lc[i] : 0.0f;
+        for (int k = c + 1; k < CB; ++k)
+            for (int i = k; i < CB; ++i) D[(size_t)i * ld + k] = fmaf(-lc[i], lc[k], D[(size_t)i * ld + k]);
+    }
+    for (int kk = 0; kk < CB; ++kk) {
+        float x[CB];
+        for (int i = 0; i < CB; ++i) {
+            float acc = (i == kk) ? 1.0f : 0.0f;
+            for (int m = 0; m < i; ++m) acc = fmaf(-L[(size_t)i * ldl + m], x[m], acc);
+            x[i] = (i < kk) ? 0.0f : acc * rd[i];
+        }
+        for (int i = 0; i < CB; ++i) Li[i * CB + kk] = x[i];
+    }
+}
+
+/* Blocked right-looking Cholesky of A (r x r, lower tiles read; destroyed), following chol.cu:182-271: step j
+ * factors tile (j, j) into L[j][j] and Li[j]; every panel tile is P_i = A[i][j] Li[j]^T (fmaf chain over
+ * m < mend(b) from +0) and is stored as L[i][j]; every trailing tile (i, k), j < k <= i, becomes A[i][k] - P_i P_k^T
+ * as an fmaf chain over m = 0..31 starting from A[i][k]. L: r x r (upper triangle zero). Li: r x 32, block j at
+ * rows 32j.. */
+void spqo_chol(float* A, int r, float tau, float* L, float* Li) {
+    fp_env();
+    const int nb = r / CB;
+    memset(L, 0, (size_t)r * r * sizeof(float));
+    float* P = (float*)malloc((size_t)r * CB * sizeof(float));   /* panel: rows 32i.. for block i */
+    for (int j = 0; j < nb; ++j) {
+        float* Dj = A + (size_t)(j * CB) * r + j * CB;
+        float* Lj = L + (size_t)(j * CB) * r + j * CB;
+        float* Lij = Li + (size_t)(j * CB) * CB;
+        spqo_diag_factor(Dj, r, tau, Lj, r, Lij);
+        #pragma omp parallel for schedule(static)
+        for (int i = j + 1; i < nb; ++i) {
+            fp_env();
+            for (int a = 0; a < CB; ++a)
+                for (int b = 0; b < CB; ++b) {
+                    float acc = 0.0f;
+                    for (int m = 0; m < mend(b); ++m)
+                        acc = fmaf(A[(size_t)(i * CB + a) * r + j * CB + m], Lij[b * CB + m], acc);
+                    P[(size_t)(i * CB + a) * CB + b] = acc;
+                    L[(size_t)(i * CB + a) * r + j * CB + b] = acc;
+                }
+        }
+        #pragma omp parallel for schedule(dynamic, 1)
+        for (int i = j + 1; i < nb; ++i) {
+            fp_env();
+            for (int k = j + 1; k <= i; ++k)
+                for (int a = 0; a < CB; ++a)
+                    for (int b = 0; b < CB; ++b) {
+                        if (i == k && b > a) continue;   /* only the lower part of diagonal tiles is ever read */
+                        float acc = A[(size_t)(i * CB + a) * r + k * CB + b];
+                        for (int m = 0; m < CB; ++m)
+                            acc = fmaf(-P[(size_t)(i * CB + a) * CB + m], P[(size_t)(k * CB + b) * CB + m], acc);
+                        A[(size_t)(i * CB + a) * r + k * CB + b] = acc;
+                    }
+        }
+    }
+    free(P);
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* TRSM (tri.py:378-412): Y = A L^-T row by row, 32-wide column blocks. Pass 1 reads a = fmaf(eps, z, s * x)     */
+/* (tri.py:391-395). Block j: acc[c] = a[32j + c]; acc[c] = fmaf(-y[m], L[32j + c][m], acc[c]) for m = 0..32j-1  */
+/* in order; y[32j + c] = fmaf chain over m' < mend(c) from +0 of acc[m'] * Li[32j + c][m'] (tri.py:396-402).   */
+/* ------------------------------------------------------------------------------------------------------------ */
+void spqo_trsm(const float* X, long ldx, int K, int r, float s, int pass1, const float* Z, float eps,
+               const float* L, const float* Li, float* Y, long ldy) {
+    const int nb = r / CB;
+    #pragma omp parallel for schedule(static)
+    for (int k = 0; k < K; ++k) {
+        fp_env();
+        float* y = Y + (size_t)k * ldy;
+        float acc[CB];
+        for (int j = 0; j < nb; ++j) {
+            for (int c = 0; c < CB; ++c) {
+                float x = X[(size_t)k * ldx + j * CB + c];
+                acc[c] = pass1 ? fmaf(eps, Z[(size_t)k * r + j * CB + c], s * x) : x;
+            }
+            for (int m = 0; m < j * CB; ++m) {
+                const float ym = -y[m];
+                for (int c = 0; c < CB; ++c) acc[c] = fmaf(ym, L[(size_t)(j * CB + c) * r + m], acc[c]);
+            }
+            for (int c = 0; c < CB; ++c) {
+                float o = 0.0f;
+                for (int m = 0; m < mend(c); ++m) o = fmaf(acc[m], Li[(size_t)(j * CB + c) * CB + m], o);
+                y[j * CB + c] = o;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* Newton-Schulz polish (kcholqr.py:16-23): D = fp32(delta - G) * 0.5; Q[k][c] = y[c] + (fmaf chain over         */
+/* m = 0..r-1 from +0 of y[m] * D[m][c]) -- the correction is rounded on its own, then added once.             */
+/* ------------------------------------------------------------------------------------------------------------ */
+void spqo_ns_D(const float* G, int r, float* D) {
+    for (int i = 0; i < r; ++i)
+        for (int j = 0; j < r; ++j) D[(size_t)i * r + j] = ((i == j ? 1.0f : 0.0f) - G[(size_t)i * r + j]) * 0.5f;
+}
+
+void spqo_ns_apply(const float* Y, long ldy, int K, int r, const float* D, float* Q, long ldq) {
+    #pragma omp parallel for schedule(static)
+    for (int k = 0; k < K; ++k) {
+        fp_env();
+        const float* y = Y + (size_t)k * ldy;
+        float* acc = (float*)malloc((size_t)r * sizeof(float));
+        for (int c = 0; c < r; ++c) acc[c] = 0.0f;
+        for (int m = 0; m < r; ++m) {
+            const float ym = y[m];
+            for (int c = 0; c < r; ++c) acc[c] = fmaf(ym, D[(size_t)m * r + c], acc[c]);
+        }
+        for (int c = 0; c < r; ++c) Q[(size_t)k * ldq + c] = y[c] + acc[c];
+        free(acc);
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* Whole call (kcholqr.py:92-112): scale, 3 x {Gram (Kahan on pass 1, scale on load; plain after), norm, shift,   */
+/* clamped Cholesky, TRSM (pass 1 with s and eps * Z)}, then ns polish steps (Kahan Gram on the last).           */
+/* Optional stage outputs (NULL to skip): Gs/Ls/Lis/Ys hold pass p at offset p*r*r, p*r*r, p*r*32, p*K*r;      */
+/* scal[0..] = s, then nrm and tau for passes 0..2.                                                          */
+/* ------------------------------------------------------------------------------------------------------------ */
+void spqo_orth(const float* X, long ldx, int K, int r, int KS, float eps, float alpha, float tau_rel, int ns,
+               float* Q, long ldq, float* Gs, float* Ls, float* Lis, float* Ys, float* scal) {
+    fp_env();
+    const int nt = r / TB, U = nt * (nt + 1) / 2;
+    const float s = spqo_pow2_scale(spqo_amax(X, ldx, K, r));
+    float* Z = (float*)malloc((size_t)K * r * sizeof(float));
+    float* G = (float*)malloc((size_t)r * r * sizeof(float));
+    float* L = (float*)malloc((size_t)r * r * sizeof(float));
+    float* Li = (float*)malloc((size_t)r * CB * sizeof(float));
+    float* Ya = (float*)malloc((size_t)K * r * sizeof(float));
+    float* Yb = (float*)malloc((size_t)K * r * sizeof(float));
+    double* np = (double*)malloc((size_t)U * 16 * sizeof(double));
+    spqo_dust(K, r, Z);
+    if (scal) scal[0] = s;
+    const float* in = X;
+    long ldin = ldx;
+    float* out = Ya;
+    for (int p = 0; p < 3; ++p) {
+        spqo_gram(in, ldin, K, r, s, p == 0, p == 0, KS, G, np);
+        const float nrm = spqo_norm(np, U * 16);
+        const float tau = spqo_shift(G, r, nrm, alpha, tau_rel);
+        if (scal) { scal[1 + 2 * p] = nrm; scal[2 + 2 * p] = tau; }
+        if (Gs) memcpy(Gs + (size_t)p * r * r, G, (size_t)r * r * sizeof(float));
+        spqo_chol(G, r, tau, L, Li);
+        if (Ls) memcpy(Ls + (size_t)p * r * r, L, (size_t)r * r * sizeof(float));
+        if (Lis) memcpy(Lis + (size_t)p * r * CB, Li, (size_t)r * CB * sizeof(float));
+        spqo_trsm(in, ldin, K, r, s, p == 0, Z, eps, L, Li, out, r);
+        if (Ys) memcpy(Ys + (size_t)p * K * r, out, (size_t)K * r * sizeof(float));
+        in = out; ldin = r;
+        out = (out == Ya) ? Yb : Ya;
+    }
+    for (int i = 0; i < ns; ++i) {
+        spqo_gram(in, r, K, r, 1.0f, 0, i == ns - 1, KS, G, NULL);
+        spqo_ns_D(G, r, L);                               /* L reused as D */
+        if (i == ns - 1) spqo_ns_apply(in, r, K, r, L, Q, ldq);
+        else { spqo_ns_apply(in, r, K, r, L, out, r); in = out; out = (out == Ya) ? Yb : Ya; }
+    }
+    if (ns == 0)
+        for (int k = 0; k < K; ++k) memcpy(Q + (size_t)k * ldq, in + (size_t)k * r, (size_t)r * sizeof(float));
+    free(Z); free(G); free(L); free(Li); free(Ya); free(Yb); free(np);
+}
