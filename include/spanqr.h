@@ -1,0 +1,109 @@
+/*
+ * spanqr.h -- C ABI of the MI355X (gfx950) implementation of spanqr's orth(X).
+ *
+ * orth(X) returns Q with orthonormal columns and span(Q) = span(X) for a tall fp32 matrix X [K, r] (K >= r), using
+ * the robust shifted Cholesky-QR of the reference ("kcholf"): power-of-2 scale on load, seeded dust in the first
+ * solve, three passes of {Gram, shift, pivot-clamped Cholesky, triangular solve}, two Newton-Schulz polish steps.
+ *
+ * Conventions
+ *   - Matrices are row-major fp32 in device memory; X and Q need 16-byte alignment and a leading dimension that is a
+ *     multiple of 4 (the contiguous [K, r] case always qualifies). X is never written.
+ *   - r must be a multiple of 64, 64 <= r <= 512, and K >= r.
+ *   - Every entry point that takes a stream only enqueues work on it: no host synchronisation, no allocation, so a
+ *     call can be captured into a hipGraph. Plan creation allocates and synchronises.
+ *   - Return value 0 means success; a negative value is an error whose message spanqr_last_error() returns (per
+ *     thread). Nothing is thrown across the ABI.
+ *   - A plan owns its workspace (dust, Gram partials, Cholesky factors, solve buffers, grid-barrier counters). Calls on
+ *     one plan must not overlap in time (same stream, or externally ordered); use one plan per concurrent stream.
+ */
+#ifndef SPANQR_H
+#define SPANQR_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct spanqr_plan spanqr_plan;
+
+enum {
+    SPANQR_OK = 0,
+    SPANQR_EINVAL = -1,     /* bad argument (shape, alignment, null pointer) */
+    SPANQR_EHIP = -2,       /* a HIP runtime call failed */
+    SPANQR_ENOMEM = -3,     /* workspace allocation failed */
+};
+
+/* Plan queries for spanqr_plan_query. */
+enum {
+    SPANQR_Q_K = 0,
+    SPANQR_Q_R = 1,
+    SPANQR_Q_SPLITS = 2,         /* Gram row splits S */
+    SPANQR_Q_SPLIT_ROWS = 3,     /* rows per split KS (a multiple of 32) */
+    SPANQR_Q_CHOL_GRID = 4,      /* workgroups of the cooperative Cholesky */
+    SPANQR_Q_WORKSPACE_MB = 5,   /* workspace size, MiB (rounded up) */
+    SPANQR_Q_DEVICE = 6,
+};
+
+/* Create a plan for X [K, r] on HIP device `device` (allocates the workspace and uploads the dust matrix).
+ * Replaces the per-call allocations and module-level caches of the reference: the dust cache _Z
+ * (candidates/kcholqr.py:26, :83-89), chol32's G clone / L / Li / barrier (candidates/kchol.py:12-18, :40-42) and the
+ * Gram partials (candidates/tri.py:371). */
+int spanqr_plan_create(int K, int r, int device, spanqr_plan** out);
+void spanqr_plan_destroy(spanqr_plan* plan);
+long spanqr_plan_query(const spanqr_plan* plan, int what);
+
+/* Q = orth(X) with the reference's keyword arguments (defaults eps 5e-7, alpha 1e-7, tau 1e-8, ns 2).
+ * Replaces orth (orth.py:13-20, the r <= 512 branch) -> kcholqr_f (candidates/kcholqr.py:92-112). stream: a
+ * hipStream_t (torch.cuda.current_stream().cuda_stream on ROCm), 0 for the null stream. */
+int spanqr_orth_f32(spanqr_plan* plan, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
+                    float tau, int ns, void* stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* spanqr_last_error(void);
+
+/* Host-side dust generator (no GPU needed): Z [K, r] row-major, unit columns, the matrix every plan uploads.
+ * Replaces _zdust (candidates/kcholqr.py:83-89), whose torch CUDA Philox stream is NVIDIA-specific; this generator
+ * is seeded with the same 20261018 and defined in the source (splitmix64 counter hash, Irwin-Hall(12) normals). */
+int spanqr_dust_host(int K, int r, float* Z);
+
+/* ---- stage entry points: one stage of the call on device buffers, for checking each kernel ---- */
+
+/* max|x| partials of X into the plan (the scale the pass-1 kernels derive from them is written to scal[0] by
+ * the pass-1 solve). Replaces torch.linalg.vector_norm(X, inf) + _pow2_scale (candidates/kcholqr.py:29-30, :102). */
+int spanqr_stage_amax(spanqr_plan* plan, const float* X, long ldx, void* stream);
+
+/* G = A^T A [r, r] (Kahan within a split when kahan != 0, fp64 across splits; scaled on load by the plan's
+ * current power-of-2 scale when use_scale != 0) and the fp64 partials of ||G||_F^2 (16 per upper 64x64 tile, or
+ * NULL). Replaces gram_f / gram_split (candidates/tri.py:324-375, :255-297) and Y.T @ Y (kcholqr.py:106). */
+int spanqr_stage_gram(spanqr_plan* plan, const float* A, long lda, int use_scale, int kahan, float* G,
+                      double* npart, void* stream);
+
+/* Clamped Cholesky of G + fp32(alpha ||G||_F) I with pivot floor fp32(tau ||G||_F) + 1e-30, ||G||_F from npart;
+ * with npart NULL, of G itself with the absolute pivot floor tau (alpha ignored), which is chol32's contract:
+ * L [r, r] lower (upper triangle of the diagonal tiles zero; upper tiles untouched) and Li [r, 32] the inverses of
+ * the 32x32 diagonal tiles; scal (3 floats, may be NULL) receives {nrm, tau, reserved}. G is not modified.
+ * Replaces the shift at candidates/kcholqr.py:107-109 and chol32 (candidates/kchol.py:35-44) -> chol_f32
+ * (candidates/cuk/chol.cu:273-276). */
+int spanqr_stage_chol(spanqr_plan* plan, const float* G, const double* npart, float alpha, float tau, float* L,
+                      float* Li, float* scal, void* stream);
+
+/* Y = A L^-T (blocked, 32-wide diagonal blocks through Li). With pass1 != 0 the operand is fmaf(eps, Z, s * A)
+ * with the plan's dust Z and scale s (spanqr_stage_amax first). Replaces trsm_f (candidates/tri.py:378-412). */
+int spanqr_stage_trsm(spanqr_plan* plan, const float* A, long lda, int pass1, float eps, const float* L,
+                      const float* Li, float* Y, long ldy, void* stream);
+
+/* One Newton-Schulz polish step Yout = Y + Y fp32(I - G) / 2 with G = Y^T Y (Kahan Gram when kahan != 0).
+ * Replaces one iteration of _ns_mm (candidates/kcholqr.py:16-23). */
+int spanqr_stage_ns(spanqr_plan* plan, const float* Y, long ldy, int kahan, float* Yout, long ldo, void* stream);
+
+/* Copy the plan's dust matrix (device) and its scalars {s, nrm0, tau0, nrm1, tau1, nrm2, tau2, barrier error}
+ * (device, 8 floats; the last is nonzero if a grid barrier of the Cholesky timed out). */
+int spanqr_plan_copy_dust(spanqr_plan* plan, float* Z, void* stream);
+int spanqr_plan_copy_scalars(spanqr_plan* plan, float* scal8, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPANQR_H */

@@ -212,11 +212,17 @@ void spqo_gram(const float* A, long lda, int K, int r, float s, int use_s, int k
     free(P); free(uti); free(utj);
 }
 
-/* sum of the norm partials in ascending index from 0.0, then nrm = sqrtf(fp32(sum)) (matrix_norm, kcholqr.py:107) */
+/* ||G||_F (matrix_norm, kcholqr.py:107) from the partials: lane sums t_l = npart[l] + npart[l + 64] + ... (from 0.0,
+ * ascending index) for l = 0..63, then a shift-down tree over t; nrm = sqrtf(fp32(total)). */
 float spqo_norm(const double* npart, int n) {
-    double s = 0.0;
-    for (int p = 0; p < n; ++p) s += npart[p];
-    return sqrtf((float)s);
+    double t[64];
+    for (int l = 0; l < 64; ++l) {
+        double s = 0.0;
+        for (int p = l; p < n; p += 64) s = s + npart[p];
+        t[l] = s;
+    }
+    row_tree64(t);
+    return sqrtf((float)t[0]);
 }
 
 /* kcholqr.py:108-109: G_ii += fp32(alpha * nrm); tau = fp32(fp32(tau_rel * nrm) + 1e-30) */

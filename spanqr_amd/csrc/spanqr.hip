@@ -1,0 +1,1117 @@
+// spanqr.hip -- MI355X (gfx950) kernels and C ABI for orth(X), a robust shifted Cholesky-QR.
+//
+// Reference algorithm: candidates/kcholqr.py:92-112 (kcholf) with its kernels candidates/tri.py:255-412 (Gram, TRSM)
+// and candidates/cuk/chol.cu:1-281 (cooperative clamped Cholesky). Everything here is fp32 on gfx950 MFMA/VALU
+// except the fp64 split sums and norm. The design is this project's own:
+//   * every dot product is one v_mfma_f32_16x16x4_f32 chain per output element, which rounds like a sequential
+//     fmaf chain in summation order, so each element has one fixed IEEE operation sequence (bit-deterministic, and
+//     equal to the CPU restatement that follows the same order);
+//   * the Gram is a split-K SYRK over upper 64x64 tiles with a fixed, shape-derived split count (no CU-count
+//     dependence), Kahan-compensated per 32-row chunk where the reference compensates, and reduced in fp64 in split
+//     order by a separate kernel that also emits fixed-order partials of ||G||_F^2;
+//   * the Cholesky is one cooperative kernel stepping 64 columns (two 32-wide reference steps) per grid barrier:
+//     workgroup 0 factors the next 64x64 diagonal block (look-ahead) while the others update the trailing 64x64
+//     tiles; the 32x32 diagonal tiles are factored in one wavefront's registers (lane = row) and inverted (lane =
+//     column) as a by-product;
+//   * the triangular solve is row-block parallel (16 rows per workgroup) and right-looking inside the block: each
+//     wavefront owns every 4th 32-column block and applies a finished block to its later blocks with MFMA.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+
+#include "../../include/spanqr.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int TB = 64;            // Gram output tile (tri.py:362 bt = 64)
+constexpr int CB = 32;            // Cholesky tile, TRSM column block (chol.cu:15, tri.py:406)
+constexpr int BK = 32;            // rows per Kahan chunk (tri.py:352-355)
+constexpr int AMAX_BLOCKS = 256;  // partial maxima written by k_amax (one per workgroup)
+constexpr int TS = 33;            // row stride of 32x32 LDS tiles
+constexpr uint32_t SPIN_LIMIT = 1u << 20;
+
+__device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float readlane(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// s = 2^-round(log2 max(m, 1e-38)), 1 for m = 0 or NaN, 0 for m = inf (kcholqr.py:29-30). mb = bits of max|x|.
+__device__ float pow2_scale_bits(uint32_t mb) {
+    if (mb == 0u || mb > 0x7f800000u) return 1.0f;
+    if (mb == 0x7f800000u) return 0.0f;
+    const float m = __uint_as_float(mb);
+    const float mm = m < 1e-38f ? 1e-38f : m;
+    const uint32_t b = __float_as_uint(mm);
+    const int ex = (int)((b >> 23) & 0xffu);
+    const int e = ex == 0 ? -126 : (ex - 127) + ((b & 0x7fffffu) >= 0x3504F4u ? 1 : 0);
+    return ldexpf(1.0f, -e);
+}
+
+// Scale from the 256 partial maxima of k_amax; every thread of a 256-thread workgroup calls it.
+__device__ float block_scale(const uint32_t* __restrict__ part) {
+    __shared__ uint32_t sm[4];
+    uint32_t m = part[threadIdx.x];
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)m, off);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    uint32_t t = sm[0];
+    for (int i = 1; i < 4; ++i) t = sm[i] > t ? sm[i] : t;
+    __syncthreads();
+    return pow2_scale_bits(t);
+}
+
+// Pivot reciprocal square root (the reference uses CUDA rsqrtf, chol.cu:45): bit-trick start and three Newton steps
+// y <- y * (1.5 - (0.5x * y) * y), each bracket one fma, so the result is a fixed function of x.
+__device__ __forceinline__ float rsqrt_sw(float x) {
+    float y = __uint_as_float(0x5f375a86u - (__float_as_uint(x) >> 1));
+    const float h = 0.5f * x;
+#pragma unroll
+    for (int it = 0; it < 3; ++it) {
+        float t = h * y;
+        t = __builtin_fmaf(-t, y, 1.5f);
+        y = y * t;
+    }
+    return y;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// max|x| partials (torch.linalg.vector_norm(X, inf), kcholqr.py:102): the largest bit pattern of |x| per workgroup;
+// NaN patterns sort above +inf, so NaN propagates as in torch.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_amax(const float* __restrict__ X, long ldx, int K, int r,
+                                              uint32_t* __restrict__ part) {
+    uint32_t m = 0;
+    const int r4 = r >> 2;
+    const int n4 = K * r4;
+    for (int e = blockIdx.x * 256 + threadIdx.x; e < n4; e += gridDim.x * 256) {
+        const int row = e / r4, c4 = e - row * r4;
+        const float4 v = *reinterpret_cast<const float4*>(X + (size_t)row * ldx + 4 * c4);
+        const uint32_t a = __float_as_uint(v.x) & 0x7fffffffu, b = __float_as_uint(v.y) & 0x7fffffffu;
+        const uint32_t c = __float_as_uint(v.z) & 0x7fffffffu, d = __float_as_uint(v.w) & 0x7fffffffu;
+        const uint32_t ab = a > b ? a : b, cd = c > d ? c : d, abcd = ab > cd ? ab : cd;
+        m = abcd > m ? abcd : m;
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)m, off);
+        m = o > m ? o : m;
+    }
+    __shared__ uint32_t sm[4];
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = sm[0];
+        for (int i = 1; i < 4; ++i) t = sm[i] > t ? sm[i] : t;
+        part[blockIdx.x] = t;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Gram partials (tri.py:255-297, 324-375): workgroup (u, sp) computes upper 64x64 tile u = (ti, tj) of A^T A over
+// rows [sp*KS, min((sp+1)*KS, K)), in 32-row chunks (rows past the split read as 0). Wave w owns the 32x32 quadrant
+// (w >> 1, w & 1). KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one
+// chain runs over the whole split. SCALE: operands are s * a with the pass-1 power-of-2 scale.
+// ---------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
+    int t = 0, rem = u;
+    while (rem >= nt - t) { rem -= nt - t; ++t; }
+    ti = t;
+    tj = t + rem;
+}
+
+template <bool KAHAN, bool SCALE>
+__global__ __launch_bounds__(256) void k_gram(const float* __restrict__ A, long lda, int K, int nt, int KS,
+                                              const uint32_t* __restrict__ amax_part, float* __restrict__ P) {
+    const int u = blockIdx.x, sp = blockIdx.y, U = gridDim.x;
+    int ti, tj;
+    upper_tile(u, nt, ti, tj);
+    float sc = 1.0f;
+    if (SCALE) sc = block_scale(amax_part);
+    __shared__ float sA[BK][TB + 16];
+    __shared__ float sB[BK][TB + 16];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int qi = w >> 1, qj = w & 1, l16 = lane & 15, lk = lane >> 4;
+    f32x4 acc[2][2], comp[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+            comp[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    const int k0 = sp * KS;
+    const int k1 = (k0 + KS < K) ? k0 + KS : K;
+    for (int kc = k0; kc < k1; kc += BK) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15, k = kc + row;
+            float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k < k1) {
+                va = *reinterpret_cast<const float4*>(A + (size_t)k * lda + ti * TB + 4 * c4);
+                vb = *reinterpret_cast<const float4*>(A + (size_t)k * lda + tj * TB + 4 * c4);
+            }
+            if (SCALE) {
+                va.x = sc * va.x; va.y = sc * va.y; va.z = sc * va.z; va.w = sc * va.w;
+                vb.x = sc * vb.x; vb.y = sc * vb.y; vb.z = sc * vb.z; vb.w = sc * vb.w;
+            }
+            *reinterpret_cast<float4*>(&sA[row][4 * c4]) = va;
+            *reinterpret_cast<float4*>(&sB[row][4 * c4]) = vb;
+        }
+        __syncthreads();
+        f32x4 part[2][2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) part[a][b] = KAHAN ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[a][b];
+#pragma unroll
+        for (int kk = 0; kk < BK / 4; ++kk) {
+            const int kr = 4 * kk + lk;
+            const float a0 = sA[kr][qi * 32 + l16], a1 = sA[kr][qi * 32 + 16 + l16];
+            const float b0 = sB[kr][qj * 32 + l16], b1 = sB[kr][qj * 32 + 16 + l16];
+            part[0][0] = mfma(a0, b0, part[0][0]);
+            part[0][1] = mfma(a0, b1, part[0][1]);
+            part[1][0] = mfma(a1, b0, part[1][0]);
+            part[1][1] = mfma(a1, b1, part[1][1]);
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                if (KAHAN) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float y = part[a][b][v] - comp[a][b][v];
+                        const float t = acc[a][b][v] + y;
+                        comp[a][b][v] = (t - acc[a][b][v]) - y;
+                        acc[a][b][v] = t;
+                    }
+                } else {
+                    acc[a][b] = part[a][b];
+                }
+            }
+        __syncthreads();
+    }
+    float* Pt = P + ((size_t)sp * U + u) * TB * TB;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                Pt[(qi * 32 + a * 16 + 4 * lk + v) * TB + qj * 32 + b * 16 + l16] = acc[a][b][v];
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Split reduction (tri.py:297/375): G = fp32(sum_s fp64(P_s)) in split order, mirrored into the lower triangle.
+// MODE 0 also writes ||G||_F^2 partials: per tile u and row quad b, squares are reduced per 64-wide row by a
+// shift-down tree, the four rows added in order, off-diagonal tiles doubled. MODE 1 writes D = fp32(I - G) * 0.5
+// for the Newton-Schulz step (kcholqr.py:21).
+// ---------------------------------------------------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int S, int nt, int r,
+                                                float* __restrict__ G, double* __restrict__ npart) {
+    const int b = blockIdx.x, u = blockIdx.y, U = gridDim.y;
+    int ti, tj;
+    upper_tile(u, nt, ti, tj);
+    const int t = threadIdx.x, row = 4 * b + (t >> 6), col = t & 63;
+    const float* p = P + (size_t)u * TB * TB + row * TB + col;
+    const size_t stride = (size_t)U * TB * TB;
+    double sum = 0.0;
+    int s = 0;
+    for (; s + 4 <= S; s += 4) {
+        const float p0 = p[(size_t)s * stride], p1 = p[(size_t)(s + 1) * stride];
+        const float p2 = p[(size_t)(s + 2) * stride], p3 = p[(size_t)(s + 3) * stride];
+        sum = sum + (double)p0;
+        sum = sum + (double)p1;
+        sum = sum + (double)p2;
+        sum = sum + (double)p3;
+    }
+    for (; s < S; ++s) sum = sum + (double)p[(size_t)s * stride];
+    const float g = (float)sum;
+    const int gi = ti * TB + row, gj = tj * TB + col;
+    if (MODE == 0) {
+        G[(size_t)gi * r + gj] = g;
+        if (ti != tj) G[(size_t)gj * r + gi] = g;
+        double q = (double)g * (double)g;
+        for (int off = 32; off >= 1; off >>= 1) q = q + __shfl_down(q, off);
+        __shared__ double sw[4];
+        if ((t & 63) == 0) sw[t >> 6] = q;
+        __syncthreads();
+        if (t == 0) {
+            const double tot = ((sw[0] + sw[1]) + sw[2]) + sw[3];
+            npart[u * 16 + b] = (ti == tj) ? tot : 2.0 * tot;
+        }
+    } else {
+        const float d = ((gi == gj ? 1.0f : 0.0f) - g) * 0.5f;
+        G[(size_t)gi * r + gj] = d;
+        if (ti != tj) G[(size_t)gj * r + gi] = d;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Cooperative clamped Cholesky (chol.cu:182-271 restated for 64-column super-steps).
+// ---------------------------------------------------------------------------------------------------------------
+
+// Grid barrier: every wave waits for its own stores, the workgroup meets, thread 0 arrives with an agent-scope
+// release and waits with agent-scope acquires (bounded: after SPIN_LIMIT polls it records an error and goes on, so
+// the kernel always ends). bar[0] counts arrivals and returns to 0, bar[1] is the generation.
+__device__ void grid_barrier(uint32_t* bar, uint32_t nblocks, uint32_t* err) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t g = __hip_atomic_load(bar + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t a = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (a == nblocks - 1) {
+            __hip_atomic_store(bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(bar + 1, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            uint32_t n = 0;
+            while (__hip_atomic_load(bar + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g) {
+                if (++n > SPIN_LIMIT) {
+                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+struct CholShared {
+    float t[11][CB][TS];   // 0: Li_a, 1: Li_b, 2: L_ba of the current diagonal block; 3..6 and 7..10: 64x64 blocks
+    float dl[CB][36];      // factored 32x32 diagonal tile (row stride 36: 16-byte rows for the inverse)
+    float rd[CB];          // pivot reciprocals of that tile
+    float bc[4];           // broadcast: nrm, shift, tau
+};
+
+// wave w computes the 16x16 block (w >> 1, w & 1) of a 32x32 tile; lane (l16, lk) holds rows 16bi + 4lk + v
+#define WAVE_COORDS                                                                  \
+    const int w_ = threadIdx.x >> 6, lane_ = threadIdx.x & 63;                       \
+    const int bi = w_ >> 1, bj = w_ & 1, l16 = lane_ & 15, lk = lane_ >> 4;          \
+    (void)bi; (void)bj; (void)l16; (void)lk
+
+// global 32x32 tile (row stride ld) -> LDS tile; adds `shift` to the diagonal when diag is set
+__device__ __forceinline__ void load_tile(float (*dst)[TS], const float* src, int ld, bool diag, float shift) {
+    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
+    const float4 v = *reinterpret_cast<const float4*>(src + (size_t)row * ld + 4 * c4);
+    float x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (diag && row == 4 * c4 + q) x[q] = x[q] + shift;
+        dst[row][4 * c4 + q] = x[q];
+    }
+}
+
+__device__ __forceinline__ void store_tile(float* dst, int ld, float (*src)[TS]) {
+    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
+    float4 v;
+    v.x = src[row][4 * c4 + 0]; v.y = src[row][4 * c4 + 1]; v.z = src[row][4 * c4 + 2]; v.w = src[row][4 * c4 + 3];
+    *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+}
+
+// out = in Li^T; chain over m < 16 (bj + 1) (Li is lower triangular). out may alias in.
+__device__ __forceinline__ void panel32(float (*out)[TS], float (*in)[TS], float (*li)[TS]) {
+    WAVE_COORDS;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < 4 * (bj + 1); ++kk)
+        acc = mfma(in[16 * bi + l16][4 * kk + lk], li[16 * bj + l16][4 * kk + lk], acc);
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) out[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+    __syncthreads();
+}
+
+// C -= Pi Pk^T (chain over m = 0..31 from C); lower: skip the upper 16x16 block
+__device__ __forceinline__ void update32(float (*C)[TS], float (*Pi)[TS], float (*Pk)[TS], bool lower) {
+    WAVE_COORDS;
+    if (!(lower && bi == 0 && bj == 1)) {
+        f32x4 acc;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] = C[16 * bi + 4 * lk + v][16 * bj + l16];
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            acc = mfma(-Pi[16 * bi + l16][4 * kk + lk], Pk[16 * bj + l16][4 * kk + lk], acc);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) C[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+    }
+    __syncthreads();
+}
+
+// acc (C-layout block of this wave) -= [Xi0 Xi1] [Xk0 Xk1]^T, chain over the 64 panel columns in order
+__device__ __forceinline__ f32x4 update64(f32x4 acc, float (*Xi0)[TS], float (*Xi1)[TS], float (*Xk0)[TS],
+                                          float (*Xk1)[TS]) {
+    WAVE_COORDS;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+        acc = mfma(-Xi0[16 * bi + l16][4 * kk + lk], Xk0[16 * bj + l16][4 * kk + lk], acc);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+        acc = mfma(-Xi1[16 * bi + l16][4 * kk + lk], Xk1[16 * bj + l16][4 * kk + lk], acc);
+    return acc;
+}
+
+// Wave 0 only: factor the 32x32 tile D (lower part) in registers, lane i = row i (chol.cu:131-142); writes the
+// factor (zeros above the diagonal) to sh.dl and the pivot reciprocals to sh.rd.
+__device__ __forceinline__ void factor32(CholShared& sh, float (*D)[TS], float tau) {
+    const int i = threadIdx.x & 31;
+    float v[CB];
+#pragma unroll
+    for (int k = 0; k < CB; ++k) v[k] = D[i][k];
+    float myrd = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+        const float piv = fmaxf(readlane(v[c], c), tau);
+        const float q = rsqrt_sw(piv);
+        const float l = (i > c) ? v[c] * q : ((i == c) ? piv * q : 0.0f);
+        myrd = (i == c) ? q : myrd;
+        v[c] = l;
+#pragma unroll
+        for (int k = c + 1; k < CB; ++k) v[k] = __builtin_fmaf(-l, readlane(l, k), v[k]);
+    }
+    if ((threadIdx.x & 63) < 32) {
+#pragma unroll
+        for (int k = 0; k < CB; ++k) sh.dl[i][k] = (k <= i) ? v[k] : 0.0f;
+        sh.rd[i] = myrd;
+    }
+}
+
+// Wave 0 only: inverse of the factored tile in sh.dl, lane kk = column kk (chol.cu:151-168): x_i = 0 for i < kk,
+// else acc = [i == kk], acc = fma(-L[i][m], x_m, acc) for m = 0..i-1, x_i = acc * rd_i.
+__device__ __forceinline__ void inverse32(CholShared& sh, float (*Li)[TS]) {
+    const int kk = threadIdx.x & 31;
+    float x[CB];
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+        float acc = (i == kk) ? 1.0f : 0.0f;
+#pragma unroll
+        for (int m = 0; m < i; ++m) acc = __builtin_fmaf(-sh.dl[i][m], x[m], acc);
+        x[i] = (i < kk) ? 0.0f : acc * sh.rd[i];
+    }
+    if ((threadIdx.x & 63) < 32) {
+#pragma unroll
+        for (int i = 0; i < CB; ++i) Li[i][kk] = x[i];
+    }
+}
+
+
+__device__ __forceinline__ void store_dl(float* dst, int ld, float (*src)[36]) {
+    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
+    const float4 v = *reinterpret_cast<const float4*>(&src[row][4 * c4]);
+    *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+}
+
+// Factor the 64x64 diagonal block held in t[7] (rows/cols 0..31), t[8] (rows 32..63 x cols 0..31), t[9] (rows and
+// cols 32..63) as two 32-wide reference steps: outputs t[0] = Li_a, t[1] = Li_b, t[2] = L_ba and writes the block's
+// L tiles and Li rows to global.
+__device__ void factor_diag64(CholShared& sh, int J, int r, float tau, float* L, float* Li) {
+    const int w = threadIdx.x >> 6;
+    const size_t o = (size_t)64 * J;
+    if (w == 0) {
+        factor32(sh, sh.t[7], tau);
+        inverse32(sh, sh.t[0]);
+    }
+    __syncthreads();
+    store_dl(L + o * r + o, r, sh.dl);
+    store_tile(Li + o * CB, CB, sh.t[0]);
+    panel32(sh.t[2], sh.t[8], sh.t[0]);          // L_ba = A_ba Li_a^T
+    store_tile(L + (o + 32) * r + o, r, sh.t[2]);
+    update32(sh.t[9], sh.t[2], sh.t[2], true);   // A_bb -= L_ba L_ba^T
+    if (w == 0) {
+        factor32(sh, sh.t[9], tau);
+        inverse32(sh, sh.t[1]);
+    }
+    __syncthreads();
+    store_dl(L + (o + 32) * r + o + 32, r, sh.dl);
+    store_tile(Li + (o + 32) * CB, CB, sh.t[1]);
+    __syncthreads();
+}
+
+// Panel of a 64-row block held in t[base..base+3] = (rows 0-31: cols 0-31, 32-63; rows 32-63: cols 0-31, 32-63)
+// against the current diagonal block (t[0..2]): Q0 = X0 Li_a^T, X1 -= Q0 L_ba^T, Q1 = X1 Li_b^T, in place.
+__device__ void super_panel(CholShared& sh, int base) {
+    for (int h = 0; h < 2; ++h) {
+        float (*x0)[TS] = sh.t[base + 2 * h];
+        float (*x1)[TS] = sh.t[base + 2 * h + 1];
+        panel32(x0, x0, sh.t[0]);
+        update32(x1, x0, sh.t[2], false);
+        panel32(x1, x1, sh.t[1]);
+    }
+}
+
+__device__ __forceinline__ void load_block64(CholShared& sh, int base, const float* src, int r) {
+    load_tile(sh.t[base + 0], src, r, false, 0.f);
+    load_tile(sh.t[base + 1], src + 32, r, false, 0.f);
+    load_tile(sh.t[base + 2], src + (size_t)32 * r, r, false, 0.f);
+    load_tile(sh.t[base + 3], src + (size_t)32 * r + 32, r, false, 0.f);
+}
+
+__device__ __forceinline__ void store_block64(float* dst, int r, CholShared& sh, int base) {
+    store_tile(dst, r, sh.t[base + 0]);
+    store_tile(dst + 32, r, sh.t[base + 1]);
+    store_tile(dst + (size_t)32 * r, r, sh.t[base + 2]);
+    store_tile(dst + (size_t)32 * r + 32, r, sh.t[base + 3]);
+}
+
+// C (in LDS) -= [Xi0 Xi1][Xk0 Xk1]^T
+__device__ __forceinline__ void update64_lds(float (*C)[TS], float (*Xi0)[TS], float (*Xi1)[TS], float (*Xk0)[TS],
+                                             float (*Xk1)[TS]) {
+    WAVE_COORDS;
+    f32x4 acc;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = C[16 * bi + 4 * lk + v][16 * bj + l16];
+    acc = update64(acc, Xi0, Xi1, Xk0, Xk1);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) C[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+}
+
+// Trailing 64x64 tiles (I, Kc), J < Kc <= I, other than (J+1, J+1), dealt round-robin to `W` workers.
+__device__ void chol_trailing(CholShared& sh, float* A, int r, int NB, int J, float shift, float* L, const float* Li,
+                              int W, int me, bool have_diag) {
+    WAVE_COORDS;
+    const size_t oJ = (size_t)64 * J;
+    int t = 0;
+    for (int I = J + 1; I < NB; ++I)
+        for (int Kc = J + 1; Kc <= I; ++Kc) {
+            if (I == J + 1 && Kc == J + 1) continue;
+            if ((t++ % W) != me) continue;
+            if (!have_diag) {
+                load_tile(sh.t[0], Li + oJ * CB, CB, false, 0.f);
+                load_tile(sh.t[1], Li + (oJ + 32) * CB, CB, false, 0.f);
+                load_tile(sh.t[2], L + (oJ + 32) * r + oJ, r, false, 0.f);
+                have_diag = true;
+            }
+            const size_t oI = (size_t)64 * I, oK = (size_t)64 * Kc;
+            const bool dg = (I == Kc);
+            load_block64(sh, 3, A + oI * r + oJ, r);
+            if (!dg) load_block64(sh, 7, A + oK * r + oJ, r);
+            f32x4 c[2][2];
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+                for (int hk = 0; hk < 2; ++hk) {
+                    if (dg && hi == 0 && hk == 1) continue;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int rr = 32 * hi + 16 * bi + 4 * lk + v, cc = 32 * hk + 16 * bj + l16;
+                        float x = A[(oI + rr) * r + oK + cc];
+                        if (J == 0 && dg && rr == cc) x = x + shift;
+                        c[hi][hk][v] = x;
+                    }
+                }
+            __syncthreads();
+            super_panel(sh, 3);
+            if (!dg) super_panel(sh, 7);
+            const int kb = dg ? 3 : 7;
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+                for (int hk = 0; hk < 2; ++hk) {
+                    if (dg && hi == 0 && hk == 1) continue;
+                    c[hi][hk] = update64(c[hi][hk], sh.t[3 + 2 * hi], sh.t[4 + 2 * hi], sh.t[kb + 2 * hk],
+                                         sh.t[kb + 1 + 2 * hk]);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int rr = 32 * hi + 16 * bi + 4 * lk + v, cc = 32 * hk + 16 * bj + l16;
+                        A[(oI + rr) * r + oK + cc] = c[hi][hk][v];
+                    }
+                }
+            if (Kc == J + 1) store_block64(L + oI * r + oJ, r, sh, 3);
+            __syncthreads();
+        }
+}
+
+// Cooperative clamped Cholesky of the Gram in A (r x r, lower tiles read, destroyed). With nnp == 0 the shift is 0
+// and tau_rel is the absolute pivot floor (chol32's contract). Otherwise ||G||_F comes from the nnp fp64 partials:
+// lane l of wave 0 sums npart[l], npart[l + 64], ... in order, then a shift-down tree over the 64 lane sums;
+// nrm = sqrtf(fp32(sum)), shift = alpha * nrm added to the diagonal on first load, tau = tau_rel * nrm + 1e-30
+// (kcholqr.py:107-109). Workgroup 0 factors diagonal blocks (look-ahead), the others update trailing tiles; one grid
+// barrier per 64 columns.
+__global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
+                                              float tau_rel, float* L, float* Li, uint32_t* bar, float* scal) {
+    __shared__ CholShared sh;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int G = gridDim.x, b = blockIdx.x, NB = r / 64;
+    uint32_t* err = bar + 2;
+    if (w == 0) {
+        double s = 0.0;
+        for (int p = lane; p < nnp; p += 64) s = s + npart[p];
+        for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_down(s, off);
+        if (lane == 0) {
+            if (nnp > 0) {
+                const float nrm = sqrtf((float)s);
+                sh.bc[0] = nrm;
+                sh.bc[1] = alpha * nrm;
+                sh.bc[2] = tau_rel * nrm + 1e-30f;
+            } else {                       // chol32 form (kchol.py:35-44): G already shifted, absolute pivot floor
+                sh.bc[0] = 0.0f;
+                sh.bc[1] = 0.0f;
+                sh.bc[2] = tau_rel;
+            }
+        }
+    }
+    __syncthreads();
+    const float shift = sh.bc[1], tau = sh.bc[2];
+    if (b == 0 && tid == 0 && scal != nullptr) {
+        scal[0] = sh.bc[0];
+        scal[1] = tau;
+    }
+    if (b == 0) {
+        load_tile(sh.t[7], A, r, true, shift);
+        load_tile(sh.t[8], A + (size_t)32 * r, r, false, 0.f);
+        load_tile(sh.t[9], A + (size_t)32 * r + 32, r, true, shift);
+        __syncthreads();
+        factor_diag64(sh, 0, r, tau, L, Li);
+    }
+    grid_barrier(bar, G, err);
+    for (int J = 0; J + 1 < NB; ++J) {
+        if (G == 1) chol_trailing(sh, A, r, NB, J, shift, L, Li, 1, 0, true);
+        if (b == 0) {
+            const size_t oJ = (size_t)64 * J, oI = oJ + 64;
+            load_block64(sh, 3, A + oI * r + oJ, r);
+            load_tile(sh.t[7], A + oI * r + oI, r, J == 0, shift);
+            load_tile(sh.t[8], A + (oI + 32) * r + oI, r, false, 0.f);
+            load_tile(sh.t[9], A + (oI + 32) * r + oI + 32, r, J == 0, shift);
+            __syncthreads();
+            super_panel(sh, 3);
+            store_block64(L + oI * r + oJ, r, sh, 3);
+            update64_lds(sh.t[7], sh.t[3], sh.t[4], sh.t[3], sh.t[4]);
+            update64_lds(sh.t[8], sh.t[5], sh.t[6], sh.t[3], sh.t[4]);
+            update64_lds(sh.t[9], sh.t[5], sh.t[6], sh.t[5], sh.t[6]);
+            __syncthreads();
+            factor_diag64(sh, J + 1, r, tau, L, Li);
+        } else {
+            chol_trailing(sh, A, r, NB, J, shift, L, Li, G - 1, b - 1, false);
+        }
+        grid_barrier(bar, G, err);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Triangular solve Y = A L^-T (tri.py:378-412), 16 rows per workgroup. Wave w owns column blocks j = w, w+4, ...
+// and keeps their accumulators (acc_j starts at a_j; pass 1: fmaf(eps, z, s * x)). For k = 0..nbc-1 the owner of
+// block k forms Y_k = acc_k Li_k^T (chain over m < 16 (c/16 + 1)), publishes it in LDS, and every wave applies it to
+// its later blocks: acc_j -= Y_k L_jk^T (chain over the 32 columns of block k), so each element's chain runs over
+// m = 0..32j-1 in order.
+// ---------------------------------------------------------------------------------------------------------------
+template <bool PASS1, int Q>
+__global__ __launch_bounds__(256) void k_trsm(const float* __restrict__ A, long lda, int K, int r,
+                                              const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
+                                              float eps, const float* __restrict__ L, const float* __restrict__ Li,
+                                              float* __restrict__ Y, long ldy, float* scal) {
+    extern __shared__ float smem[];
+    const int ldsy = r + 4;
+    float* sY = smem;                      // [16][r + 4]
+    float* sAcc = smem + 16 * ldsy;        // [4][16][33]
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
+    const int row0 = blockIdx.x * 16, nbc = r / CB;
+    float sc = 1.0f;
+    if (PASS1) {
+        sc = block_scale(amax_part);
+        if (blockIdx.x == 0 && tid == 0 && scal != nullptr) scal[0] = sc;
+    }
+    f32x4 acc[Q][2];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int j = w + 4 * q;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = row0 + 4 * lk + v, col = CB * j + 16 * cb + l16;
+                float x = 0.0f;
+                if (j < nbc && row < K) {
+                    x = A[(size_t)row * lda + col];
+                    if (PASS1) x = __builtin_fmaf(eps, Z[(size_t)row * r + col], sc * x);
+                }
+                acc[q][cb][v] = x;
+            }
+    }
+#pragma unroll
+    for (int qk = 0; qk < Q; ++qk) {
+        for (int ow = 0; ow < 4; ++ow) {
+            const int k = 4 * qk + ow;
+            if (k >= nbc) break;
+            if (w == ow) {
+                float* sa = sAcc + w * 16 * 33;
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) sa[(4 * lk + v) * 33 + 16 * cb + l16] = acc[qk][cb][v];
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) {
+                    f32x4 y = {0.f, 0.f, 0.f, 0.f};
+                    for (int kk = 0; kk < 4 * (cb + 1); ++kk)
+                        y = mfma(sa[l16 * 33 + 4 * kk + lk], Li[(size_t)(CB * k + 16 * cb + l16) * CB + 4 * kk + lk], y);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int rl = 4 * lk + v, col = CB * k + 16 * cb + l16;
+                        sY[rl * ldsy + col] = y[v];
+                        if (row0 + rl < K) Y[(size_t)(row0 + rl) * ldy + col] = y[v];
+                    }
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const int j = w + 4 * q;
+                if (j > k && j < nbc) {
+#pragma unroll
+                    for (int kk = 0; kk < 8; ++kk) {
+                        const float a = -sY[l16 * ldsy + CB * k + 4 * kk + lk];
+#pragma unroll
+                        for (int cb = 0; cb < 2; ++cb)
+                            acc[q][cb] = mfma(a, L[(size_t)(CB * j + 16 * cb + l16) * r + CB * k + 4 * kk + lk],
+                                              acc[q][cb]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Newton-Schulz apply (kcholqr.py:22, addmm(Y, Y, D)): Out = Y + fp32(Y D), the product an MFMA chain over
+// m = 0..r-1 from 0 and added to Y once. 32x64 output tile per workgroup; wave w: rows 16(w >> 1), 2 column blocks.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_nsapply(const float* __restrict__ Yin, long ldy, int K, int r,
+                                                 const float* __restrict__ D, float* __restrict__ Out, long ldo) {
+    __shared__ float sY[32][33];
+    __shared__ float sD[32][68];
+    const int row0 = blockIdx.x * 32, col0 = blockIdx.y * 64;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
+    const int rb = w >> 1, cbase = (w & 1) * 2;
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (int m0 = 0; m0 < r; m0 += 32) {
+        {
+            const int row = tid >> 3, c4 = tid & 7;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (row0 + row < K) v = *reinterpret_cast<const float4*>(Yin + (size_t)(row0 + row) * ldy + m0 + 4 * c4);
+            sY[row][4 * c4 + 0] = v.x; sY[row][4 * c4 + 1] = v.y; sY[row][4 * c4 + 2] = v.z; sY[row][4 * c4 + 3] = v.w;
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15;
+            *reinterpret_cast<float4*>(&sD[row][4 * c4]) =
+                *reinterpret_cast<const float4*>(D + (size_t)(m0 + row) * r + col0 + 4 * c4);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            const float a = sY[16 * rb + l16][4 * kk + lk];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) acc[c] = mfma(a, sD[4 * kk + lk][16 * (cbase + c) + l16], acc[c]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = row0 + 16 * rb + 4 * lk + v, col = col0 + 16 * (cbase + c) + l16;
+            if (row < K) Out[(size_t)row * ldo + col] = Yin[(size_t)row * ldy + col] + acc[c][v];
+        }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------------------------------------------
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIPCHK(x)                                                                                 \
+    do {                                                                                          \
+        hipError_t e_ = (x);                                                                      \
+        if (e_ != hipSuccess) return fail(SPANQR_EHIP, "%s: %s", #x, hipGetErrorString(e_));      \
+    } while (0)
+
+// keeps the caller's current device and restores it on scope exit
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = false;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess && (prev == dev || hipSetDevice(dev) == hipSuccess)) ok = true;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+}  // namespace
+
+struct spanqr_plan {
+    int K = 0, r = 0, device = 0;
+    int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0;
+    size_t bytes = 0;
+    char* base = nullptr;
+    float *Z = nullptr, *P = nullptr, *G = nullptr, *L = nullptr, *Li = nullptr, *Y0 = nullptr, *Y1 = nullptr;
+    float* scal = nullptr;     // s, nrm0, tau0, nrm1, tau1, nrm2, tau2, barrier error (as float bits)
+    float* chscal = nullptr;   // per-launch Cholesky scalars (nrm, tau, err)
+    double* npart = nullptr;
+    uint32_t* amax_part = nullptr;
+    uint32_t* bar = nullptr;   // [count, generation, error, pad]
+};
+
+namespace {
+
+// Gram split policy: about 512 workgroups over the U upper tiles, at least 4 chunks of 32 rows per split; fixed by
+// (K, r) alone so results do not depend on the device.
+void split_policy(int K, int U, int* S_out, int* KS_out) {
+    int S = (512 + U - 1) / U;
+    const int cap = (K + 4 * BK - 1) / (4 * BK);
+    if (S > cap) S = cap;
+    if (S < 1) S = 1;
+    const int KS = ((K + S - 1) / S + BK - 1) / BK * BK;
+    *KS_out = KS;
+    *S_out = (K + KS - 1) / KS;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_mat(const spanqr_plan* p, const float* M, long ld, const char* name) {
+    if (M == nullptr) return fail(SPANQR_EINVAL, "%s is null", name);
+    if (!aligned16(M)) return fail(SPANQR_EINVAL, "%s must be 16-byte aligned", name);
+    if (ld < p->r || (ld & 3)) return fail(SPANQR_EINVAL, "leading dimension of %s (%ld) must be >= r and a multiple of 4",
+                                           name, ld);
+    return SPANQR_OK;
+}
+
+size_t trsm_lds(int r) { return (size_t)(16 * (r + 4) + 4 * 16 * 33) * sizeof(float); }
+
+void launch_gram(const spanqr_plan* p, const float* A, long lda, bool scale, bool kahan, hipStream_t st) {
+    const dim3 grid(p->U, p->S);
+    if (kahan && scale) k_gram<true, true><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    else if (kahan) k_gram<true, false><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    else if (scale) k_gram<false, true><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    else k_gram<false, false><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+}
+
+void launch_reduce(const spanqr_plan* p, int mode, float* out, hipStream_t st) {
+    const dim3 grid(16, p->U);
+    if (mode == 0) k_reduce<0><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart);
+    else k_reduce<1><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart);
+}
+
+int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t st, int nnp) {
+    float* A = p->G;
+    int r = p->r;
+    const double* np = p->npart;
+    float* L = p->L;
+    float* Li = p->Li;
+    uint32_t* bar = p->bar;
+    void* args[] = {&A, &r, (void*)&np, &nnp, &alpha, &tau, &L, &Li, &bar, &scal};
+    HIPCHK(hipLaunchCooperativeKernel((const void*)k_chol, dim3(p->chol_grid), dim3(256), args, 0, st));
+    return SPANQR_OK;
+}
+
+void launch_trsm(const spanqr_plan* p, const float* A, long lda, bool pass1, float eps, const float* L,
+                 const float* Li, float* Y, long ldy, hipStream_t st) {
+    const dim3 grid((p->K + 15) / 16);
+    const size_t lds = trsm_lds(p->r);
+    float* scal = p->scal;
+#define TRSM_CASE(QQ)                                                                                            \
+    case QQ:                                                                                                     \
+        if (pass1) k_trsm<true, QQ><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, L, Li, \
+                                                            Y, ldy, scal);                                       \
+        else k_trsm<false, QQ><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, L, Li, Y,   \
+                                                       ldy, scal);                                               \
+        break;
+    switch (p->trsm_q) {
+        TRSM_CASE(1)
+        TRSM_CASE(2)
+        TRSM_CASE(3)
+        TRSM_CASE(4)
+        default: break;
+    }
+#undef TRSM_CASE
+}
+
+void launch_nsapply(const spanqr_plan* p, const float* Y, long ldy, float* Out, long ldo, hipStream_t st) {
+    const dim3 grid((p->K + 31) / 32, p->r / 64);
+    k_nsapply<<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* spanqr_last_error(void) { return g_err.c_str(); }
+
+int spanqr_dust_host(int K, int r, float* Z) {
+    if (K <= 0 || r <= 0 || Z == nullptr) return fail(SPANQR_EINVAL, "dust: bad arguments");
+    const uint64_t key = mix64(20261018ull);
+    double* n2 = (double*)calloc((size_t)r, sizeof(double));
+    if (!n2) return fail(SPANQR_ENOMEM, "dust: out of host memory");
+    for (int k = 0; k < K; ++k)
+        for (int c = 0; c < r; ++c) {
+            const uint64_t n = (uint64_t)k * (uint64_t)r + (uint64_t)c;
+            uint64_t S = 0;
+            for (uint64_t j = 0; j < 6; ++j) {
+                const uint64_t wv = mix64(key + (6 * n + j + 1) * 0x9E3779B97F4A7C15ull);
+                S += (wv & 0xffffffffull) + (wv >> 32);
+            }
+            const float z = (float)ldexp((double)((int64_t)S - (int64_t)6 * 4294967295ll), -32);
+            Z[(size_t)k * r + c] = z;
+            n2[c] += (double)z * (double)z;
+        }
+    for (int c = 0; c < r; ++c) n2[c] = sqrt(n2[c]);
+    for (int k = 0; k < K; ++k)
+        for (int c = 0; c < r; ++c) Z[(size_t)k * r + c] = (float)((double)Z[(size_t)k * r + c] / n2[c]);
+    free(n2);
+    return SPANQR_OK;
+}
+
+int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
+    if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
+    *out = nullptr;
+    if (r < 64 || r > 512 || (r % 64) != 0) return fail(SPANQR_EINVAL, "r = %d: must be a multiple of 64 in [64, 512]", r);
+    if (K < r) return fail(SPANQR_EINVAL, "K = %d < r = %d", K, r);
+    if ((long)K * r >= (1L << 30)) return fail(SPANQR_EINVAL, "K * r too large");
+    DeviceGuard dg(device);
+    if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", device);
+    spanqr_plan* p = new spanqr_plan;
+    p->K = K; p->r = r; p->device = device;
+    p->nt = r / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / 64;
+    split_policy(K, p->U, &p->S, &p->KS);
+    const int ntrail = p->NB * (p->NB - 1) / 2 - 1;
+    p->chol_grid = 1 + (ntrail > 0 ? ntrail : 0);
+    if (p->chol_grid > 64) p->chol_grid = 64;
+    p->trsm_q = (r / CB + 3) / 4;
+    int occ = 0, cus = 0;
+    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol, 256, 0));
+    HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+    if (occ * cus < p->chol_grid) {
+        const int need = p->chol_grid;
+        delete p;
+        return fail(SPANQR_EHIP, "cooperative Cholesky needs %d co-resident workgroups, device holds %d", need,
+                    occ * cus);
+    }
+    auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const size_t nKr = (size_t)K * r * sizeof(float);
+    const size_t sz_Z = al(nKr), sz_P = al((size_t)p->S * p->U * TB * TB * sizeof(float));
+    const size_t sz_rr = al((size_t)r * r * sizeof(float)), sz_Li = al((size_t)r * CB * sizeof(float));
+    const size_t sz_Y = al(nKr), sz_sc = 256, sz_np = al((size_t)16 * p->U * sizeof(double));
+    const size_t sz_am = al(AMAX_BLOCKS * sizeof(uint32_t)), sz_bar = 256;
+    p->bytes = sz_Z + sz_P + 2 * sz_rr + sz_Li + 2 * sz_Y + 2 * sz_sc + sz_np + sz_am + sz_bar;
+    if (hipMalloc((void**)&p->base, p->bytes) != hipSuccess) {
+        const size_t nb = p->bytes;
+        delete p;
+        return fail(SPANQR_ENOMEM, "workspace allocation of %zu bytes failed", nb);
+    }
+    char* c = p->base;
+    p->Z = (float*)c; c += sz_Z;
+    p->P = (float*)c; c += sz_P;
+    p->G = (float*)c; c += sz_rr;
+    p->L = (float*)c; c += sz_rr;
+    p->Li = (float*)c; c += sz_Li;
+    p->Y0 = (float*)c; c += sz_Y;
+    p->Y1 = (float*)c; c += sz_Y;
+    p->scal = (float*)c; c += sz_sc;
+    p->chscal = (float*)c; c += sz_sc;
+    p->npart = (double*)c; c += sz_np;
+    p->amax_part = (uint32_t*)c; c += sz_am;
+    p->bar = (uint32_t*)c; c += sz_bar;
+    float* hz = (float*)malloc(nKr);
+    int rc = hz ? spanqr_dust_host(K, r, hz) : fail(SPANQR_ENOMEM, "host dust buffer");
+    if (rc == SPANQR_OK) {
+        if (hipMemcpy(p->Z, hz, nKr, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemset(p->L, 0, sz_rr) != hipSuccess || hipMemset(p->scal, 0, 2 * sz_sc) != hipSuccess ||
+            hipMemset(p->bar, 0, sz_bar) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+            rc = fail(SPANQR_EHIP, "plan upload failed");
+    }
+    free(hz);
+    if (rc != SPANQR_OK) {
+        (void)hipFree(p->base);
+        delete p;
+        return rc;
+    }
+    *out = p;
+    return SPANQR_OK;
+}
+
+void spanqr_plan_destroy(spanqr_plan* p) {
+    if (!p) return;
+    DeviceGuard dg(p->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(p->base);
+    delete p;
+}
+
+long spanqr_plan_query(const spanqr_plan* p, int what) {
+    if (!p) return -1;
+    switch (what) {
+        case SPANQR_Q_K: return p->K;
+        case SPANQR_Q_R: return p->r;
+        case SPANQR_Q_SPLITS: return p->S;
+        case SPANQR_Q_SPLIT_ROWS: return p->KS;
+        case SPANQR_Q_CHOL_GRID: return p->chol_grid;
+        case SPANQR_Q_WORKSPACE_MB: return (long)((p->bytes + (1u << 20) - 1) >> 20);
+        case SPANQR_Q_DEVICE: return p->device;
+        default: return -1;
+    }
+}
+
+int spanqr_orth_f32(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, float eps, float alpha, float tau,
+                    int ns, void* stream) {
+    if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    int rc = check_mat(p, X, ldx, "X");
+    if (rc) return rc;
+    if ((rc = check_mat(p, Q, ldq, "Q"))) return rc;
+    if (ns < 0) return fail(SPANQR_EINVAL, "ns = %d < 0", ns);
+    DeviceGuard dg(p->device);
+    if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
+    hipStream_t st = (hipStream_t)stream;
+    k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(X, ldx, p->K, p->r, p->amax_part);
+    const float* in = X;
+    long ldin = ldx;
+    float* bufs[2] = {p->Y0, p->Y1};
+    int cur = 0;
+    for (int pass = 0; pass < 3; ++pass) {
+        launch_gram(p, in, ldin, pass == 0, pass == 0, st);
+        launch_reduce(p, 0, p->G, st);
+        if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U))) return rc;
+        launch_trsm(p, in, ldin, pass == 0, eps, p->L, p->Li, bufs[cur], p->r, st);
+        in = bufs[cur];
+        ldin = p->r;
+        cur ^= 1;
+    }
+    for (int i = 0; i < ns; ++i) {
+        launch_gram(p, in, ldin, false, i == ns - 1, st);
+        launch_reduce(p, 1, p->G, st);
+        if (i == ns - 1) {
+            launch_nsapply(p, in, ldin, Q, ldq, st);
+        } else {
+            launch_nsapply(p, in, ldin, bufs[cur], p->r, st);
+            in = bufs[cur];
+            cur ^= 1;
+        }
+    }
+    if (ns == 0) HIPCHK(hipMemcpy2DAsync(Q, ldq * sizeof(float), in, ldin * sizeof(float), p->r * sizeof(float), p->K,
+                                         hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
+int spanqr_stage_amax(spanqr_plan* p, const float* X, long ldx, void* stream) {
+    if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    int rc = check_mat(p, X, ldx, "X");
+    if (rc) return rc;
+    DeviceGuard dg(p->device);
+    k_amax<<<AMAX_BLOCKS, 256, 0, (hipStream_t)stream>>>(X, ldx, p->K, p->r, p->amax_part);
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
+int spanqr_stage_gram(spanqr_plan* p, const float* A, long lda, int use_scale, int kahan, float* G, double* npart,
+                      void* stream) {
+    if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    int rc = check_mat(p, A, lda, "A");
+    if (rc) return rc;
+    if (!G) return fail(SPANQR_EINVAL, "G is null");
+    DeviceGuard dg(p->device);
+    hipStream_t st = (hipStream_t)stream;
+    launch_gram(p, A, lda, use_scale != 0, kahan != 0, st);
+    launch_reduce(p, 0, p->G, st);
+    HIPCHK(hipMemcpyAsync(G, p->G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
+    if (npart) HIPCHK(hipMemcpyAsync(npart, p->npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
+int spanqr_stage_chol(spanqr_plan* p, const float* G, const double* npart, float alpha, float tau, float* L,
+                      float* Li, float* scal, void* stream) {
+    if (!p || !G || !L || !Li) return fail(SPANQR_EINVAL, "null argument");
+    DeviceGuard dg(p->device);
+    hipStream_t st = (hipStream_t)stream;
+    HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
+    if (npart) HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
+    int rc = launch_chol(p, alpha, tau, p->chscal, st, npart ? 16 * p->U : 0);
+    if (rc) return rc;
+    HIPCHK(hipMemcpyAsync(L, p->L, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemcpyAsync(Li, p->Li, (size_t)p->r * CB * sizeof(float), hipMemcpyDeviceToDevice, st));
+    if (scal) {
+        HIPCHK(hipMemcpyAsync(scal, p->chscal, 2 * sizeof(float), hipMemcpyDeviceToDevice, st));
+        HIPCHK(hipMemcpyAsync(scal + 2, p->bar + 2, sizeof(float), hipMemcpyDeviceToDevice, st));
+    }
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
+int spanqr_stage_trsm(spanqr_plan* p, const float* A, long lda, int pass1, float eps, const float* L, const float* Li,
+                      float* Y, long ldy, void* stream) {
+    if (!p || !L || !Li) return fail(SPANQR_EINVAL, "null argument");
+    int rc = check_mat(p, A, lda, "A");
+    if (rc) return rc;
+    if ((rc = check_mat(p, Y, ldy, "Y"))) return rc;
+    DeviceGuard dg(p->device);
+    launch_trsm(p, A, lda, pass1 != 0, eps, L, Li, Y, ldy, (hipStream_t)stream);
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
+int spanqr_stage_ns(spanqr_plan* p, const float* Y, long ldy, int kahan, float* Yout, long ldo, void* stream) {
+    if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    int rc = check_mat(p, Y, ldy, "Y");
+    if (rc) return rc;
+    if ((rc = check_mat(p, Yout, ldo, "Yout"))) return rc;
+    DeviceGuard dg(p->device);
+    hipStream_t st = (hipStream_t)stream;
+    launch_gram(p, Y, ldy, false, kahan != 0, st);
+    launch_reduce(p, 1, p->G, st);
+    launch_nsapply(p, Y, ldy, Yout, ldo, st);
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
+int spanqr_plan_copy_dust(spanqr_plan* p, float* Z, void* stream) {
+    if (!p || !Z) return fail(SPANQR_EINVAL, "null argument");
+    DeviceGuard dg(p->device);
+    HIPCHK(hipMemcpyAsync(Z, p->Z, (size_t)p->K * p->r * sizeof(float), hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    return SPANQR_OK;
+}
+
+int spanqr_plan_copy_scalars(spanqr_plan* p, float* scal8, void* stream) {
+    if (!p || !scal8) return fail(SPANQR_EINVAL, "null argument");
+    DeviceGuard dg(p->device);
+    hipStream_t st = (hipStream_t)stream;
+    HIPCHK(hipMemcpyAsync(scal8, p->scal, 7 * sizeof(float), hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemcpyAsync(scal8 + 7, p->bar + 2, sizeof(float), hipMemcpyDeviceToDevice, st));
+    return SPANQR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,66 @@
+"""orth(X) on MI355X: the robust shifted Cholesky-QR of candidates/kcholqr.py:92-112 ("kcholf") through the native
+library. The signature and keyword arguments are the reference's; the whole call is enqueued on the current stream
+with no host synchronisation.
+"""
+import torch
+
+from . import _lib
+from .plan import get_plan, stream_handle
+
+CB = 32          # Cholesky tile (chol.cu:15 TB = 32)
+TILE = 64        # the native kernels need r to be a multiple of this
+R_MAX = 512      # orth.py:18: wider X goes through block Gram-Schmidt in the reference
+
+
+def _check_input(X):
+    if not isinstance(X, torch.Tensor) or X.dim() != 2:
+        raise ValueError("orth: X must be a 2-D tensor [K, r]")
+    if X.dtype != torch.float32:
+        raise TypeError(f"orth: X must be float32, got {X.dtype}")
+    if X.device.type != "cuda":
+        raise TypeError("orth: X must be on a GPU (ROCm device); the hot path has no CPU implementation")
+
+
+def _prepare(X):
+    """contiguous (kcholqr.py:100) and 16-byte aligned (a view with an odd storage offset is copied)"""
+    X = X.contiguous()
+    if X.data_ptr() % 16:
+        X = X.clone()
+    return X
+
+
+def kcholqr_f(X, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
+    """Q = orth(X) for fp32 X [K, r] on a ROCm device, r a multiple of 64 in [64, 512], K >= r
+    (candidates/kcholqr.py:92-112). eps: dust scale (first solve only); alpha: diagonal shift relative to ||G||_F;
+    tau: pivot clamp relative to ||G||_F (plus 1e-30); ns: Newton-Schulz polish steps (the last with a Kahan Gram).
+    """
+    _check_input(X)
+    K, r = X.shape
+    if r % TILE or r > R_MAX or K < r:
+        raise ValueError(f"kcholqr_f: shape [{K}, {r}] needs r % {TILE} == 0, r <= {R_MAX} and K >= r")
+    X = _prepare(X)
+    dev = X.device
+    plan = get_plan(K, r, dev)
+    Q = torch.empty_like(X)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().spanqr_orth_f32(plan.handle, X.data_ptr(), r, Q.data_ptr(), r, float(eps), float(alpha),
+                                               float(tau), int(ns), stream_handle(dev)))
+    return Q
+
+
+def orth(X):
+    """Orthonormal basis of the column span of X (fp32 GPU [K, r], K >= r), as orth.py:13-20: Q^T Q = I and
+    span(Q) = span(X); rank-deficient or zero X is completed with orthonormal directions (never zero or NaN columns).
+    Deterministic and free of host synchronisation.
+
+    Shapes outside the native kernels follow the reference's dispatch: r not a multiple of 32 (kcholqr.py:98-99)
+    and, here, r a multiple of 32 but not of 64, or K < r, go to torch.linalg.qr; r > 512 (the reference's block
+    Gram-Schmidt branch, orth.py:18-19) is not implemented yet and raises.
+    """
+    _check_input(X)
+    K, r = X.shape
+    if r > R_MAX and r % 256 == 0:
+        raise NotImplementedError("orth: r > 512 (block Gram-Schmidt over 256-column blocks) is not implemented")
+    if r % TILE or K < r or r > R_MAX:
+        return torch.linalg.qr(X)[0]
+    return kcholqr_f(X)

@@ -1,0 +1,75 @@
+"""Plans: one native workspace per (K, r, device, stream).
+
+A plan owns the dust matrix, the Gram partials, the Cholesky factors, the solve buffers and the Cholesky's
+grid-barrier counters (include/spanqr.h). The reference keeps module-level caches instead (the dust cache
+candidates/kcholqr.py:26, the per-device barrier buffer candidates/kchol.py:12-18) and allocates the rest per call.
+Plans are keyed by stream as well, so calls on different streams never share a workspace or a barrier.
+"""
+import ctypes
+import threading
+
+import torch
+
+from . import _lib
+
+
+class Plan:
+    def __init__(self, K, r, device_index):
+        self.K, self.r, self.device = int(K), int(r), int(device_index)
+        h = ctypes.c_void_p()
+        _lib.check(_lib.lib().spanqr_plan_create(self.K, self.r, self.device, ctypes.byref(h)))
+        self.handle = h
+
+    def query(self, what):
+        return int(_lib.lib().spanqr_plan_query(self.handle, what))
+
+    @property
+    def splits(self):
+        return self.query(_lib.Q_SPLITS)
+
+    @property
+    def split_rows(self):
+        return self.query(_lib.Q_SPLIT_ROWS)
+
+    @property
+    def chol_grid(self):
+        return self.query(_lib.Q_CHOL_GRID)
+
+    def close(self):
+        if self.handle:
+            _lib.lib().spanqr_plan_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 (interpreter shutdown)
+            pass
+
+
+_PLANS = {}
+_LOCK = threading.Lock()
+
+
+def stream_handle(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def get_plan(K, r, device):
+    """the cached plan for (K, r) on `device` and the current stream"""
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (int(K), int(r), idx, stream_handle(idx))
+    with _LOCK:
+        p = _PLANS.get(key)
+        if p is None:
+            p = Plan(K, r, idx)
+            _PLANS[key] = p
+        return p
+
+
+def clear_plans():
+    with _LOCK:
+        for p in _PLANS.values():
+            p.close()
+        _PLANS.clear()

@@ -1,0 +1,158 @@
+"""MI355X kernels against the CPU oracle, bit for bit, stage by stage and end to end.
+
+Every output element of the HIP kernels follows the operation order of oracle/kcholf_oracle.c (an fp32 MFMA chain
+on gfx950 rounds like a sequential fmaf chain), so equality is exact: compared as uint32 bit patterns.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from spanqr_amd import orth, stages
+from spanqr_amd.plan import get_plan
+from spanqr_amd.qrbench import gen
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(t):
+    a = t.detach().cpu().numpy() if isinstance(t, torch.Tensor) else np.asarray(t)
+    return np.ascontiguousarray(a).view(np.uint32 if a.dtype == np.float32 else np.uint64)
+
+
+def assert_bits(gpu, ref, what):
+    g, o = bits(gpu), bits(ref)
+    if not np.array_equal(g, o):
+        gf = (gpu.detach().cpu().numpy() if isinstance(gpu, torch.Tensor) else gpu).astype(np.float64)
+        of = np.asarray(ref, np.float64)
+        bad = np.argwhere(g != o)
+        raise AssertionError(f"{what}: {len(bad)} of {g.size} elements differ; first at {bad[0].tolist()}: "
+                             f"gpu {gf[tuple(bad[0])]!r} oracle {of[tuple(bad[0])]!r}; max abs diff "
+                             f"{np.abs(gf - of).max():.3e}")
+
+
+def case_x(K, r, name="mixed_c4", seed=0):
+    return next(gen.make_cases(K, r, [name], (seed,))).X
+
+
+SHAPES = [(256, 64), (256, 128), (384, 256), (768, 512)]
+
+
+@pytest.mark.parametrize("K,r", SHAPES)
+def test_dust_on_device(cuda, K, r):
+    print(f"dust {K}x{r}", flush=True)
+    Z = stages.dust(K, r, cuda)
+    assert_bits(Z, oracle.dust(K, r), "dust")
+
+
+@pytest.mark.parametrize("K,r", SHAPES)
+@pytest.mark.parametrize("kahan", [True, False])
+def test_gram(cuda, K, r, kahan):
+    print(f"gram {K}x{r} kahan={kahan}", flush=True)
+    X = case_x(K, r)
+    plan = get_plan(K, r, cuda)
+    G, npart = stages.gram(X.to(cuda), kahan)
+    Go, npo = oracle.gram(X.numpy(), plan.split_rows, kahan)
+    assert_bits(G, Go, "G")
+    assert_bits(npart, npo, "norm partials")
+
+
+@pytest.mark.parametrize("K,r", SHAPES)
+def test_gram_scaled(cuda, K, r):
+    print(f"gram scaled {K}x{r}", flush=True)
+    X = case_x(K, r, "huge_1e25")
+    plan = get_plan(K, r, cuda)
+    Xd = X.to(cuda)
+    stages.amax(Xd)
+    G, npart = stages.gram(Xd, True, use_scale=True)
+    s = oracle.pow2_scale(oracle.amax(X.numpy()))
+    Go, npo = oracle.gram(X.numpy(), plan.split_rows, True, s=s)
+    assert_bits(G, Go, "G (scaled)")
+    assert_bits(npart, npo, "norm partials (scaled)")
+
+
+@pytest.mark.parametrize("K,r", SHAPES)
+@pytest.mark.parametrize("name", ["mixed_c4", "rank_half", "zero"])
+def test_chol(cuda, K, r, name):
+    print(f"chol {K}x{r} {name}", flush=True)
+    X = case_x(K, r, name)
+    plan = get_plan(K, r, cuda)
+    Go, npo = oracle.gram(X.numpy(), plan.split_rows, True)
+    L, Li, sc = stages.chol(torch.from_numpy(Go).to(cuda), torch.from_numpy(npo).to(cuda), K)
+    nrm = oracle.norm(npo)
+    Gs, tau = oracle.shift(Go, nrm)
+    Lo, Lio = oracle.chol(Gs, tau)
+    sc = sc.cpu().numpy()
+    assert sc[2] == 0, "grid barrier timed out"
+    assert_bits(sc[:2], np.array([nrm, tau], np.float32), "nrm, tau")
+    assert_bits(torch.tril(L), Lo, "L")
+    assert_bits(Li, Lio, "Li")
+
+
+@pytest.mark.parametrize("K,r", SHAPES)
+def test_chol32_absolute(cuda, K, r):
+    print(f"chol32 {K}x{r}", flush=True)
+    X = case_x(K, r, "mixed_c8")
+    G = X.double().T @ X.double()
+    G = (G + 1e-7 * torch.linalg.matrix_norm(G) * torch.eye(r, dtype=torch.float64)).float().numpy()
+    tau = np.float32(1e-6)
+    L, Li = stages.chol32(torch.from_numpy(G).to(cuda), float(tau), K)
+    Lo, Lio = oracle.chol(G, tau)
+    assert_bits(torch.tril(L), Lo, "L")
+    assert_bits(Li, Lio, "Li")
+
+
+@pytest.mark.parametrize("K,r", SHAPES)
+@pytest.mark.parametrize("pass1", [True, False])
+def test_trsm(cuda, K, r, pass1):
+    print(f"trsm {K}x{r} pass1={pass1}", flush=True)
+    X = case_x(K, r, "ttf_cu4_t1e-2")
+    plan = get_plan(K, r, cuda)
+    Xn = X.numpy()
+    s = oracle.pow2_scale(oracle.amax(Xn))
+    Go, npo = oracle.gram(Xn, plan.split_rows, True, s=s)
+    Gs, tau = oracle.shift(Go, oracle.norm(npo))
+    Lo, Lio = oracle.chol(Gs, tau)
+    Xd = X.to(cuda)
+    if pass1:
+        stages.amax(Xd)
+    Y = stages.trsm(Xd, torch.from_numpy(Lo).to(cuda), torch.from_numpy(Lio).to(cuda), pass1=pass1)
+    if pass1:
+        Yo = oracle.trsm(Xn, Lo, Lio, s=s, Z=oracle.dust(K, r), eps=5e-7)
+    else:
+        Yo = oracle.trsm(Xn, Lo, Lio)
+    assert_bits(Y, Yo, "Y")
+
+
+@pytest.mark.parametrize("K,r", SHAPES)
+@pytest.mark.parametrize("kahan", [True, False])
+def test_ns_step(cuda, K, r, kahan):
+    print(f"ns {K}x{r} kahan={kahan}", flush=True)
+    X = case_x(K, r, "mixed_c2")
+    Y = (torch.linalg.qr(X.double())[0].float() * 1.0001).contiguous()
+    plan = get_plan(K, r, cuda)
+    out = stages.ns_step(Y.to(cuda), kahan)
+    Go, _ = oracle.gram(Y.numpy(), plan.split_rows, kahan)
+    Yo = oracle.ns_apply(Y.numpy(), oracle.ns_D(Go))
+    assert_bits(out, Yo, "NS step")
+
+
+ORTH_CASES = [(256, 64, "mixed_c4"), (256, 128, "zero"), (384, 256, "rank_half"), (768, 512, "ttf_cu4_t1e-2"),
+              (768, 512, "dup_cols"), (1024, 256, "huge_1e25"), (1024, 256, "tiny_1e-25")]
+
+
+@pytest.mark.parametrize("K,r,name", ORTH_CASES)
+def test_orth_bit_exact(cuda, K, r, name):
+    print(f"orth {K}x{r} {name}", flush=True)
+    X = case_x(K, r, name)
+    Xd = X.to(cuda)
+    X0 = Xd.clone()
+    Q1 = orth(Xd)
+    Q2 = orth(Xd)
+    torch.cuda.synchronize()
+    assert_bits(Q1, Q2, "repeat")
+    assert_bits(Xd, X0, "input intact")
+    plan = get_plan(K, r, cuda)
+    assert stages.scalars(K, r, cuda)[7].item() == 0, "grid barrier timed out"
+    Qo = oracle.orth(X.numpy(), plan.split_rows)
+    assert_bits(Q1, Qo, "Q")
