@@ -59,6 +59,20 @@ long spanqr_plan_query(const spanqr_plan* plan, int what);
 int spanqr_orth_f32(spanqr_plan* plan, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
                     float tau, int ns, void* stream);
 
+/* Profiling form of spanqr_orth_f32: the same kernels on the same stream with a HIP event after each, then waits
+ * for the stream (host synchronisation: not for the hot path). ms[i] receives the time of kernel i in launch order
+ * (amax; per pass gram, reduce, chol, trsm; per polish step gram, reduce, apply); *n_out their number.
+ * No counterpart in the reference (its bench times whole calls, qrbench/bench.py:28-53). */
+int spanqr_profile_orth(spanqr_plan* plan, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
+                        float tau, int ns, void* stream, float* ms, int max_n, int* n_out);
+
+/* Profiling form of the Cholesky stage (spanqr_stage_chol with npart): runs an instrumented copy of the kernel whose
+ * workgroup 0 stamps the device wall clock at each phase of every 64-column step, copies the stamps to host memory
+ * (12 per step, r/64 steps; see the kernel source for the slots) and waits for the stream. *tick_ns: nanoseconds per
+ * wall-clock tick. The reference keeps similar stamps behind a debug define (candidates/cuk/chol.cu:17-23). */
+int spanqr_profile_chol(spanqr_plan* plan, const float* G, const double* npart, float alpha, float tau,
+                        unsigned long long* stamps_out, double* tick_ns, void* stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* spanqr_last_error(void);
 

@@ -27,6 +27,8 @@ SIGNATURES = {
     "spanqr_plan_destroy": (None, [_P]),
     "spanqr_plan_query": (_L, [_P, _I]),
     "spanqr_orth_f32": (_I, [_P, _P, _L, _P, _L, _F, _F, _F, _I, _P]),
+    "spanqr_profile_orth": (_I, [_P, _P, _L, _P, _L, _F, _F, _F, _I, _P, _P, _I, ctypes.POINTER(ctypes.c_int)]),
+    "spanqr_profile_chol": (_I, [_P, _P, _P, _F, _F, _P, ctypes.POINTER(ctypes.c_double), _P]),
     "spanqr_last_error": (ctypes.c_char_p, []),
     "spanqr_dust_host": (_I, [_I, _I, _P]),
     "spanqr_stage_amax": (_I, [_P, _P, _L, _P]),

@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 // Grid barrier: every wave waits for its own stores, the workgroup meets, thread 0 arrives with an agent-scope
 // release and waits with agent-scope acquires (bounded: after SPIN_LIMIT polls it records an error and goes on, so
 // the kernel always ends). bar[0] counts arrivals and returns to 0, bar[1] is the generation.
-__device__ void grid_barrier(uint32_t* bar, uint32_t nblocks, uint32_t* err) {
+__device__ __forceinline__ void grid_barrier(uint32_t* bar, uint32_t nblocks, uint32_t* err) {
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -298,6 +298,8 @@ __device__ void grid_barrier(uint32_t* bar, uint32_t nblocks, uint32_t* err) {
 struct CholShared {
     float t[11][CB][TS];   // 0: Li_a, 1: Li_b, 2: L_ba of the current diagonal block; 3..6 and 7..10: 64x64 blocks
     float dl[CB][36];      // factored 32x32 diagonal tile (row stride 36: 16-byte rows for the inverse)
+    float xs[16][36];      // inverse rows 0..15 (MFMA operand), then the rows 16..31 partial sums
+    float bl[CB];          // column broadcast in the tile factor
     float rd[CB];          // pivot reciprocals of that tile
     float bc[4];           // broadcast: nrm, shift, tau
 };
@@ -369,48 +371,114 @@ __device__ __forceinline__ f32x4 update64(f32x4 acc, float (*Xi0)[TS], float (*X
 }
 
 // Wave 0 only: factor the 32x32 tile D (lower part) in registers, lane i = row i (chol.cu:131-142); writes the
-// factor (zeros above the diagonal) to sh.dl and the pivot reciprocals to sh.rd.
+// factor (zeros above the diagonal) to sh.dl and the pivot reciprocals to sh.rd. Column c: every lane scales its
+// entry (l_i), then updates its remaining entries v[k] -= l_i l_k (eager right-looking order, each element's updates
+// in column order). Only the update of column c+1 is on the critical path, so l_{c+1} comes by v_readlane and the
+// next pivot is formed right away; the other l_k go through LDS and their updates overlap the next pivot chain.
 __device__ __forceinline__ void factor32(CholShared& sh, float (*D)[TS], float tau) {
-    const int i = threadIdx.x & 31;
+    const int lane = threadIdx.x & 63, i = lane & 31;
     float v[CB];
 #pragma unroll
     for (int k = 0; k < CB; ++k) v[k] = D[i][k];
     float myrd = 0.0f;
+    float piv = fmaxf(readlane(v[0], 0), tau);
+    float q = rsqrt_sw(piv);
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-        const float piv = fmaxf(readlane(v[c], c), tau);
-        const float q = rsqrt_sw(piv);
         const float l = (i > c) ? v[c] * q : ((i == c) ? piv * q : 0.0f);
         myrd = (i == c) ? q : myrd;
         v[c] = l;
+        if (c + 1 < CB) {
+            v[c + 1] = __builtin_fmaf(-l, readlane(l, c + 1), v[c + 1]);
+            const float pn = fmaxf(readlane(v[c + 1], c + 1), tau);
+            const float qn = rsqrt_sw(pn);
+            if (c + 2 < CB) {
+                if (lane < 32) sh.bl[i] = l;
+                __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int k = c + 1; k < CB; ++k) v[k] = __builtin_fmaf(-l, readlane(l, k), v[k]);
+                for (int k0 = (c + 2) & ~3; k0 < CB; k0 += 4) {
+                    const float4 l4 = *reinterpret_cast<const float4*>(&sh.bl[k0]);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        if (k0 + t > c + 1) v[k0 + t] = __builtin_fmaf(-l, lv[t], v[k0 + t]);
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+            piv = pn;
+            q = qn;
+        }
     }
-    if ((threadIdx.x & 63) < 32) {
+    if (lane < 32) {
 #pragma unroll
         for (int k = 0; k < CB; ++k) sh.dl[i][k] = (k <= i) ? v[k] : 0.0f;
         sh.rd[i] = myrd;
     }
+    __builtin_amdgcn_wave_barrier();
 }
 
-// Wave 0 only: inverse of the factored tile in sh.dl, lane kk = column kk (chol.cu:151-168): x_i = 0 for i < kk,
-// else acc = [i == kk], acc = fma(-L[i][m], x_m, acc) for m = 0..i-1, x_i = acc * rd_i.
+// Wave 0 only: inverse of the factored tile in sh.dl, column kk in lane kk (chol.cu:151-168): x_i = 0 for i < kk,
+// else acc = [i == kk], acc = fma(-L[i][m], x_m, acc) for m = 0..i-1 in order, x_i = acc * rd_i. Rows 0..15 by
+// substitution; for rows 16..31 the terms m < 16 are one MFMA chain (16 rows x 32 columns, k = m in order), then
+// substitution continues with m = 16..i-1.
 __device__ __forceinline__ void inverse32(CholShared& sh, float (*Li)[TS]) {
-    const int kk = threadIdx.x & 31;
+    const int lane = threadIdx.x & 63, kk = lane & 31, l16 = lane & 15, lk = lane >> 4;
     float x[CB];
 #pragma unroll
-    for (int i = 0; i < CB; ++i) {
+    for (int i = 0; i < 16; ++i) {
         float acc = (i == kk) ? 1.0f : 0.0f;
 #pragma unroll
         for (int m = 0; m < i; ++m) acc = __builtin_fmaf(-sh.dl[i][m], x[m], acc);
         x[i] = (i < kk) ? 0.0f : acc * sh.rd[i];
     }
-    if ((threadIdx.x & 63) < 32) {
+    if (lane < 32) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sh.xs[i][kk] = x[i];
+    }
+    __builtin_amdgcn_wave_barrier();
+    f32x4 acc2[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc2[cb][v] = (16 + 4 * lk + v == 16 * cb + l16) ? 1.0f : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            acc2[cb] = mfma(-sh.dl[16 + l16][4 * q + lk], sh.xs[4 * q + lk][16 * cb + l16], acc2[cb]);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sh.xs[4 * lk + v][16 * cb + l16] = acc2[cb][v];
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 16; i < CB; ++i) {
+        float acc = sh.xs[i - 16][kk];
+#pragma unroll
+        for (int m = 16; m < i; ++m) acc = __builtin_fmaf(-sh.dl[i][m], x[m], acc);
+        x[i] = (i < kk) ? 0.0f : acc * sh.rd[i];
+    }
+    if (lane < 32) {
 #pragma unroll
         for (int i = 0; i < CB; ++i) Li[i][kk] = x[i];
     }
+    __builtin_amdgcn_wave_barrier();
 }
 
+// transposed stores: dst[c][r'] = src[r'][c] (for the solve's coalesced operand reads)
+__device__ __forceinline__ void store_tile_T(float* dst, int ld, float (*src)[TS]) {
+    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
+    float4 v;
+    v.x = src[4 * c4 + 0][row]; v.y = src[4 * c4 + 1][row]; v.z = src[4 * c4 + 2][row]; v.w = src[4 * c4 + 3][row];
+    *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+}
+
+__device__ __forceinline__ void store_dl_T(float* dst, int ld, float (*src)[36]) {
+    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
+    float4 v;
+    v.x = src[4 * c4 + 0][row]; v.y = src[4 * c4 + 1][row]; v.z = src[4 * c4 + 2][row]; v.w = src[4 * c4 + 3][row];
+    *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+}
 
 __device__ __forceinline__ void store_dl(float* dst, int ld, float (*src)[36]) {
     const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
@@ -421,32 +489,41 @@ __device__ __forceinline__ void store_dl(float* dst, int ld, float (*src)[36]) {
 // Factor the 64x64 diagonal block held in t[7] (rows/cols 0..31), t[8] (rows 32..63 x cols 0..31), t[9] (rows and
 // cols 32..63) as two 32-wide reference steps: outputs t[0] = Li_a, t[1] = Li_b, t[2] = L_ba and writes the block's
 // L tiles and Li rows to global.
-__device__ void factor_diag64(CholShared& sh, int J, int r, float tau, float* L, float* Li) {
+__device__ __forceinline__ void factor_diag64(CholShared& sh, int J, int r, float tau, float* L, float* Li, float* Lt,
+                                              float* Lit, uint64_t* stamp = nullptr) {
     const int w = threadIdx.x >> 6;
     const size_t o = (size_t)64 * J;
     if (w == 0) {
         factor32(sh, sh.t[7], tau);
+        if (stamp && threadIdx.x == 0) stamp[0] = wall_clock64();
         inverse32(sh, sh.t[0]);
+        if (stamp && threadIdx.x == 0) stamp[1] = wall_clock64();
     }
     __syncthreads();
     store_dl(L + o * r + o, r, sh.dl);
+    store_dl_T(Lt + o * r + o, r, sh.dl);
     store_tile(Li + o * CB, CB, sh.t[0]);
+    store_tile_T(Lit + o * CB, CB, sh.t[0]);
     panel32(sh.t[2], sh.t[8], sh.t[0]);          // L_ba = A_ba Li_a^T
     store_tile(L + (o + 32) * r + o, r, sh.t[2]);
+    store_tile_T(Lt + o * r + o + 32, r, sh.t[2]);
     update32(sh.t[9], sh.t[2], sh.t[2], true);   // A_bb -= L_ba L_ba^T
+    if (stamp && threadIdx.x == 0) stamp[2] = wall_clock64();
     if (w == 0) {
         factor32(sh, sh.t[9], tau);
         inverse32(sh, sh.t[1]);
     }
     __syncthreads();
     store_dl(L + (o + 32) * r + o + 32, r, sh.dl);
+    store_dl_T(Lt + (o + 32) * r + o + 32, r, sh.dl);
     store_tile(Li + (o + 32) * CB, CB, sh.t[1]);
+    store_tile_T(Lit + (o + 32) * CB, CB, sh.t[1]);
     __syncthreads();
 }
 
 // Panel of a 64-row block held in t[base..base+3] = (rows 0-31: cols 0-31, 32-63; rows 32-63: cols 0-31, 32-63)
 // against the current diagonal block (t[0..2]): Q0 = X0 Li_a^T, X1 -= Q0 L_ba^T, Q1 = X1 Li_b^T, in place.
-__device__ void super_panel(CholShared& sh, int base) {
+__device__ __forceinline__ void super_panel(CholShared& sh, int base) {
     for (int h = 0; h < 2; ++h) {
         float (*x0)[TS] = sh.t[base + 2 * h];
         float (*x1)[TS] = sh.t[base + 2 * h + 1];
@@ -470,6 +547,14 @@ __device__ __forceinline__ void store_block64(float* dst, int r, CholShared& sh,
     store_tile(dst + (size_t)32 * r + 32, r, sh.t[base + 3]);
 }
 
+// the transposed block: dst (row stride r) receives block^T, i.e. tile (h, c) of the block goes to (c, h)
+__device__ __forceinline__ void store_block64_T(float* dst, int r, CholShared& sh, int base) {
+    store_tile_T(dst, r, sh.t[base + 0]);
+    store_tile_T(dst + (size_t)32 * r, r, sh.t[base + 1]);
+    store_tile_T(dst + 32, r, sh.t[base + 2]);
+    store_tile_T(dst + (size_t)32 * r + 32, r, sh.t[base + 3]);
+}
+
 // C (in LDS) -= [Xi0 Xi1][Xk0 Xk1]^T
 __device__ __forceinline__ void update64_lds(float (*C)[TS], float (*Xi0)[TS], float (*Xi1)[TS], float (*Xk0)[TS],
                                              float (*Xk1)[TS]) {
@@ -483,8 +568,8 @@ __device__ __forceinline__ void update64_lds(float (*C)[TS], float (*Xi0)[TS], f
 }
 
 // Trailing 64x64 tiles (I, Kc), J < Kc <= I, other than (J+1, J+1), dealt round-robin to `W` workers.
-__device__ void chol_trailing(CholShared& sh, float* A, int r, int NB, int J, float shift, float* L, const float* Li,
-                              int W, int me, bool have_diag) {
+__device__ __forceinline__ void chol_trailing(CholShared& sh, float* A, int r, int NB, int J, float shift, float* L, const float* Li,
+                                              float* Lt, int W, int me, bool have_diag) {
     WAVE_COORDS;
     const size_t oJ = (size_t)64 * J;
     int t = 0;
@@ -533,7 +618,10 @@ __device__ void chol_trailing(CholShared& sh, float* A, int r, int NB, int J, fl
                         A[(oI + rr) * r + oK + cc] = c[hi][hk][v];
                     }
                 }
-            if (Kc == J + 1) store_block64(L + oI * r + oJ, r, sh, 3);
+            if (Kc == J + 1) {
+                store_block64(L + oI * r + oJ, r, sh, 3);
+                store_block64_T(Lt + oJ * r + oI, r, sh, 3);
+            }
             __syncthreads();
         }
 }
@@ -544,12 +632,22 @@ __device__ void chol_trailing(CholShared& sh, float* A, int r, int NB, int J, fl
 // nrm = sqrtf(fp32(sum)), shift = alpha * nrm added to the diagonal on first load, tau = tau_rel * nrm + 1e-30
 // (kcholqr.py:107-109). Workgroup 0 factors diagonal blocks (look-ahead), the others update trailing tiles; one grid
 // barrier per 64 columns.
+template <bool STAMP>
 __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
-                                              float tau_rel, float* L, float* Li, uint32_t* bar, float* scal) {
+                                              float tau_rel, float* L, float* Li, float* Lt, float* Lit, uint32_t* bar,
+                                              float* scal, uint64_t* stamps) {
     __shared__ CholShared sh;
+    // STAMP: workgroup 0 records wall_clock64() at phase boundaries, 12 slots per 64-column step s: 0 loads done,
+    // 1 panel done, 2 diagonal update done, 3 first tile factored, 4 first tile inverted, 5 second tile update done,
+    // 6 block done, 7 after the grid barrier; step 0 also has 9 kernel start, 8 norm done.
+#define CHOL_STAMP(J_, k_)                                                                  \
+    do {                                                                                    \
+        if (STAMP && b == 0 && threadIdx.x == 0) stamps[(J_) * 12 + (k_)] = wall_clock64(); \
+    } while (0)
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int G = gridDim.x, b = blockIdx.x, NB = r / 64;
     uint32_t* err = bar + 2;
+    CHOL_STAMP(0, 9);
     if (w == 0) {
         double s = 0.0;
         for (int p = lane; p < nnp; p += 64) s = s + npart[p];
@@ -569,6 +667,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     }
     __syncthreads();
     const float shift = sh.bc[1], tau = sh.bc[2];
+    CHOL_STAMP(0, 8);
     if (b == 0 && tid == 0 && scal != nullptr) {
         scal[0] = sh.bc[0];
         scal[1] = tau;
@@ -578,11 +677,14 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         load_tile(sh.t[8], A + (size_t)32 * r, r, false, 0.f);
         load_tile(sh.t[9], A + (size_t)32 * r + 32, r, true, shift);
         __syncthreads();
-        factor_diag64(sh, 0, r, tau, L, Li);
+        CHOL_STAMP(0, 2);
+        factor_diag64(sh, 0, r, tau, L, Li, Lt, Lit, STAMP ? stamps + 3 : nullptr);
+        CHOL_STAMP(0, 6);
     }
     grid_barrier(bar, G, err);
+    CHOL_STAMP(0, 7);
     for (int J = 0; J + 1 < NB; ++J) {
-        if (G == 1) chol_trailing(sh, A, r, NB, J, shift, L, Li, 1, 0, true);
+        if (G == 1) chol_trailing(sh, A, r, NB, J, shift, L, Li, Lt, 1, 0, true);
         if (b == 0) {
             const size_t oJ = (size_t)64 * J, oI = oJ + 64;
             load_block64(sh, 3, A + oI * r + oJ, r);
@@ -590,101 +692,203 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             load_tile(sh.t[8], A + (oI + 32) * r + oI, r, false, 0.f);
             load_tile(sh.t[9], A + (oI + 32) * r + oI + 32, r, J == 0, shift);
             __syncthreads();
+            CHOL_STAMP(J + 1, 0);
             super_panel(sh, 3);
+            CHOL_STAMP(J + 1, 1);
             store_block64(L + oI * r + oJ, r, sh, 3);
+            store_block64_T(Lt + oJ * r + oI, r, sh, 3);
             update64_lds(sh.t[7], sh.t[3], sh.t[4], sh.t[3], sh.t[4]);
             update64_lds(sh.t[8], sh.t[5], sh.t[6], sh.t[3], sh.t[4]);
             update64_lds(sh.t[9], sh.t[5], sh.t[6], sh.t[5], sh.t[6]);
             __syncthreads();
-            factor_diag64(sh, J + 1, r, tau, L, Li);
+            CHOL_STAMP(J + 1, 2);
+            factor_diag64(sh, J + 1, r, tau, L, Li, Lt, Lit, STAMP ? stamps + 12 * (J + 1) + 3 : nullptr);
+            CHOL_STAMP(J + 1, 6);
         } else {
-            chol_trailing(sh, A, r, NB, J, shift, L, Li, G - 1, b - 1, false);
+            chol_trailing(sh, A, r, NB, J, shift, L, Li, Lt, G - 1, b - 1, false);
         }
         grid_barrier(bar, G, err);
+        CHOL_STAMP(J + 1, 7);
     }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Triangular solve Y = A L^-T (tri.py:378-412), 16 rows per workgroup. Wave w owns column blocks j = w, w+4, ...
-// and keeps their accumulators (acc_j starts at a_j; pass 1: fmaf(eps, z, s * x)). For k = 0..nbc-1 the owner of
-// block k forms Y_k = acc_k Li_k^T (chain over m < 16 (c/16 + 1)), publishes it in LDS, and every wave applies it to
-// its later blocks: acc_j -= Y_k L_jk^T (chain over the 32 columns of block k), so each element's chain runs over
-// m = 0..32j-1 in order.
+// Triangular solve Y = A L^-T (tri.py:378-412). A workgroup takes RB blocks of 16 rows; wave w owns the 32-column
+// blocks j = w, w+4, ... of all of them and keeps their accumulators (acc_j starts at a_j; pass 1:
+// fmaf(eps, z, s * x)). For k = 0..nbc-1 the owner of block k forms Y_k = acc_k Li_k^T (chain over
+// m < 16 (c/16 + 1)), publishes it in LDS behind a flag, and every wave applies it to its later blocks:
+// acc_j -= Y_k L_jk^T (chain over the 32 columns of block k), so each element's chain runs over m = 0..32j-1 in
+// order. Waves synchronise only through those per-block flags (bounded waits); each wave prefetches the L and Li
+// operands of step k+1 into registers while it works on step k. The operands come from the transposed copies Lt = L^T
+// and Lit (each 32x32 block of Li transposed), which the Cholesky writes, so 16 lanes read 16 consecutive floats.
 // ---------------------------------------------------------------------------------------------------------------
-template <bool PASS1, int Q>
+constexpr uint32_t FLAG_SPIN_LIMIT = 1u << 22;
+
+template <int Q>
+struct TrsmOps {
+    float l[Q][2][8];    // L_jk B operands: [owned block][column half][kk]
+};
+
+// Li_k B operands (block-lower: kk < 4 (cb + 1)) for the owner of block k
+__device__ __forceinline__ void trsm_fetch_li(float (&li)[2][8], const float* __restrict__ Lit, int nbc, int k, int l16,
+                                              int lk) {
+    if (k >= nbc) return;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            if (kk < 4 * (cb + 1)) li[cb][kk] = Lit[(size_t)(CB * k + 4 * kk + lk) * CB + 16 * cb + l16];
+}
+
+template <int Q>
+__device__ __forceinline__ void trsm_fetch(TrsmOps<Q>& o, const float* __restrict__ Lt, const float* __restrict__ Lit,
+                                           int r, int nbc, int k, int w, int l16, int lk) {
+    if (k >= nbc) return;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int j = w + 4 * q;
+        if (j > k && j < nbc) {
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk)
+                    o.l[q][cb][kk] = Lt[(size_t)(CB * k + 4 * kk + lk) * r + CB * j + 16 * cb + l16];
+        }
+    }
+}
+
+template <bool PASS1, int Q, int RB>
 __global__ __launch_bounds__(256) void k_trsm(const float* __restrict__ A, long lda, int K, int r,
                                               const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
-                                              float eps, const float* __restrict__ L, const float* __restrict__ Li,
+                                              float eps, const float* __restrict__ Lt, const float* __restrict__ Lit,
                                               float* __restrict__ Y, long ldy, float* scal) {
     extern __shared__ float smem[];
     const int ldsy = r + 4;
-    float* sY = smem;                      // [16][r + 4]
-    float* sAcc = smem + 16 * ldsy;        // [4][16][33]
+    float* sY = smem;                          // [16 RB][r + 4]: finished Y columns (MFMA A operands)
+    float* sAcc = sY + 16 * RB * ldsy;         // [4][16][33]: per-wave transpose of the block being finished
+    uint32_t* sFlag = reinterpret_cast<uint32_t*>(sAcc + 4 * 16 * 33);   // [nbc]
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
-    const int row0 = blockIdx.x * 16, nbc = r / CB;
+    const int row0 = blockIdx.x * 16 * RB, nbc = r / CB;
     float sc = 1.0f;
     if (PASS1) {
         sc = block_scale(amax_part);
         if (blockIdx.x == 0 && tid == 0 && scal != nullptr) scal[0] = sc;
     }
-    f32x4 acc[Q][2];
+    for (int k = tid; k < nbc; k += 256) sFlag[k] = 0u;
+    f32x4 acc[RB][Q][2];
 #pragma unroll
-    for (int q = 0; q < Q; ++q) {
-        const int j = w + 4 * q;
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
+        for (int q = 0; q < Q; ++q) {
+            const int j = w + 4 * q;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = row0 + 4 * lk + v, col = CB * j + 16 * cb + l16;
-                float x = 0.0f;
-                if (j < nbc && row < K) {
-                    x = A[(size_t)row * lda + col];
-                    if (PASS1) x = __builtin_fmaf(eps, Z[(size_t)row * r + col], sc * x);
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = row0 + 16 * rb + 4 * lk + v, col = CB * j + 16 * cb + l16;
+                    float x = 0.0f;
+                    if (j < nbc && row < K) {
+                        x = A[(size_t)row * lda + col];
+                        if (PASS1) x = __builtin_fmaf(eps, Z[(size_t)row * r + col], sc * x);
+                    }
+                    acc[rb][q][cb][v] = x;
                 }
-                acc[q][cb][v] = x;
+        }
+    TrsmOps<Q> cur, nxt;
+    trsm_fetch<Q>(cur, Lt, Lit, r, nbc, 0, w, l16, lk);
+    float li[2][8];   // Li of this wave's next block to finish (fetched four steps ahead)
+    trsm_fetch_li(li, Lit, nbc, w, l16, lk);
+    __syncthreads();   // flags cleared
+    // finish block k (owner only): Y_k = acc_k Li_k^T into sY and Y, then raise its flag
+    auto finish = [&](int k, int qk) {
+        float* sa = sAcc + w * 16 * 33;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) sa[(4 * lk + v) * 33 + 16 * cb + l16] = acc[rb][qk][cb][v];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk)
+                    if (kk < 4 * (cb + 1)) y = mfma(sa[l16 * 33 + 4 * kk + lk], li[cb][kk], y);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int rl = 16 * rb + 4 * lk + v, col = CB * k + 16 * cb + l16;
+                    sY[rl * ldsy + col] = y[v];
+                    if (row0 + rl < K) Y[(size_t)(row0 + rl) * ldy + col] = y[v];
+                }
             }
-    }
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (lane == 0) __hip_atomic_store(&sFlag[k], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        trsm_fetch_li(li, Lit, nbc, k + 4, l16, lk);
+    };
+    // acc_j -= Y_k L_jk^T for owned block q
+    auto apply = [&](int k, int q) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const float a = -sY[(16 * rb + l16) * ldsy + CB * k + 4 * kk + lk];
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) acc[rb][q][cb] = mfma(a, cur.l[q][cb][kk], acc[rb][q][cb]);
+            }
+    };
+    if (w == 0) finish(0, 0);
 #pragma unroll
     for (int qk = 0; qk < Q; ++qk) {
+#pragma unroll
         for (int ow = 0; ow < 4; ++ow) {
             const int k = 4 * qk + ow;
-            if (k >= nbc) break;
-            if (w == ow) {
-                float* sa = sAcc + w * 16 * 33;
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) sa[(4 * lk + v) * 33 + 16 * cb + l16] = acc[qk][cb][v];
-                __builtin_amdgcn_wave_barrier();
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb) {
-                    f32x4 y = {0.f, 0.f, 0.f, 0.f};
-                    for (int kk = 0; kk < 4 * (cb + 1); ++kk)
-                        y = mfma(sa[l16 * 33 + 4 * kk + lk], Li[(size_t)(CB * k + 16 * cb + l16) * CB + 4 * kk + lk], y);
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int rl = 4 * lk + v, col = CB * k + 16 * cb + l16;
-                        sY[rl * ldsy + col] = y[v];
-                        if (row0 + rl < K) Y[(size_t)(row0 + rl) * ldy + col] = y[v];
+            if (k < nbc) {
+                trsm_fetch<Q>(nxt, Lt, Lit, r, nbc, k + 1, w, l16, lk);
+                if (w != ow) {
+                    uint32_t n = 0;
+                    while (__hip_atomic_load(&sFlag[k], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u) {
+                        if (++n > FLAG_SPIN_LIMIT) break;
+                        __builtin_amdgcn_s_sleep(1);
                     }
                 }
-            }
-            __syncthreads();
+                // the owner of block k+1 brings it up to date and publishes it before its other updates
+                const int kn = k + 1, qn = kn >> 2;
 #pragma unroll
-            for (int q = 0; q < Q; ++q) {
-                const int j = w + 4 * q;
-                if (j > k && j < nbc) {
-#pragma unroll
-                    for (int kk = 0; kk < 8; ++kk) {
-                        const float a = -sY[l16 * ldsy + CB * k + 4 * kk + lk];
-#pragma unroll
-                        for (int cb = 0; cb < 2; ++cb)
-                            acc[q][cb] = mfma(a, L[(size_t)(CB * j + 16 * cb + l16) * r + CB * k + 4 * kk + lk],
-                                              acc[q][cb]);
-                    }
+                for (int q = 0; q < Q; ++q) {
+                    const int j = w + 4 * q;
+                    if (j == kn && j < nbc) apply(k, q);
                 }
+#pragma unroll
+                for (int q = 0; q < Q; ++q) {
+                    const int j = w + 4 * q;
+                    if (j == kn && j < nbc) finish(kn, q);
+                }
+                (void)qn;
+#pragma unroll
+                for (int q = 0; q < Q; ++q) {
+                    const int j = w + 4 * q;
+                    if (j > kn && j < nbc) apply(k, q);
+                }
+                cur = nxt;
             }
         }
+    }
+}
+
+// Lt = L^T (lower tiles of L, r x r) and Lit = per-32-block transposes of Li (r x 32), for the stage entry point that
+// takes row-major L and Li.
+__global__ __launch_bounds__(256) void k_transpose_factors(const float* __restrict__ L, const float* __restrict__ Li,
+                                                           int r, float* __restrict__ Lt, float* __restrict__ Lit) {
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e < r * r) {
+        const int i = e / r, j = e - i * r;
+        Lt[(size_t)j * r + i] = L[e];
+    }
+    if (e < r * CB) {
+        const int i = e / CB, m = e - i * CB, blk = i / CB, c = i - blk * CB;
+        Lit[(size_t)(blk * CB + m) * CB + c] = Li[e];
     }
 }
 
@@ -776,15 +980,19 @@ inline uint64_t mix64(uint64_t z) {
 
 struct spanqr_plan {
     int K = 0, r = 0, device = 0;
-    int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0;
+    int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0, trsm_rb = 1;
     size_t bytes = 0;
     char* base = nullptr;
     float *Z = nullptr, *P = nullptr, *G = nullptr, *L = nullptr, *Li = nullptr, *Y0 = nullptr, *Y1 = nullptr;
+    float *Lt = nullptr, *Lit = nullptr;   // L^T and the per-block transposes of Li (solve operands)
     float* scal = nullptr;     // s, nrm0, tau0, nrm1, tau1, nrm2, tau2, barrier error (as float bits)
     float* chscal = nullptr;   // per-launch Cholesky scalars (nrm, tau, err)
     double* npart = nullptr;
     uint32_t* amax_part = nullptr;
     uint32_t* bar = nullptr;   // [count, generation, error, pad]
+    uint64_t* stamps = nullptr;  // Cholesky phase stamps (profiling), 12 per 64-column step
+    hipEvent_t ev[64] = {};    // profiling: one event before and after each kernel of a call
+    int nev = 0;
 };
 
 namespace {
@@ -811,7 +1019,7 @@ int check_mat(const spanqr_plan* p, const float* M, long ld, const char* name) {
     return SPANQR_OK;
 }
 
-size_t trsm_lds(int r) { return (size_t)(16 * (r + 4) + 4 * 16 * 33) * sizeof(float); }
+size_t trsm_lds(int r, int rb) { return (size_t)(16 * rb * (r + 4) + 4 * 16 * 33 + r / CB) * sizeof(float); }
 
 void launch_gram(const spanqr_plan* p, const float* A, long lda, bool scale, bool kahan, hipStream_t st) {
     const dim3 grid(p->U, p->S);
@@ -827,43 +1035,133 @@ void launch_reduce(const spanqr_plan* p, int mode, float* out, hipStream_t st) {
     else k_reduce<1><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart);
 }
 
-int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t st, int nnp) {
+int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t st, int nnp, bool stamp = false) {
     float* A = p->G;
     int r = p->r;
     const double* np = p->npart;
     float* L = p->L;
     float* Li = p->Li;
     uint32_t* bar = p->bar;
-    void* args[] = {&A, &r, (void*)&np, &nnp, &alpha, &tau, &L, &Li, &bar, &scal};
-    HIPCHK(hipLaunchCooperativeKernel((const void*)k_chol, dim3(p->chol_grid), dim3(256), args, 0, st));
+    uint64_t* stamps = p->stamps;
+    float* Lt = p->Lt;
+    float* Lit = p->Lit;
+    void* args[] = {&A, &r, (void*)&np, &nnp, &alpha, &tau, &L, &Li, &Lt, &Lit, &bar, &scal, &stamps};
+    const void* fn = stamp ? (const void*)k_chol<true> : (const void*)k_chol<false>;
+    HIPCHK(hipLaunchCooperativeKernel(fn, dim3(p->chol_grid), dim3(256), args, 0, st));
     return SPANQR_OK;
+}
+
+template <int Q, int RB>
+hipError_t trsm_set_lds(int r) {
+    const int need = (int)trsm_lds(r, RB);
+    hipError_t e = hipFuncSetAttribute((const void*)k_trsm<true, Q, RB>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)k_trsm<false, Q, RB>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
+    return e;
+}
+
+hipError_t trsm_set_lds_plan(int q, int rb, int r) {
+#define TRSM_ATTR(QQ)                                         \
+    case QQ:                                                  \
+        if (rb == 4) return trsm_set_lds<QQ, 4>(r);           \
+        if (rb == 2) return trsm_set_lds<QQ, 2>(r);           \
+        return trsm_set_lds<QQ, 1>(r);
+    switch (q) {
+        TRSM_ATTR(1)
+        TRSM_ATTR(2)
+        TRSM_ATTR(3)
+        default:
+        TRSM_ATTR(4)
+    }
+#undef TRSM_ATTR
+}
+
+template <int Q, int RB>
+void launch_trsm_t(const spanqr_plan* p, const float* A, long lda, bool pass1, float eps, const float* L,
+                   const float* Li, float* Y, long ldy, hipStream_t st) {
+    const dim3 grid((p->K + 16 * RB - 1) / (16 * RB));
+    const size_t lds = trsm_lds(p->r, RB);
+    if (pass1) k_trsm<true, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, L, Li, Y, ldy,
+                                                           p->scal);
+    else k_trsm<false, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, L, Li, Y, ldy,
+                                                      p->scal);
+}
+
+template <int Q>
+void launch_trsm_q(const spanqr_plan* p, const float* A, long lda, bool pass1, float eps, const float* L,
+                   const float* Li, float* Y, long ldy, hipStream_t st) {
+    switch (p->trsm_rb) {
+        case 4: launch_trsm_t<Q, 4>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
+        case 2: launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
+        default: launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
+    }
 }
 
 void launch_trsm(const spanqr_plan* p, const float* A, long lda, bool pass1, float eps, const float* L,
                  const float* Li, float* Y, long ldy, hipStream_t st) {
-    const dim3 grid((p->K + 15) / 16);
-    const size_t lds = trsm_lds(p->r);
-    float* scal = p->scal;
-#define TRSM_CASE(QQ)                                                                                            \
-    case QQ:                                                                                                     \
-        if (pass1) k_trsm<true, QQ><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, L, Li, \
-                                                            Y, ldy, scal);                                       \
-        else k_trsm<false, QQ><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, L, Li, Y,   \
-                                                       ldy, scal);                                               \
-        break;
     switch (p->trsm_q) {
-        TRSM_CASE(1)
-        TRSM_CASE(2)
-        TRSM_CASE(3)
-        TRSM_CASE(4)
-        default: break;
+        case 1: launch_trsm_q<1>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
+        case 2: launch_trsm_q<2>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
+        case 3: launch_trsm_q<3>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
+        default: launch_trsm_q<4>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
     }
-#undef TRSM_CASE
 }
 
 void launch_nsapply(const spanqr_plan* p, const float* Y, long ldy, float* Out, long ldo, hipStream_t st) {
     const dim3 grid((p->K + 31) / 32, p->r / 64);
     k_nsapply<<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo);
+}
+
+
+// The whole call on one stream: amax, 3 x {gram, reduce, chol, trsm}, ns x {gram, reduce, nsapply}.
+// With rec, an event is recorded after every kernel (profiling).
+int enqueue_orth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, float eps, float alpha, float tau,
+                 int ns, hipStream_t st, bool rec) {
+    int rc;
+    auto mark = [&]() -> int {
+        if (rec) {
+            HIPCHK(hipEventRecord(p->ev[p->nev], st));
+            ++p->nev;
+        }
+        return SPANQR_OK;
+    };
+    k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(X, ldx, p->K, p->r, p->amax_part);
+    if ((rc = mark())) return rc;
+    const float* in = X;
+    long ldin = ldx;
+    float* bufs[2] = {p->Y0, p->Y1};
+    int cur = 0;
+    for (int pass = 0; pass < 3; ++pass) {
+        launch_gram(p, in, ldin, pass == 0, pass == 0, st);
+        if ((rc = mark())) return rc;
+        launch_reduce(p, 0, p->G, st);
+        if ((rc = mark())) return rc;
+        if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U))) return rc;
+        if ((rc = mark())) return rc;
+        launch_trsm(p, in, ldin, pass == 0, eps, p->Lt, p->Lit, bufs[cur], p->r, st);
+        if ((rc = mark())) return rc;
+        in = bufs[cur];
+        ldin = p->r;
+        cur ^= 1;
+    }
+    for (int i = 0; i < ns; ++i) {
+        launch_gram(p, in, ldin, false, i == ns - 1, st);
+        if ((rc = mark())) return rc;
+        launch_reduce(p, 1, p->G, st);
+        if ((rc = mark())) return rc;
+        if (i == ns - 1) {
+            launch_nsapply(p, in, ldin, Q, ldq, st);
+        } else {
+            launch_nsapply(p, in, ldin, bufs[cur], p->r, st);
+            in = bufs[cur];
+            cur ^= 1;
+        }
+        if ((rc = mark())) return rc;
+    }
+    if (ns == 0) HIPCHK(hipMemcpy2DAsync(Q, ldq * sizeof(float), in, ldin * sizeof(float), p->r * sizeof(float), p->K,
+                                         hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
 }
 
 }  // namespace
@@ -912,8 +1210,24 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
     p->chol_grid = 1 + (ntrail > 0 ? ntrail : 0);
     if (p->chol_grid > 64) p->chol_grid = 64;
     p->trsm_q = (r / CB + 3) / 4;
+    // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU
+    p->trsm_rb = ((K + 15) / 16 >= 2048) ? 4 : ((K + 15) / 16 >= 1024 ? 2 : 1);
+    {
+        const size_t need = trsm_lds(r, p->trsm_rb);
+        int maxsh = 0;
+        HIPCHK(hipDeviceGetAttribute(&maxsh, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+        if ((size_t)maxsh < need) {
+            delete p;
+            return fail(SPANQR_EHIP, "the solve needs %zu bytes of LDS per workgroup, device allows %d", need, maxsh);
+        }
+        const hipError_t e = trsm_set_lds_plan(p->trsm_q, p->trsm_rb, r);
+        if (e != hipSuccess) {
+            delete p;
+            return fail(SPANQR_EHIP, "setting the solve's LDS size failed: %s", hipGetErrorString(e));
+        }
+    }
     int occ = 0, cus = 0;
-    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol, 256, 0));
+    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol<true>, 256, 0));
     HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
     if (occ * cus < p->chol_grid) {
         const int need = p->chol_grid;
@@ -926,8 +1240,8 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
     const size_t sz_Z = al(nKr), sz_P = al((size_t)p->S * p->U * TB * TB * sizeof(float));
     const size_t sz_rr = al((size_t)r * r * sizeof(float)), sz_Li = al((size_t)r * CB * sizeof(float));
     const size_t sz_Y = al(nKr), sz_sc = 256, sz_np = al((size_t)16 * p->U * sizeof(double));
-    const size_t sz_am = al(AMAX_BLOCKS * sizeof(uint32_t)), sz_bar = 256;
-    p->bytes = sz_Z + sz_P + 2 * sz_rr + sz_Li + 2 * sz_Y + 2 * sz_sc + sz_np + sz_am + sz_bar;
+    const size_t sz_am = al(AMAX_BLOCKS * sizeof(uint32_t)), sz_bar = 256, sz_st = al(12 * 8 * sizeof(uint64_t));
+    p->bytes = sz_Z + sz_P + 3 * sz_rr + 2 * sz_Li + 2 * sz_Y + 2 * sz_sc + sz_np + sz_am + sz_bar + sz_st;
     if (hipMalloc((void**)&p->base, p->bytes) != hipSuccess) {
         const size_t nb = p->bytes;
         delete p;
@@ -939,6 +1253,8 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
     p->G = (float*)c; c += sz_rr;
     p->L = (float*)c; c += sz_rr;
     p->Li = (float*)c; c += sz_Li;
+    p->Lt = (float*)c; c += sz_rr;
+    p->Lit = (float*)c; c += sz_Li;
     p->Y0 = (float*)c; c += sz_Y;
     p->Y1 = (float*)c; c += sz_Y;
     p->scal = (float*)c; c += sz_sc;
@@ -946,11 +1262,12 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
     p->npart = (double*)c; c += sz_np;
     p->amax_part = (uint32_t*)c; c += sz_am;
     p->bar = (uint32_t*)c; c += sz_bar;
+    p->stamps = (uint64_t*)c; c += sz_st;
     float* hz = (float*)malloc(nKr);
     int rc = hz ? spanqr_dust_host(K, r, hz) : fail(SPANQR_ENOMEM, "host dust buffer");
     if (rc == SPANQR_OK) {
         if (hipMemcpy(p->Z, hz, nKr, hipMemcpyHostToDevice) != hipSuccess ||
-            hipMemset(p->L, 0, sz_rr) != hipSuccess || hipMemset(p->scal, 0, 2 * sz_sc) != hipSuccess ||
+            hipMemset(p->L, 0, sz_rr) != hipSuccess || hipMemset(p->Lt, 0, sz_rr) != hipSuccess || hipMemset(p->scal, 0, 2 * sz_sc) != hipSuccess ||
             hipMemset(p->bar, 0, sz_bar) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
             rc = fail(SPANQR_EHIP, "plan upload failed");
     }
@@ -968,6 +1285,8 @@ void spanqr_plan_destroy(spanqr_plan* p) {
     if (!p) return;
     DeviceGuard dg(p->device);
     (void)hipDeviceSynchronize();
+    for (int i = 0; i < 64; ++i)
+        if (p->ev[i]) (void)hipEventDestroy(p->ev[i]);
     (void)hipFree(p->base);
     delete p;
 }
@@ -995,35 +1314,27 @@ int spanqr_orth_f32(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq
     if (ns < 0) return fail(SPANQR_EINVAL, "ns = %d < 0", ns);
     DeviceGuard dg(p->device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
+    return enqueue_orth(p, X, ldx, Q, ldq, eps, alpha, tau, ns, (hipStream_t)stream, false);
+}
+
+int spanqr_profile_orth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
+                        float tau, int ns, void* stream, float* ms, int max_n, int* n_out) {
+    if (!p || !ms || !n_out) return fail(SPANQR_EINVAL, "null argument");
+    int rc = check_mat(p, X, ldx, "X");
+    if (rc) return rc;
+    if ((rc = check_mat(p, Q, ldq, "Q"))) return rc;
+    if (ns < 0 || 1 + 12 + 3 * ns > 63) return fail(SPANQR_EINVAL, "ns = %d out of range for profiling", ns);
+    DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
-    k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(X, ldx, p->K, p->r, p->amax_part);
-    const float* in = X;
-    long ldin = ldx;
-    float* bufs[2] = {p->Y0, p->Y1};
-    int cur = 0;
-    for (int pass = 0; pass < 3; ++pass) {
-        launch_gram(p, in, ldin, pass == 0, pass == 0, st);
-        launch_reduce(p, 0, p->G, st);
-        if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U))) return rc;
-        launch_trsm(p, in, ldin, pass == 0, eps, p->L, p->Li, bufs[cur], p->r, st);
-        in = bufs[cur];
-        ldin = p->r;
-        cur ^= 1;
-    }
-    for (int i = 0; i < ns; ++i) {
-        launch_gram(p, in, ldin, false, i == ns - 1, st);
-        launch_reduce(p, 1, p->G, st);
-        if (i == ns - 1) {
-            launch_nsapply(p, in, ldin, Q, ldq, st);
-        } else {
-            launch_nsapply(p, in, ldin, bufs[cur], p->r, st);
-            in = bufs[cur];
-            cur ^= 1;
-        }
-    }
-    if (ns == 0) HIPCHK(hipMemcpy2DAsync(Q, ldq * sizeof(float), in, ldin * sizeof(float), p->r * sizeof(float), p->K,
-                                         hipMemcpyDeviceToDevice, st));
-    HIPCHK(hipGetLastError());
+    for (int i = 0; i < 64; ++i)
+        if (!p->ev[i]) HIPCHK(hipEventCreate(&p->ev[i]));
+    HIPCHK(hipEventRecord(p->ev[0], st));
+    p->nev = 1;
+    if ((rc = enqueue_orth(p, X, ldx, Q, ldq, eps, alpha, tau, ns, st, true))) return rc;
+    HIPCHK(hipEventSynchronize(p->ev[p->nev - 1]));
+    const int n = p->nev - 1 < max_n ? p->nev - 1 : max_n;
+    for (int i = 0; i < n; ++i) HIPCHK(hipEventElapsedTime(&ms[i], p->ev[i], p->ev[i + 1]));
+    *n_out = n;
     return SPANQR_OK;
 }
 
@@ -1079,7 +1390,9 @@ int spanqr_stage_trsm(spanqr_plan* p, const float* A, long lda, int pass1, float
     if (rc) return rc;
     if ((rc = check_mat(p, Y, ldy, "Y"))) return rc;
     DeviceGuard dg(p->device);
-    launch_trsm(p, A, lda, pass1 != 0, eps, L, Li, Y, ldy, (hipStream_t)stream);
+    hipStream_t st = (hipStream_t)stream;
+    k_transpose_factors<<<(p->r * p->r + 255) / 256, 256, 0, st>>>(L, Li, p->r, p->Lt, p->Lit);
+    launch_trsm(p, A, lda, pass1 != 0, eps, p->Lt, p->Lit, Y, ldy, st);
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
@@ -1095,6 +1408,24 @@ int spanqr_stage_ns(spanqr_plan* p, const float* Y, long ldy, int kahan, float* 
     launch_reduce(p, 1, p->G, st);
     launch_nsapply(p, Y, ldy, Yout, ldo, st);
     HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
+int spanqr_profile_chol(spanqr_plan* p, const float* G, const double* npart, float alpha, float tau,
+                        unsigned long long* stamps_out, double* tick_ns, void* stream) {
+    if (!p || !G || !npart || !stamps_out || !tick_ns) return fail(SPANQR_EINVAL, "null argument");
+    DeviceGuard dg(p->device);
+    hipStream_t st = (hipStream_t)stream;
+    HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemsetAsync(p->stamps, 0, 12 * 8 * sizeof(uint64_t), st));
+    int rc = launch_chol(p, alpha, tau, p->chscal, st, 16 * p->U, true);
+    if (rc) return rc;
+    HIPCHK(hipMemcpyAsync(stamps_out, p->stamps, (size_t)12 * p->NB * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    int khz = 0;
+    HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, p->device));
+    *tick_ns = khz > 0 ? 1e6 / khz : 0.0;
     return SPANQR_OK;
 }
 
