@@ -40,7 +40,7 @@ enum {
     SPANQR_Q_R = 1,
     SPANQR_Q_SPLITS = 2,         /* Gram row splits S */
     SPANQR_Q_SPLIT_ROWS = 3,     /* rows per split KS (a multiple of 32) */
-    SPANQR_Q_CHOL_GRID = 4,      /* workgroups of the cooperative Cholesky */
+    SPANQR_Q_CHOL_GRID = 4,      /* workgroups of the grid-synchronised Cholesky */
     SPANQR_Q_WORKSPACE_MB = 5,   /* workspace size, MiB (rounded up) */
     SPANQR_Q_DEVICE = 6,
 };

@@ -1,7 +1,7 @@
 // spanqr.hip -- MI355X (gfx950) kernels and C ABI for orth(X), a robust shifted Cholesky-QR.
 //
 // Reference algorithm: candidates/kcholqr.py:92-112 (kcholf) with its kernels candidates/tri.py:255-412 (Gram, TRSM)
-// and candidates/cuk/chol.cu:1-281 (cooperative clamped Cholesky). Everything here is fp32 on gfx950 MFMA/VALU
+// and candidates/cuk/chol.cu:1-281 (grid-synchronised clamped Cholesky). Everything here is fp32 on gfx950 MFMA/VALU
 // except the fp64 split sums and norm. The design is this project's own:
 //   * every dot product is one v_mfma_f32_16x16x4_f32 chain per output element, which rounds like a sequential
 //     fmaf chain in summation order, so each element has one fixed IEEE operation sequence (bit-deterministic, and
@@ -9,7 +9,7 @@
 //   * the Gram is a split-K SYRK over upper 64x64 tiles with a fixed, shape-derived split count (no CU-count
 //     dependence), Kahan-compensated per 32-row chunk where the reference compensates, and reduced in fp64 in split
 //     order by a separate kernel that also emits fixed-order partials of ||G||_F^2;
-//   * the Cholesky is one cooperative kernel stepping 64 columns (two 32-wide reference steps) per grid barrier:
+//   * the Cholesky is one persistent, grid-synchronised kernel stepping 64 columns (two 32-wide reference steps) per grid barrier:
 //     workgroup 0 factors the next 64x64 diagonal block (look-ahead) while the others update the trailing 64x64
 //     tiles; the 32x32 diagonal tiles are factored in one wavefront's registers (lane = row) and inverted (lane =
 //     column) as a by-product;
@@ -266,13 +266,16 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Cooperative clamped Cholesky (chol.cu:182-271 restated for 64-column super-steps).
+// Grid-synchronised clamped Cholesky (chol.cu:182-271 restated for 64-column super-steps).
 // ---------------------------------------------------------------------------------------------------------------
 
 // Grid barrier: every wave waits for its own stores, the workgroup meets, thread 0 arrives with an agent-scope
 // release and waits with agent-scope acquires (bounded: after SPIN_LIMIT polls it records an error and goes on, so
-// the kernel always ends). bar[0] counts arrivals and returns to 0, bar[1] is the generation.
-__device__ __forceinline__ void grid_barrier(uint32_t* bar, uint32_t nblocks, uint32_t* err) {
+// the kernel always ends; once it has timed out, `dead` makes its later waits return at once). bar[0] counts
+// arrivals and returns to 0, bar[1] is the generation. The grid is launched as an ordinary dispatch of at most 64
+// workgroups; plan creation checks that the device holds them all at once (occupancy x CUs), which is what the
+// barrier needs.
+__device__ __forceinline__ void grid_barrier(uint32_t* bar, uint32_t nblocks, uint32_t* err, bool& dead) {
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -283,9 +286,10 @@ __device__ __forceinline__ void grid_barrier(uint32_t* bar, uint32_t nblocks, ui
             __hip_atomic_fetch_add(bar + 1, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         } else {
             uint32_t n = 0;
-            while (__hip_atomic_load(bar + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g) {
+            while (!dead && __hip_atomic_load(bar + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g) {
                 if (++n > SPIN_LIMIT) {
                     __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    dead = true;
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
@@ -626,7 +630,7 @@ __device__ __forceinline__ void chol_trailing(CholShared& sh, float* A, int r, i
         }
 }
 
-// Cooperative clamped Cholesky of the Gram in A (r x r, lower tiles read, destroyed). With nnp == 0 the shift is 0
+// Grid-synchronised clamped Cholesky of the Gram in A (r x r, lower tiles read, destroyed). With nnp == 0 the shift is 0
 // and tau_rel is the absolute pivot floor (chol32's contract). Otherwise ||G||_F comes from the nnp fp64 partials:
 // lane l of wave 0 sums npart[l], npart[l + 64], ... in order, then a shift-down tree over the 64 lane sums;
 // nrm = sqrtf(fp32(sum)), shift = alpha * nrm added to the diagonal on first load, tau = tau_rel * nrm + 1e-30
@@ -647,6 +651,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int G = gridDim.x, b = blockIdx.x, NB = r / 64;
     uint32_t* err = bar + 2;
+    bool dead = false;     // thread 0's barrier timed out once (only thread 0 reads it)
     CHOL_STAMP(0, 9);
     if (w == 0) {
         double s = 0.0;
@@ -681,7 +686,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         factor_diag64(sh, 0, r, tau, L, Li, Lt, Lit, STAMP ? stamps + 3 : nullptr);
         CHOL_STAMP(0, 6);
     }
-    grid_barrier(bar, G, err);
+    grid_barrier(bar, G, err, dead);
     CHOL_STAMP(0, 7);
     for (int J = 0; J + 1 < NB; ++J) {
         if (G == 1) chol_trailing(sh, A, r, NB, J, shift, L, Li, Lt, 1, 0, true);
@@ -707,7 +712,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         } else {
             chol_trailing(sh, A, r, NB, J, shift, L, Li, Lt, G - 1, b - 1, false);
         }
-        grid_barrier(bar, G, err);
+        grid_barrier(bar, G, err, dead);
         CHOL_STAMP(J + 1, 7);
     }
 }
@@ -1045,9 +1050,12 @@ int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t
     uint64_t* stamps = p->stamps;
     float* Lt = p->Lt;
     float* Lit = p->Lit;
-    void* args[] = {&A, &r, (void*)&np, &nnp, &alpha, &tau, &L, &Li, &Lt, &Lit, &bar, &scal, &stamps};
-    const void* fn = stamp ? (const void*)k_chol<true> : (const void*)k_chol<false>;
-    HIPCHK(hipLaunchCooperativeKernel(fn, dim3(p->chol_grid), dim3(256), args, 0, st));
+    // an ordinary launch: plan creation has checked that all chol_grid workgroups fit on the device at once
+    if (stamp)
+        k_chol<true><<<p->chol_grid, 256, 0, st>>>(A, r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, scal, stamps);
+    else
+        k_chol<false><<<p->chol_grid, 256, 0, st>>>(A, r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, scal, stamps);
+    HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
 
@@ -1232,7 +1240,7 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
     if (occ * cus < p->chol_grid) {
         const int need = p->chol_grid;
         delete p;
-        return fail(SPANQR_EHIP, "cooperative Cholesky needs %d co-resident workgroups, device holds %d", need,
+        return fail(SPANQR_EHIP, "the Cholesky needs %d co-resident workgroups, device holds %d", need,
                     occ * cus);
     }
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };

@@ -5,12 +5,22 @@ grid-barrier counters (include/spanqr.h). The reference keeps module-level cache
 candidates/kcholqr.py:26, the per-device barrier buffer candidates/kchol.py:12-18) and allocates the rest per call.
 Plans are keyed by stream as well, so calls on different streams never share a workspace or a barrier.
 """
+import atexit
 import ctypes
 import threading
 
 import torch
 
 from . import _lib
+
+# At interpreter exit the process releases device memory by itself; destroying plans then would call into a HIP
+# runtime (and any attached profiler) that may already be shutting down.
+_SHUTTING_DOWN = [False]
+
+
+@atexit.register
+def _mark_shutdown():
+    _SHUTTING_DOWN[0] = True
 
 
 class Plan:
@@ -36,9 +46,9 @@ class Plan:
         return self.query(_lib.Q_CHOL_GRID)
 
     def close(self):
-        if self.handle:
+        if self.handle and not _SHUTTING_DOWN[0]:
             _lib.lib().spanqr_plan_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:
