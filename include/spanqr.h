@@ -81,6 +81,12 @@ const char* spanqr_last_error(void);
  * is seeded with the same 20261018 and defined in the source (splitmix64 counter hash, Irwin-Hall(12) normals). */
 int spanqr_dust_host(int K, int r, float* Z);
 
+/* Host-side split policy (no GPU needed): rows per Gram split KS (a multiple of 32) for X [K, r]; the Gram runs
+ * ceil(K / KS) splits. Same rule as gram_f (candidates/tri.py:364-367) with a fixed target of 512 workgroups in place
+ * of 3 x the device's SM count, so the summation order, and with it every bit of Q, is the same on every device.
+ * Returns SPANQR_EINVAL for a shape the plan would reject. */
+int spanqr_split_rows(int K, int r);
+
 /* ---- stage entry points: one stage of the call on device buffers, for checking each kernel ---- */
 
 /* max|x| partials of X into the plan (the scale the pass-1 kernels derive from them is written to scal[0] by

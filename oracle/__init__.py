@@ -11,6 +11,7 @@ Two restatements of candidates/kcholqr.py:92-112 live here:
 
 Arrays are numpy, row-major, float32 unless stated.
 """
+import contextlib
 import ctypes
 import os
 import subprocess
@@ -34,37 +35,55 @@ def build():
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
 
 
+def _bind(L):
+    c_int, c_long, c_float = ctypes.c_int, ctypes.c_long, ctypes.c_float
+    L.spqo_amax.argtypes = [_f32p, c_long, c_int, c_int]
+    L.spqo_amax.restype = c_float
+    L.spqo_pow2_scale.argtypes = [c_float]
+    L.spqo_pow2_scale.restype = c_float
+    L.spqo_rsqrt.argtypes = [c_float]
+    L.spqo_rsqrt.restype = c_float
+    L.spqo_dust.argtypes = [c_int, c_int, _f32p]
+    L.spqo_gram_splits.argtypes = [c_int, c_int]
+    L.spqo_gram_splits.restype = c_int
+    L.spqo_gram.argtypes = [_f32p, c_long, c_int, c_int, c_float, c_int, c_int, c_int, _f32p, _vp]
+    L.spqo_norm.argtypes = [_f64p, c_int]
+    L.spqo_norm.restype = c_float
+    L.spqo_shift.argtypes = [_f32p, c_int, c_float, c_float, c_float]
+    L.spqo_shift.restype = c_float
+    L.spqo_diag_factor.argtypes = [_f32p, c_long, c_float, _f32p, c_long, _f32p]
+    L.spqo_chol.argtypes = [_f32p, c_int, c_float, _f32p, _f32p]
+    L.spqo_trsm.argtypes = [_f32p, c_long, c_int, c_int, c_float, c_int, _vp, c_float, _f32p, _f32p, _f32p, c_long]
+    L.spqo_ns_D.argtypes = [_f32p, c_int, _f32p]
+    L.spqo_ns_apply.argtypes = [_f32p, c_long, c_int, c_int, _f32p, _f32p, c_long]
+    L.spqo_orth.argtypes = [_f32p, c_long, c_int, c_int, c_int, c_float, c_float, c_float, c_int, _f32p, c_long,
+                            _vp, _vp, _vp, _vp, _vp]
+    return L
+
+
 def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(_LIB_PATH):
             build()
-        L = ctypes.CDLL(_LIB_PATH)
-        c_int, c_long, c_float = ctypes.c_int, ctypes.c_long, ctypes.c_float
-        L.spqo_amax.argtypes = [_f32p, c_long, c_int, c_int]
-        L.spqo_amax.restype = c_float
-        L.spqo_pow2_scale.argtypes = [c_float]
-        L.spqo_pow2_scale.restype = c_float
-        L.spqo_rsqrt.argtypes = [c_float]
-        L.spqo_rsqrt.restype = c_float
-        L.spqo_dust.argtypes = [c_int, c_int, _f32p]
-        L.spqo_gram_splits.argtypes = [c_int, c_int]
-        L.spqo_gram_splits.restype = c_int
-        L.spqo_gram.argtypes = [_f32p, c_long, c_int, c_int, c_float, c_int, c_int, c_int, _f32p, _vp]
-        L.spqo_norm.argtypes = [_f64p, c_int]
-        L.spqo_norm.restype = c_float
-        L.spqo_shift.argtypes = [_f32p, c_int, c_float, c_float, c_float]
-        L.spqo_shift.restype = c_float
-        L.spqo_diag_factor.argtypes = [_f32p, c_long, c_float, _f32p, c_long, _f32p]
-        L.spqo_chol.argtypes = [_f32p, c_int, c_float, _f32p, _f32p]
-        L.spqo_trsm.argtypes = [_f32p, c_long, c_int, c_int, c_float, c_int, _vp, c_float, _f32p, _f32p, _f32p,
-                                c_long]
-        L.spqo_ns_D.argtypes = [_f32p, c_int, _f32p]
-        L.spqo_ns_apply.argtypes = [_f32p, c_long, c_int, c_int, _f32p, _f32p, c_long]
-        L.spqo_orth.argtypes = [_f32p, c_long, c_int, c_int, c_int, c_float, c_float, c_float, c_int, _f32p, c_long,
-                                _vp, _vp, _vp, _vp, _vp]
-        _lib = L
+        _lib = _bind(ctypes.CDLL(_LIB_PATH))
     return _lib
+
+
+@contextlib.contextmanager
+def planted(n, workdir):
+    """inside the block, every function of this module runs a copy of the oracle built with planted defect n
+    (kcholf_oracle.c, PLANTED(n)); for the tests that show the oracle's checks catch such mistakes"""
+    global _lib
+    path = os.path.join(str(workdir), f"liboracle_plant{n}.so")
+    if not os.path.exists(path):
+        subprocess.run(["make", "-s", "-C", _HERE, f"PLANT={n}", f"OUT={path}"], check=True)
+    saved = lib()
+    _lib = _bind(ctypes.CDLL(path))
+    try:
+        yield
+    finally:
+        _lib = saved
 
 
 def _c32(a):

@@ -36,6 +36,13 @@
 #include <string.h>
 #include <xmmintrin.h>
 
+/* Planted defects for the tests that show the oracle's checks catch plausible mistakes: built with -DPLANT=n, the
+ * oracle carries defect n (listed where PLANTED(n) appears); the default build has none. */
+#ifndef PLANT
+#define PLANT 0
+#endif
+#define PLANTED(n) (PLANT == (n))
+
 #define TB 64   /* Gram output tile width (tri.py:362 uses bt = 64) */
 #define CB 32   /* Cholesky diagonal tile and TRSM column block width (chol.cu:15 TB = 32, tri.py:406 bs = 32) */
 #define BK 32   /* rows per Kahan chunk in the compensated Gram (tri.py:352-355 uses BK = 32) */
@@ -62,19 +69,17 @@ float spqo_amax(const float* X, long ldx, int K, int r) {
     return u2f(m);
 }
 
-/* Closed form of _pow2_scale. With mm = max(m, fp32(1e-38)) = 1.f * 2^e (or subnormal), round(log2 mm) is e when
- * 1.f < sqrt(2) and e + 1 when 1.f > sqrt(2) (no fp32 mantissa equals sqrt(2); the first fp32 above it has
- * mantissa field 0x3504F4). Subnormal mm lies in [fp32(1e-38), 2^-126), whose log2 rounds to -126. */
+/* _pow2_scale (kcholqr.py:29-30): s = 2^-round(log2(max(m, 1e-38))) with torch's fp32 log2 and round half to even;
+ * 1 for m = 0 or NaN (torch.where(m > 0, ..., 1)); 0 for m = inf (exp2(-inf)). y = fp32(log2(double(mm))) is the
+ * correctly rounded fp32 log2: near the half-integers, where the rounding decides, the double result is never within
+ * its own error of an fp32 rounding boundary (checked over every exponent by the tests). y is exactly e + 0.5 for a
+ * band of mantissas around sqrt(2) that widens with |e|; rintf then picks the even neighbour, as torch.round does. */
 float spqo_pow2_scale(float m) {
-    if (!(m > 0.0f)) return 1.0f;            /* 0 or NaN: torch.where(m > 0, ..., 1) */
-    if (isinf(m)) return 0.0f;               /* exp2(-inf) */
-    float mm = m < 1e-38f ? 1e-38f : m;
-    uint32_t b = f2u(mm);
-    int ex = (int)((b >> 23) & 0xffu);
-    int e;
-    if (ex == 0) e = -126;
-    else e = (ex - 127) + ((b & 0x7fffffu) >= 0x3504F4u ? 1 : 0);
-    return ldexpf(1.0f, -e);
+    if (!(m > 0.0f)) return 1.0f;
+    if (isinf(m)) return 0.0f;
+    const float mm = m < 1e-38f ? 1e-38f : m;
+    const float y = (float)log2((double)mm);
+    return ldexpf(1.0f, -(int)(PLANTED(10) ? ceilf(y) : rintf(y)));   /* 10: rounds up */
 }
 
 /* ------------------------------------------------------------------------------------------------------------ */
@@ -115,7 +120,7 @@ void spqo_dust(int K, int r, float* Z) {
             Z[(size_t)k * r + c] = z;
             n2[c] += (double)z * (double)z;
         }
-    for (int c = 0; c < r; ++c) n2[c] = sqrt(n2[c]);
+    for (int c = 0; c < r; ++c) n2[c] = PLANTED(9) ? 1.0 : sqrt(n2[c]);   /* 9: columns not normalised */
     for (int k = 0; k < K; ++k)
         for (int c = 0; c < r; ++c) Z[(size_t)k * r + c] = (float)((double)Z[(size_t)k * r + c] / n2[c]);
     free(n2);
@@ -177,7 +182,7 @@ void spqo_gram(const float* A, long lda, int K, int r, float s, int use_s, int k
             if (kahan)
                 for (int i = 0; i < TB; ++i)
                     for (int j = 0; j < TB; ++j) {
-                        float y = part[i][j] - comp[i][j];
+                        float y = PLANTED(6) ? part[i][j] + comp[i][j] : part[i][j] - comp[i][j];   /* 6 */
                         float t = acc[i][j] + y;
                         comp[i][j] = (t - acc[i][j]) - y;
                         acc[i][j] = t;
@@ -227,7 +232,7 @@ float spqo_norm(const double* npart, int n) {
 
 /* kcholqr.py:108-109: G_ii += fp32(alpha * nrm); tau = fp32(fp32(tau_rel * nrm) + 1e-30) */
 float spqo_shift(float* G, int r, float nrm, float alpha, float tau_rel) {
-    const float sh = alpha * nrm;
+    const float sh = PLANTED(7) ? 0.0f : alpha * nrm;   /* 7: no shift */
     for (int i = 0; i < r; ++i) G[(size_t)i * r + i] = G[(size_t)i * r + i] + sh;
     return tau_rel * nrm + 1e-30f;
 }
@@ -262,7 +267,7 @@ float spqo_rsqrt(float x) {
 void spqo_diag_factor(float* D, long ld, float tau, float* L, long ldl, float* Li) {
     float rd[CB], lc[CB];
     for (int c = 0; c < CB; ++c) {
-        float piv = fmaxf(D[(size_t)c * ld + c], tau);
+        float piv = PLANTED(8) ? fminf(D[(size_t)c * ld + c], tau) : fmaxf(D[(size_t)c * ld + c], tau);   /* 8 */
         float q = spqo_rsqrt(piv);
         rd[c] = q;
         lc[c] = piv * q;
@@ -276,7 +281,7 @@ void spqo_diag_factor(float* D, long ld, float tau, float* L, long ldl, float* L
         for (int i = 0; i < CB; ++i) {
             float acc = (i == kk) ? 1.0f : 0.0f;
             for (int m = 0; m < i; ++m) acc = fmaf(-L[(size_t)i * ldl + m], x[m], acc);
-            x[i] = (i < kk) ? 0.0f : acc * rd[i];
+            x[i] = (i < kk) ? 0.0f : acc * rd[PLANTED(2) ? kk : i];   /* 2: wrong reciprocal */
         }
         for (int i = 0; i < CB; ++i) Li[i * CB + kk] = x[i];
     }
@@ -304,7 +309,8 @@ void spqo_chol(float* A, int r, float tau, float* L, float* Li) {
                 for (int b = 0; b < CB; ++b) {
                     float acc = 0.0f;
                     for (int m = 0; m < mend(b); ++m)
-                        acc = fmaf(A[(size_t)(i * CB + a) * r + j * CB + m], Lij[b * CB + m], acc);
+                        acc = fmaf(A[(size_t)(i * CB + a) * r + j * CB + m], PLANTED(3) ? Lij[m * CB + b] : Lij[b * CB + m],
+                                   acc);   /* 3: Li transposed */
                     P[(size_t)(i * CB + a) * CB + b] = acc;
                     L[(size_t)(i * CB + a) * r + j * CB + b] = acc;
                 }
@@ -318,7 +324,8 @@ void spqo_chol(float* A, int r, float tau, float* L, float* Li) {
                         if (i == k && b > a) continue;   /* only the lower part of diagonal tiles is ever read */
                         float acc = A[(size_t)(i * CB + a) * r + k * CB + b];
                         for (int m = 0; m < CB; ++m)
-                            acc = fmaf(-P[(size_t)(i * CB + a) * CB + m], P[(size_t)(k * CB + b) * CB + m], acc);
+                            acc = fmaf(PLANTED(1) ? P[(size_t)(i * CB + a) * CB + m] : -P[(size_t)(i * CB + a) * CB + m],
+                                        P[(size_t)(k * CB + b) * CB + m], acc);   /* 1: update sign */
                         A[(size_t)(i * CB + a) * r + k * CB + b] = acc;
                     }
         }
@@ -346,7 +353,9 @@ void spqo_trsm(const float* X, long ldx, int K, int r, float s, int pass1, const
             }
             for (int m = 0; m < j * CB; ++m) {
                 const float ym = -y[m];
-                for (int c = 0; c < CB; ++c) acc[c] = fmaf(ym, L[(size_t)(j * CB + c) * r + m], acc[c]);
+                for (int c = 0; c < CB; ++c)
+                    acc[c] = fmaf(ym, PLANTED(4) ? L[(size_t)m * r + j * CB + c] : L[(size_t)(j * CB + c) * r + m],
+                                  acc[c]);   /* 4: L transposed */
             }
             for (int c = 0; c < CB; ++c) {
                 float o = 0.0f;
@@ -363,7 +372,7 @@ void spqo_trsm(const float* X, long ldx, int K, int r, float s, int pass1, const
 /* ------------------------------------------------------------------------------------------------------------ */
 void spqo_ns_D(const float* G, int r, float* D) {
     for (int i = 0; i < r; ++i)
-        for (int j = 0; j < r; ++j) D[(size_t)i * r + j] = ((i == j ? 1.0f : 0.0f) - G[(size_t)i * r + j]) * 0.5f;
+        for (int j = 0; j < r; ++j) D[(size_t)i * r + j] = ((i == j ? 1.0f : 0.0f) - G[(size_t)i * r + j]) * (PLANTED(5) ? 1.0f : 0.5f);   /* 5 */
 }
 
 void spqo_ns_apply(const float* Y, long ldy, int K, int r, const float* D, float* Q, long ldq) {

@@ -31,6 +31,7 @@ SIGNATURES = {
     "spanqr_profile_chol": (_I, [_P, _P, _P, _F, _F, _P, ctypes.POINTER(ctypes.c_double), _P]),
     "spanqr_last_error": (ctypes.c_char_p, []),
     "spanqr_dust_host": (_I, [_I, _I, _P]),
+    "spanqr_split_rows": (_I, [_I, _I]),
     "spanqr_stage_amax": (_I, [_P, _P, _L, _P]),
     "spanqr_stage_gram": (_I, [_P, _P, _L, _I, _I, _P, _P, _P]),
     "spanqr_stage_chol": (_I, [_P, _P, _P, _F, _F, _P, _P, _P, _P]),

@@ -50,16 +50,15 @@ __device__ __forceinline__ float readlane(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-// s = 2^-round(log2 max(m, 1e-38)), 1 for m = 0 or NaN, 0 for m = inf (kcholqr.py:29-30). mb = bits of max|x|.
+// s = 2^-round(log2 max(m, 1e-38)) (kcholqr.py:29-30): torch's fp32 log2 (here the correctly rounded one, from a
+// double log2) and round half to even; 1 for m = 0 or NaN, 0 for m = inf. mb = bits of max|x|.
 __device__ float pow2_scale_bits(uint32_t mb) {
     if (mb == 0u || mb > 0x7f800000u) return 1.0f;
     if (mb == 0x7f800000u) return 0.0f;
     const float m = __uint_as_float(mb);
     const float mm = m < 1e-38f ? 1e-38f : m;
-    const uint32_t b = __float_as_uint(mm);
-    const int ex = (int)((b >> 23) & 0xffu);
-    const int e = ex == 0 ? -126 : (ex - 127) + ((b & 0x7fffffu) >= 0x3504F4u ? 1 : 0);
-    return ldexpf(1.0f, -e);
+    const float y = (float)log2((double)mm);
+    return ldexpf(1.0f, -(int)rintf(y));
 }
 
 // Scale from the 256 partial maxima of k_amax; every thread of a 256-thread workgroup calls it.
@@ -1202,12 +1201,27 @@ int spanqr_dust_host(int K, int r, float* Z) {
     return SPANQR_OK;
 }
 
-int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
-    if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
-    *out = nullptr;
+static int check_shape(int K, int r) {
     if (r < 64 || r > 512 || (r % 64) != 0) return fail(SPANQR_EINVAL, "r = %d: must be a multiple of 64 in [64, 512]", r);
     if (K < r) return fail(SPANQR_EINVAL, "K = %d < r = %d", K, r);
     if ((long)K * r >= (1L << 30)) return fail(SPANQR_EINVAL, "K * r too large");
+    return SPANQR_OK;
+}
+
+int spanqr_split_rows(int K, int r) {
+    const int rc = check_shape(K, r);
+    if (rc != SPANQR_OK) return rc;
+    const int nt = r / TB;
+    int S = 0, KS = 0;
+    split_policy(K, nt * (nt + 1) / 2, &S, &KS);
+    return KS;
+}
+
+int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
+    if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
+    *out = nullptr;
+    const int shape_rc = check_shape(K, r);
+    if (shape_rc != SPANQR_OK) return shape_rc;
     DeviceGuard dg(device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", device);
     spanqr_plan* p = new spanqr_plan;

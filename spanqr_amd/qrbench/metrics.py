@@ -112,6 +112,46 @@ def bits_equal(A, B):
         A.contiguous().view(torch.int32).cpu(), B.contiguous().view(torch.int32).cpu()))
 
 
+def run_checked(fn, X, ref, check_sync=True):
+    """(Result, Q): calls fn(X) three times -- warm-up, under torch's sync-debug "error" mode (a host sync raises),
+    again for determinism -- then evaluates and checks that X was left intact (metrics.py:109-141). On CPU tensors
+    the sync check is skipped. A crash becomes a reported error."""
+    on_gpu = X.device.type == "cuda"
+    X0 = X.clone()
+    res = Result()
+    sync = torch.cuda.synchronize if on_gpu else (lambda: None)
+    try:
+        fn(X)
+        sync()
+        if check_sync and on_gpu:
+            prev = torch.cuda.get_sync_debug_mode()
+            torch.cuda.set_sync_debug_mode("error")
+            try:
+                Q1 = fn(X)
+            except RuntimeError as e:
+                if "synchroniz" not in str(e).lower():
+                    raise
+                res.sync_free = False
+                torch.cuda.set_sync_debug_mode(prev)
+                Q1 = fn(X)
+            finally:
+                torch.cuda.set_sync_debug_mode(prev)
+        else:
+            Q1 = fn(X)
+        Q2 = fn(X)
+        sync()
+    except Exception as e:  # noqa: BLE001 (a crash is a reported failure)
+        if on_gpu:
+            torch.cuda.set_sync_debug_mode(0)
+        res.error = f"{type(e).__name__}: {str(e).splitlines()[0][:120] if str(e) else ''}"
+        return res, None
+    ev = evaluate(Q1, X, ref)
+    ev.sync_free = res.sync_free
+    ev.deterministic = bits_equal(Q1, Q2)
+    ev.input_intact = bits_equal(X, X0)
+    return ev, Q1
+
+
 def householder(X):
     """the span comparator: fp32 Householder QR (the current TTF orth, qrbench/methods.py:47-50)"""
     return torch.linalg.qr(X)[0]

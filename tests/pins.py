@@ -1,0 +1,351 @@
+"""Checks that pin the CPU oracle (oracle/) to the reference's algorithm without running the reference.
+
+Each check returns a list of failure messages (empty: pinned). They compare the oracle with what fixes the answer
+independently of the oracle's own code: torch's CPU evaluation of the reference's own expressions
+(candidates/kcholqr.py:29-30, :16-23, :107-109), fp64 textbook linear algebra (Cholesky, triangular solve, Gram)
+under rounding-error bounds, closed forms and special cases (zero Gram, clamped pivots, NaN pivots), invariants
+(exact power-of-2 scaling, symmetry, unit dust columns) and the published splitmix64 sequence. tests/test_oracle.py
+runs them on the oracle (all must pass) and on copies of the oracle built with a planted defect (each defect must
+make at least one check fail).
+"""
+import math
+
+import numpy as np
+import torch
+
+import oracle
+
+U32 = 2.0 ** -24
+F32 = np.float32
+
+
+def _ulps(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return np.abs(np.asarray(got, np.float64) - ref) / np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+
+
+# ---- power-of-2 scale (kcholqr.py:29-30) ----
+
+def torch_pow2_scale(m):
+    """the reference's expression, evaluated by torch on the CPU (fp32)"""
+    t = torch.as_tensor(np.asarray(m, np.float32))
+    return torch.where(t > 0, torch.exp2(-torch.round(torch.log2(t.clamp_min(1e-38)))), torch.ones_like(t)).numpy()
+
+
+def scale_windows():
+    """every float whose log2 lies near a half-integer (mantissa near sqrt(2)) for all 254 exponents, plus the
+    binade ends: where round(log2) is decided"""
+    mant = np.concatenate([np.arange(0x3504C0, 0x350530, dtype=np.uint32),
+                           np.array([0, 1, 0x200000, 0x400000, 0x7FFFFF], np.uint32)])
+    e = np.arange(1, 255, dtype=np.uint32)
+    return ((e[:, None] << np.uint32(23)) | mant[None, :]).ravel().view(np.float32)
+
+
+def check_scale():
+    f = []
+    x = scale_windows()
+    got = np.array([oracle.pow2_scale(v) for v in x], np.float32)
+    want = torch_pow2_scale(x)
+    bad = np.nonzero(got != want)[0]
+    if len(bad):
+        f.append(f"pow2_scale differs from torch's round(log2) at {len(bad)} of {len(x)} values, e.g. "
+                 f"m={x[bad[0]]!r}: {got[bad[0]]} vs {want[bad[0]]}")
+    known = {0.0: 1.0, float("nan"): 1.0, float("inf"): 0.0, 1.0: 1.0, 2.0 ** 20: 2.0 ** -20, 1.25 * 2.0 ** 7: 2.0 ** -7,
+             1.5 * 2.0 ** 7: 2.0 ** -8, 1.5 * 2.0 ** -9: 2.0 ** 8, 1e-40: 2.0 ** 126, 1e-25: 2.0 ** 83, 1e25: 2.0 ** -83}
+    for m, s in known.items():
+        if oracle.pow2_scale(m) != F32(s):
+            f.append(f"pow2_scale({m}) = {oracle.pow2_scale(m)}, expected {s}")
+    # invariant: s is a power of 2 and max|s x| lands in [2^-1/2, 2^1/2] (up to the half-way band)
+    rng = np.random.default_rng(1)
+    m = (10.0 ** rng.uniform(-37, 37, 2000)).astype(np.float32)
+    for v in m:
+        s = float(oracle.pow2_scale(v))
+        if math.frexp(s)[0] != 0.5 or not (2 ** -0.5 * (1 - 1e-6) <= v * s <= 2 ** 0.5 * (1 + 1e-6)):
+            f.append(f"pow2_scale({v}) = {s} breaks the invariant")
+            break
+    return f
+
+
+def check_scale_rounding_margin():
+    """the oracle and the kernels take fp32(log2) from a double log2; near the half-integers (where it decides the
+    result) the double value must sit far from every fp32 rounding boundary, so any log2 within a few double ulps
+    gives the same fp32 value"""
+    x = scale_windows()
+    l = np.log2(x.astype(np.float64))
+    y = l.astype(np.float32)
+    lo = np.nextafter(y, np.float32(-np.inf)).astype(np.float64)
+    hi = np.nextafter(y, np.float32(np.inf)).astype(np.float64)
+    yd = y.astype(np.float64)
+    gap = np.minimum(np.abs(l - (yd + lo) / 2), np.abs(l - (yd + hi) / 2))
+    worst = float((gap / np.spacing(np.abs(l))).min())
+    return [] if worst > 64 else [f"double log2 within {worst} double ulps of an fp32 rounding boundary"]
+
+
+# ---- pivot reciprocal square root (chol.cu:45 uses rsqrtf) ----
+
+def check_rsqrt():
+    rng = np.random.default_rng(2)
+    x = (10.0 ** rng.uniform(-37.9, 38, 5000)).astype(np.float32)
+    x = np.concatenate([x, np.float32([1e-30, 1.0, 2.0, 4.0, 0.25, 3.0, 1e-8])])
+    got = np.array([oracle.rsqrt(v) for v in x], np.float32)
+    err = _ulps(got, 1.0 / np.sqrt(x.astype(np.float64)))
+    return [] if err.max() <= 2.5 else [f"rsqrt error {err.max():.2f} ulp > 2.5"]
+
+
+# ---- dust (this project's generator, seeded with the reference's 20261018, kcholqr.py:83-89) ----
+
+MASK64 = (1 << 64) - 1
+GOLDEN = 0x9E3779B97F4A7C15
+
+
+def mix64(z):
+    """splitmix64's output function (Steele, Lea, Flood 2014; Vigna's splitmix64.c)"""
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & MASK64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & MASK64
+    return z ^ (z >> 31)
+
+
+def dust_spec(K, r, seed=20261018):
+    """the generator's written definition, in exact integer and double arithmetic"""
+    key = mix64(seed)
+    raw = np.empty((K, r), np.float32)
+    for k in range(K):
+        for c in range(r):
+            n = k * r + c
+            S = 0
+            for j in range(6):
+                w = mix64((key + (6 * n + j + 1) * GOLDEN) & MASK64)
+                S += (w & 0xFFFFFFFF) + (w >> 32)
+            raw[k, c] = np.float32(math.ldexp(float(S - 6 * 0xFFFFFFFF), -32))
+    return raw, None
+
+
+def check_dust():
+    f = []
+    # splitmix64 seeded with 0: first outputs as published
+    state, outs = 0, []
+    for _ in range(2):
+        state = (state + GOLDEN) & MASK64
+        outs.append(mix64(state))
+    if outs != [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4]:
+        f.append("splitmix64 restatement does not reproduce the published sequence")
+    K, r = 7, 5
+    raw, _ = dust_spec(K, r)
+    nrm = []
+    for c in range(r):
+        acc = 0.0
+        for k in range(K):                      # ascending k, in double
+            acc += float(raw[k, c]) * float(raw[k, c])
+        nrm.append(math.sqrt(acc))
+    nrm = np.array(nrm)
+    Z = oracle.dust(K, r)
+    want = (raw.astype(np.float64) / nrm).astype(np.float32)
+    if not np.array_equal(Z, want):
+        f.append(f"dust differs from its definition (max diff {np.abs(Z - want).max():.3e})")
+    Zb = oracle.dust(512, 64)
+    cn = np.sqrt((Zb.astype(np.float64) ** 2).sum(axis=0))
+    if not np.abs(cn - 1).max() <= 1e-6:
+        f.append(f"dust columns are not unit (max |norm - 1| {np.abs(cn - 1).max():.2e})")
+    zk = Zb.astype(np.float64) * math.sqrt(512)
+    if not (abs(zk.mean()) <= 0.02 and abs(zk.var() - 1) <= 0.03):
+        f.append(f"dust entries not ~N(0, 1/K): mean {zk.mean():.3f} var {zk.var():.3f}")
+    return f
+
+
+# ---- Gram (tri.py:255-297, 324-375) ----
+
+def check_gram():
+    f = []
+    rng = np.random.default_rng(3)
+    K, r, KS = 200, 128, 64                 # ragged last split (200 = 3 x 64 + 8)
+    X = rng.standard_normal((K, r)).astype(np.float32)
+    X[:, 5] *= 1e3
+    G64 = X.astype(np.float64).T @ X.astype(np.float64)
+    A64 = np.abs(X.astype(np.float64)).T @ np.abs(X.astype(np.float64))
+    for kahan, c in ((True, 4.0), (False, KS + 8.0)):
+        G, npart = oracle.gram(X, KS, kahan)
+        ratio = (np.abs(G - G64) / (A64 * U32)).max()
+        if not ratio <= c:
+            f.append(f"gram(kahan={kahan}) error {ratio:.1f} u|X|^T|X| > {c}")
+        if not np.array_equal(G, G.T):
+            f.append("gram not exactly symmetric")
+        fro2 = float((G.astype(np.float64) ** 2).sum())
+        if not abs(npart.sum() - fro2) <= 1e-12 * fro2:
+            f.append("norm partials do not sum to ||G||_F^2")
+        if not abs(float(oracle.norm(npart)) - math.sqrt(fro2)) <= 2 * U32 * math.sqrt(fro2):
+            f.append("norm() is not ||G||_F")
+    # one long split (128 chunks of 32 rows): Kahan compensation across chunks keeps the error near 1 u|X|^T|X|
+    # where a plain chain reaches tens of u
+    X2 = (rng.standard_normal((4096, 64)) + 3.0).astype(np.float32)
+    X2d = X2.astype(np.float64)
+    G2, _ = oracle.gram(X2, 4096, True)
+    ratio = (np.abs(G2 - X2d.T @ X2d) / (np.abs(X2d).T @ np.abs(X2d) * U32)).max()
+    if not ratio <= 4.0:
+        f.append(f"Kahan Gram over one 4096-row split: error {ratio:.1f} u|X|^T|X| > 4")
+    # scaling by a power of 2 on load is exact
+    s = F32(2.0 ** -7)
+    Gs, _ = oracle.gram(X, KS, True, s=s)
+    Gp, _ = oracle.gram(X * s, KS, True)
+    if not np.array_equal(Gs, Gp):
+        f.append("gram with scale on load differs from the Gram of the scaled matrix")
+    if oracle.gram_splits(200, 64) != 4 or oracle.gram_splits(256, 64) != 4:
+        f.append("gram_splits is not ceil(K / KS)")
+    return f
+
+
+# ---- shift and clamp floor (kcholqr.py:107-109) ----
+
+def check_shift():
+    f = []
+    rng = np.random.default_rng(4)
+    G = rng.standard_normal((64, 64)).astype(np.float32)
+    nrm = F32(123.456)
+    Gs, tau = oracle.shift(G, nrm)
+    t = torch.from_numpy(G.copy())
+    t.diagonal().add_(torch.tensor(1e-7, dtype=torch.float32) * torch.tensor(float(nrm), dtype=torch.float32))
+    tt = torch.tensor(1e-8, dtype=torch.float32) * torch.tensor(float(nrm), dtype=torch.float32) + 1e-30
+    if not np.array_equal(Gs, t.numpy()):
+        f.append("shift differs from G.diagonal().add_(alpha * nrm)")
+    if tau != F32(tt.item()):
+        f.append(f"tau {tau} differs from tau * nrm + 1e-30 = {tt.item()}")
+    return f
+
+
+# ---- clamped Cholesky (chol.cu:115-271) ----
+
+def _spd(r, cond, seed):
+    rng = np.random.default_rng(seed)
+    Qm, _ = np.linalg.qr(rng.standard_normal((r, r)))
+    s = np.logspace(0, -math.log10(cond), r)
+    return ((Qm * s) @ Qm.T).astype(np.float32)
+
+
+def check_chol():
+    f = []
+    r = 128
+    G = _spd(r, 100.0, 5)
+    L, Li = oracle.chol(G, 1e-30)
+    L64 = torch.linalg.cholesky(torch.from_numpy(G.astype(np.float64))).numpy()
+    rel = np.abs(L - L64).max() / np.abs(L64).max()
+    if not rel <= 1e-5:
+        f.append(f"chol differs from fp64 Cholesky by {rel:.2e}")
+    if not np.abs(np.triu(L, 1)).max() == 0:
+        f.append("chol: upper triangle not zero")
+    res = np.abs(L.astype(np.float64) @ L.T - G).max() / np.abs(G).max()
+    if not res <= 1e-5:
+        f.append(f"chol residual {res:.2e}")
+    for j in range(r // 32):
+        Ljj = L[32 * j:32 * j + 32, 32 * j:32 * j + 32].astype(np.float64)
+        e = np.abs(Li[32 * j:32 * j + 32].astype(np.float64) @ Ljj - np.eye(32)).max()
+        if not e <= 1e-4:
+            f.append(f"Li block {j} is not the inverse of the diagonal tile ({e:.2e})")
+            break
+        if not np.abs(np.triu(Li[32 * j:32 * j + 32], 1)).max() == 0:
+            f.append("Li not lower triangular")
+            break
+    # zero Gram: every pivot clamps to tau -> L = sqrt(tau) I
+    Lz, Liz = oracle.chol(np.zeros((64, 64), np.float32), 1e-30)
+    if not (np.abs(np.diag(Lz) / 1e-15 - 1).max() <= 1e-6 and np.abs(Lz - np.diag(np.diag(Lz))).max() == 0):
+        f.append("chol of zero is not sqrt(tau) I")
+    if not np.abs(np.diag(Liz[:32]) * 1e-15 - 1).max() <= 1e-6:
+        f.append("Li of zero Gram is not I / sqrt(tau)")
+    # rank 32 of 96: pivots 33.. clamp to tau (chosen far above the rounding noise)
+    rng = np.random.default_rng(6)
+    B = rng.standard_normal((96, 32)).astype(np.float64)
+    Gr = (B @ B.T).astype(np.float32)
+    tau = 1e-3 * float(np.abs(Gr).max())
+    Lr, _ = oracle.chol(Gr, tau)
+    d = np.diag(Lr)[32:]
+    if not np.abs(d / math.sqrt(tau) - 1).max() <= 1e-5:
+        f.append("clamped pivots of a rank-deficient Gram are not sqrt(tau)")
+    # NaN pivot -> tau (fmaxf ignores NaN, chol.cu:9)
+    Gn = _spd(64, 10.0, 7)
+    Gn[3, 3] = np.nan
+    Ln, _ = oracle.chol(Gn, 0.5)
+    if not abs(Ln[3, 3] / math.sqrt(0.5) - 1) < 1e-6:
+        f.append("NaN pivot not clamped to tau")
+    return f
+
+
+# ---- triangular solve (tri.py:378-412) ----
+
+def check_trsm():
+    f = []
+    r, K = 128, 100
+    G = _spd(r, 50.0, 8)
+    L, Li = oracle.chol(G, 1e-30)
+    rng = np.random.default_rng(9)
+    A = rng.standard_normal((K, r)).astype(np.float32)
+    Y = oracle.trsm(A, L, Li)
+    Y64 = torch.linalg.solve_triangular(torch.from_numpy(L.astype(np.float64)),
+                                        torch.from_numpy(A.astype(np.float64)).T, upper=False).T.numpy()
+    rel = np.abs(Y - Y64).max() / np.abs(Y64).max()
+    if not rel <= 1e-5:
+        f.append(f"trsm differs from fp64 solve_triangular by {rel:.2e}")
+    # pass-1 operand fmaf(eps, z, s x): with eps = 0 it is exactly s x
+    s = F32(0.25)
+    Z = oracle.dust(K, r)
+    Y1 = oracle.trsm(A, L, Li, s=s, Z=Z, eps=0.0)
+    Y0 = oracle.trsm(A * s, L, Li)
+    if not np.array_equal(Y1, Y0):
+        f.append("trsm pass-1 operand with eps = 0 is not s * x")
+    Ye = oracle.trsm(A, L, Li, s=s, Z=Z, eps=1e-3)
+    Ye64 = torch.linalg.solve_triangular(torch.from_numpy(L.astype(np.float64)),
+                                         torch.from_numpy((0.25 * A + 1e-3 * Z).astype(np.float64)).T,
+                                         upper=False).T.numpy()
+    if not np.abs(Ye - Ye64).max() / np.abs(Ye64).max() <= 1e-5:
+        f.append("trsm pass-1 operand is not s x + eps z")
+    return f
+
+
+# ---- Newton-Schulz polish (kcholqr.py:16-23) ----
+
+def check_ns():
+    f = []
+    rng = np.random.default_rng(10)
+    K, r = 300, 64
+    Q0, _ = np.linalg.qr(rng.standard_normal((K, r)))
+    E = 1e-3 * rng.standard_normal((r, r))
+    Y = (Q0 @ (np.eye(r) + (E + E.T) / 2)).astype(np.float32)
+    G = (Y.astype(np.float64).T @ Y).astype(np.float32)
+    D = oracle.ns_D(G)
+    Dt = torch.eye(r).sub_(torch.from_numpy(G)).mul_(0.5).numpy()     # the reference's expression
+    if not np.array_equal(D, Dt):
+        f.append("ns_D differs from eye(r).sub_(G).mul_(0.5)")
+    Q = oracle.ns_apply(Y, D)
+    Q64 = Y.astype(np.float64) + Y.astype(np.float64) @ D.astype(np.float64)
+    if not np.abs(Q - Q64).max() <= 4 * U32 * np.abs(Q64).max():
+        f.append("ns_apply is not Y + Y D")
+    e0 = np.abs(Y.astype(np.float64).T @ Y - np.eye(r)).max()
+    e1 = np.abs(Q.astype(np.float64).T @ Q - np.eye(r)).max()
+    if not e1 < max(10 * e0 ** 2, 2e-6):
+        f.append(f"one polish step does not square the orthogonality error ({e0:.2e} -> {e1:.2e})")
+    return f
+
+
+# ---- whole call on small shapes ----
+
+def check_orth_small():
+    from spanqr_amd.qrbench import gen, metrics
+    f = []
+    K, r = 256, 128
+    for name in ("mixed_c2", "mixed_c8", "zero", "rank_half", "huge_1e25"):
+        c = next(gen.make_cases(K, r, [name], (0,)))
+        Q = oracle.orth(c.X.numpy(), 64)
+        ref = metrics.reference(c.X)
+        res = metrics.evaluate(torch.from_numpy(Q), c.X, ref)
+        hh = metrics.evaluate(metrics.householder(c.X), c.X, ref)
+        fails = res.failures(span_ref=hh.span_n, orth_tol=metrics.ORTH_TOL_TARGET)
+        if fails:
+            f.append(f"orth {name}: {fails}")
+        if name == "mixed_c2":
+            # thin-QR uniqueness: on a well-conditioned X the result is Householder's Q up to column signs
+            Qh, Rh = torch.linalg.qr(c.X.double())
+            Qh = (Qh * torch.sign(torch.diagonal(Rh))).numpy()
+            if not np.abs(Q - Qh).max() <= 1e-4:
+                f.append(f"orth mixed_c2 is not the thin-QR Q ({np.abs(Q - Qh).max():.2e})")
+    return f
+
+
+ALL = [check_scale, check_scale_rounding_margin, check_rsqrt, check_dust, check_gram, check_shift, check_chol,
+       check_trsm, check_ns, check_orth_small]

@@ -1,0 +1,82 @@
+"""The C ABI library without a GPU: it loads, exports exactly what include/spanqr.h declares, and its host-side
+pieces (dust generator, split policy, argument checks) behave; the product path refuses to run without the HIP
+library or off the GPU (there is no CPU fallback)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import spanqr_amd
+from spanqr_amd import _lib
+
+
+def test_header_and_bindings_agree():
+    assert set(_lib.exported_symbols_in_header()) == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _lib.exported_symbols_in_header() if not hasattr(L, n)]
+    assert not missing
+
+
+@pytest.mark.parametrize("K,r", [(7, 5), (300, 64), (1024, 256)])
+def test_host_dust_is_the_oracle_dust(K, r):
+    Z = np.empty((K, r), np.float32)
+    _lib.check(_lib.lib().spanqr_dust_host(K, r, Z.ctypes.data_as(ctypes.c_void_p)))
+    assert np.array_equal(Z.view(np.uint32), oracle.dust(K, r).view(np.uint32))
+
+
+def test_split_policy():
+    f = _lib.lib().spanqr_split_rows
+    # tri.py:364-367 with 512 target workgroups: S = min(ceil(512 / U), ceil(K / 128)), KS = 32 ceil(ceil(K/S) / 32)
+    for K, r in [(1024, 256), (2048, 256), (3584, 256), (768, 512), (2048, 512), (5120, 256), (17408, 256),
+                 (64, 64), (100, 64), (12345, 192)]:
+        nt = r // 64
+        U = nt * (nt + 1) // 2
+        S = max(1, min(-(-512 // U), -(-K // 128)))
+        KS = 32 * -(-(-(-K // S)) // 32)
+        assert f(K, r) == KS, (K, r)
+        assert KS % 32 == 0 and -(-K // KS) <= S
+    for K, r in [(100, 128), (1024, 96), (1024, 576), (1024, 0)]:
+        assert f(K, r) == -1
+        assert _lib.lib().spanqr_last_error()
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")
+def test_plan_create_without_gpu_fails_cleanly():
+    h = ctypes.c_void_p()
+    rc = _lib.lib().spanqr_plan_create(1024, 256, 0, ctypes.byref(h))
+    assert rc == -2 and not h.value
+    assert _lib.lib().spanqr_last_error()
+
+
+def test_bad_shapes_rejected_before_any_device_work():
+    h = ctypes.c_void_p()
+    assert _lib.lib().spanqr_plan_create(100, 128, 0, ctypes.byref(h)) == -1
+    assert _lib.lib().spanqr_plan_create(1024, 96, 0, ctypes.byref(h)) == -1
+    assert _lib.lib().spanqr_plan_create(1024, 256, 0, None) == -1
+
+
+def test_orth_refuses_cpu_tensors():
+    X = torch.randn(256, 128)
+    with pytest.raises(TypeError):
+        spanqr_amd.orth(X)
+    with pytest.raises(TypeError):
+        spanqr_amd.kcholqr_f(X)
+    with pytest.raises(TypeError):
+        spanqr_amd.orth(X.double())
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libspanqr.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(ImportError):
+        _lib.lib()
+
+
+def test_top_level_orth_is_the_package_orth():
+    import orth as top
+    assert top.orth is spanqr_amd.orth

@@ -1,0 +1,150 @@
+"""orth() on the MI355X through the C ABI: the robustness gates of the spec on the adversarial set, the benchmark
+inputs, the power-of-2 scale at its rounding edges, strided operands, and hipGraph capture. Every Q is also compared
+bit for bit with the CPU oracle on the same input."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from spanqr_amd import _lib, kcholqr_f, orth, stages
+from spanqr_amd.plan import get_plan, stream_handle
+from spanqr_amd.qrbench import gen, metrics
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_bits(a, b, what):
+    a = a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else a
+    b = b.detach().cpu().numpy() if isinstance(b, torch.Tensor) else b
+    same = np.array_equal(np.ascontiguousarray(a).view(np.uint32), np.ascontiguousarray(b).view(np.uint32))
+    if not same:
+        d = np.abs(a.astype(np.float64) - b.astype(np.float64))
+        raise AssertionError(f"{what}: {int((a.view(np.uint32) != b.view(np.uint32)).sum())} elements differ, "
+                             f"max abs diff {np.nanmax(d):.3e}")
+
+
+def gate(X, Q, what):
+    """the spec's robustness gates: no collapsed columns, max|Q^T Q - I| <= 2e-7, the reference's span rule"""
+    ref = metrics.reference(X)
+    res = metrics.evaluate(Q, X.to(Q.device), ref)
+    hh = metrics.evaluate(metrics.householder(X.cpu()), X.cpu(), ref)
+    fails = res.failures(span_ref=hh.span_n, orth_tol=metrics.ORTH_TOL_TARGET)
+    assert not fails, f"{what}: {fails} (orth {res.orth:.3e}, span_n {res.span_n:.2f})"
+
+
+ADV_SHAPES = [(768, 512), (2048, 512)]
+ADV_NAMES = ["cond1e14", "rank1", "right_half_zero", "dup64", "zero", "cond1e8_x1e-25", "cond1e8_x1e25"]
+
+
+@pytest.fixture(scope="module")
+def adversarial_inputs():
+    return {(K, r): gen.adversarial(K, r) for K, r in ADV_SHAPES}
+
+
+@pytest.mark.parametrize("K,r", ADV_SHAPES)
+@pytest.mark.parametrize("name", ADV_NAMES)
+def test_adversarial(cuda, adversarial_inputs, K, r, name):
+    print(f"adversarial {K}x{r} {name}", flush=True)
+    X = adversarial_inputs[(K, r)][name]
+    Xd = X.to(cuda)
+    res, Q = metrics.run_checked(orth, Xd, metrics.reference(X))
+    assert not res.error, res.error
+    assert res.deterministic and res.input_intact and res.sync_free
+    assert stages.scalars(K, r, cuda)[7].item() == 0, "grid barrier timed out"
+    gate(X, Q, name)
+    assert_bits(Q, oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows), "Q vs oracle")
+
+
+@pytest.mark.parametrize("K,r", [(1024, 256), (2048, 256), (3584, 256), (5120, 256), (6144, 256), (768, 512),
+                                 (2048, 512)])
+def test_benchmark_inputs(cuda, K, r):
+    print(f"bench input {K}x{r}", flush=True)
+    X = gen.bench_input(K, r, seed=0)
+    Q = orth(X.to(cuda))
+    gate(X, Q, f"{K}x{r}")
+    assert_bits(Q, oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows), "Q vs oracle")
+
+
+def _tie_band_values():
+    """max|x| values at the edges of round(log2): mantissas around sqrt(2) at small, middle and large exponents,
+    where fp32 log2 lands exactly on e + 1/2 and round-half-even decides"""
+    out = []
+    for e in (-120, -63, -2, -1, 0, 1, 2, 3, 41, 100, 126):
+        for mb in (0x3504C0, 0x3504F3, 0x3504F4, 0x3504F8, 0x350510):
+            out.append(float(np.array([((e + 127) << 23) | mb], np.uint32).view(np.float32)[0]))
+    return out
+
+
+def test_pow2_scale_edges(cuda):
+    K, r = 256, 64
+    rng = np.random.default_rng(0)
+    base = (0.5 * rng.uniform(-1, 1, (K, r))).astype(np.float32)
+    for m in _tie_band_values():
+        X = (base * np.float32(m)).astype(np.float32)
+        X[3, 5] = np.float32(m)
+        Q = orth(torch.from_numpy(X).to(cuda))
+        s = stages.scalars(K, r, cuda)[0].item()
+        assert np.float32(s) == oracle.pow2_scale(np.float32(m)), f"max {m!r}: scale {s} vs {oracle.pow2_scale(m)}"
+        assert_bits(Q, oracle.orth(X, get_plan(K, r, cuda).split_rows), f"Q at max {m!r}")
+
+
+def test_strided_operands(cuda):
+    """ldx > r and ldq > r through the C ABI (the reference copies to contiguous first, kcholqr.py:100)"""
+    K, r, pad = 1024, 256, 12
+    X = next(gen.make_cases(K, r, ["mixed_c6"], (0,))).X
+    Xp = torch.full((K, r + pad), float("nan"), device=cuda)
+    Xp[:, :r] = X.to(cuda)
+    Qp = torch.full((K, r + pad), -7.0, device=cuda)
+    plan = get_plan(K, r, cuda)
+    _lib.check(_lib.lib().spanqr_orth_f32(plan.handle, Xp.data_ptr(), r + pad, Qp.data_ptr(), r + pad, 5e-7, 1e-7,
+                                          1e-8, 2, stream_handle(cuda)))
+    torch.cuda.synchronize()
+    assert torch.all(Qp[:, r:] == -7.0), "wrote outside Q's columns"
+    assert_bits(Qp[:, :r].contiguous(), kcholqr_f(X.to(cuda)), "strided vs contiguous")
+
+
+def test_abi_rejects_bad_operands(cuda):
+    K, r = 256, 64
+    plan = get_plan(K, r, cuda)
+    X = torch.zeros(K, r + 1, device=cuda)
+    Q = torch.zeros(K, r, device=cuda)
+    f = _lib.lib().spanqr_orth_f32
+    st = stream_handle(cuda)
+    assert f(plan.handle, X.data_ptr(), r + 1, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2, st) == -1   # ld % 4
+    assert f(plan.handle, X.data_ptr() + 4, r, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2, st) == -1   # alignment
+    assert f(plan.handle, None, r, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2, st) == -1
+    assert f(plan.handle, X.data_ptr(), r, Q.data_ptr(), r - 4, 5e-7, 1e-7, 1e-8, 2, st) == -1   # ldq < r
+    assert _lib.lib().spanqr_last_error()
+
+
+def test_graph_capture_replays(cuda):
+    """the whole call captured into one hipGraph; replays with eager work in between equal the eager result"""
+    K, r = 2048, 256
+    X = gen.bench_input(K, r, seed=1).to(cuda)
+    Qe = kcholqr_f(X)
+    st = torch.cuda.Stream(cuda)
+    st.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(st):
+        kcholqr_f(X)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        Qg = kcholqr_f(X)
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert_bits(Qg, Qe, f"replay {i}")
+        kcholqr_f(torch.randn(K, r, device=cuda))    # eager work on another plan's stream between replays
+        torch.cuda.synchronize()
+
+
+def test_keyword_arguments(cuda):
+    """eps, alpha, tau and ns reach the kernels as the reference's keywords (kcholqr.py:92)"""
+    K, r = 512, 128
+    X = next(gen.make_cases(K, r, ["mixed_c8"], (0,))).X
+    KS = get_plan(K, r, cuda).split_rows
+    for kw in (dict(eps=1e-6), dict(alpha=1e-6), dict(tau=1e-7), dict(ns=1), dict(ns=0), dict(ns=3)):
+        Q = kcholqr_f(X.to(cuda), **kw)
+        assert_bits(Q, oracle.orth(X.numpy(), KS, **kw), f"kcholqr_f({kw})")

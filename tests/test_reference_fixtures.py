@@ -1,0 +1,86 @@
+"""The oracle against the reference's own saved results (results/synth_kcholf.json, RTX 4080 Laptop, and
+results/synth_kcholf_rtx5060ti.json), kept as data in tests/golden/reference_synth_metrics.json
+(tests/golden/make_fixtures.py).
+
+Those files hold no Q, only metrics of the reference's Q and the condition number of each input, so:
+  * the restated generator (spanqr_amd/qrbench/gen.py) must rebuild the same inputs: its cond matches the saved cond
+    wherever the two reference GPUs agree on it (full-rank cases; for rank-deficient ones cond is rounding noise);
+  * on the same inputs the oracle's Q must meet the same gates as the reference's and land at comparable metrics.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from spanqr_amd import _lib
+from spanqr_amd.qrbench import gen, metrics
+
+FIX = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_synth_metrics.json")
+DEVS = ("rtx4080_laptop", "rtx5060ti")
+SHAPES = [(1024, 256), (768, 512)]
+SLOW_SHAPES = [(2048, 256), (3584, 256), (2048, 512)]
+
+
+@pytest.fixture(scope="module")
+def rows():
+    with open(FIX) as f:
+        return json.load(f)["rows"]
+
+
+def _cases(K, r):
+    return list(gen.make_cases(K, r, seeds=(0, 1)))
+
+
+def _check_shape(K, r, rows):
+    KS = _lib.lib().spanqr_split_rows(K, r)
+    assert KS > 0
+    n_fp = 0
+    for c in _cases(K, r):
+        want = rows[f"{K}x{r}/{c.name}"]
+        ref = metrics.reference(c.X)
+        cond = metrics.cond_of(ref)
+        saved = [want[d]["cond"] for d in DEVS]
+        if all(math.isfinite(v) for v in saved) and abs(saved[0] - saved[1]) < 1e-6 * saved[0]:
+            # below ~1e7 the smallest singular value sits far above the fp32 rounding level of X, so cond is fixed
+            # by X's bits (a fingerprint); above it, it also carries the SVD's own rounding (the GPUs differ ~1e-9)
+            tol = 1e-10 if saved[0] < 1e7 else 1e-8
+            n_fp += saved[0] < 1e7
+            err = min(abs(cond - v) / v for v in saved)
+            assert err < tol, f"{c.name}: cond {cond!r} vs saved {saved}"
+        Q = oracle.orth(c.X.numpy(), KS)
+        assert np.array_equal(Q, oracle.orth(c.X.numpy(), KS)), f"{c.name}: not deterministic"
+        res = metrics.evaluate(torch.from_numpy(Q), c.X, ref)
+        ref_orth = max(want[d]["orth"] for d in DEVS)
+        ref_span = max(want[d]["span_n"] for d in DEVS)
+        ref_hh = max(want[d]["hh_span_n"] for d in DEVS)
+        assert res.bad_cols == 0 == want[DEVS[0]]["bad_cols"], c.name
+        assert res.finite, c.name
+        assert res.orth <= metrics.ORTH_TOL_TARGET, f"{c.name}: orth {res.orth:.3e}"
+        assert res.orth <= 2 * ref_orth, f"{c.name}: orth {res.orth:.3e} vs the reference's {ref_orth:.3e}"
+        # the reference's span rule, with its own Householder figure, and the same order as its kcholf
+        assert res.span_n <= max(metrics.SPAN_RATIO * ref_hh, metrics.SPAN_FLOOR), c.name
+        assert res.span_n <= 3 * ref_span + 1, f"{c.name}: span_n {res.span_n:.2f} vs the reference's {ref_span:.2f}"
+    assert n_fp >= 16, "too few exact cond fingerprints"
+
+
+@pytest.mark.parametrize("K,r", SHAPES, ids=lambda v: str(v))
+def test_oracle_matches_reference_results(K, r, rows):
+    _check_shape(K, r, rows)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("K,r", SLOW_SHAPES, ids=lambda v: str(v))
+def test_oracle_matches_reference_results_large(K, r, rows):
+    _check_shape(K, r, rows)
+
+
+def test_fixture_covers_reference_grid(rows):
+    shapes = {k.split("/")[0] for k in rows}
+    assert shapes == {f"{K}x{r}" for K, r in gen.ALL_SHAPES}
+    assert len(rows) == 8 * 22 * 2
+    names = set(gen.case_names())
+    assert {k.split("/")[1] for k in rows} == names
