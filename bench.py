@@ -1,16 +1,17 @@
 """Benchmark of orth(X) on one MI355X: microseconds per orth() call, max|Q^T Q - I|, and the roofline of each kernel.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S] [--no-cpu] [--no-graph]
 
 Workload (the reference's 0.8B TTF layer shapes): K x r in {1024x256, 2048x256, 3584x256}, two seeds each, X = V (U^T U)
 + u^T U with N = K (U's singular values log-uniform over [1, 1e4], u unit-RMS Gaussian), generated on the CPU and
 resident on the GPU before timing. One step = one orth() call on each of the six inputs; every input has its own
 captured hipGraph. `value` = timed wall time / (steps x 6) in microseconds (lower is better).
 
-Also reported: per-shape back-to-back time, the 768x512 and 17408x256 shapes (quoted targets), the per-kernel profile
-(HIP events recorded after every kernel of one call, on the call's stream) with algorithmic flops and bytes per
-kernel, and a CPU baseline (the C restatement of the algorithm in oracle/, OpenMP, on the host; plus CPU
-torch.linalg.qr) on a bounded sample.
+Also reported: per-shape back-to-back time; the 768x512 and 17408x256 shapes (the quoted targets); per kernel the
+average launch duration at each workload shape (HIP events around back-to-back launches on the call's stream) with
+its algorithmic flops and bytes; the roofline of the dominant kernel and of the whole call; the Cholesky's latency
+per diagonal step; a CPU baseline on a bounded sample (the C restatement in oracle/, OpenMP, on the host, plus CPU
+torch.linalg.qr).
 """
 import argparse
 import ctypes
@@ -25,7 +26,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from spanqr_amd import _lib, kcholqr_f  # noqa: E402
+from spanqr_amd import _lib, kcholqr_f, stages  # noqa: E402
 from spanqr_amd.plan import get_plan, stream_handle  # noqa: E402
 from spanqr_amd.qrbench import gen  # noqa: E402
 
@@ -35,45 +36,64 @@ SEEDS = (0, 1)
 TARGET_SHAPES = [(768, 512), (17408, 256)]
 PEAK_FP32_TFLOPS = 157.3     # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
-KERNELS = (["amax"] + [f"{k}{p}" for p in range(1, 4) for k in ("gram", "reduce", "chol", "trsm")]
-           + [f"ns_{k}{i}" for i in range(1, 3) for k in ("gram", "reduce", "apply")])
 
 
-def algorithmic(name, K, r):
-    """(flops, bytes) per launch of kernel `name` at (K, r): the per-unit figures of one orth() call, split by
-    kernel. Gram: K r (r+1) flops (symmetric), reads X once; TRSM: K r (r+1) flops, reads A (and Z on pass 1),
-    writes Y; NS apply: 2 K r^2 flops, reads Y, writes Q; Cholesky: r^3/3 flops; amax reads X; reduce: overhead."""
+# kernel families of one call: (name, spanqr_profile_kernel id, launches per call)
+FAMILIES = [("amax", _lib.K_AMAX, 1), ("gram_pass1", _lib.K_GRAM_PASS1, 1), ("gram", _lib.K_GRAM, 4),
+            ("reduce", _lib.K_REDUCE, 5), ("chol", _lib.K_CHOL, 3), ("trsm_pass1", _lib.K_TRSM_PASS1, 1),
+            ("trsm", _lib.K_TRSM, 2), ("ns_apply", _lib.K_NS_APPLY, 2)]
+
+
+def algorithmic(family, K, r):
+    """(flops, HBM bytes) of one launch at (K, r): Gram K r (r+1) flops (symmetric half) reading X once; solve
+    K r (r+1) flops reading A (and Z on pass 1) and writing Y; NS apply 2 K r^2 flops reading Y and writing Q;
+    Cholesky r^3 / 3 flops; amax reads X; the reduce moves only r x r partials (not counted)."""
     kr = 4.0 * K * r
-    if name == "amax":
-        return 0.0, kr
-    if name.startswith("gram") or name.startswith("ns_gram"):
-        return float(K) * r * (r + 1), kr
-    if name.startswith("trsm"):
-        return float(K) * r * (r + 1), (3 if name == "trsm1" else 2) * kr
-    if name.startswith("ns_apply"):
-        return 2.0 * K * r * r, 2 * kr
-    if name.startswith("chol"):
-        return r ** 3 / 3.0, 0.0
-    return 0.0, 0.0
+    return {"amax": (0.0, kr), "gram_pass1": (K * r * (r + 1.0), kr), "gram": (K * r * (r + 1.0), kr),
+            "reduce": (0.0, 0.0), "chol": (r ** 3 / 3.0, 0.0), "trsm_pass1": (K * r * (r + 1.0), 3 * kr),
+            "trsm": (K * r * (r + 1.0), 2 * kr), "ns_apply": (2.0 * K * r * r, 2 * kr)}[family]
 
 
-def family(name):
-    for f in ("ns_gram", "ns_reduce", "ns_apply", "gram", "reduce", "chol", "trsm", "amax"):
-        if name.startswith(f):
-            return f
-    return name
+def call_work(K, r):
+    """(flops, bytes) of one orth() call: 8 K r (r+1) + 4 K r^2 + r^3 flops, 68 K r bytes (17 fp32 passes over X)"""
+    return 8.0 * K * r * (r + 1) + 4.0 * K * r * r + float(r) ** 3, 68.0 * K * r
 
 
-def profile_call(X):
-    """per-kernel milliseconds of one orth() call on the current stream (events after every kernel)"""
+def kernel_avg_us(X, which, reps):
+    """average duration of one kernel of the call at X's shape: reps back-to-back launches between two HIP events on
+    the current stream (spanqr_profile_kernel), after one orth() call has filled the plan's workspace"""
     K, r = X.shape
+    kcholqr_f(X)
     plan = get_plan(K, r, X.device)
-    Q = torch.empty_like(X)
-    ms = (ctypes.c_float * 64)()
-    n = ctypes.c_int()
-    _lib.check(_lib.lib().spanqr_profile_orth(plan.handle, X.data_ptr(), r, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2,
-                                              stream_handle(X.device), ms, 64, ctypes.byref(n)))
-    return list(ms[:n.value])
+    ms = ctypes.c_float()
+    _lib.check(_lib.lib().spanqr_profile_kernel(plan.handle, which, reps, ctypes.byref(ms), stream_handle(X.device)))
+    return ms.value * 1000.0
+
+
+def chol_steps_us(X):
+    """per 64-column step of the Cholesky (two 32-wide diagonal steps), from the device wall clock stamped by
+    workgroup 0 of an instrumented copy of the kernel: list of microseconds, first step from kernel start"""
+    K, r = X.shape
+    kcholqr_f(X)
+    plan = get_plan(K, r, X.device)
+    G, npart = stages.gram(X, kahan=True, use_scale=True)
+    stamps = (ctypes.c_ulonglong * (12 * (r // 64)))()
+    tick = ctypes.c_double()
+    _lib.check(_lib.lib().spanqr_profile_chol(plan.handle, G.data_ptr(), npart.data_ptr(), 1e-7, 1e-8, stamps,
+                                              ctypes.byref(tick), stream_handle(X.device)))
+    t = [stamps[9]] + [stamps[12 * j + 7] for j in range(r // 64)]
+    return [(b - a) * tick.value / 1000.0 for a, b in zip(t, t[1:])]
+
+
+def traffic_bytes(family):
+    """HBM bytes per launch of a kernel family at the workload, from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
+    recorded in profiles/traffic.json (None if that kernel has no record)"""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            rec = json.load(f).get(family)
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else rec.get("bytes_per_launch")
 
 
 def capture(X):
@@ -156,10 +176,11 @@ def main(argv=None):
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="direct launches instead of one hipGraph per input")
+    p.add_argument("--kernel-reps", type=int, default=100, help="launches per kernel timing")
     a = p.parse_args(argv)
     if a.gpus != 1:
-        print(f"bench.py runs on one GPU: orth() on a single MI355X is the benchmark; --gpus {a.gpus} is not "
-              "supported (see DESIGN.md for how the work would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU: orth() of one matrix runs on a single MI355X and this build has no "
+              f"multi-GPU path, so --gpus {a.gpus} is not supported", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -211,30 +232,45 @@ def main(argv=None):
         targets[f"{K}x{r}"] = {"us_per_call": time_graph(g), "orth": orth_error(q)}
         del g
 
-    # per-kernel profile over the workload inputs (events on the call's stream)
-    fam_ms, fam_n, fam_flops, fam_bytes, kern = {}, {}, {}, {}, {}
-    for (K, r, s), X in inputs.items():
-        ms = [statistics.median(v) for v in zip(*[profile_call(X) for _ in range(5)])]
-        for name, t in zip(KERNELS, ms):
-            f = family(name)
-            fl, by = algorithmic(name, K, r)
-            fam_ms[f] = fam_ms.get(f, 0.0) + t
-            fam_n[f] = fam_n.get(f, 0) + 1
-            fam_flops[f] = fam_flops.get(f, 0.0) + fl
-            fam_bytes[f] = fam_bytes.get(f, 0.0) + by
-            kern.setdefault(name, []).append(t * 1000.0)
-    stages = {}
-    for f in fam_ms:
-        secs = fam_ms[f] / 1000.0
-        stages[f] = {"us_per_launch": fam_ms[f] * 1000.0 / fam_n[f], "share": fam_ms[f] / sum(fam_ms.values()),
-                     "tflops": fam_flops[f] / secs / 1e12, "gbs": fam_bytes[f] / secs / 1e9,
-                     "mfma_frac": fam_flops[f] / secs / 1e12 / PEAK_FP32_TFLOPS,
-                     "hbm_frac": fam_bytes[f] / secs / 1e9 / PEAK_HBM_GBS}
-    dom = max(fam_ms, key=fam_ms.get)
-    ds = stages[dom]
-    roofline = {"bound": "mfma", "kernel": dom, "achieved": ds["tflops"], "peak": PEAK_FP32_TFLOPS,
-                "unit": "TFLOP/s", "frac": ds["mfma_frac"], "traffic": None,
-                "note": "algorithmic flops per launch / average launch time from HIP events on the call's stream"}
+    # per kernel: average launch duration at each workload shape (HIP events around back-to-back launches)
+    kernels = {}
+    call_us = {}
+    for K, r in WORKLOAD_SHAPES:
+        X = inputs[(K, r, 0)]
+        tot = 0.0
+        for fam, which, per_call in FAMILIES:
+            us = kernel_avg_us(X, which, a.kernel_reps)
+            fl, by = algorithmic(fam, K, r)
+            kernels.setdefault(fam, {})[f"{K}x{r}"] = {
+                "us": us, "per_call": per_call, "tflops": fl / us / 1e6, "gbs": by / us / 1e3,
+                "mfma_frac": fl / us / 1e6 / PEAK_FP32_TFLOPS, "hbm_frac": by / us / 1e3 / PEAK_HBM_GBS}
+            tot += per_call * us
+        call_us[f"{K}x{r}"] = tot
+    share = {fam: sum(v[s_]["us"] * v[s_]["per_call"] for s_ in v) / sum(call_us.values())
+             for fam, v in kernels.items()}
+    dom = max(share, key=share.get)
+    dk = kernels[dom]
+    avg_us = statistics.mean(v["us"] for v in dk.values())
+    fl = statistics.mean(algorithmic(dom, K, r)[0] for K, r in WORKLOAD_SHAPES)
+    by = statistics.mean(algorithmic(dom, K, r)[1] for K, r in WORKLOAD_SHAPES)
+    bound = "mfma" if fl / PEAK_FP32_TFLOPS >= by / PEAK_HBM_GBS * 1e-3 else "hbm"
+    achieved = fl / avg_us / 1e6 if bound == "mfma" else by / avg_us / 1e3
+    peak = PEAK_FP32_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
+    roofline = {"bound": bound, "kernel": dom, "achieved": achieved, "peak": peak,
+                "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "frac": achieved / peak,
+                "traffic": traffic_bytes(dom), "avg_launch_us": avg_us, "share_of_call": share[dom],
+                "note": "algorithmic work per launch / average launch duration (HIP events around back-to-back "
+                        "launches on the call's stream); the Cholesky is latency-bound (its critical path is a chain "
+                        "of r pivots), so its roofline fraction is small by construction"}
+    call_roof = {}
+    for K, r in WORKLOAD_SHAPES:
+        F, B = call_work(K, r)
+        t = per_shape[f"{K}x{r}"] * 1e-6
+        call_roof[f"{K}x{r}"] = {"tflops": F / t / 1e12, "mfma_frac": F / t / 1e12 / PEAK_FP32_TFLOPS,
+                                 "gbs": B / t / 1e9, "hbm_frac": B / t / 1e9 / PEAK_HBM_GBS}
+    steps = chol_steps_us(inputs[(WORKLOAD_SHAPES[0][0], WORKLOAD_SHAPES[0][1], 0)])
+    chol_info = {"r": WORKLOAD_SHAPES[0][1], "us_per_64col_step": steps, "us_per_32col_diag_step":
+                 statistics.mean(steps) / 2, "note": "device wall clock stamped by workgroup 0 (instrumented copy)"}
 
     cpu = None if a.no_cpu else cpu_baseline({(K, r): inputs[(K, r, 0)] for K, r in WORKLOAD_SHAPES}, a.cpu_seconds)
     line = {
@@ -245,8 +281,8 @@ def main(argv=None):
                                "hipGraph per input", "shapes": [f"{K}x{r}" for K, r in WORKLOAD_SHAPES],
                    "seeds": list(SEEDS), "calls_per_step": calls, "graphs": not a.no_graph},
         "orth_max": orth_max, "per_shape_us": per_shape, "target_shapes": targets,
-        "roofline": roofline, "stages": stages,
-        "kernels_us": {k: statistics.mean(v) for k, v in kern.items()},
+        "roofline": roofline, "call_roofline": call_roof, "kernels": kernels, "kernel_share": share,
+        "sum_of_kernels_us": call_us, "cholesky": chol_info,
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(dev),
     }

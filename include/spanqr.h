@@ -73,6 +73,23 @@ int spanqr_profile_orth(spanqr_plan* plan, const float* X, long ldx, float* Q, l
 int spanqr_profile_chol(spanqr_plan* plan, const float* G, const double* npart, float alpha, float tau,
                         unsigned long long* stamps_out, double* tick_ns, void* stream);
 
+/* Kernels for spanqr_profile_kernel (the pass-1 forms read the power-of-2 scale and, for the solve, the dust). */
+enum {
+    SPANQR_K_AMAX = 0,
+    SPANQR_K_GRAM_PASS1 = 1,     /* Kahan Gram, scaled on load */
+    SPANQR_K_GRAM = 2,           /* plain Gram */
+    SPANQR_K_REDUCE = 3,         /* fp64 split reduction + norm partials */
+    SPANQR_K_CHOL = 4,           /* grid-synchronised clamped Cholesky */
+    SPANQR_K_TRSM_PASS1 = 5,     /* solve with the fused s * x + eps * z operand */
+    SPANQR_K_TRSM = 6,           /* solve */
+    SPANQR_K_NS_APPLY = 7,       /* Newton-Schulz correction Y + Y D */
+};
+
+/* Average duration of one kernel of the call: `reps` back-to-back launches on the plan's own workspace, between two
+ * HIP events on `stream`, after one untimed launch; waits for the stream. For timing only: it leaves the workspace
+ * in an unspecified state (the next spanqr_orth_f32 rebuilds what it needs). No counterpart in the reference. */
+int spanqr_profile_kernel(spanqr_plan* plan, int which, int reps, float* avg_ms, void* stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* spanqr_last_error(void);
 

@@ -19,6 +19,8 @@ HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
 
 # plan queries (include/spanqr.h)
 Q_K, Q_R, Q_SPLITS, Q_SPLIT_ROWS, Q_CHOL_GRID, Q_WORKSPACE_MB, Q_DEVICE = range(7)
+# kernels for spanqr_profile_kernel
+K_AMAX, K_GRAM_PASS1, K_GRAM, K_REDUCE, K_CHOL, K_TRSM_PASS1, K_TRSM, K_NS_APPLY = range(8)
 
 # every exported symbol of include/spanqr.h: (restype, argtypes)
 _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float
@@ -29,6 +31,7 @@ SIGNATURES = {
     "spanqr_orth_f32": (_I, [_P, _P, _L, _P, _L, _F, _F, _F, _I, _P]),
     "spanqr_profile_orth": (_I, [_P, _P, _L, _P, _L, _F, _F, _F, _I, _P, _P, _I, ctypes.POINTER(ctypes.c_int)]),
     "spanqr_profile_chol": (_I, [_P, _P, _P, _F, _F, _P, ctypes.POINTER(ctypes.c_double), _P]),
+    "spanqr_profile_kernel": (_I, [_P, _I, _I, ctypes.POINTER(ctypes.c_float), _P]),
     "spanqr_last_error": (ctypes.c_char_p, []),
     "spanqr_dust_host": (_I, [_I, _I, _P]),
     "spanqr_split_rows": (_I, [_I, _I]),

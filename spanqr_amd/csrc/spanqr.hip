@@ -1360,6 +1360,43 @@ int spanqr_profile_orth(spanqr_plan* p, const float* X, long ldx, float* Q, long
     return SPANQR_OK;
 }
 
+int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, void* stream) {
+    if (!p || !avg_ms) return fail(SPANQR_EINVAL, "null argument");
+    if (reps < 1 || reps > 100000) return fail(SPANQR_EINVAL, "reps = %d out of range", reps);
+    if (which < SPANQR_K_AMAX || which > SPANQR_K_NS_APPLY) return fail(SPANQR_EINVAL, "unknown kernel %d", which);
+    DeviceGuard dg(p->device);
+    if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
+    hipStream_t st = (hipStream_t)stream;
+    for (int i = 0; i < 2; ++i)
+        if (!p->ev[i]) HIPCHK(hipEventCreate(&p->ev[i]));
+    const int r = p->r;
+    auto launch = [&]() -> int {
+        switch (which) {
+            case SPANQR_K_AMAX: k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(p->Y0, r, p->K, r, p->amax_part); break;
+            case SPANQR_K_GRAM_PASS1: launch_gram(p, p->Y0, r, true, true, st); break;
+            case SPANQR_K_GRAM: launch_gram(p, p->Y0, r, false, false, st); break;
+            case SPANQR_K_REDUCE: launch_reduce(p, 0, p->G, st); break;
+            case SPANQR_K_CHOL: return launch_chol(p, 1e-7f, 1e-8f, p->scal + 1, st, 16 * p->U);
+            case SPANQR_K_TRSM_PASS1: launch_trsm(p, p->Y0, r, true, 5e-7f, p->Lt, p->Lit, p->Y1, r, st); break;
+            case SPANQR_K_TRSM: launch_trsm(p, p->Y0, r, false, 0.0f, p->Lt, p->Lit, p->Y1, r, st); break;
+            case SPANQR_K_NS_APPLY: launch_nsapply(p, p->Y0, r, p->Y1, r, st); break;
+        }
+        return SPANQR_OK;
+    };
+    int rc;
+    if ((rc = launch())) return rc;
+    HIPCHK(hipEventRecord(p->ev[0], st));
+    for (int i = 0; i < reps; ++i)
+        if ((rc = launch())) return rc;
+    HIPCHK(hipEventRecord(p->ev[1], st));
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipEventSynchronize(p->ev[1]));
+    float ms = 0.0f;
+    HIPCHK(hipEventElapsedTime(&ms, p->ev[0], p->ev[1]));
+    *avg_ms = ms / (float)reps;
+    return SPANQR_OK;
+}
+
 int spanqr_stage_amax(spanqr_plan* p, const float* X, long ldx, void* stream) {
     if (!p) return fail(SPANQR_EINVAL, "plan is null");
     int rc = check_mat(p, X, ldx, "X");
