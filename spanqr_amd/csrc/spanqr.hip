@@ -300,10 +300,8 @@ __device__ __forceinline__ void grid_barrier(uint32_t* bar, uint32_t nblocks, ui
 
 struct CholShared {
     float t[11][CB][TS];   // 0: Li_a, 1: Li_b, 2: L_ba of the current diagonal block; 3..6 and 7..10: 64x64 blocks
-    float dl[CB][36];      // factored 32x32 diagonal tile (row stride 36: 16-byte rows for the inverse)
-    float xs[16][36];      // inverse rows 0..15 (MFMA operand), then the rows 16..31 partial sums
-    float bl[CB];          // column broadcast in the tile factor
-    float rd[CB];          // pivot reciprocals of that tile
+    float dl[CB][36];      // factored 32x32 diagonal tile (row stride 36: 16-byte rows)
+    alignas(16) float bl[CB];   // column broadcast in the tile factor
     float bc[4];           // broadcast: nrm, shift, tau
 };
 
@@ -373,30 +371,36 @@ __device__ __forceinline__ f32x4 update64(f32x4 acc, float (*Xi0)[TS], float (*X
     return acc;
 }
 
-// Wave 0 only: factor the 32x32 tile D (lower part) in registers, lane i = row i (chol.cu:131-142); writes the
-// factor (zeros above the diagonal) to sh.dl and the pivot reciprocals to sh.rd. Column c: every lane scales its
-// entry (l_i), then updates its remaining entries v[k] -= l_i l_k (eager right-looking order, each element's updates
-// in column order). Only the update of column c+1 is on the critical path, so l_{c+1} comes by v_readlane and the
-// next pivot is formed right away; the other l_k go through LDS and their updates overlap the next pivot chain.
-__device__ __forceinline__ void factor32(CholShared& sh, float (*D)[TS], float tau) {
+// Wave 0 only: factor the 32x32 tile D (lower part) and invert the factor in one pass (chol.cu:131-168).
+// Lanes 0..31 hold row i of D; lanes 32..63 hold column kk of the identity, which becomes column kk of the inverse.
+// Column c: the pivot piv = fmaxf(D_cc, tau) and q = rsqrt(piv) are uniform; a factor lane's value is
+// l_i = D_ic q (piv q on the diagonal, 0 above it), an inverse lane's is x_c = acc_c q (0 for c < kk). Both halves
+// then run the same rank-1 update R[k] = fma(-own, l_k, R[k]) for k > c, which is the factor's trailing update
+// D_ik -= l_i l_k and the inverse's forward substitution acc_k -= L_kc x_c, each element's chain in column order.
+// Only the update of column c+1 is on the critical path: l_{c+1} comes by v_readlane and the next pivot is formed
+// right away; the other l_k are broadcast through LDS and their updates overlap the next pivot chain.
+// Writes the factor (zeros above the diagonal) to sh.dl and the inverse to Li.
+__device__ __forceinline__ void factor_inv32(CholShared& sh, float (*D)[TS], float tau, float (*Li)[TS]) {
     const int lane = threadIdx.x & 63, i = lane & 31;
-    float v[CB];
+    const bool fl = lane < 32;
+    float R[CB];
 #pragma unroll
-    for (int k = 0; k < CB; ++k) v[k] = D[i][k];
-    float myrd = 0.0f;
-    float piv = fmaxf(readlane(v[0], 0), tau);
+    for (int k = 0; k < CB; ++k) R[k] = fl ? D[i][k] : (k == i ? 1.0f : 0.0f);
+    float piv = fmaxf(readlane(R[0], 0), tau);
     float q = rsqrt_sw(piv);
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-        const float l = (i > c) ? v[c] * q : ((i == c) ? piv * q : 0.0f);
-        myrd = (i == c) ? q : myrd;
-        v[c] = l;
+        const float sc = R[c] * q;
+        const float lf = (i > c) ? sc : ((i == c) ? piv * q : 0.0f);
+        const float xi = (c < i) ? 0.0f : sc;
+        const float own = fl ? lf : xi;
+        R[c] = own;
         if (c + 1 < CB) {
-            v[c + 1] = __builtin_fmaf(-l, readlane(l, c + 1), v[c + 1]);
-            const float pn = fmaxf(readlane(v[c + 1], c + 1), tau);
+            R[c + 1] = __builtin_fmaf(-own, readlane(own, c + 1), R[c + 1]);
+            const float pn = fmaxf(readlane(R[c + 1], c + 1), tau);
             const float qn = rsqrt_sw(pn);
             if (c + 2 < CB) {
-                if (lane < 32) sh.bl[i] = l;
+                if (fl) sh.bl[i] = own;
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll
                 for (int k0 = (c + 2) & ~3; k0 < CB; k0 += 4) {
@@ -404,7 +408,7 @@ __device__ __forceinline__ void factor32(CholShared& sh, float (*D)[TS], float t
                     const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
                     for (int t = 0; t < 4; ++t)
-                        if (k0 + t > c + 1) v[k0 + t] = __builtin_fmaf(-l, lv[t], v[k0 + t]);
+                        if (k0 + t > c + 1) R[k0 + t] = __builtin_fmaf(-own, lv[t], R[k0 + t]);
                 }
                 __builtin_amdgcn_wave_barrier();
             }
@@ -412,58 +416,12 @@ __device__ __forceinline__ void factor32(CholShared& sh, float (*D)[TS], float t
             q = qn;
         }
     }
-    if (lane < 32) {
+    if (fl) {
 #pragma unroll
-        for (int k = 0; k < CB; ++k) sh.dl[i][k] = (k <= i) ? v[k] : 0.0f;
-        sh.rd[i] = myrd;
-    }
-    __builtin_amdgcn_wave_barrier();
-}
-
-// Wave 0 only: inverse of the factored tile in sh.dl, column kk in lane kk (chol.cu:151-168): x_i = 0 for i < kk,
-// else acc = [i == kk], acc = fma(-L[i][m], x_m, acc) for m = 0..i-1 in order, x_i = acc * rd_i. Rows 0..15 by
-// substitution; for rows 16..31 the terms m < 16 are one MFMA chain (16 rows x 32 columns, k = m in order), then
-// substitution continues with m = 16..i-1.
-__device__ __forceinline__ void inverse32(CholShared& sh, float (*Li)[TS]) {
-    const int lane = threadIdx.x & 63, kk = lane & 31, l16 = lane & 15, lk = lane >> 4;
-    float x[CB];
+        for (int k = 0; k < CB; ++k) sh.dl[i][k] = (k <= i) ? R[k] : 0.0f;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        float acc = (i == kk) ? 1.0f : 0.0f;
-#pragma unroll
-        for (int m = 0; m < i; ++m) acc = __builtin_fmaf(-sh.dl[i][m], x[m], acc);
-        x[i] = (i < kk) ? 0.0f : acc * sh.rd[i];
-    }
-    if (lane < 32) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sh.xs[i][kk] = x[i];
-    }
-    __builtin_amdgcn_wave_barrier();
-    f32x4 acc2[2];
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc2[cb][v] = (16 + 4 * lk + v == 16 * cb + l16) ? 1.0f : 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            acc2[cb] = mfma(-sh.dl[16 + l16][4 * q + lk], sh.xs[4 * q + lk][16 * cb + l16], acc2[cb]);
-    }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sh.xs[4 * lk + v][16 * cb + l16] = acc2[cb][v];
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int i = 16; i < CB; ++i) {
-        float acc = sh.xs[i - 16][kk];
-#pragma unroll
-        for (int m = 16; m < i; ++m) acc = __builtin_fmaf(-sh.dl[i][m], x[m], acc);
-        x[i] = (i < kk) ? 0.0f : acc * sh.rd[i];
-    }
-    if (lane < 32) {
-#pragma unroll
-        for (int i = 0; i < CB; ++i) Li[i][kk] = x[i];
+        for (int k = 0; k < CB; ++k) Li[k][i] = R[k];
     }
     __builtin_amdgcn_wave_barrier();
 }
@@ -497,10 +455,8 @@ __device__ __forceinline__ void factor_diag64(CholShared& sh, int J, int r, floa
     const int w = threadIdx.x >> 6;
     const size_t o = (size_t)64 * J;
     if (w == 0) {
-        factor32(sh, sh.t[7], tau);
-        if (stamp && threadIdx.x == 0) stamp[0] = wall_clock64();
-        inverse32(sh, sh.t[0]);
-        if (stamp && threadIdx.x == 0) stamp[1] = wall_clock64();
+        factor_inv32(sh, sh.t[7], tau, sh.t[0]);
+        if (stamp && threadIdx.x == 0) stamp[0] = stamp[1] = wall_clock64();
     }
     __syncthreads();
     store_dl(L + o * r + o, r, sh.dl);
@@ -512,10 +468,7 @@ __device__ __forceinline__ void factor_diag64(CholShared& sh, int J, int r, floa
     store_tile_T(Lt + o * r + o + 32, r, sh.t[2]);
     update32(sh.t[9], sh.t[2], sh.t[2], true);   // A_bb -= L_ba L_ba^T
     if (stamp && threadIdx.x == 0) stamp[2] = wall_clock64();
-    if (w == 0) {
-        factor32(sh, sh.t[9], tau);
-        inverse32(sh, sh.t[1]);
-    }
+    if (w == 0) factor_inv32(sh, sh.t[9], tau, sh.t[1]);
     __syncthreads();
     store_dl(L + (o + 32) * r + o + 32, r, sh.dl);
     store_dl_T(Lt + (o + 32) * r + o + 32, r, sh.dl);
@@ -641,7 +594,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
                                               float* scal, uint64_t* stamps) {
     __shared__ CholShared sh;
     // STAMP: workgroup 0 records wall_clock64() at phase boundaries, 12 slots per 64-column step s: 0 loads done,
-    // 1 panel done, 2 diagonal update done, 3 first tile factored, 4 first tile inverted, 5 second tile update done,
+    // 1 panel done, 2 diagonal update done, 3 and 4 first tile factored and inverted, 5 second tile update done,
     // 6 block done, 7 after the grid barrier; step 0 also has 9 kernel start, 8 norm done.
 #define CHOL_STAMP(J_, k_)                                                                  \
     do {                                                                                    \
