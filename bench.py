@@ -71,18 +71,19 @@ def kernel_avg_us(X, which, reps):
 
 
 def chol_steps_us(X):
-    """per 64-column step of the Cholesky (two 32-wide diagonal steps), from the device wall clock stamped by
-    workgroup 0 of an instrumented copy of the kernel: list of microseconds, first step from kernel start"""
+    """per 32-column diagonal step of the Cholesky: the device wall clock stamped by workgroup 0 of an instrumented
+    copy of the kernel (spanqr_profile_chol): list of (step us, of which tile factor + next-row wait us)"""
     K, r = X.shape
     kcholqr_f(X)
     plan = get_plan(K, r, X.device)
     G, npart = stages.gram(X, kahan=True, use_scale=True)
-    stamps = (ctypes.c_ulonglong * (12 * (r // 64)))()
+    nb = r // 32
+    stamps = (ctypes.c_ulonglong * (6 * nb))()
     tick = ctypes.c_double()
     _lib.check(_lib.lib().spanqr_profile_chol(plan.handle, G.data_ptr(), npart.data_ptr(), 1e-7, 1e-8, stamps,
                                               ctypes.byref(tick), stream_handle(X.device)))
-    t = [stamps[9]] + [stamps[12 * j + 7] for j in range(r // 64)]
-    return [(b - a) * tick.value / 1000.0 for a, b in zip(t, t[1:])]
+    us = lambda a, b: (stamps[b] - stamps[a]) * tick.value / 1000.0
+    return [(us(1 + 4 * j, 1 + 4 * (j + 1)), us(1 + 4 * j, 2 + 4 * j)) for j in range(nb)]
 
 
 def traffic_bytes(family):
@@ -269,8 +270,10 @@ def main(argv=None):
         call_roof[f"{K}x{r}"] = {"tflops": F / t / 1e12, "mfma_frac": F / t / 1e12 / PEAK_FP32_TFLOPS,
                                  "gbs": B / t / 1e9, "hbm_frac": B / t / 1e9 / PEAK_HBM_GBS}
     steps = chol_steps_us(inputs[(WORKLOAD_SHAPES[0][0], WORKLOAD_SHAPES[0][1], 0)])
-    chol_info = {"r": WORKLOAD_SHAPES[0][1], "us_per_64col_step": steps, "us_per_32col_diag_step":
-                 statistics.mean(steps) / 2, "note": "device wall clock stamped by workgroup 0 (instrumented copy)"}
+    chol_info = {"r": WORKLOAD_SHAPES[0][1], "us_per_32col_step": [round(a, 2) for a, _ in steps],
+                 "us_factor_and_wait": [round(b, 2) for _, b in steps],
+                 "us_per_32col_diag_step": statistics.mean(a for a, _ in steps),
+                 "note": "device wall clock stamped by workgroup 0 of an instrumented copy of the kernel"}
 
     cpu = None if a.no_cpu else cpu_baseline({(K, r): inputs[(K, r, 0)] for K, r in WORKLOAD_SHAPES}, a.cpu_seconds)
     line = {

@@ -40,7 +40,7 @@ enum {
     SPANQR_Q_R = 1,
     SPANQR_Q_SPLITS = 2,         /* Gram row splits S */
     SPANQR_Q_SPLIT_ROWS = 3,     /* rows per split KS (a multiple of 32) */
-    SPANQR_Q_CHOL_GRID = 4,      /* workgroups of the grid-synchronised Cholesky */
+    SPANQR_Q_CHOL_GRID = 4,      /* workgroups of the Cholesky (max(1, r/32 - 2)) */
     SPANQR_Q_WORKSPACE_MB = 5,   /* workspace size, MiB (rounded up) */
     SPANQR_Q_DEVICE = 6,
 };
@@ -67,9 +67,10 @@ int spanqr_profile_orth(spanqr_plan* plan, const float* X, long ldx, float* Q, l
                         float tau, int ns, void* stream, float* ms, int max_n, int* n_out);
 
 /* Profiling form of the Cholesky stage (spanqr_stage_chol with npart): runs an instrumented copy of the kernel whose
- * workgroup 0 stamps the device wall clock at each phase of every 64-column step, copies the stamps to host memory
- * (12 per step, r/64 steps; see the kernel source for the slots) and waits for the stream. *tick_ns: nanoseconds per
- * wall-clock tick. The reference keeps similar stamps behind a debug define (candidates/cuk/chol.cu:17-23). */
+ * workgroup 0 stamps the device wall clock, copies 6 r/32 stamps to host memory and waits for the stream: [0] kernel
+ * start; for each 32-column diagonal step j, [1 + 4j] step start, [2 + 4j] tile factored and the next tile row
+ * fetched, [3 + 4j] look-ahead done; [1 + 4 r/32] end; the rest zero. *tick_ns: nanoseconds per wall-clock tick. The
+ * reference keeps similar stamps behind a debug define (candidates/cuk/chol.cu:17-23). */
 int spanqr_profile_chol(spanqr_plan* plan, const float* G, const double* npart, float alpha, float tau,
                         unsigned long long* stamps_out, double* tick_ns, void* stream);
 

@@ -265,45 +265,25 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Grid-synchronised clamped Cholesky (chol.cu:182-271 restated for 64-column super-steps).
+// Clamped Cholesky (chol.cu:115-271): one persistent kernel over 32x32 tiles T(i, k), i >= k, nb = r / 32 tile rows,
+// synchronised by per-tile flags instead of grid barriers.
+//   * Workgroup 0 runs the critical chain. Step j: wave 0 factors T(j, j) and inverts the factor in one pass; at the
+//     same time wave 1 fetches tile row j+2 (T(j+2, j-1..j+2), handed over by its owner through column block j-2)
+//     and brings it through block j-1 (panel L(j+2, j-1) with the previous step's Li_{j-1}, L(j, j-1), L(j+1, j-1)
+//     still in LDS), and wave 2 publishes the previous step's L tiles and Li. Then all waves form the panels
+//     L(j+1, j), L(j+2, j) and apply column block j to T(j+1, j+1), T(j+2, j+1), T(j+2, j+2) (look-ahead over the
+//     next two tile rows).
+//   * Workgroup i-3 owns tile row i >= 4 for the whole factorisation, in LDS. For column block j = 0..i-4 in order:
+//     panel L(i, j) = T(i, j) Li_j^T (published), then T(i, k) -= L(i, j) L(k, j)^T for k = j+1..i with the other
+//     rows' panels of block j fetched together; after block i-4 it hands T(i, i-3..i) to workgroup 0, two steps
+//     before workgroup 0 needs them.
+// Every element keeps the reference order: updates by column block in increasing order, each one MFMA chain over the
+// block's 32 columns. A producer publishes with an agent-scope release after its stores; a consumer polls with
+// bounded waits (after SPIN_LIMIT polls it records an error and stops waiting, so the kernel always ends). Each
+// workgroup waits only on work earlier in the (column block, panel before update) order, which with all
+// workgroups resident (checked at plan creation) rules out deadlock. Flags hold the call number of the workgroup's
+// own counter, so nothing is reset between calls.
 // ---------------------------------------------------------------------------------------------------------------
-
-// Grid barrier: every wave waits for its own stores, the workgroup meets, thread 0 arrives with an agent-scope
-// release and waits with agent-scope acquires (bounded: after SPIN_LIMIT polls it records an error and goes on, so
-// the kernel always ends; once it has timed out, `dead` makes its later waits return at once). bar[0] counts
-// arrivals and returns to 0, bar[1] is the generation. The grid is launched as an ordinary dispatch of at most 64
-// workgroups; plan creation checks that the device holds them all at once (occupancy x CUs), which is what the
-// barrier needs.
-__device__ __forceinline__ void grid_barrier(uint32_t* bar, uint32_t nblocks, uint32_t* err, bool& dead) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t g = __hip_atomic_load(bar + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t a = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        if (a == nblocks - 1) {
-            __hip_atomic_store(bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(bar + 1, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            uint32_t n = 0;
-            while (!dead && __hip_atomic_load(bar + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g) {
-                if (++n > SPIN_LIMIT) {
-                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    dead = true;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-    }
-    __syncthreads();
-}
-
-struct CholShared {
-    float t[11][CB][TS];   // 0: Li_a, 1: Li_b, 2: L_ba of the current diagonal block; 3..6 and 7..10: 64x64 blocks
-    float dl[CB][36];      // factored 32x32 diagonal tile (row stride 36: 16-byte rows)
-    alignas(16) float bl[CB];   // column broadcast in the tile factor
-    float bc[4];           // broadcast: nrm, shift, tau
-};
 
 // wave w computes the 16x16 block (w >> 1, w & 1) of a 32x32 tile; lane (l16, lk) holds rows 16bi + 4lk + v
 #define WAVE_COORDS                                                                  \
@@ -311,27 +291,45 @@ struct CholShared {
     const int bi = w_ >> 1, bj = w_ & 1, l16 = lane_ & 15, lk = lane_ >> 4;          \
     (void)bi; (void)bj; (void)l16; (void)lk
 
-// global 32x32 tile (row stride ld) -> LDS tile; adds `shift` to the diagonal when diag is set
-__device__ __forceinline__ void load_tile(float (*dst)[TS], const float* src, int ld, bool diag, float shift) {
-    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
-    const float4 v = *reinterpret_cast<const float4*>(src + (size_t)row * ld + 4 * c4);
-    float x[4] = {v.x, v.y, v.z, v.w};
+typedef float Tile[CB][TS];
+
+// global 32x32 tile (row stride ld) -> LDS tile by threads t0, t0 + nthr, ... of the workgroup; adds `shift` to the
+// diagonal when diag is set
+__device__ __forceinline__ void load_tile(Tile& dst, const float* src, int ld, bool diag, float shift, int t = -1,
+                                          int nthr = 256) {
+    for (int e = (t < 0 ? (int)threadIdx.x : t); e < 256; e += nthr) {
+        const int row = e >> 3, c4 = e & 7;
+        const float4 v = *reinterpret_cast<const float4*>(src + (size_t)row * ld + 4 * c4);
+        float x[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        if (diag && row == 4 * c4 + q) x[q] = x[q] + shift;
-        dst[row][4 * c4 + q] = x[q];
+        for (int q = 0; q < 4; ++q) {
+            if (diag && row == 4 * c4 + q) x[q] = x[q] + shift;
+            dst[row][4 * c4 + q] = x[q];
+        }
     }
 }
 
-__device__ __forceinline__ void store_tile(float* dst, int ld, float (*src)[TS]) {
-    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
-    float4 v;
-    v.x = src[row][4 * c4 + 0]; v.y = src[row][4 * c4 + 1]; v.z = src[row][4 * c4 + 2]; v.w = src[row][4 * c4 + 3];
-    *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+__device__ __forceinline__ void store_tile(float* dst, int ld, const Tile& src, int t = -1, int nthr = 256) {
+    for (int e = (t < 0 ? (int)threadIdx.x : t); e < 256; e += nthr) {
+        const int row = e >> 3, c4 = e & 7;
+        float4 v;
+        v.x = src[row][4 * c4 + 0]; v.y = src[row][4 * c4 + 1]; v.z = src[row][4 * c4 + 2]; v.w = src[row][4 * c4 + 3];
+        *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+    }
 }
 
-// out = in Li^T; chain over m < 16 (bj + 1) (Li is lower triangular). out may alias in.
-__device__ __forceinline__ void panel32(float (*out)[TS], float (*in)[TS], float (*li)[TS]) {
+// transposed store: dst[c][r'] = src[r'][c] (the solve reads L^T and the Li blocks transposed, coalesced)
+__device__ __forceinline__ void store_tile_T(float* dst, int ld, const Tile& src, int t = -1, int nthr = 256) {
+    for (int e = (t < 0 ? (int)threadIdx.x : t); e < 256; e += nthr) {
+        const int row = e >> 3, c4 = e & 7;
+        float4 v;
+        v.x = src[4 * c4 + 0][row]; v.y = src[4 * c4 + 1][row]; v.z = src[4 * c4 + 2][row]; v.w = src[4 * c4 + 3][row];
+        *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+    }
+}
+
+// out = in Li^T; chain over m < 16 (bj + 1) (Li is lower triangular, chol.cu panel). out may alias in.
+__device__ __forceinline__ void panel32(Tile& out, const Tile& in, const Tile& li) {
     WAVE_COORDS;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int kk = 0; kk < 4 * (bj + 1); ++kk)
@@ -342,8 +340,8 @@ __device__ __forceinline__ void panel32(float (*out)[TS], float (*in)[TS], float
     __syncthreads();
 }
 
-// C -= Pi Pk^T (chain over m = 0..31 from C); lower: skip the upper 16x16 block
-__device__ __forceinline__ void update32(float (*C)[TS], float (*Pi)[TS], float (*Pk)[TS], bool lower) {
+// dst = C - Pi Pk^T (chain over m = 0..31 starting from C); lower: skip the upper 16x16 block. dst may alias C.
+__device__ __forceinline__ void update32(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk, bool lower) {
     WAVE_COORDS;
     if (!(lower && bi == 0 && bj == 1)) {
         f32x4 acc;
@@ -353,22 +351,60 @@ __device__ __forceinline__ void update32(float (*C)[TS], float (*Pi)[TS], float 
         for (int kk = 0; kk < 8; ++kk)
             acc = mfma(-Pi[16 * bi + l16][4 * kk + lk], Pk[16 * bj + l16][4 * kk + lk], acc);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) C[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+        for (int v = 0; v < 4; ++v) dst[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
     }
     __syncthreads();
 }
 
-// acc (C-layout block of this wave) -= [Xi0 Xi1] [Xk0 Xk1]^T, chain over the 64 panel columns in order
-__device__ __forceinline__ f32x4 update64(f32x4 acc, float (*Xi0)[TS], float (*Xi1)[TS], float (*Xk0)[TS],
-                                          float (*Xk1)[TS]) {
+// Two panels in one phase: outA = inA Li^T, outB = inB Li^T (outputs must not alias the inputs)
+__device__ __forceinline__ void panel32x2(Tile& outA, const Tile& inA, Tile& outB, const Tile& inB, const Tile& li) {
     WAVE_COORDS;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < 4 * (bj + 1); ++kk) {
+        const float lv = li[16 * bj + l16][4 * kk + lk];
+        a = mfma(inA[16 * bi + l16][4 * kk + lk], lv, a);
+        c = mfma(inB[16 * bi + l16][4 * kk + lk], lv, c);
+    }
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-        acc = mfma(-Xi0[16 * bi + l16][4 * kk + lk], Xk0[16 * bj + l16][4 * kk + lk], acc);
+    for (int v = 0; v < 4; ++v) {
+        outA[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
+        outB[16 * bi + 4 * lk + v][16 * bj + l16] = c[v];
+    }
+    __syncthreads();
+}
+
+// One wave: a whole 32x32 tile, quadrant by quadrant. out = in Li^T (out must not alias in).
+__device__ __forceinline__ void panel32_wave(Tile& out, const Tile& in, const Tile& li) {
+    const int lane = threadIdx.x & 63, l16 = lane & 15, lk = lane >> 4;
+    for (int qd = 0; qd < 4; ++qd) {
+        const int bi = qd >> 1, bj = qd & 1;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < 4 * (bj + 1); ++kk)
+            acc = mfma(in[16 * bi + l16][4 * kk + lk], li[16 * bj + l16][4 * kk + lk], acc);
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-        acc = mfma(-Xi1[16 * bi + l16][4 * kk + lk], Xk1[16 * bj + l16][4 * kk + lk], acc);
-    return acc;
+        for (int v = 0; v < 4; ++v) out[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the tile is written before this wave reads it back
+    __builtin_amdgcn_wave_barrier();
+}
+
+// One wave: C -= Pi Pk^T in place, quadrant by quadrant (lower: skip the upper 16x16 block)
+__device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Tile& Pk, bool lower) {
+    const int lane = threadIdx.x & 63, l16 = lane & 15, lk = lane >> 4;
+    for (int qd = 0; qd < 4; ++qd) {
+        const int bi = qd >> 1, bj = qd & 1;
+        if (lower && qd == 1) continue;
+        f32x4 acc;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] = C[16 * bi + 4 * lk + v][16 * bj + l16];
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            acc = mfma(-Pi[16 * bi + l16][4 * kk + lk], Pk[16 * bj + l16][4 * kk + lk], acc);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) C[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
 }
 
 // Wave 0 only: factor the 32x32 tile D (lower part) and invert the factor in one pass (chol.cu:131-168).
@@ -378,9 +414,9 @@ __device__ __forceinline__ f32x4 update64(f32x4 acc, float (*Xi0)[TS], float (*X
 // then run the same rank-1 update R[k] = fma(-own, l_k, R[k]) for k > c, which is the factor's trailing update
 // D_ik -= l_i l_k and the inverse's forward substitution acc_k -= L_kc x_c, each element's chain in column order.
 // Only the update of column c+1 is on the critical path: l_{c+1} comes by v_readlane and the next pivot is formed
-// right away; the other l_k are broadcast through LDS and their updates overlap the next pivot chain.
-// Writes the factor (zeros above the diagonal) to sh.dl and the inverse to Li.
-__device__ __forceinline__ void factor_inv32(CholShared& sh, float (*D)[TS], float tau, float (*Li)[TS]) {
+// right away; the other l_k are broadcast through LDS (bl) and their updates overlap the next pivot chain.
+// Writes the factor (zeros above the diagonal) to dl and the inverse to Li.
+__device__ __forceinline__ void factor_inv32(float* bl, const Tile& D, float tau, Tile& dl, Tile& Li) {
     const int lane = threadIdx.x & 63, i = lane & 31;
     const bool fl = lane < 32;
     float R[CB];
@@ -400,11 +436,11 @@ __device__ __forceinline__ void factor_inv32(CholShared& sh, float (*D)[TS], flo
             const float pn = fmaxf(readlane(R[c + 1], c + 1), tau);
             const float qn = rsqrt_sw(pn);
             if (c + 2 < CB) {
-                if (fl) sh.bl[i] = own;
+                if (fl) bl[i] = own;
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll
                 for (int k0 = (c + 2) & ~3; k0 < CB; k0 += 4) {
-                    const float4 l4 = *reinterpret_cast<const float4*>(&sh.bl[k0]);
+                    const float4 l4 = *reinterpret_cast<const float4*>(&bl[k0]);
                     const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
                     for (int t = 0; t < 4; ++t)
@@ -418,7 +454,7 @@ __device__ __forceinline__ void factor_inv32(CholShared& sh, float (*D)[TS], flo
     }
     if (fl) {
 #pragma unroll
-        for (int k = 0; k < CB; ++k) sh.dl[i][k] = (k <= i) ? R[k] : 0.0f;
+        for (int k = 0; k < CB; ++k) dl[i][k] = (k <= i) ? R[k] : 0.0f;
     } else {
 #pragma unroll
         for (int k = 0; k < CB; ++k) Li[k][i] = R[k];
@@ -426,247 +462,272 @@ __device__ __forceinline__ void factor_inv32(CholShared& sh, float (*D)[TS], flo
     __builtin_amdgcn_wave_barrier();
 }
 
-// transposed stores: dst[c][r'] = src[r'][c] (for the solve's coalesced operand reads)
-__device__ __forceinline__ void store_tile_T(float* dst, int ld, float (*src)[TS]) {
-    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
-    float4 v;
-    v.x = src[4 * c4 + 0][row]; v.y = src[4 * c4 + 1][row]; v.z = src[4 * c4 + 2][row]; v.w = src[4 * c4 + 3][row];
-    *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
-}
-
-__device__ __forceinline__ void store_dl_T(float* dst, int ld, float (*src)[36]) {
-    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
-    float4 v;
-    v.x = src[4 * c4 + 0][row]; v.y = src[4 * c4 + 1][row]; v.z = src[4 * c4 + 2][row]; v.w = src[4 * c4 + 3][row];
-    *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
-}
-
-__device__ __forceinline__ void store_dl(float* dst, int ld, float (*src)[36]) {
-    const int row = threadIdx.x >> 3, c4 = threadIdx.x & 7;
-    const float4 v = *reinterpret_cast<const float4*>(&src[row][4 * c4]);
-    *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
-}
-
-// Factor the 64x64 diagonal block held in t[7] (rows/cols 0..31), t[8] (rows 32..63 x cols 0..31), t[9] (rows and
-// cols 32..63) as two 32-wide reference steps: outputs t[0] = Li_a, t[1] = Li_b, t[2] = L_ba and writes the block's
-// L tiles and Li rows to global.
-__device__ __forceinline__ void factor_diag64(CholShared& sh, int J, int r, float tau, float* L, float* Li, float* Lt,
-                                              float* Lit, uint64_t* stamp = nullptr) {
-    const int w = threadIdx.x >> 6;
-    const size_t o = (size_t)64 * J;
-    if (w == 0) {
-        factor_inv32(sh, sh.t[7], tau, sh.t[0]);
-        if (stamp && threadIdx.x == 0) stamp[0] = stamp[1] = wall_clock64();
-    }
-    __syncthreads();
-    store_dl(L + o * r + o, r, sh.dl);
-    store_dl_T(Lt + o * r + o, r, sh.dl);
-    store_tile(Li + o * CB, CB, sh.t[0]);
-    store_tile_T(Lit + o * CB, CB, sh.t[0]);
-    panel32(sh.t[2], sh.t[8], sh.t[0]);          // L_ba = A_ba Li_a^T
-    store_tile(L + (o + 32) * r + o, r, sh.t[2]);
-    store_tile_T(Lt + o * r + o + 32, r, sh.t[2]);
-    update32(sh.t[9], sh.t[2], sh.t[2], true);   // A_bb -= L_ba L_ba^T
-    if (stamp && threadIdx.x == 0) stamp[2] = wall_clock64();
-    if (w == 0) factor_inv32(sh, sh.t[9], tau, sh.t[1]);
-    __syncthreads();
-    store_dl(L + (o + 32) * r + o + 32, r, sh.dl);
-    store_dl_T(Lt + (o + 32) * r + o + 32, r, sh.dl);
-    store_tile(Li + (o + 32) * CB, CB, sh.t[1]);
-    store_tile_T(Lit + (o + 32) * CB, CB, sh.t[1]);
-    __syncthreads();
-}
-
-// Panel of a 64-row block held in t[base..base+3] = (rows 0-31: cols 0-31, 32-63; rows 32-63: cols 0-31, 32-63)
-// against the current diagonal block (t[0..2]): Q0 = X0 Li_a^T, X1 -= Q0 L_ba^T, Q1 = X1 Li_b^T, in place.
-__device__ __forceinline__ void super_panel(CholShared& sh, int base) {
-    for (int h = 0; h < 2; ++h) {
-        float (*x0)[TS] = sh.t[base + 2 * h];
-        float (*x1)[TS] = sh.t[base + 2 * h + 1];
-        panel32(x0, x0, sh.t[0]);
-        update32(x1, x0, sh.t[2], false);
-        panel32(x1, x1, sh.t[1]);
-    }
-}
-
-__device__ __forceinline__ void load_block64(CholShared& sh, int base, const float* src, int r) {
-    load_tile(sh.t[base + 0], src, r, false, 0.f);
-    load_tile(sh.t[base + 1], src + 32, r, false, 0.f);
-    load_tile(sh.t[base + 2], src + (size_t)32 * r, r, false, 0.f);
-    load_tile(sh.t[base + 3], src + (size_t)32 * r + 32, r, false, 0.f);
-}
-
-__device__ __forceinline__ void store_block64(float* dst, int r, CholShared& sh, int base) {
-    store_tile(dst, r, sh.t[base + 0]);
-    store_tile(dst + 32, r, sh.t[base + 1]);
-    store_tile(dst + (size_t)32 * r, r, sh.t[base + 2]);
-    store_tile(dst + (size_t)32 * r + 32, r, sh.t[base + 3]);
-}
-
-// the transposed block: dst (row stride r) receives block^T, i.e. tile (h, c) of the block goes to (c, h)
-__device__ __forceinline__ void store_block64_T(float* dst, int r, CholShared& sh, int base) {
-    store_tile_T(dst, r, sh.t[base + 0]);
-    store_tile_T(dst + (size_t)32 * r, r, sh.t[base + 1]);
-    store_tile_T(dst + 32, r, sh.t[base + 2]);
-    store_tile_T(dst + (size_t)32 * r + 32, r, sh.t[base + 3]);
-}
-
-// C (in LDS) -= [Xi0 Xi1][Xk0 Xk1]^T
-__device__ __forceinline__ void update64_lds(float (*C)[TS], float (*Xi0)[TS], float (*Xi1)[TS], float (*Xk0)[TS],
-                                             float (*Xk1)[TS]) {
-    WAVE_COORDS;
-    f32x4 acc;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] = C[16 * bi + 4 * lk + v][16 * bj + l16];
-    acc = update64(acc, Xi0, Xi1, Xk0, Xk1);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) C[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
-}
-
-// Trailing 64x64 tiles (I, Kc), J < Kc <= I, other than (J+1, J+1), dealt round-robin to `W` workers.
-__device__ __forceinline__ void chol_trailing(CholShared& sh, float* A, int r, int NB, int J, float shift, float* L, const float* Li,
-                                              float* Lt, int W, int me, bool have_diag) {
-    WAVE_COORDS;
-    const size_t oJ = (size_t)64 * J;
-    int t = 0;
-    for (int I = J + 1; I < NB; ++I)
-        for (int Kc = J + 1; Kc <= I; ++Kc) {
-            if (I == J + 1 && Kc == J + 1) continue;
-            if ((t++ % W) != me) continue;
-            if (!have_diag) {
-                load_tile(sh.t[0], Li + oJ * CB, CB, false, 0.f);
-                load_tile(sh.t[1], Li + (oJ + 32) * CB, CB, false, 0.f);
-                load_tile(sh.t[2], L + (oJ + 32) * r + oJ, r, false, 0.f);
-                have_diag = true;
-            }
-            const size_t oI = (size_t)64 * I, oK = (size_t)64 * Kc;
-            const bool dg = (I == Kc);
-            load_block64(sh, 3, A + oI * r + oJ, r);
-            if (!dg) load_block64(sh, 7, A + oK * r + oJ, r);
-            f32x4 c[2][2];
-#pragma unroll
-            for (int hi = 0; hi < 2; ++hi)
-#pragma unroll
-                for (int hk = 0; hk < 2; ++hk) {
-                    if (dg && hi == 0 && hk == 1) continue;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int rr = 32 * hi + 16 * bi + 4 * lk + v, cc = 32 * hk + 16 * bj + l16;
-                        float x = A[(oI + rr) * r + oK + cc];
-                        if (J == 0 && dg && rr == cc) x = x + shift;
-                        c[hi][hk][v] = x;
-                    }
-                }
-            __syncthreads();
-            super_panel(sh, 3);
-            if (!dg) super_panel(sh, 7);
-            const int kb = dg ? 3 : 7;
-#pragma unroll
-            for (int hi = 0; hi < 2; ++hi)
-#pragma unroll
-                for (int hk = 0; hk < 2; ++hk) {
-                    if (dg && hi == 0 && hk == 1) continue;
-                    c[hi][hk] = update64(c[hi][hk], sh.t[3 + 2 * hi], sh.t[4 + 2 * hi], sh.t[kb + 2 * hk],
-                                         sh.t[kb + 1 + 2 * hk]);
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int rr = 32 * hi + 16 * bi + 4 * lk + v, cc = 32 * hk + 16 * bj + l16;
-                        A[(oI + rr) * r + oK + cc] = c[hi][hk][v];
-                    }
-                }
-            if (Kc == J + 1) {
-                store_block64(L + oI * r + oJ, r, sh, 3);
-                store_block64_T(Lt + oJ * r + oI, r, sh, 3);
-            }
-            __syncthreads();
+// Poll an agent-scope flag until it holds `ep` (bounded), then acquire. Called by one lane.
+__device__ __forceinline__ void wait_flag(const uint32_t* f, uint32_t ep, uint32_t* err, bool& dead) {
+    uint32_t n = 0;
+    while (!dead && __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != ep) {
+        if (++n > SPIN_LIMIT) {
+            __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            dead = true;
+            break;
         }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
-// Grid-synchronised clamped Cholesky of the Gram in A (r x r, lower tiles read, destroyed). With nnp == 0 the shift is 0
-// and tau_rel is the absolute pivot floor (chol32's contract). Otherwise ||G||_F comes from the nnp fp64 partials:
-// lane l of wave 0 sums npart[l], npart[l + 64], ... in order, then a shift-down tree over the 64 lane sums;
-// nrm = sqrtf(fp32(sum)), shift = alpha * nrm added to the diagonal on first load, tau = tau_rel * nrm + 1e-30
-// (kcholqr.py:107-109). Workgroup 0 factors diagonal blocks (look-ahead), the others update trailing tiles; one grid
-// barrier per 64 columns.
+// Publish: the calling lane's wave (or, after a workgroup sync, the workgroup) has its stores issued; wait for them,
+// then store the flag with agent-scope release.
+__device__ __forceinline__ void publish_flag(uint32_t* f, uint32_t ep) {
+    __hip_atomic_store(f, ep, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Barrier of waves 1 and 2 of a workgroup (wave 0 keeps running): an LDS counter that each wave's lane 0 bumps
+// after its own LDS writes have completed, then waits for (bounded) until it reaches `target` (2 per barrier).
+__device__ __forceinline__ void pair_barrier(uint32_t* ctr, uint32_t target, uint32_t* err, bool& dead) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    if ((threadIdx.x & 63) == 0) {
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        uint32_t n = 0;
+        while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+            if (++n > SPIN_LIMIT) {
+                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                dead = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+constexpr int CH_WG0_TILES = 18;   // workgroup 0: D[2], X1, R2[4], dl[2], li[2], P1[2], P2[2], C2[2], H
+
+struct CholWG0 {
+    Tile D[2];      // D[j & 1]: T(j, j) through block j-1 (factored at step j); D[(j+1) & 1]: T(j+1, j+1)
+    Tile X1;        // T(j+1, j) through block j-1 (its panel is L(j+1, j))
+    Tile R2[4];     // tile row j+2: T(j+2, j-1..j+2) as handed over (through block j-2), then through block j-1
+    Tile dl[2];     // L(j, j)
+    Tile li[2];     // Li_j
+    Tile P1[2];     // L(j+1, j)
+    Tile P2[2];     // L(j+2, j)
+    Tile C2[2];     // L(j+2, j-1) (the catch-up panel of row j+2)
+    Tile H;         // L(j+2, j-2): the owner's last panel of row j+2
+};
+
+size_t chol_lds_bytes(int r) {
+    const int nb = r / CB;
+    const int owner_tiles = 2 * nb;       // a tile row (up to nb tiles), the panels of one column block and Li_j
+    const int tiles = owner_tiles > CH_WG0_TILES ? owner_tiles : CH_WG0_TILES;
+    return (size_t)tiles * sizeof(Tile) + 64 * sizeof(float);
+}
+
+// nb = r/32 tile rows; grid = max(1, nb - 3) workgroups. With nnp == 0 the shift is 0 and tau_rel is the absolute
+// pivot floor (chol32's contract); otherwise ||G||_F comes from the nnp fp64 partials: lane l of wave 0 sums
+// npart[l], npart[l + 64], ... in order, then a shift-down tree over the 64 lane sums; nrm = sqrtf(fp32(sum)),
+// shift = alpha * nrm added to the diagonal on first load, tau = tau_rel * nrm + 1e-30 (kcholqr.py:107-109).
+// flags: [nb * nb] panel flags (L(i, j) published; (j, j): L(j, j) and Li_j), [nb] hand-over flags (tile row i),
+// [64] per-workgroup call counters. STAMP: workgroup 0 records wall_clock64() at 1 + 4j + s for step j: s = 0 step
+// start, 1 tile factored and row j+2 fetched, 2 look-ahead done; slot 0 is the kernel start, 1 + 4 nb the end.
 template <bool STAMP>
 __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
                                               float tau_rel, float* L, float* Li, float* Lt, float* Lit, uint32_t* bar,
-                                              float* scal, uint64_t* stamps) {
-    __shared__ CholShared sh;
-    // STAMP: workgroup 0 records wall_clock64() at phase boundaries, 12 slots per 64-column step s: 0 loads done,
-    // 1 panel done, 2 diagonal update done, 3 and 4 first tile factored and inverted, 5 second tile update done,
-    // 6 block done, 7 after the grid barrier; step 0 also has 9 kernel start, 8 norm done.
-#define CHOL_STAMP(J_, k_)                                                                  \
-    do {                                                                                    \
-        if (STAMP && b == 0 && threadIdx.x == 0) stamps[(J_) * 12 + (k_)] = wall_clock64(); \
-    } while (0)
+                                              uint32_t* flags, float* scal, uint64_t* stamps) {
+    extern __shared__ float4 chol_lds[];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int G = gridDim.x, b = blockIdx.x, NB = r / 64;
+    const int b = blockIdx.x, nb = r / CB;
     uint32_t* err = bar + 2;
-    bool dead = false;     // thread 0's barrier timed out once (only thread 0 reads it)
-    CHOL_STAMP(0, 9);
+    uint32_t* flagL = flags;
+    uint32_t* flagT = flags + nb * nb;
+    uint32_t* cnt = flags + nb * nb + nb;
+    bool dead = false;
+    if (STAMP && b == 0 && tid == 0) stamps[0] = wall_clock64();
+    const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
+    float* misc = reinterpret_cast<float*>(chol_lds);   // [0..3] nrm, shift, tau; [32..63] tile-factor broadcast
+    Tile* tiles = reinterpret_cast<Tile*>(misc + 64);
     if (w == 0) {
         double s = 0.0;
         for (int p = lane; p < nnp; p += 64) s = s + npart[p];
         for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_down(s, off);
         if (lane == 0) {
+            reinterpret_cast<uint32_t*>(misc)[4] = 0u;
             if (nnp > 0) {
                 const float nrm = sqrtf((float)s);
-                sh.bc[0] = nrm;
-                sh.bc[1] = alpha * nrm;
-                sh.bc[2] = tau_rel * nrm + 1e-30f;
-            } else {                       // chol32 form (kchol.py:35-44): G already shifted, absolute pivot floor
-                sh.bc[0] = 0.0f;
-                sh.bc[1] = 0.0f;
-                sh.bc[2] = tau_rel;
+                misc[0] = nrm;
+                misc[1] = alpha * nrm;
+                misc[2] = tau_rel * nrm + 1e-30f;
+            } else {
+                misc[0] = 0.0f;
+                misc[1] = 0.0f;
+                misc[2] = tau_rel;
             }
         }
     }
     __syncthreads();
-    const float shift = sh.bc[1], tau = sh.bc[2];
-    CHOL_STAMP(0, 8);
-    if (b == 0 && tid == 0 && scal != nullptr) {
-        scal[0] = sh.bc[0];
-        scal[1] = tau;
-    }
+    const float shift = misc[1], tau = misc[2];
+    float* bl = misc + 32;
+
     if (b == 0) {
-        load_tile(sh.t[7], A, r, true, shift);
-        load_tile(sh.t[8], A + (size_t)32 * r, r, false, 0.f);
-        load_tile(sh.t[9], A + (size_t)32 * r + 32, r, true, shift);
-        __syncthreads();
-        CHOL_STAMP(0, 2);
-        factor_diag64(sh, 0, r, tau, L, Li, Lt, Lit, STAMP ? stamps + 3 : nullptr);
-        CHOL_STAMP(0, 6);
-    }
-    grid_barrier(bar, G, err, dead);
-    CHOL_STAMP(0, 7);
-    for (int J = 0; J + 1 < NB; ++J) {
-        if (G == 1) chol_trailing(sh, A, r, NB, J, shift, L, Li, Lt, 1, 0, true);
-        if (b == 0) {
-            const size_t oJ = (size_t)64 * J, oI = oJ + 64;
-            load_block64(sh, 3, A + oI * r + oJ, r);
-            load_tile(sh.t[7], A + oI * r + oI, r, J == 0, shift);
-            load_tile(sh.t[8], A + (oI + 32) * r + oI, r, false, 0.f);
-            load_tile(sh.t[9], A + (oI + 32) * r + oI + 32, r, J == 0, shift);
-            __syncthreads();
-            CHOL_STAMP(J + 1, 0);
-            super_panel(sh, 3);
-            CHOL_STAMP(J + 1, 1);
-            store_block64(L + oI * r + oJ, r, sh, 3);
-            store_block64_T(Lt + oJ * r + oI, r, sh, 3);
-            update64_lds(sh.t[7], sh.t[3], sh.t[4], sh.t[3], sh.t[4]);
-            update64_lds(sh.t[8], sh.t[5], sh.t[6], sh.t[3], sh.t[4]);
-            update64_lds(sh.t[9], sh.t[5], sh.t[6], sh.t[5], sh.t[6]);
-            __syncthreads();
-            CHOL_STAMP(J + 1, 2);
-            factor_diag64(sh, J + 1, r, tau, L, Li, Lt, Lit, STAMP ? stamps + 12 * (J + 1) + 3 : nullptr);
-            CHOL_STAMP(J + 1, 6);
-        } else {
-            chol_trailing(sh, A, r, NB, J, shift, L, Li, Lt, G - 1, b - 1, false);
+        if (tid == 0 && scal != nullptr) {
+            scal[0] = misc[0];
+            scal[1] = tau;
         }
-        grid_barrier(bar, G, err, dead);
-        CHOL_STAMP(J + 1, 7);
+        CholWG0& z = *reinterpret_cast<CholWG0*>(tiles);
+        uint32_t* pbar = reinterpret_cast<uint32_t*>(misc + 4);   // waves 1-2 barrier counter (zeroed below)
+        uint32_t npb = 0;
+        load_tile(z.D[0], A, r, true, shift);
+        if (nb > 1) {
+            load_tile(z.X1, A + (size_t)CB * r, r, false, 0.f);
+            load_tile(z.D[1], A + (size_t)CB * r + CB, r, true, shift);
+        }
+        __syncthreads();
+        // wave 3: publish L(j, j), Li_j, L(j+1, j), L(j+2, j) of step j (parity q = j & 1)
+        auto publish = [&](int j) {
+            const int q = j & 1;
+            const size_t o = (size_t)CB * j;
+            store_tile(L + o * r + o, r, z.dl[q], lane, 64);
+            store_tile_T(Lt + o * r + o, r, z.dl[q], lane, 64);
+            store_tile(Li + o * CB, CB, z.li[q], lane, 64);
+            store_tile_T(Lit + o * CB, CB, z.li[q], lane, 64);
+            if (j + 1 < nb) {
+                store_tile(L + (o + CB) * r + o, r, z.P1[q], lane, 64);
+                store_tile_T(Lt + o * r + o + CB, r, z.P1[q], lane, 64);
+            }
+            if (j + 2 < nb) {
+                store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
+                store_tile_T(Lt + o * r + o + 2 * CB, r, z.P2[q], lane, 64);
+            }
+            if (lane == 0) {
+                publish_flag(flagL + j * nb + j, ep);
+                if (j + 1 < nb) publish_flag(flagL + (j + 1) * nb + j, ep);
+                if (j + 2 < nb) publish_flag(flagL + (j + 2) * nb + j, ep);
+            }
+        };
+        for (int j = 0; j < nb; ++j) {
+            const int p = j & 1, pp = p ^ 1;
+            if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
+            if (w == 0) {
+                factor_inv32(bl, z.D[p], tau, z.dl[p], z.li[p]);
+            } else if (w <= 2) {
+                // waves 1-2: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram)
+                if (j + 2 < nb) {
+                    const int i2 = j + 2, wl = (w - 1) * 64 + lane;
+                    if (j <= 1) {
+                        for (int t = (j == 0 ? 1 : 0); t < 4; ++t)
+                            load_tile(z.R2[t], A + (size_t)CB * i2 * r + (size_t)CB * (j - 1 + t), r, t == 3, shift,
+                                      wl, 128);
+                    } else {
+                        if (lane == 0) wait_flag(flagT + i2, ep, err, dead);
+                        __builtin_amdgcn_wave_barrier();
+                        for (int t = 0; t < 4; ++t)
+                            load_tile(z.R2[t], A + (size_t)CB * i2 * r + (size_t)CB * (j - 1 + t), r, false, 0.f,
+                                      wl, 128);
+                        load_tile(z.H, L + (size_t)CB * i2 * r + (size_t)CB * (j - 2), r, false, 0.f, wl, 128);
+                    }
+                    pair_barrier(pbar, 2 * ++npb, err, dead);
+                    if (j >= 1) {
+                        if (w == 1)
+                            panel32_wave(z.C2[p], z.R2[0], z.li[pp]);                  // L(j+2, j-1)
+                        else if (j >= 2)
+                            update32_wave(z.R2[2], z.H, z.C2[pp], false);  // T(j+2, j+1), block j-2 (owner skips it)
+                        pair_barrier(pbar, 2 * ++npb, err, dead);
+                        if (w == 1) {
+                            update32_wave(z.R2[1], z.C2[p], z.P1[pp], false);          // T(j+2, j), block j-1
+                            update32_wave(z.R2[3], z.C2[p], z.C2[p], true);            // T(j+2, j+2)
+                        } else {
+                            update32_wave(z.R2[2], z.C2[p], z.P2[pp], false);          // T(j+2, j+1)
+                            // the owners of rows j+4.. need L(j+2, j-1) for block j-1
+                            const size_t o = (size_t)CB * (j - 1);
+                            store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
+                            store_tile_T(Lt + o * r + o + 3 * CB, r, z.C2[p], lane, 64);
+                            if (lane == 0) publish_flag(flagL + (j + 2) * nb + j - 1, ep);
+                        }
+                    }
+                }
+            } else {
+                if (j >= 1) publish(j - 1);                                             // wave 3
+            }
+            __syncthreads();
+            if (STAMP && tid == 0) stamps[2 + 4 * j] = wall_clock64();
+            if (j + 2 < nb) {
+                panel32x2(z.P1[p], z.X1, z.P2[p], z.R2[1], z.li[p]);            // L(j+1, j), L(j+2, j)
+                {
+                    WAVE_COORDS;   // the three updates of block j, one phase
+                    f32x4 a1, a2, a3;
+                    const bool up = (bi == 0 && bj == 1);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        a1[v] = z.D[pp][16 * bi + 4 * lk + v][16 * bj + l16];
+                        a2[v] = z.R2[2][16 * bi + 4 * lk + v][16 * bj + l16];
+                        a3[v] = z.R2[3][16 * bi + 4 * lk + v][16 * bj + l16];
+                    }
+#pragma unroll
+                    for (int kk = 0; kk < 8; ++kk) {
+                        const float p1i = z.P1[p][16 * bi + l16][4 * kk + lk], p1k = z.P1[p][16 * bj + l16][4 * kk + lk];
+                        const float p2i = z.P2[p][16 * bi + l16][4 * kk + lk], p2k = z.P2[p][16 * bj + l16][4 * kk + lk];
+                        a1 = mfma(-p1i, p1k, a1);      // T(j+1, j+1) -= L(j+1, j) L(j+1, j)^T
+                        a2 = mfma(-p2i, p1k, a2);      // T(j+2, j+1) -= L(j+2, j) L(j+1, j)^T
+                        a3 = mfma(-p2i, p2k, a3);      // T(j+2, j+2) -= L(j+2, j) L(j+2, j)^T
+                    }
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        if (!up) z.D[pp][16 * bi + 4 * lk + v][16 * bj + l16] = a1[v];
+                        z.X1[16 * bi + 4 * lk + v][16 * bj + l16] = a2[v];
+                        if (!up) z.D[p][16 * bi + 4 * lk + v][16 * bj + l16] = a3[v];
+                    }
+                    __syncthreads();
+                }
+            } else if (j + 1 < nb) {
+                panel32(z.P1[p], z.X1, z.li[p]);
+                update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true);
+            }
+            if (STAMP && tid == 0) stamps[3 + 4 * j] = wall_clock64();
+        }
+        if (w == 3) publish(nb - 1);
+        if (STAMP && tid == 0) stamps[1 + 4 * nb] = wall_clock64();
+    } else {
+        // tile row i = b + 3 (i >= 4): rt[k] = T(i, k); op[k] = L(k, j) of the current column block
+        const int i = b + 3;
+        Tile* rt = tiles;
+        Tile* op = tiles + nb;
+        Tile& lij = op[nb - 1];              // Li_j (op[k] is used for k < i <= nb - 1 only)
+        for (int k = 0; k <= i; ++k) load_tile(rt[k], A + (size_t)CB * i * r + (size_t)CB * k, r, k == i, shift);
+        for (int j = 0; j + 4 <= i; ++j) {
+            // panel L(i, j) = T(i, j) Li_j^T
+            if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead);
+            __syncthreads();
+            load_tile(lij, Li + (size_t)CB * j * CB, CB, false, 0.f);
+            __syncthreads();
+            panel32(rt[j], rt[j], lij);
+            store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j]);
+            store_tile_T(Lt + (size_t)CB * j * r + (size_t)CB * i, r, rt[j]);
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+            __syncthreads();
+            if (tid == 0) publish_flag(flagL + i * nb + j, ep);
+            // block j's panels of the rows between: L(k, j), k = j+1..i-1, all fetched before the updates. At the
+            // last block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed.
+            const int kend = (j + 4 == i) ? i - 1 : i;
+            if (tid == 0)
+                for (int k = j + 1; k < kend; ++k) wait_flag(flagL + k * nb + j, ep, err, dead);
+            __syncthreads();
+            for (int k = j + 1; k < kend; ++k)
+                load_tile(op[k], L + (size_t)CB * k * r + (size_t)CB * j, r, false, 0.f);
+            __syncthreads();
+            for (int k = j + 1; k <= i; ++k)
+                if (!(j + 4 == i && k == i - 1)) update32(rt[k], rt[k], rt[j], k == i ? rt[j] : op[k], k == i);
+            if (j + 4 == i) {
+                // hand T(i, i-3..i) to workgroup 0
+                for (int t = 0; t < 4; ++t)
+                    store_tile(A + (size_t)CB * i * r + (size_t)CB * (i - 3 + t), r, rt[i - 3 + t]);
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+                if (tid == 0) publish_flag(flagT + i, ep);
+            }
+        }
     }
+    __syncthreads();
+    if (tid == 0) cnt[b] = ep;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -946,8 +1007,9 @@ struct spanqr_plan {
     float* chscal = nullptr;   // per-launch Cholesky scalars (nrm, tau, err)
     double* npart = nullptr;
     uint32_t* amax_part = nullptr;
-    uint32_t* bar = nullptr;   // [count, generation, error, pad]
-    uint64_t* stamps = nullptr;  // Cholesky phase stamps (profiling), 12 per 64-column step
+    uint32_t* bar = nullptr;   // [unused, unused, error, pad]
+    uint64_t* stamps = nullptr;  // Cholesky phase stamps (profiling): start, then 4 per 32-column step
+    uint32_t* flags = nullptr;   // Cholesky dataflow flags and per-workgroup call counters
     hipEvent_t ev[64] = {};    // profiling: one event before and after each kernel of a call
     int nev = 0;
 };
@@ -999,14 +1061,18 @@ int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t
     float* L = p->L;
     float* Li = p->Li;
     uint32_t* bar = p->bar;
+    uint32_t* flags = p->flags;
     uint64_t* stamps = p->stamps;
     float* Lt = p->Lt;
     float* Lit = p->Lit;
+    const size_t lds = chol_lds_bytes(r);
     // an ordinary launch: plan creation has checked that all chol_grid workgroups fit on the device at once
     if (stamp)
-        k_chol<true><<<p->chol_grid, 256, 0, st>>>(A, r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, scal, stamps);
+        k_chol<true><<<p->chol_grid, 256, lds, st>>>(A, r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, flags, scal,
+                                                     stamps);
     else
-        k_chol<false><<<p->chol_grid, 256, 0, st>>>(A, r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, scal, stamps);
+        k_chol<false><<<p->chol_grid, 256, lds, st>>>(A, r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, flags, scal,
+                                                      stamps);
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
@@ -1181,9 +1247,7 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
     p->K = K; p->r = r; p->device = device;
     p->nt = r / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / 64;
     split_policy(K, p->U, &p->S, &p->KS);
-    const int ntrail = p->NB * (p->NB - 1) / 2 - 1;
-    p->chol_grid = 1 + (ntrail > 0 ? ntrail : 0);
-    if (p->chol_grid > 64) p->chol_grid = 64;
+    p->chol_grid = (r / CB > 4) ? r / CB - 3 : 1;     // workgroup 0 + one per tile row 4..r/32-1
     p->trsm_q = (r / CB + 3) / 4;
     // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU
     p->trsm_rb = ((K + 15) / 16 >= 2048) ? 4 : ((K + 15) / 16 >= 1024 ? 2 : 1);
@@ -1202,7 +1266,17 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
         }
     }
     int occ = 0, cus = 0;
-    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol<true>, 256, 0));
+    {
+        const int need = (int)chol_lds_bytes(r);
+        hipError_t e = hipFuncSetAttribute((const void*)k_chol<true>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)k_chol<false>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
+        if (e != hipSuccess) {
+            delete p;
+            return fail(SPANQR_EHIP, "setting the Cholesky's LDS size (%d bytes) failed: %s", need, hipGetErrorString(e));
+        }
+    }
+    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol<true>, 256, chol_lds_bytes(r)));
     HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
     if (occ * cus < p->chol_grid) {
         const int need = p->chol_grid;
@@ -1216,7 +1290,8 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
     const size_t sz_rr = al((size_t)r * r * sizeof(float)), sz_Li = al((size_t)r * CB * sizeof(float));
     const size_t sz_Y = al(nKr), sz_sc = 256, sz_np = al((size_t)16 * p->U * sizeof(double));
     const size_t sz_am = al(AMAX_BLOCKS * sizeof(uint32_t)), sz_bar = 256, sz_st = al(12 * 8 * sizeof(uint64_t));
-    p->bytes = sz_Z + sz_P + 3 * sz_rr + 2 * sz_Li + 2 * sz_Y + 2 * sz_sc + sz_np + sz_am + sz_bar + sz_st;
+    const size_t sz_fl = al((16 * 16 + 16 + 64) * sizeof(uint32_t));
+    p->bytes = sz_Z + sz_P + 3 * sz_rr + 2 * sz_Li + 2 * sz_Y + 2 * sz_sc + sz_np + sz_am + sz_bar + sz_st + sz_fl;
     if (hipMalloc((void**)&p->base, p->bytes) != hipSuccess) {
         const size_t nb = p->bytes;
         delete p;
@@ -1238,12 +1313,14 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
     p->amax_part = (uint32_t*)c; c += sz_am;
     p->bar = (uint32_t*)c; c += sz_bar;
     p->stamps = (uint64_t*)c; c += sz_st;
+    p->flags = (uint32_t*)c; c += sz_fl;
     float* hz = (float*)malloc(nKr);
     int rc = hz ? spanqr_dust_host(K, r, hz) : fail(SPANQR_ENOMEM, "host dust buffer");
     if (rc == SPANQR_OK) {
         if (hipMemcpy(p->Z, hz, nKr, hipMemcpyHostToDevice) != hipSuccess ||
             hipMemset(p->L, 0, sz_rr) != hipSuccess || hipMemset(p->Lt, 0, sz_rr) != hipSuccess || hipMemset(p->scal, 0, 2 * sz_sc) != hipSuccess ||
-            hipMemset(p->bar, 0, sz_bar) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+            hipMemset(p->bar, 0, sz_bar) != hipSuccess || hipMemset(p->flags, 0, sz_fl) != hipSuccess ||
+            hipDeviceSynchronize() != hipSuccess)
             rc = fail(SPANQR_EHIP, "plan upload failed");
     }
     free(hz);
