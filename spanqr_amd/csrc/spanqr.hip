@@ -328,12 +328,50 @@ __device__ __forceinline__ void store_tile_T(float* dst, int ld, const Tile& src
     }
 }
 
+// Up to NMAX global 32x32 tiles -> LDS tiles dst[0..n-1] by NTHR threads (thread index t): every global load is
+// issued before the first LDS write, so the batch costs one memory latency. Tile q comes from srcf(q) with row
+// stride ld and gets `shift` on its diagonal when (diag_mask >> q) & 1.
+template <int NMAX, int NTHR, class SrcF>
+__device__ __forceinline__ void load_tiles(Tile* dst, int n, int ld, uint32_t diag_mask, float shift, int t,
+                                           SrcF srcf) {
+    constexpr int PER = 256 / NTHR;           // float4 per thread per tile
+    float4 v[NMAX][PER];
+#pragma unroll
+    for (int q = 0; q < NMAX; ++q)
+        if (q < n)
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const int e = t + u * NTHR, row = e >> 3, c4 = e & 7;
+                v[q][u] = *reinterpret_cast<const float4*>(srcf(q) + (size_t)row * ld + 4 * c4);
+            }
+#pragma unroll
+    for (int q = 0; q < NMAX; ++q)
+        if (q < n)
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const int e = t + u * NTHR, row = e >> 3, c4 = e & 7;
+                float x[4] = {v[q][u].x, v[q][u].y, v[q][u].z, v[q][u].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if (((diag_mask >> q) & 1) && row == 4 * c4 + c) x[c] = x[c] + shift;
+                    dst[q][row][4 * c4 + c] = x[c];
+                }
+            }
+}
+
 // out = in Li^T; chain over m < 16 (bj + 1) (Li is lower triangular, chol.cu panel). out may alias in.
 __device__ __forceinline__ void panel32(Tile& out, const Tile& in, const Tile& li) {
     WAVE_COORDS;
+    float a[8], b[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+        a[kk] = in[16 * bi + l16][4 * kk + lk];
+        b[kk] = li[16 * bj + l16][4 * kk + lk];
+    }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int kk = 0; kk < 4 * (bj + 1); ++kk)
-        acc = mfma(in[16 * bi + l16][4 * kk + lk], li[16 * bj + l16][4 * kk + lk], acc);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+        if (kk < 4 * (bj + 1)) acc = mfma(a[kk], b[kk], acc);
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < 4; ++v) out[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
@@ -359,12 +397,20 @@ __device__ __forceinline__ void update32(Tile& dst, const Tile& C, const Tile& P
 // Two panels in one phase: outA = inA Li^T, outB = inB Li^T (outputs must not alias the inputs)
 __device__ __forceinline__ void panel32x2(Tile& outA, const Tile& inA, Tile& outB, const Tile& inB, const Tile& li) {
     WAVE_COORDS;
-    f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
-    for (int kk = 0; kk < 4 * (bj + 1); ++kk) {
-        const float lv = li[16 * bj + l16][4 * kk + lk];
-        a = mfma(inA[16 * bi + l16][4 * kk + lk], lv, a);
-        c = mfma(inB[16 * bi + l16][4 * kk + lk], lv, c);
+    float xa[8], xb[8], lv[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+        xa[kk] = inA[16 * bi + l16][4 * kk + lk];
+        xb[kk] = inB[16 * bi + l16][4 * kk + lk];
+        lv[kk] = li[16 * bj + l16][4 * kk + lk];
     }
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+        if (kk < 4 * (bj + 1)) {
+            a = mfma(xa[kk], lv[kk], a);
+            c = mfma(xb[kk], lv[kk], c);
+        }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         outA[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
@@ -373,36 +419,62 @@ __device__ __forceinline__ void panel32x2(Tile& outA, const Tile& inA, Tile& out
     __syncthreads();
 }
 
-// One wave: a whole 32x32 tile, quadrant by quadrant. out = in Li^T (out must not alias in).
+// One wave, a whole 32x32 tile: out = in Li^T (out must not alias in). Each operand element is read from LDS once and
+// the four quadrants' MFMA chains (over m < 16 (bj + 1)) are interleaved.
 __device__ __forceinline__ void panel32_wave(Tile& out, const Tile& in, const Tile& li) {
     const int lane = threadIdx.x & 63, l16 = lane & 15, lk = lane >> 4;
-    for (int qd = 0; qd < 4; ++qd) {
-        const int bi = qd >> 1, bj = qd & 1;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int kk = 0; kk < 4 * (bj + 1); ++kk)
-            acc = mfma(in[16 * bi + l16][4 * kk + lk], li[16 * bj + l16][4 * kk + lk], acc);
+    float a[2][8], b[2][8];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) out[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
-    }
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            a[h][kk] = in[16 * h + l16][4 * kk + lk];
+            b[h][kk] = (kk < 4 * (h + 1)) ? li[16 * h + l16][4 * kk + lk] : 0.0f;
+        }
+    f32x4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            const int bi = qd >> 1, bj = qd & 1;
+            if (kk < 4 * (bj + 1)) acc[qd] = mfma(a[bi][kk], b[bj][kk], acc[qd]);
+        }
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) out[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16] = acc[qd][v];
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the tile is written before this wave reads it back
     __builtin_amdgcn_wave_barrier();
 }
 
-// One wave: C -= Pi Pk^T in place, quadrant by quadrant (lower: skip the upper 16x16 block)
-__device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Tile& Pk, bool lower) {
+// One wave, a whole 32x32 tile: C -= Pi Pk^T in place (LOWER: the upper 16x16 block is left alone); operands read
+// once, the quadrants' chains (over m = 0..31 from C) interleaved.
+template <bool LOWER>
+__device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Tile& Pk) {
     const int lane = threadIdx.x & 63, l16 = lane & 15, lk = lane >> 4;
-    for (int qd = 0; qd < 4; ++qd) {
-        const int bi = qd >> 1, bj = qd & 1;
-        if (lower && qd == 1) continue;
-        f32x4 acc;
+    float a[2][8], b[2][8];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[v] = C[16 * bi + 4 * lk + v][16 * bj + l16];
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-            acc = mfma(-Pi[16 * bi + l16][4 * kk + lk], Pk[16 * bj + l16][4 * kk + lk], acc);
+        for (int kk = 0; kk < 8; ++kk) {
+            a[h][kk] = -Pi[16 * h + l16][4 * kk + lk];
+            b[h][kk] = Pk[16 * h + l16][4 * kk + lk];
+        }
+    f32x4 acc[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) C[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
-    }
+    for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[qd][v] = C[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd)
+            if (!(LOWER && qd == 1)) acc[qd] = mfma(a[qd >> 1][kk], b[qd & 1][kk], acc[qd]);
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd)
+        if (!(LOWER && qd == 1))
+#pragma unroll
+            for (int v = 0; v < 4; ++v) C[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16] = acc[qd][v];
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();
 }
@@ -476,15 +548,22 @@ __device__ __forceinline__ void wait_flag(const uint32_t* f, uint32_t ep, uint32
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
-// Publish: the calling lane's wave (or, after a workgroup sync, the workgroup) has its stores issued; wait for them,
-// then store the flag with agent-scope release.
+// Publish: the calling lane's wave (or, after a workgroup sync, the workgroup) has its stores issued. release()
+// waits for them and makes them visible at agent scope (one L2 write-back); the flags that follow are plain
+// agent-scope stores.
+__device__ __forceinline__ void release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void set_flag(uint32_t* f, uint32_t ep) {
+    __hip_atomic_store(f, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void publish_flag(uint32_t* f, uint32_t ep) {
-    __hip_atomic_store(f, ep, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    release();
+    set_flag(f, ep);
 }
 
-// Barrier of waves 1 and 2 of a workgroup (wave 0 keeps running): an LDS counter that each wave's lane 0 bumps
-// after its own LDS writes have completed, then waits for (bounded) until it reaches `target` (2 per barrier).
-__device__ __forceinline__ void pair_barrier(uint32_t* ctr, uint32_t target, uint32_t* err, bool& dead) {
+// Barrier of some waves of a workgroup while the others keep running: an LDS counter that each participating
+// wave's lane 0 bumps after its own LDS writes have completed, then waits for (bounded) until it reaches `target`
+// (the number of participants times the number of times this barrier has been passed).
+__device__ __forceinline__ void wave_group_barrier(uint32_t* ctr, uint32_t target, uint32_t* err, bool& dead) {
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
     if ((threadIdx.x & 63) == 0) {
@@ -502,18 +581,19 @@ __device__ __forceinline__ void pair_barrier(uint32_t* ctr, uint32_t target, uin
     __builtin_amdgcn_wave_barrier();
 }
 
+constexpr int CH_MAXROW = 16;      // tiles in a tile row at most (r <= 512)
 constexpr int CH_WG0_TILES = 18;   // workgroup 0: D[2], X1, R2[4], dl[2], li[2], P1[2], P2[2], C2[2], H
 
 struct CholWG0 {
     Tile D[2];      // D[j & 1]: T(j, j) through block j-1 (factored at step j); D[(j+1) & 1]: T(j+1, j+1)
     Tile X1;        // T(j+1, j) through block j-1 (its panel is L(j+1, j))
-    Tile R2[4];     // tile row j+2: T(j+2, j-1..j+2) as handed over (through block j-2), then through block j-1
+    Tile R2[5];     // tile row j+2: T(j+2, j-1..j+2) as handed over (through block j-2), then through block j-1;
+                    // R2[4] = L(j+2, j-2): the owner's last panel of row j+2
     Tile dl[2];     // L(j, j)
     Tile li[2];     // Li_j
     Tile P1[2];     // L(j+1, j)
     Tile P2[2];     // L(j+2, j)
     Tile C2[2];     // L(j+2, j-1) (the catch-up panel of row j+2)
-    Tile H;         // L(j+2, j-2): the owner's last panel of row j+2
 };
 
 size_t chol_lds_bytes(int r) {
@@ -552,6 +632,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_down(s, off);
         if (lane == 0) {
             reinterpret_cast<uint32_t*>(misc)[4] = 0u;
+            reinterpret_cast<uint32_t*>(misc)[5] = 0u;
             if (nnp > 0) {
                 const float nrm = sqrtf((float)s);
                 misc[0] = nrm;
@@ -574,8 +655,9 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             scal[1] = tau;
         }
         CholWG0& z = *reinterpret_cast<CholWG0*>(tiles);
-        uint32_t* pbar = reinterpret_cast<uint32_t*>(misc + 4);   // waves 1-2 barrier counter (zeroed below)
-        uint32_t npb = 0;
+        uint32_t* bar12 = reinterpret_cast<uint32_t*>(misc + 4);    // waves 1-2 barrier counter (zeroed below)
+        uint32_t* bar123 = reinterpret_cast<uint32_t*>(misc + 5);   // waves 1-3 barrier counter
+        uint32_t n12 = 0, n123 = 0;
         load_tile(z.D[0], A, r, true, shift);
         if (nb > 1) {
             load_tile(z.X1, A + (size_t)CB * r, r, false, 0.f);
@@ -599,9 +681,10 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
                 store_tile_T(Lt + o * r + o + 2 * CB, r, z.P2[q], lane, 64);
             }
             if (lane == 0) {
-                publish_flag(flagL + j * nb + j, ep);
-                if (j + 1 < nb) publish_flag(flagL + (j + 1) * nb + j, ep);
-                if (j + 2 < nb) publish_flag(flagL + (j + 2) * nb + j, ep);
+                release();
+                set_flag(flagL + j * nb + j, ep);
+                if (j + 1 < nb) set_flag(flagL + (j + 1) * nb + j, ep);
+                if (j + 2 < nb) set_flag(flagL + (j + 2) * nb + j, ep);
             }
         };
         for (int j = 0; j < nb; ++j) {
@@ -609,44 +692,51 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
             if (w == 0) {
                 factor_inv32(bl, z.D[p], tau, z.dl[p], z.li[p]);
-            } else if (w <= 2) {
-                // waves 1-2: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram)
-                if (j + 2 < nb) {
+            } else {
+                // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram). Waves 1-2 fetch it
+                // while wave 3 publishes the previous step; then L(j+2, j-1) (wave 1) and the block j-2 update of
+                // T(j+2, j+1) that its owner left (wave 2); then block j-1 on T(j+2, j) (wave 1), T(j+2, j+1)
+                // (wave 2) and T(j+2, j+2) (wave 3, which then publishes L(j+2, j-1)).
+                const bool row2 = j + 2 < nb;
+                if (w == 3) {
+                    if (j >= 1) publish(j - 1);
+                } else if (row2) {
                     const int i2 = j + 2, wl = (w - 1) * 64 + lane;
+                    const float* rowp = A + (size_t)CB * i2 * r;
                     if (j <= 1) {
-                        for (int t = (j == 0 ? 1 : 0); t < 4; ++t)
-                            load_tile(z.R2[t], A + (size_t)CB * i2 * r + (size_t)CB * (j - 1 + t), r, t == 3, shift,
-                                      wl, 128);
+                        const int t0 = (j == 0) ? 1 : 0;     // row 2: T(2, 0..2) into R2[1..3]; row 3: T(3, 0..3)
+                        load_tiles<4, 128>(&z.R2[t0], 4 - t0, r, 1u << (3 - t0), shift, wl,
+                                           [&](int q) { return rowp + CB * (j - 1 + t0 + q); });
                     } else {
                         if (lane == 0) wait_flag(flagT + i2, ep, err, dead);
                         __builtin_amdgcn_wave_barrier();
-                        for (int t = 0; t < 4; ++t)
-                            load_tile(z.R2[t], A + (size_t)CB * i2 * r + (size_t)CB * (j - 1 + t), r, false, 0.f,
-                                      wl, 128);
-                        load_tile(z.H, L + (size_t)CB * i2 * r + (size_t)CB * (j - 2), r, false, 0.f, wl, 128);
+                        const float* hp = L + (size_t)CB * i2 * r + (size_t)CB * (j - 2);     // into R2[4] = H
+                        load_tiles<5, 128>(&z.R2[0], 5, r, 0u, 0.f, wl,
+                                           [&](int q) { return q < 4 ? rowp + CB * (j - 1 + q) : hp; });
                     }
-                    pair_barrier(pbar, 2 * ++npb, err, dead);
+                    wave_group_barrier(bar12, 2 * ++n12, err, dead);
                     if (j >= 1) {
                         if (w == 1)
                             panel32_wave(z.C2[p], z.R2[0], z.li[pp]);                  // L(j+2, j-1)
                         else if (j >= 2)
-                            update32_wave(z.R2[2], z.H, z.C2[pp], false);  // T(j+2, j+1), block j-2 (owner skips it)
-                        pair_barrier(pbar, 2 * ++npb, err, dead);
-                        if (w == 1) {
-                            update32_wave(z.R2[1], z.C2[p], z.P1[pp], false);          // T(j+2, j), block j-1
-                            update32_wave(z.R2[3], z.C2[p], z.C2[p], true);            // T(j+2, j+2)
-                        } else {
-                            update32_wave(z.R2[2], z.C2[p], z.P2[pp], false);          // T(j+2, j+1)
-                            // the owners of rows j+4.. need L(j+2, j-1) for block j-1
-                            const size_t o = (size_t)CB * (j - 1);
-                            store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
-                            store_tile_T(Lt + o * r + o + 3 * CB, r, z.C2[p], lane, 64);
-                            if (lane == 0) publish_flag(flagL + (j + 2) * nb + j - 1, ep);
-                        }
+                            update32_wave<false>(z.R2[2], z.R2[4], z.C2[pp]);  // T(j+2, j+1), block j-2 (owner skips it)
                     }
                 }
-            } else {
-                if (j >= 1) publish(j - 1);                                             // wave 3
+                if (row2 && j >= 1) {
+                    wave_group_barrier(bar123, 3 * ++n123, err, dead);
+                    if (w == 1) {
+                        update32_wave<false>(z.R2[1], z.C2[p], z.P1[pp]);              // T(j+2, j), block j-1
+                    } else if (w == 2) {
+                        update32_wave<false>(z.R2[2], z.C2[p], z.P2[pp]);              // T(j+2, j+1)
+                    } else {
+                        update32_wave<true>(z.R2[3], z.C2[p], z.C2[p]);                // T(j+2, j+2)
+                        // the owners of rows j+4.. need L(j+2, j-1) for block j-1
+                        const size_t o = (size_t)CB * (j - 1);
+                        store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
+                        store_tile_T(Lt + o * r + o + 3 * CB, r, z.C2[p], lane, 64);
+                        if (lane == 0) publish_flag(flagL + (j + 2) * nb + j - 1, ep);
+                    }
+                }
             }
             __syncthreads();
             if (STAMP && tid == 0) stamps[2 + 4 * j] = wall_clock64();
@@ -692,7 +782,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         Tile* rt = tiles;
         Tile* op = tiles + nb;
         Tile& lij = op[nb - 1];              // Li_j (op[k] is used for k < i <= nb - 1 only)
-        for (int k = 0; k <= i; ++k) load_tile(rt[k], A + (size_t)CB * i * r + (size_t)CB * k, r, k == i, shift);
+        load_tiles<CH_MAXROW, 256>(rt, i + 1, r, 1u << i, shift, tid,
+                                   [&](int q) { return A + (size_t)CB * i * r + (size_t)CB * q; });
         for (int j = 0; j + 4 <= i; ++j) {
             // panel L(i, j) = T(i, j) Li_j^T
             if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead);
@@ -702,6 +793,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             panel32(rt[j], rt[j], lij);
             store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j]);
             store_tile_T(Lt + (size_t)CB * j * r + (size_t)CB * i, r, rt[j]);
+            // publish L(i, j) before waiting on the other rows (so no row waits on a chain of rows)
             __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
             __syncthreads();
             if (tid == 0) publish_flag(flagL + i * nb + j, ep);
@@ -711,11 +803,25 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             if (tid == 0)
                 for (int k = j + 1; k < kend; ++k) wait_flag(flagL + k * nb + j, ep, err, dead);
             __syncthreads();
-            for (int k = j + 1; k < kend; ++k)
-                load_tile(op[k], L + (size_t)CB * k * r + (size_t)CB * j, r, false, 0.f);
+            load_tiles<CH_MAXROW, 256>(&op[j + 1], kend - j - 1, r, 0u, 0.f, tid,
+                                       [&](int q) { return L + (size_t)CB * (j + 1 + q) * r + (size_t)CB * j; });
             __syncthreads();
-            for (int k = j + 1; k <= i; ++k)
-                if (!(j + 4 == i && k == i - 1)) update32(rt[k], rt[k], rt[j], k == i ? rt[j] : op[k], k == i);
+            {
+                WAVE_COORDS;   // every tile's quadrant (bi, bj) in one phase: the tiles are independent
+                for (int k = j + 1; k <= i; ++k) {
+                    if ((j + 4 == i && k == i - 1) || (k == i && bi == 0 && bj == 1)) continue;
+                    const Tile& Pk = (k == i) ? rt[j] : op[k];
+                    f32x4 acc;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[v] = rt[k][16 * bi + 4 * lk + v][16 * bj + l16];
+#pragma unroll
+                    for (int kk = 0; kk < 8; ++kk)
+                        acc = mfma(-rt[j][16 * bi + l16][4 * kk + lk], Pk[16 * bj + l16][4 * kk + lk], acc);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) rt[k][16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+                }
+                __syncthreads();
+            }
             if (j + 4 == i) {
                 // hand T(i, i-3..i) to workgroup 0
                 for (int t = 0; t < 4; ++t)
