@@ -359,6 +359,20 @@ __device__ __forceinline__ void load_tiles(Tile* dst, int n, int ld, uint32_t di
             }
 }
 
+// the lower triangle of a diagonal tile (zeros above the diagonal), straight and transposed
+__device__ __forceinline__ void store_tile_lower(float* dst, int ld, const Tile& src, bool transpose, int t, int nthr) {
+    for (int e = t; e < 256; e += nthr) {
+        const int row = e >> 3, c4 = e & 7;
+        float x[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int col = 4 * c4 + c;
+            x[c] = transpose ? ((row <= col) ? src[col][row] : 0.0f) : ((col <= row) ? src[row][col] : 0.0f);
+        }
+        *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = make_float4(x[0], x[1], x[2], x[3]);
+    }
+}
+
 // out = in Li^T; chain over m < 16 (bj + 1) (Li is lower triangular, chol.cu panel). out may alias in.
 __device__ __forceinline__ void panel32(Tile& out, const Tile& in, const Tile& li) {
     WAVE_COORDS;
@@ -480,35 +494,39 @@ __device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Til
 }
 
 // Wave 0 only: factor the 32x32 tile D (lower part) and invert the factor in one pass (chol.cu:131-168).
-// Lanes 0..31 hold row i of D; lanes 32..63 hold column kk of the identity, which becomes column kk of the inverse.
-// Column c: the pivot piv = fmaxf(D_cc, tau) and q = rsqrt(piv) are uniform; a factor lane's value is
-// l_i = D_ic q (piv q on the diagonal, 0 above it), an inverse lane's is x_c = acc_c q (0 for c < kk). Both halves
-// then run the same rank-1 update R[k] = fma(-own, l_k, R[k]) for k > c, which is the factor's trailing update
-// D_ik -= l_i l_k and the inverse's forward substitution acc_k -= L_kc x_c, each element's chain in column order.
-// Only the update of column c+1 is on the critical path: l_{c+1} comes by v_readlane and the next pivot is formed
-// right away; the other l_k are broadcast through LDS (bl) and their updates overlap the next pivot chain.
-// Writes the factor (zeros above the diagonal) to dl and the inverse to Li.
-__device__ __forceinline__ void factor_inv32(float* bl, const Tile& D, float tau, Tile& dl, Tile& Li) {
+// Lanes 0..31 hold row i of D; lanes 32..63 start from column kk of the identity (from the LDS tile `id`), which
+// becomes column kk of the inverse. Column c: piv = fmaxf(D_cc, tau) and q = rsqrt(piv) are uniform; every lane
+// forms own = R[c] q, which is l_i = D_ic q on a factor lane below the diagonal and x_c = acc_c q on an inverse lane
+// (exactly +0 while c < kk: those registers stay +0). The factor's diagonal entry is piv q, which differs from
+// R[c] q only when the pivot was clamped; it is used nowhere but the output, so it is recorded in pq[c] and patched
+// in at the end (a factor lane above the diagonal computes values that only its own dead upper-triangle registers
+// see). Then both halves run the same rank-1 update R[k] = fma(-own, l_k, R[k]) for k > c: the factor's trailing
+// update D_ik -= l_i l_k and the inverse's forward substitution acc_k -= L_kc x_c, each element's chain in column
+// order. Only the update of column c+1 is on the critical path: l_{c+1} comes by v_readlane and the next pivot is
+// formed right away; the other l_k are broadcast through LDS (bl) and their updates overlap the next pivot chain.
+// No lane-dependent selects: their masks would all be hoisted and spilled. Writes the factor to dl (the upper
+// triangle is left unspecified: publishers zero it) and the inverse to Li.
+__device__ __forceinline__ void factor_inv32(float* bl, float* pq, const Tile& id, const Tile& D, float tau, Tile& dl,
+                                             Tile& Li) {
     const int lane = threadIdx.x & 63, i = lane & 31;
     const bool fl = lane < 32;
+    const float* src = fl ? &D[i][0] : &id[i][0];
     float R[CB];
 #pragma unroll
-    for (int k = 0; k < CB; ++k) R[k] = fl ? D[i][k] : (k == i ? 1.0f : 0.0f);
+    for (int k = 0; k < CB; ++k) R[k] = src[k];
     float piv = fmaxf(readlane(R[0], 0), tau);
     float q = rsqrt_sw(piv);
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-        const float sc = R[c] * q;
-        const float lf = (i > c) ? sc : ((i == c) ? piv * q : 0.0f);
-        const float xi = (c < i) ? 0.0f : sc;
-        const float own = fl ? lf : xi;
+        const float own = R[c] * q;
+        pq[c] = piv * q;
         R[c] = own;
         if (c + 1 < CB) {
             R[c + 1] = __builtin_fmaf(-own, readlane(own, c + 1), R[c + 1]);
             const float pn = fmaxf(readlane(R[c + 1], c + 1), tau);
             const float qn = rsqrt_sw(pn);
             if (c + 2 < CB) {
-                if (fl) bl[i] = own;
+                bl[lane] = own;
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll
                 for (int k0 = (c + 2) & ~3; k0 < CB; k0 += 4) {
@@ -524,13 +542,13 @@ __device__ __forceinline__ void factor_inv32(float* bl, const Tile& D, float tau
             q = qn;
         }
     }
-    if (fl) {
+    float* dst = fl ? &dl[i][0] : &Li[0][i];
+    const int step = fl ? 1 : TS;
 #pragma unroll
-        for (int k = 0; k < CB; ++k) dl[i][k] = (k <= i) ? R[k] : 0.0f;
-    } else {
-#pragma unroll
-        for (int k = 0; k < CB; ++k) Li[k][i] = R[k];
-    }
+    for (int k = 0; k < CB; ++k) dst[k * step] = R[k];
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    if (fl) dl[i][i] = pq[i];
     __builtin_amdgcn_wave_barrier();
 }
 
@@ -582,7 +600,7 @@ __device__ __forceinline__ void wave_group_barrier(uint32_t* ctr, uint32_t targe
 }
 
 constexpr int CH_MAXROW = 16;      // tiles in a tile row at most (r <= 512)
-constexpr int CH_WG0_TILES = 18;   // workgroup 0: D[2], X1, R2[4], dl[2], li[2], P1[2], P2[2], C2[2], H
+constexpr int CH_WG0_TILES = 19;   // workgroup 0: D[2], X1, R2[5], dl[2], li[2], P1[2], P2[2], C2[2], id
 
 struct CholWG0 {
     Tile D[2];      // D[j & 1]: T(j, j) through block j-1 (factored at step j); D[(j+1) & 1]: T(j+1, j+1)
@@ -594,13 +612,14 @@ struct CholWG0 {
     Tile P1[2];     // L(j+1, j)
     Tile P2[2];     // L(j+2, j)
     Tile C2[2];     // L(j+2, j-1) (the catch-up panel of row j+2)
+    Tile id;        // identity (the tile factor's inverse lanes start from it)
 };
 
 size_t chol_lds_bytes(int r) {
     const int nb = r / CB;
     const int owner_tiles = 2 * nb;       // a tile row (up to nb tiles), the panels of one column block and Li_j
     const int tiles = owner_tiles > CH_WG0_TILES ? owner_tiles : CH_WG0_TILES;
-    return (size_t)tiles * sizeof(Tile) + 64 * sizeof(float);
+    return (size_t)tiles * sizeof(Tile) + 128 * sizeof(float);
 }
 
 // nb = r/32 tile rows; grid = max(1, nb - 3) workgroups. With nnp == 0 the shift is 0 and tau_rel is the absolute
@@ -624,8 +643,10 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     bool dead = false;
     if (STAMP && b == 0 && tid == 0) stamps[0] = wall_clock64();
     const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
-    float* misc = reinterpret_cast<float*>(chol_lds);   // [0..3] nrm, shift, tau; [32..63] tile-factor broadcast
-    Tile* tiles = reinterpret_cast<Tile*>(misc + 64);
+    // misc: [0..2] nrm, shift, tau; [4..5] wave-group barrier counters; [32..95] tile-factor broadcast;
+    // [96..127] the tile factor's diagonal
+    float* misc = reinterpret_cast<float*>(chol_lds);
+    Tile* tiles = reinterpret_cast<Tile*>(misc + 128);
     if (w == 0) {
         double s = 0.0;
         for (int p = lane; p < nnp; p += 64) s = s + npart[p];
@@ -648,6 +669,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     __syncthreads();
     const float shift = misc[1], tau = misc[2];
     float* bl = misc + 32;
+    float* pq = misc + 96;
 
     if (b == 0) {
         if (tid == 0 && scal != nullptr) {
@@ -658,6 +680,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         uint32_t* bar12 = reinterpret_cast<uint32_t*>(misc + 4);    // waves 1-2 barrier counter (zeroed below)
         uint32_t* bar123 = reinterpret_cast<uint32_t*>(misc + 5);   // waves 1-3 barrier counter
         uint32_t n12 = 0, n123 = 0;
+        for (int e = tid; e < CB * CB; e += 256) z.id[e >> 5][e & 31] = ((e >> 5) == (e & 31)) ? 1.0f : 0.0f;
         load_tile(z.D[0], A, r, true, shift);
         if (nb > 1) {
             load_tile(z.X1, A + (size_t)CB * r, r, false, 0.f);
@@ -668,8 +691,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         auto publish = [&](int j) {
             const int q = j & 1;
             const size_t o = (size_t)CB * j;
-            store_tile(L + o * r + o, r, z.dl[q], lane, 64);
-            store_tile_T(Lt + o * r + o, r, z.dl[q], lane, 64);
+            store_tile_lower(L + o * r + o, r, z.dl[q], false, lane, 64);
+            store_tile_lower(Lt + o * r + o, r, z.dl[q], true, lane, 64);
             store_tile(Li + o * CB, CB, z.li[q], lane, 64);
             store_tile_T(Lit + o * CB, CB, z.li[q], lane, 64);
             if (j + 1 < nb) {
@@ -691,7 +714,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             const int p = j & 1, pp = p ^ 1;
             if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
             if (w == 0) {
-                factor_inv32(bl, z.D[p], tau, z.dl[p], z.li[p]);
+                factor_inv32(bl, pq, z.id, z.D[p], tau, z.dl[p], z.li[p]);
             } else {
                 // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram). Waves 1-2 fetch it
                 // while wave 3 publishes the previous step; then L(j+2, j-1) (wave 1) and the block j-2 update of
