@@ -7,7 +7,8 @@ Workload (the reference's 0.8B TTF layer shapes): K x r in {1024x256, 2048x256, 
 resident on the GPU before timing. One step = one orth() call on each of the six inputs; every input has its own
 captured hipGraph. `value` = timed wall time / (steps x 6) in microseconds (lower is better).
 
-Also reported: per-shape back-to-back time; the 768x512 and 17408x256 shapes (the quoted targets); per kernel the
+Also reported: per-shape back-to-back time; the 768x512 and 17408x256 shapes (the quoted targets); the batched
+layer set (12 x 768x512 + 12 x 2048x512, one hipGraph per shape group, against 24 single-call graphs); per kernel the
 average launch duration at each workload shape (HIP events around back-to-back launches on the call's stream) with
 its algorithmic flops and bytes; the roofline of the dominant kernel and of the whole call; the Cholesky's latency
 per diagonal step; a CPU baseline on a bounded sample (the C restatement in oracle/, OpenMP, on the host, plus CPU
@@ -26,7 +27,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from spanqr_amd import _lib, kcholqr_f, stages  # noqa: E402
+from spanqr_amd import _lib, kcholqr_f, kcholqr_f_many, stages  # noqa: E402
 from spanqr_amd.plan import get_plan, stream_handle  # noqa: E402
 from spanqr_amd.qrbench import gen  # noqa: E402
 
@@ -34,6 +35,7 @@ METRIC = "µs per orth() call at K×r (median); max|QᵀQ−I|; % of HBM/MFMA ro
 WORKLOAD_SHAPES = [(1024, 256), (2048, 256), (3584, 256)]
 SEEDS = (0, 1)
 TARGET_SHAPES = [(768, 512), (17408, 256)]
+BATCH_GROUPS = [(768, 512, 12), (2048, 512, 12)]   # the 110M model's attention and down_proj layers
 PEAK_FP32_TFLOPS = 157.3     # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 
@@ -109,6 +111,64 @@ def capture(X):
         Q = kcholqr_f(X)
     torch.cuda.synchronize()
     return g, Q
+
+
+def capture_many(Xs):
+    """(graph, [Q]): one batched call on the same-shape list Xs captured into a hipGraph on a side stream"""
+    st = torch.cuda.Stream(Xs[0].device)
+    st.wait_stream(torch.cuda.current_stream(Xs[0].device))
+    with torch.cuda.stream(st):
+        kcholqr_f_many(Xs)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        Qs = kcholqr_f_many(Xs)
+    torch.cuda.synchronize()
+    return g, Qs
+
+
+def time_replays(graphs, steps, reps=5):
+    """median over `reps` of the time of `steps` rounds of replaying every graph once, microseconds per round"""
+    out = []
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(steps):
+            for g in graphs:
+                g.replay()
+        e.record()
+        torch.cuda.synchronize()
+        out.append(s.elapsed_time(e) * 1000.0 / steps)
+    return statistics.median(out)
+
+
+def batched_layers(dev, steps):
+    """the batched layer set: per training step, orth of 12 layers at 768x512 and 12 at 2048x512 (independent
+    inputs of the cond-1e8 generator, seeds 100 + i), as two batched graphs (one per shape group) and as 24
+    single-call graphs; Q of the two forms compared bit for bit"""
+    groups = []
+    for gi, (K, r, n) in enumerate(BATCH_GROUPS):
+        groups.append([gen.ttf_uu(K, r, N=K, seed=100 + 12 * gi + i).to(dev) for i in range(n)])
+    single = [capture(X) for grp in groups for X in grp]
+    batched = [capture_many(grp) for grp in groups]
+    for g, _q in single + batched:
+        g.replay()
+    torch.cuda.synchronize()
+    q_single = [q for _g, q in single]
+    q_batched = [q for _g, qs in batched for q in qs]
+    same = all(torch.equal(a.view(torch.int32), b.view(torch.int32)) for a, b in zip(q_single, q_batched))
+    t_single = time_replays([g for g, _q in single], steps)
+    t_batched = time_replays([g for g, _q in batched], steps)
+    res = {"layers": sum(n for _k, _r, n in BATCH_GROUPS),
+           "groups": [f"{n} x {K}x{r}" for K, r, n in BATCH_GROUPS],
+           "us_per_step_batched": t_batched, "us_per_step_sequential": t_single,
+           "speedup": t_single / t_batched, "bitwise_equal_to_single_calls": same,
+           "orth_max": max(orth_error(q) for q in q_batched),
+           "chol_per_launch": {f"{K}x{r}": get_plan(K, r, dev, n).chol_batch for K, r, n in BATCH_GROUPS}}
+    del single, batched
+    torch.cuda.synchronize()
+    return res
 
 
 def orth_error(Q):
@@ -233,6 +293,8 @@ def main(argv=None):
         targets[f"{K}x{r}"] = {"us_per_call": time_graph(g), "orth": orth_error(q)}
         del g
 
+    batched = batched_layers(dev, max(1, min(a.steps, 20)))
+
     # per kernel: average launch duration at each workload shape (HIP events around back-to-back launches)
     kernels = {}
     call_us = {}
@@ -283,7 +345,7 @@ def main(argv=None):
         "config": {"workload": "0.8B TTF layers: orth() at 1024x256, 2048x256, 3584x256, 2 seeds each, one "
                                "hipGraph per input", "shapes": [f"{K}x{r}" for K, r in WORKLOAD_SHAPES],
                    "seeds": list(SEEDS), "calls_per_step": calls, "graphs": not a.no_graph},
-        "orth_max": orth_max, "per_shape_us": per_shape, "target_shapes": targets,
+        "orth_max": orth_max, "per_shape_us": per_shape, "target_shapes": targets, "batched_layers": batched,
         "roofline": roofline, "call_roofline": call_roof, "kernels": kernels, "kernel_share": share,
         "sum_of_kernels_us": call_us, "cholesky": chol_info,
         "cpu_baseline": cpu,

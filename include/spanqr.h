@@ -27,6 +27,9 @@ extern "C" {
 
 typedef struct spanqr_plan spanqr_plan;
 
+/* Most matrices one spanqr_orth_batched_f32 call takes. */
+#define SPANQR_MAX_BATCH 32
+
 enum {
     SPANQR_OK = 0,
     SPANQR_EINVAL = -1,     /* bad argument (shape, alignment, null pointer) */
@@ -40,9 +43,11 @@ enum {
     SPANQR_Q_R = 1,
     SPANQR_Q_SPLITS = 2,         /* Gram row splits S */
     SPANQR_Q_SPLIT_ROWS = 3,     /* rows per split KS (a multiple of 32) */
-    SPANQR_Q_CHOL_GRID = 4,      /* workgroups of the Cholesky (max(1, r/32 - 2)) */
+    SPANQR_Q_CHOL_GRID = 4,      /* workgroups of one matrix's Cholesky (max(1, r/32 - 3)) */
     SPANQR_Q_WORKSPACE_MB = 5,   /* workspace size, MiB (rounded up) */
     SPANQR_Q_DEVICE = 6,
+    SPANQR_Q_BATCH = 7,          /* matrices per call the plan holds workspace for */
+    SPANQR_Q_CHOL_BATCH = 8,     /* matrices per Cholesky launch (all their workgroups fit on the device at once) */
 };
 
 /* Create a plan for X [K, r] on HIP device `device` (allocates the workspace and uploads the dust matrix).
@@ -50,6 +55,10 @@ enum {
  * (candidates/kcholqr.py:26, :83-89), chol32's G clone / L / Li / barrier (candidates/kchol.py:12-18, :40-42) and the
  * Gram partials (candidates/tri.py:371). */
 int spanqr_plan_create(int K, int r, int device, spanqr_plan** out);
+
+/* Plan for up to `batch` (1..SPANQR_MAX_BATCH) matrices [K, r] per call (spanqr_orth_batched_f32): one workspace
+ * per matrix, one shared dust matrix. spanqr_plan_create is the batch = 1 case. */
+int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan** out);
 void spanqr_plan_destroy(spanqr_plan* plan);
 long spanqr_plan_query(const spanqr_plan* plan, int what);
 
@@ -58,6 +67,15 @@ long spanqr_plan_query(const spanqr_plan* plan, int what);
  * hipStream_t (torch.cuda.current_stream().cuda_stream on ROCm), 0 for the null stream. */
 int spanqr_orth_f32(spanqr_plan* plan, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
                     float tau, int ns, void* stream);
+
+/* Q[i] = orth(X[i]) for the n <= batch matrices of one shape group: X and Q are host arrays of n device pointers
+ * (read at the call, so a captured graph keeps them), all with leading dimensions ldx and ldq. Each kernel of the
+ * call runs once for all n matrices (blockIdx.z is the matrix); the Cholesky runs in launches of at most
+ * SPANQR_Q_CHOL_BATCH matrices. Q[i] is bit-identical to spanqr_orth_f32 on X[i] alone. No counterpart in the
+ * reference, whose caller orthonormalises layer by layer (qrbench/methods.py:47-50) and names batching as the next
+ * step (README.md:91-92, METHODS.md:93, :102-103). */
+int spanqr_orth_batched_f32(spanqr_plan* plan, int n, const float* const* X, long ldx, float* const* Q, long ldq,
+                            float eps, float alpha, float tau, int ns, void* stream);
 
 /* Profiling form of spanqr_orth_f32: the same kernels on the same stream with a HIP event after each, then waits
  * for the stream (host synchronisation: not for the hot path). ms[i] receives the time of kernel i in launch order
@@ -80,7 +98,7 @@ enum {
     SPANQR_K_GRAM_PASS1 = 1,     /* Kahan Gram, scaled on load */
     SPANQR_K_GRAM = 2,           /* plain Gram */
     SPANQR_K_REDUCE = 3,         /* fp64 split reduction + norm partials */
-    SPANQR_K_CHOL = 4,           /* grid-synchronised clamped Cholesky */
+    SPANQR_K_CHOL = 4,           /* flag-synchronised clamped Cholesky */
     SPANQR_K_TRSM_PASS1 = 5,     /* solve with the fused s * x + eps * z operand */
     SPANQR_K_TRSM = 6,           /* solve */
     SPANQR_K_NS_APPLY = 7,       /* Newton-Schulz correction Y + Y D */
@@ -135,8 +153,8 @@ int spanqr_stage_trsm(spanqr_plan* plan, const float* A, long lda, int pass1, fl
  * Replaces one iteration of _ns_mm (candidates/kcholqr.py:16-23). */
 int spanqr_stage_ns(spanqr_plan* plan, const float* Y, long ldy, int kahan, float* Yout, long ldo, void* stream);
 
-/* Copy the plan's dust matrix (device) and its scalars {s, nrm0, tau0, nrm1, tau1, nrm2, tau2, barrier error}
- * (device, 8 floats; the last is nonzero if a grid barrier of the Cholesky timed out). */
+/* Copy the plan's dust matrix (device) and the scalars of the last call's first matrix {s, nrm0, tau0, nrm1, tau1,
+ * nrm2, tau2, wait error} (device, 8 floats; the last is nonzero if a bounded wait of the Cholesky timed out). */
 int spanqr_plan_copy_dust(spanqr_plan* plan, float* Z, void* stream);
 int spanqr_plan_copy_scalars(spanqr_plan* plan, float* scal8, void* stream);
 

@@ -2,7 +2,8 @@
 
     from orth import orth
     Q = orth(X)          # X: fp32 GPU [K, r] -> Q: fp32 [K, r], orthonormal columns, span(Q) = span(X)
+    Qs = orth_many(Xs)   # the same for a list of layers, batched per shape group (not in the reference)
 """
-from spanqr_amd import orth  # noqa: F401
+from spanqr_amd import orth, orth_many  # noqa: F401
 
-__all__ = ["orth"]
+__all__ = ["orth", "orth_many"]

@@ -18,7 +18,8 @@ HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 # plan queries (include/spanqr.h)
-Q_K, Q_R, Q_SPLITS, Q_SPLIT_ROWS, Q_CHOL_GRID, Q_WORKSPACE_MB, Q_DEVICE = range(7)
+Q_K, Q_R, Q_SPLITS, Q_SPLIT_ROWS, Q_CHOL_GRID, Q_WORKSPACE_MB, Q_DEVICE, Q_BATCH, Q_CHOL_BATCH = range(9)
+MAX_BATCH = 32   # SPANQR_MAX_BATCH
 # kernels for spanqr_profile_kernel
 K_AMAX, K_GRAM_PASS1, K_GRAM, K_REDUCE, K_CHOL, K_TRSM_PASS1, K_TRSM, K_NS_APPLY = range(8)
 
@@ -26,9 +27,11 @@ K_AMAX, K_GRAM_PASS1, K_GRAM, K_REDUCE, K_CHOL, K_TRSM_PASS1, K_TRSM, K_NS_APPLY
 _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float
 SIGNATURES = {
     "spanqr_plan_create": (_I, [_I, _I, _I, ctypes.POINTER(ctypes.c_void_p)]),
+    "spanqr_plan_create_batched": (_I, [_I, _I, _I, _I, ctypes.POINTER(ctypes.c_void_p)]),
     "spanqr_plan_destroy": (None, [_P]),
     "spanqr_plan_query": (_L, [_P, _I]),
     "spanqr_orth_f32": (_I, [_P, _P, _L, _P, _L, _F, _F, _F, _I, _P]),
+    "spanqr_orth_batched_f32": (_I, [_P, _I, _P, _L, _P, _L, _F, _F, _F, _I, _P]),
     "spanqr_profile_orth": (_I, [_P, _P, _L, _P, _L, _F, _F, _F, _I, _P, _P, _I, ctypes.POINTER(ctypes.c_int)]),
     "spanqr_profile_chol": (_I, [_P, _P, _P, _F, _F, _P, ctypes.POINTER(ctypes.c_double), _P]),
     "spanqr_profile_kernel": (_I, [_P, _I, _I, ctypes.POINTER(ctypes.c_float), _P]),

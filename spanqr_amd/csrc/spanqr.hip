@@ -41,6 +41,20 @@ constexpr int BK = 32;            // rows per Kahan chunk (tri.py:352-355)
 constexpr int AMAX_BLOCKS = 256;  // partial maxima written by k_amax (one per workgroup)
 constexpr int TS = 33;            // row stride of 32x32 LDS tiles
 constexpr uint32_t SPIN_LIMIT = 1u << 20;
+// Per-matrix strides of the small per-call buffers when a plan runs a batch of same-shape matrices (blockIdx.z is
+// the matrix): scalars (floats), error word and padding (uint32), Cholesky flags (uint32).
+constexpr int SCAL_STRIDE = 16;
+constexpr int BAR_STRIDE = 64;
+constexpr int FLAG_STRIDE = 384;   // >= 16 * 16 panel flags + 16 hand-over flags + 64 call counters
+
+// The caller's matrices of one launch, passed by value (a captured graph keeps the pointers): matrix z of the
+// batch is p[z]. Plan-owned [K, r] buffers are passed the same way.
+struct MatsIn {
+    const float* p[SPANQR_MAX_BATCH];
+};
+struct MatsOut {
+    float* p[SPANQR_MAX_BATCH];
+};
 
 __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -95,8 +109,9 @@ __device__ __forceinline__ float rsqrt_sw(float x) {
 // max|x| partials (torch.linalg.vector_norm(X, inf), kcholqr.py:102): the largest bit pattern of |x| per workgroup;
 // NaN patterns sort above +inf, so NaN propagates as in torch.
 // ---------------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_amax(const float* __restrict__ X, long ldx, int K, int r,
-                                              uint32_t* __restrict__ part) {
+__global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, int r, uint32_t* __restrict__ part) {
+    const float* __restrict__ X = Xs.p[blockIdx.z];
+    part += (size_t)blockIdx.z * AMAX_BLOCKS;
     uint32_t m = 0;
     const int r4 = r >> 2;
     const int n4 = K * r4;
@@ -136,9 +151,12 @@ __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
 }
 
 template <bool KAHAN, bool SCALE>
-__global__ __launch_bounds__(256) void k_gram(const float* __restrict__ A, long lda, int K, int nt, int KS,
+__global__ __launch_bounds__(256) void k_gram(const MatsIn As, long lda, int K, int nt, int KS,
                                               const uint32_t* __restrict__ amax_part, float* __restrict__ P) {
     const int u = blockIdx.x, sp = blockIdx.y, U = gridDim.x;
+    const float* __restrict__ A = As.p[blockIdx.z];
+    amax_part += (size_t)blockIdx.z * AMAX_BLOCKS;
+    P += (size_t)blockIdx.z * gridDim.y * U * TB * TB;
     int ti, tj;
     upper_tile(u, nt, ti, tj);
     float sc = 1.0f;
@@ -227,6 +245,9 @@ template <int MODE>
 __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int S, int nt, int r,
                                                 float* __restrict__ G, double* __restrict__ npart) {
     const int b = blockIdx.x, u = blockIdx.y, U = gridDim.y;
+    P += (size_t)blockIdx.z * S * U * TB * TB;
+    G += (size_t)blockIdx.z * r * r;
+    npart += (size_t)blockIdx.z * 16 * U;
     int ti, tj;
     upper_tile(u, nt, ti, tj);
     const int t = threadIdx.x, row = 4 * b + (t >> 6), col = t & 63;
@@ -636,6 +657,18 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     extern __shared__ float4 chol_lds[];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int b = blockIdx.x, nb = r / CB;
+    {
+        const size_t z = blockIdx.z;   // matrix of the batch
+        A += z * r * r;
+        L += z * r * r;
+        Lt += z * r * r;
+        Li += z * r * CB;
+        Lit += z * r * CB;
+        npart += z * nnp;
+        bar += z * BAR_STRIDE;
+        flags += z * FLAG_STRIDE;
+        if (scal != nullptr) scal += z * SCAL_STRIDE;
+    }
     uint32_t* err = bar + 2;
     uint32_t* flagL = flags;
     uint32_t* flagT = flags + nb * nb;
@@ -905,11 +938,17 @@ __device__ __forceinline__ void trsm_fetch(TrsmOps<Q>& o, const float* __restric
 }
 
 template <bool PASS1, int Q, int RB>
-__global__ __launch_bounds__(256) void k_trsm(const float* __restrict__ A, long lda, int K, int r,
+__global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, int r,
                                               const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
                                               float eps, const float* __restrict__ Lt, const float* __restrict__ Lit,
-                                              float* __restrict__ Y, long ldy, float* scal) {
+                                              const MatsOut Ys, long ldy, float* scal) {
     extern __shared__ float smem[];
+    const float* __restrict__ A = As.p[blockIdx.z];
+    float* __restrict__ Y = Ys.p[blockIdx.z];
+    amax_part += (size_t)blockIdx.z * AMAX_BLOCKS;
+    Lt += (size_t)blockIdx.z * r * r;
+    Lit += (size_t)blockIdx.z * r * CB;
+    if (scal != nullptr) scal += (size_t)blockIdx.z * SCAL_STRIDE;
     const int ldsy = r + 4;
     float* sY = smem;                          // [16 RB][r + 4]: finished Y columns (MFMA A operands)
     float* sAcc = sY + 16 * RB * ldsy;         // [4][16][33]: per-wave transpose of the block being finished
@@ -1043,8 +1082,11 @@ __global__ __launch_bounds__(256) void k_transpose_factors(const float* __restri
 // Newton-Schulz apply (kcholqr.py:22, addmm(Y, Y, D)): Out = Y + fp32(Y D), the product an MFMA chain over
 // m = 0..r-1 from 0 and added to Y once. 32x64 output tile per workgroup; wave w: rows 16(w >> 1), 2 column blocks.
 // ---------------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_nsapply(const float* __restrict__ Yin, long ldy, int K, int r,
-                                                 const float* __restrict__ D, float* __restrict__ Out, long ldo) {
+__global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int K, int r, const float* __restrict__ D,
+                                                 const MatsOut Outs, long ldo) {
+    const float* __restrict__ Yin = Ys.p[blockIdx.z];
+    float* __restrict__ Out = Outs.p[blockIdx.z];
+    D += (size_t)blockIdx.z * r * r;
     __shared__ float sY[32][33];
     __shared__ float sD[32][68];
     const int row0 = blockIdx.x * 32, col0 = blockIdx.y * 64;
@@ -1127,6 +1169,7 @@ inline uint64_t mix64(uint64_t z) {
 
 struct spanqr_plan {
     int K = 0, r = 0, device = 0;
+    int batch = 1, chol_bmax = 1;   // matrices per call; matrices per Cholesky launch
     int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0, trsm_rb = 1;
     size_t bytes = 0;
     char* base = nullptr;
@@ -1136,7 +1179,7 @@ struct spanqr_plan {
     float* chscal = nullptr;   // per-launch Cholesky scalars (nrm, tau, err)
     double* npart = nullptr;
     uint32_t* amax_part = nullptr;
-    uint32_t* bar = nullptr;   // [unused, unused, error, pad]
+    uint32_t* bar = nullptr;   // per matrix: [unused, unused, wait error, ...]
     uint64_t* stamps = nullptr;  // Cholesky phase stamps (profiling): start, then 4 per 32-column step
     uint32_t* flags = nullptr;   // Cholesky dataflow flags and per-workgroup call counters
     hipEvent_t ev[64] = {};    // profiling: one event before and after each kernel of a call
@@ -1169,40 +1212,69 @@ int check_mat(const spanqr_plan* p, const float* M, long ld, const char* name) {
 
 size_t trsm_lds(int r, int rb) { return (size_t)(16 * rb * (r + 4) + 4 * 16 * 33 + r / CB) * sizeof(float); }
 
-void launch_gram(const spanqr_plan* p, const float* A, long lda, bool scale, bool kahan, hipStream_t st) {
-    const dim3 grid(p->U, p->S);
+MatsIn mats_in(const float* const* X, int n) {
+    MatsIn m{};
+    for (int i = 0; i < n; ++i) m.p[i] = X[i];
+    return m;
+}
+MatsOut mats_out(float* const* X, int n) {
+    MatsOut m{};
+    for (int i = 0; i < n; ++i) m.p[i] = X[i];
+    return m;
+}
+// a plan-owned [K, r] buffer of every matrix (stride K r)
+MatsIn buf_in(const spanqr_plan* p, const float* base) {
+    MatsIn m{};
+    for (int i = 0; i < p->batch; ++i) m.p[i] = base + (size_t)i * p->K * p->r;
+    return m;
+}
+MatsOut buf_out(const spanqr_plan* p, float* base) {
+    MatsOut m{};
+    for (int i = 0; i < p->batch; ++i) m.p[i] = base + (size_t)i * p->K * p->r;
+    return m;
+}
+
+void launch_gram(const spanqr_plan* p, const MatsIn& A, long lda, int n, bool scale, bool kahan, hipStream_t st) {
+    const dim3 grid(p->U, p->S, n);
     if (kahan && scale) k_gram<true, true><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
     else if (kahan) k_gram<true, false><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
     else if (scale) k_gram<false, true><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
     else k_gram<false, false><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
 }
 
-void launch_reduce(const spanqr_plan* p, int mode, float* out, hipStream_t st) {
-    const dim3 grid(16, p->U);
+void launch_reduce(const spanqr_plan* p, int mode, float* out, int n, hipStream_t st) {
+    const dim3 grid(16, p->U, n);
     if (mode == 0) k_reduce<0><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart);
     else k_reduce<1><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart);
 }
 
-int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t st, int nnp, bool stamp = false) {
-    float* A = p->G;
-    int r = p->r;
-    const double* np = p->npart;
-    float* L = p->L;
-    float* Li = p->Li;
-    uint32_t* bar = p->bar;
-    uint32_t* flags = p->flags;
-    uint64_t* stamps = p->stamps;
-    float* Lt = p->Lt;
-    float* Lit = p->Lit;
-    const size_t lds = chol_lds_bytes(r);
-    // an ordinary launch: plan creation has checked that all chol_grid workgroups fit on the device at once
-    if (stamp)
-        k_chol<true><<<p->chol_grid, 256, lds, st>>>(A, r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, flags, scal,
-                                                     stamps);
-    else
-        k_chol<false><<<p->chol_grid, 256, lds, st>>>(A, r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, flags, scal,
-                                                      stamps);
-    HIPCHK(hipGetLastError());
+// Cholesky of the n matrices in p->G, in launches of at most chol_bmax matrices: plan creation has checked that
+// chol_bmax * chol_grid workgroups fit on the device at once, which the flag waits of one launch rely on.
+// scal: the first matrix's scalar pair (stride SCAL_STRIDE per matrix) or null.
+int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t st, int nnp, int n,
+                bool stamp = false) {
+    const size_t r = p->r;
+    const size_t lds = chol_lds_bytes(p->r);
+    for (int z0 = 0; z0 < n; z0 += p->chol_bmax) {
+        const int nz = (n - z0 < p->chol_bmax) ? n - z0 : p->chol_bmax;
+        float* A = p->G + z0 * r * r;
+        const double* np = p->npart + (size_t)z0 * nnp;
+        float* L = p->L + z0 * r * r;
+        float* Lt = p->Lt + z0 * r * r;
+        float* Li = p->Li + z0 * r * CB;
+        float* Lit = p->Lit + z0 * r * CB;
+        uint32_t* bar = p->bar + (size_t)z0 * BAR_STRIDE;
+        uint32_t* flags = p->flags + (size_t)z0 * FLAG_STRIDE;
+        float* sc = scal ? scal + (size_t)z0 * SCAL_STRIDE : nullptr;
+        const dim3 grid(p->chol_grid, 1, nz);
+        if (stamp)
+            k_chol<true><<<grid, 256, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, flags, sc,
+                                                 p->stamps);
+        else
+            k_chol<false><<<grid, 256, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, flags, sc,
+                                                  p->stamps);
+        HIPCHK(hipGetLastError());
+    }
     return SPANQR_OK;
 }
 
@@ -1232,9 +1304,9 @@ hipError_t trsm_set_lds_plan(int q, int rb, int r) {
 }
 
 template <int Q, int RB>
-void launch_trsm_t(const spanqr_plan* p, const float* A, long lda, bool pass1, float eps, const float* L,
-                   const float* Li, float* Y, long ldy, hipStream_t st) {
-    const dim3 grid((p->K + 16 * RB - 1) / (16 * RB));
+void launch_trsm_t(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const float* L,
+                   const float* Li, const MatsOut& Y, long ldy, int n, hipStream_t st) {
+    const dim3 grid((p->K + 16 * RB - 1) / (16 * RB), 1, n);
     const size_t lds = trsm_lds(p->r, RB);
     if (pass1) k_trsm<true, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, L, Li, Y, ldy,
                                                            p->scal);
@@ -1243,35 +1315,38 @@ void launch_trsm_t(const spanqr_plan* p, const float* A, long lda, bool pass1, f
 }
 
 template <int Q>
-void launch_trsm_q(const spanqr_plan* p, const float* A, long lda, bool pass1, float eps, const float* L,
-                   const float* Li, float* Y, long ldy, hipStream_t st) {
+void launch_trsm_q(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const float* L,
+                   const float* Li, const MatsOut& Y, long ldy, int n, hipStream_t st) {
     switch (p->trsm_rb) {
-        case 4: launch_trsm_t<Q, 4>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
-        case 2: launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
-        default: launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
+        case 4: launch_trsm_t<Q, 4>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
+        case 2: launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
+        default: launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
     }
 }
 
-void launch_trsm(const spanqr_plan* p, const float* A, long lda, bool pass1, float eps, const float* L,
-                 const float* Li, float* Y, long ldy, hipStream_t st) {
+// Y = A L^-T for the n matrices; L, Li are the plan's transposed factors of matrix 0 (stride r r and r 32)
+void launch_trsm(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const float* L,
+                 const float* Li, const MatsOut& Y, long ldy, int n, hipStream_t st) {
     switch (p->trsm_q) {
-        case 1: launch_trsm_q<1>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
-        case 2: launch_trsm_q<2>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
-        case 3: launch_trsm_q<3>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
-        default: launch_trsm_q<4>(p, A, lda, pass1, eps, L, Li, Y, ldy, st); break;
+        case 1: launch_trsm_q<1>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
+        case 2: launch_trsm_q<2>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
+        case 3: launch_trsm_q<3>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
+        default: launch_trsm_q<4>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
     }
 }
 
-void launch_nsapply(const spanqr_plan* p, const float* Y, long ldy, float* Out, long ldo, hipStream_t st) {
-    const dim3 grid((p->K + 31) / 32, p->r / 64);
+void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsOut& Out, long ldo, int n,
+                    hipStream_t st) {
+    const dim3 grid((p->K + 31) / 32, p->r / 64, n);
     k_nsapply<<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo);
 }
 
 
-// The whole call on one stream: amax, 3 x {gram, reduce, chol, trsm}, ns x {gram, reduce, nsapply}.
-// With rec, an event is recorded after every kernel (profiling).
-int enqueue_orth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, float eps, float alpha, float tau,
-                 int ns, hipStream_t st, bool rec) {
+// The whole call on one stream for n matrices: amax, 3 x {gram, reduce, chol, trsm}, ns x {gram, reduce, nsapply},
+// each kernel launched once for all n (the Cholesky in groups of chol_bmax). With rec, an event is recorded after
+// every kernel (profiling).
+int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut& Q, long ldq, float eps, float alpha,
+                 float tau, int ns, hipStream_t st, bool rec) {
     int rc;
     auto mark = [&]() -> int {
         if (rec) {
@@ -1280,41 +1355,44 @@ int enqueue_orth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, f
         }
         return SPANQR_OK;
     };
-    k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(X, ldx, p->K, p->r, p->amax_part);
+    k_amax<<<dim3(AMAX_BLOCKS, 1, n), 256, 0, st>>>(X, ldx, p->K, p->r, p->amax_part);
     if ((rc = mark())) return rc;
-    const float* in = X;
+    const MatsIn bin[2] = {buf_in(p, p->Y0), buf_in(p, p->Y1)};
+    const MatsOut bout[2] = {buf_out(p, p->Y0), buf_out(p, p->Y1)};
+    const MatsIn* in = &X;
     long ldin = ldx;
-    float* bufs[2] = {p->Y0, p->Y1};
     int cur = 0;
     for (int pass = 0; pass < 3; ++pass) {
-        launch_gram(p, in, ldin, pass == 0, pass == 0, st);
+        launch_gram(p, *in, ldin, n, pass == 0, pass == 0, st);
         if ((rc = mark())) return rc;
-        launch_reduce(p, 0, p->G, st);
+        launch_reduce(p, 0, p->G, n, st);
         if ((rc = mark())) return rc;
-        if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U))) return rc;
+        if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U, n))) return rc;
         if ((rc = mark())) return rc;
-        launch_trsm(p, in, ldin, pass == 0, eps, p->Lt, p->Lit, bufs[cur], p->r, st);
+        launch_trsm(p, *in, ldin, pass == 0, eps, p->Lt, p->Lit, bout[cur], p->r, n, st);
         if ((rc = mark())) return rc;
-        in = bufs[cur];
+        in = &bin[cur];
         ldin = p->r;
         cur ^= 1;
     }
     for (int i = 0; i < ns; ++i) {
-        launch_gram(p, in, ldin, false, i == ns - 1, st);
+        launch_gram(p, *in, ldin, n, false, i == ns - 1, st);
         if ((rc = mark())) return rc;
-        launch_reduce(p, 1, p->G, st);
+        launch_reduce(p, 1, p->G, n, st);
         if ((rc = mark())) return rc;
         if (i == ns - 1) {
-            launch_nsapply(p, in, ldin, Q, ldq, st);
+            launch_nsapply(p, *in, ldin, Q, ldq, n, st);
         } else {
-            launch_nsapply(p, in, ldin, bufs[cur], p->r, st);
-            in = bufs[cur];
+            launch_nsapply(p, *in, ldin, bout[cur], p->r, n, st);
+            in = &bin[cur];
             cur ^= 1;
         }
         if ((rc = mark())) return rc;
     }
-    if (ns == 0) HIPCHK(hipMemcpy2DAsync(Q, ldq * sizeof(float), in, ldin * sizeof(float), p->r * sizeof(float), p->K,
-                                         hipMemcpyDeviceToDevice, st));
+    if (ns == 0)
+        for (int z = 0; z < n; ++z)
+            HIPCHK(hipMemcpy2DAsync(Q.p[z], ldq * sizeof(float), in->p[z], ldin * sizeof(float), p->r * sizeof(float),
+                                    p->K, hipMemcpyDeviceToDevice, st));
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
@@ -1366,14 +1444,20 @@ int spanqr_split_rows(int K, int r) {
 }
 
 int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
+    return spanqr_plan_create_batched(K, r, 1, device, out);
+}
+
+int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan** out) {
     if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
     *out = nullptr;
     const int shape_rc = check_shape(K, r);
     if (shape_rc != SPANQR_OK) return shape_rc;
+    if (batch < 1 || batch > SPANQR_MAX_BATCH)
+        return fail(SPANQR_EINVAL, "batch = %d: must be in [1, %d]", batch, SPANQR_MAX_BATCH);
     DeviceGuard dg(device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", device);
     spanqr_plan* p = new spanqr_plan;
-    p->K = K; p->r = r; p->device = device;
+    p->K = K; p->r = r; p->device = device; p->batch = batch;
     p->nt = r / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / 64;
     split_policy(K, p->U, &p->S, &p->KS);
     p->chol_grid = (r / CB > 4) ? r / CB - 3 : 1;     // workgroup 0 + one per tile row 4..r/32-1
@@ -1413,13 +1497,18 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
         return fail(SPANQR_EHIP, "the Cholesky needs %d co-resident workgroups, device holds %d", need,
                     occ * cus);
     }
+    p->chol_bmax = (occ * cus) / p->chol_grid;
+    if (p->chol_bmax > batch) p->chol_bmax = batch;
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const size_t B = (size_t)batch;
     const size_t nKr = (size_t)K * r * sizeof(float);
-    const size_t sz_Z = al(nKr), sz_P = al((size_t)p->S * p->U * TB * TB * sizeof(float));
-    const size_t sz_rr = al((size_t)r * r * sizeof(float)), sz_Li = al((size_t)r * CB * sizeof(float));
-    const size_t sz_Y = al(nKr), sz_sc = 256, sz_np = al((size_t)16 * p->U * sizeof(double));
-    const size_t sz_am = al(AMAX_BLOCKS * sizeof(uint32_t)), sz_bar = 256, sz_st = al(12 * 8 * sizeof(uint64_t));
-    const size_t sz_fl = al((16 * 16 + 16 + 64) * sizeof(uint32_t));
+    const size_t sz_Z = al(nKr), sz_P = al(B * p->S * p->U * TB * TB * sizeof(float));
+    const size_t sz_rr = al(B * r * r * sizeof(float)), sz_Li = al(B * r * CB * sizeof(float));
+    const size_t sz_Y = al(B * nKr), sz_sc = al(B * SCAL_STRIDE * sizeof(float));
+    const size_t sz_np = al(B * 16 * p->U * sizeof(double));
+    const size_t sz_am = al(B * AMAX_BLOCKS * sizeof(uint32_t)), sz_bar = al(B * BAR_STRIDE * sizeof(uint32_t));
+    const size_t sz_st = al(2 * (4 * (512 / CB) + 2) * sizeof(uint64_t));
+    const size_t sz_fl = al(B * FLAG_STRIDE * sizeof(uint32_t));
     p->bytes = sz_Z + sz_P + 3 * sz_rr + 2 * sz_Li + 2 * sz_Y + 2 * sz_sc + sz_np + sz_am + sz_bar + sz_st + sz_fl;
     if (hipMalloc((void**)&p->base, p->bytes) != hipSuccess) {
         const size_t nb = p->bytes;
@@ -1482,6 +1571,8 @@ long spanqr_plan_query(const spanqr_plan* p, int what) {
         case SPANQR_Q_CHOL_GRID: return p->chol_grid;
         case SPANQR_Q_WORKSPACE_MB: return (long)((p->bytes + (1u << 20) - 1) >> 20);
         case SPANQR_Q_DEVICE: return p->device;
+        case SPANQR_Q_BATCH: return p->batch;
+        case SPANQR_Q_CHOL_BATCH: return p->chol_bmax;
         default: return -1;
     }
 }
@@ -1495,7 +1586,28 @@ int spanqr_orth_f32(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq
     if (ns < 0) return fail(SPANQR_EINVAL, "ns = %d < 0", ns);
     DeviceGuard dg(p->device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
-    return enqueue_orth(p, X, ldx, Q, ldq, eps, alpha, tau, ns, (hipStream_t)stream, false);
+    return enqueue_orth(p, 1, mats_in(&X, 1), ldx, mats_out(&Q, 1), ldq, eps, alpha, tau, ns, (hipStream_t)stream,
+                        false);
+}
+
+int spanqr_orth_batched_f32(spanqr_plan* p, int n, const float* const* X, long ldx, float* const* Q, long ldq,
+                            float eps, float alpha, float tau, int ns, void* stream) {
+    if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    if (n < 1 || n > p->batch) return fail(SPANQR_EINVAL, "n = %d: must be in [1, %d] (the plan's batch)", n, p->batch);
+    if (!X || !Q) return fail(SPANQR_EINVAL, "pointer arrays must not be null");
+    int rc;
+    char name[32];
+    for (int i = 0; i < n; ++i) {
+        snprintf(name, sizeof name, "X[%d]", i);
+        if ((rc = check_mat(p, X[i], ldx, name))) return rc;
+        snprintf(name, sizeof name, "Q[%d]", i);
+        if ((rc = check_mat(p, Q[i], ldq, name))) return rc;
+    }
+    if (ns < 0) return fail(SPANQR_EINVAL, "ns = %d < 0", ns);
+    DeviceGuard dg(p->device);
+    if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
+    return enqueue_orth(p, n, mats_in(X, n), ldx, mats_out(Q, n), ldq, eps, alpha, tau, ns, (hipStream_t)stream,
+                        false);
 }
 
 int spanqr_profile_orth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
@@ -1511,7 +1623,7 @@ int spanqr_profile_orth(spanqr_plan* p, const float* X, long ldx, float* Q, long
         if (!p->ev[i]) HIPCHK(hipEventCreate(&p->ev[i]));
     HIPCHK(hipEventRecord(p->ev[0], st));
     p->nev = 1;
-    if ((rc = enqueue_orth(p, X, ldx, Q, ldq, eps, alpha, tau, ns, st, true))) return rc;
+    if ((rc = enqueue_orth(p, 1, mats_in(&X, 1), ldx, mats_out(&Q, 1), ldq, eps, alpha, tau, ns, st, true))) return rc;
     HIPCHK(hipEventSynchronize(p->ev[p->nev - 1]));
     const int n = p->nev - 1 < max_n ? p->nev - 1 : max_n;
     for (int i = 0; i < n; ++i) HIPCHK(hipEventElapsedTime(&ms[i], p->ev[i], p->ev[i + 1]));
@@ -1529,16 +1641,18 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
     for (int i = 0; i < 2; ++i)
         if (!p->ev[i]) HIPCHK(hipEventCreate(&p->ev[i]));
     const int r = p->r;
+    const MatsIn y0 = buf_in(p, p->Y0);
+    const MatsOut y1 = buf_out(p, p->Y1);
     auto launch = [&]() -> int {
         switch (which) {
-            case SPANQR_K_AMAX: k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(p->Y0, r, p->K, r, p->amax_part); break;
-            case SPANQR_K_GRAM_PASS1: launch_gram(p, p->Y0, r, true, true, st); break;
-            case SPANQR_K_GRAM: launch_gram(p, p->Y0, r, false, false, st); break;
-            case SPANQR_K_REDUCE: launch_reduce(p, 0, p->G, st); break;
-            case SPANQR_K_CHOL: return launch_chol(p, 1e-7f, 1e-8f, p->scal + 1, st, 16 * p->U);
-            case SPANQR_K_TRSM_PASS1: launch_trsm(p, p->Y0, r, true, 5e-7f, p->Lt, p->Lit, p->Y1, r, st); break;
-            case SPANQR_K_TRSM: launch_trsm(p, p->Y0, r, false, 0.0f, p->Lt, p->Lit, p->Y1, r, st); break;
-            case SPANQR_K_NS_APPLY: launch_nsapply(p, p->Y0, r, p->Y1, r, st); break;
+            case SPANQR_K_AMAX: k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(y0, r, p->K, r, p->amax_part); break;
+            case SPANQR_K_GRAM_PASS1: launch_gram(p, y0, r, 1, true, true, st); break;
+            case SPANQR_K_GRAM: launch_gram(p, y0, r, 1, false, false, st); break;
+            case SPANQR_K_REDUCE: launch_reduce(p, 0, p->G, 1, st); break;
+            case SPANQR_K_CHOL: return launch_chol(p, 1e-7f, 1e-8f, p->scal + 1, st, 16 * p->U, 1);
+            case SPANQR_K_TRSM_PASS1: launch_trsm(p, y0, r, true, 5e-7f, p->Lt, p->Lit, y1, r, 1, st); break;
+            case SPANQR_K_TRSM: launch_trsm(p, y0, r, false, 0.0f, p->Lt, p->Lit, y1, r, 1, st); break;
+            case SPANQR_K_NS_APPLY: launch_nsapply(p, y0, r, y1, r, 1, st); break;
         }
         return SPANQR_OK;
     };
@@ -1561,7 +1675,7 @@ int spanqr_stage_amax(spanqr_plan* p, const float* X, long ldx, void* stream) {
     int rc = check_mat(p, X, ldx, "X");
     if (rc) return rc;
     DeviceGuard dg(p->device);
-    k_amax<<<AMAX_BLOCKS, 256, 0, (hipStream_t)stream>>>(X, ldx, p->K, p->r, p->amax_part);
+    k_amax<<<AMAX_BLOCKS, 256, 0, (hipStream_t)stream>>>(mats_in(&X, 1), ldx, p->K, p->r, p->amax_part);
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
@@ -1574,8 +1688,8 @@ int spanqr_stage_gram(spanqr_plan* p, const float* A, long lda, int use_scale, i
     if (!G) return fail(SPANQR_EINVAL, "G is null");
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
-    launch_gram(p, A, lda, use_scale != 0, kahan != 0, st);
-    launch_reduce(p, 0, p->G, st);
+    launch_gram(p, mats_in(&A, 1), lda, 1, use_scale != 0, kahan != 0, st);
+    launch_reduce(p, 0, p->G, 1, st);
     HIPCHK(hipMemcpyAsync(G, p->G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
     if (npart) HIPCHK(hipMemcpyAsync(npart, p->npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipGetLastError());
@@ -1589,7 +1703,7 @@ int spanqr_stage_chol(spanqr_plan* p, const float* G, const double* npart, float
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
     if (npart) HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
-    int rc = launch_chol(p, alpha, tau, p->chscal, st, npart ? 16 * p->U : 0);
+    int rc = launch_chol(p, alpha, tau, p->chscal, st, npart ? 16 * p->U : 0, 1);
     if (rc) return rc;
     HIPCHK(hipMemcpyAsync(L, p->L, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipMemcpyAsync(Li, p->Li, (size_t)p->r * CB * sizeof(float), hipMemcpyDeviceToDevice, st));
@@ -1610,7 +1724,7 @@ int spanqr_stage_trsm(spanqr_plan* p, const float* A, long lda, int pass1, float
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
     k_transpose_factors<<<(p->r * p->r + 255) / 256, 256, 0, st>>>(L, Li, p->r, p->Lt, p->Lit);
-    launch_trsm(p, A, lda, pass1 != 0, eps, p->Lt, p->Lit, Y, ldy, st);
+    launch_trsm(p, mats_in(&A, 1), lda, pass1 != 0, eps, p->Lt, p->Lit, mats_out(&Y, 1), ldy, 1, st);
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
@@ -1622,9 +1736,9 @@ int spanqr_stage_ns(spanqr_plan* p, const float* Y, long ldy, int kahan, float* 
     if ((rc = check_mat(p, Yout, ldo, "Yout"))) return rc;
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
-    launch_gram(p, Y, ldy, false, kahan != 0, st);
-    launch_reduce(p, 1, p->G, st);
-    launch_nsapply(p, Y, ldy, Yout, ldo, st);
+    launch_gram(p, mats_in(&Y, 1), ldy, 1, false, kahan != 0, st);
+    launch_reduce(p, 1, p->G, 1, st);
+    launch_nsapply(p, mats_in(&Y, 1), ldy, mats_out(&Yout, 1), ldo, 1, st);
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
@@ -1636,8 +1750,8 @@ int spanqr_profile_chol(spanqr_plan* p, const float* G, const double* npart, flo
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
-    HIPCHK(hipMemsetAsync(p->stamps, 0, 12 * 8 * sizeof(uint64_t), st));
-    int rc = launch_chol(p, alpha, tau, p->chscal, st, 16 * p->U, true);
+    HIPCHK(hipMemsetAsync(p->stamps, 0, (size_t)12 * p->NB * sizeof(uint64_t), st));
+    int rc = launch_chol(p, alpha, tau, p->chscal, st, 16 * p->U, 1, true);
     if (rc) return rc;
     HIPCHK(hipMemcpyAsync(stamps_out, p->stamps, (size_t)12 * p->NB * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));

@@ -2,6 +2,8 @@
 library. The signature and keyword arguments are the reference's; the whole call is enqueued on the current stream
 with no host synchronisation.
 """
+import ctypes
+
 import torch
 
 from . import _lib
@@ -46,6 +48,60 @@ def kcholqr_f(X, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
         _lib.check(_lib.lib().spanqr_orth_f32(plan.handle, X.data_ptr(), r, Q.data_ptr(), r, float(eps), float(alpha),
                                                float(tau), int(ns), stream_handle(dev)))
     return Q
+
+
+def kcholqr_f_many(Xs, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
+    """[kcholqr_f(X) for X in Xs] for same-shape fp32 matrices on one device, in launches that cover up to
+    32 matrices each (one kernel per stage for the whole group; the Cholesky in groups that fit the device at once).
+    Every Q is bit-identical to kcholqr_f on that X alone. No counterpart in the reference, whose optimizer calls
+    orth once per layer (qrbench/methods.py:47-50).
+    """
+    Xs = list(Xs)
+    if not Xs:
+        return []
+    for X in Xs:
+        _check_input(X)
+    K, r = Xs[0].shape
+    dev = Xs[0].device
+    for X in Xs:
+        if tuple(X.shape) != (K, r) or X.device != dev:
+            raise ValueError("kcholqr_f_many: every X must have the same shape and device")
+    if r % TILE or r > R_MAX or K < r:
+        raise ValueError(f"kcholqr_f_many: shape [{K}, {r}] needs r % {TILE} == 0, r <= {R_MAX} and K >= r")
+    Xs = [_prepare(X) for X in Xs]
+    Qs = [torch.empty_like(X) for X in Xs]
+    n_all = len(Xs)
+    plan = get_plan(K, r, dev, min(n_all, _lib.MAX_BATCH))
+    with torch.cuda.device(dev):
+        for i0 in range(0, n_all, plan.batch):
+            xs, qs = Xs[i0:i0 + plan.batch], Qs[i0:i0 + plan.batch]
+            n = len(xs)
+            xp = (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs])
+            qp = (ctypes.c_void_p * n)(*[q.data_ptr() for q in qs])
+            _lib.check(_lib.lib().spanqr_orth_batched_f32(plan.handle, n, xp, r, qp, r, float(eps), float(alpha),
+                                                          float(tau), int(ns), stream_handle(dev)))
+    return Qs
+
+
+def orth_many(Xs):
+    """[orth(X) for X in Xs] with the matrices grouped by shape and device: each group of native shapes runs as
+    batched launches (kcholqr_f_many), so the latency-bound Cholesky of a group costs about as much as one. Results
+    come back in input order and are bit-identical to orth(X) on each X.
+    """
+    Xs = list(Xs)
+    out = [None] * len(Xs)
+    groups = {}
+    for i, X in enumerate(Xs):
+        _check_input(X)
+        K, r = X.shape
+        if r % TILE == 0 and r <= R_MAX and K >= r:
+            groups.setdefault((K, r, X.device), []).append(i)
+        else:
+            out[i] = orth(X)
+    for idx in groups.values():
+        for i, Q in zip(idx, kcholqr_f_many([Xs[i] for i in idx])):
+            out[i] = Q
+    return out
 
 
 def orth(X):

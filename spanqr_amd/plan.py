@@ -1,4 +1,4 @@
-"""Plans: one native workspace per (K, r, device, stream).
+"""Plans: one native workspace per (K, r, batch, device, stream).
 
 A plan owns the dust matrix, the Gram partials, the Cholesky factors, the solve buffers and the Cholesky's
 grid-barrier counters (include/spanqr.h). The reference keeps module-level caches instead (the dust cache
@@ -24,10 +24,10 @@ def _mark_shutdown():
 
 
 class Plan:
-    def __init__(self, K, r, device_index):
-        self.K, self.r, self.device = int(K), int(r), int(device_index)
+    def __init__(self, K, r, device_index, batch=1):
+        self.K, self.r, self.device, self.batch = int(K), int(r), int(device_index), int(batch)
         h = ctypes.c_void_p()
-        _lib.check(_lib.lib().spanqr_plan_create(self.K, self.r, self.device, ctypes.byref(h)))
+        _lib.check(_lib.lib().spanqr_plan_create_batched(self.K, self.r, self.batch, self.device, ctypes.byref(h)))
         self.handle = h
 
     def query(self, what):
@@ -44,6 +44,10 @@ class Plan:
     @property
     def chol_grid(self):
         return self.query(_lib.Q_CHOL_GRID)
+
+    @property
+    def chol_batch(self):
+        return self.query(_lib.Q_CHOL_BATCH)
 
     def close(self):
         if self.handle and not _SHUTTING_DOWN[0]:
@@ -65,15 +69,15 @@ def stream_handle(device):
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def get_plan(K, r, device):
-    """the cached plan for (K, r) on `device` and the current stream"""
+def get_plan(K, r, device, batch=1):
+    """the cached plan for (K, r) and `batch` matrices per call on `device` and the current stream"""
     dev = torch.device(device)
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    key = (int(K), int(r), idx, stream_handle(idx))
+    key = (int(K), int(r), int(batch), idx, stream_handle(idx))
     with _LOCK:
         p = _PLANS.get(key)
         if p is None:
-            p = Plan(K, r, idx)
+            p = Plan(K, r, idx, batch)
             _PLANS[key] = p
         return p
 

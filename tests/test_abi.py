@@ -60,6 +60,19 @@ def test_bad_shapes_rejected_before_any_device_work():
     assert _lib.lib().spanqr_plan_create(1024, 256, 0, None) == -1
 
 
+def test_batched_plan_arguments_checked_before_any_device_work():
+    h = ctypes.c_void_p()
+    f = _lib.lib().spanqr_plan_create_batched
+    for batch in (0, -1, _lib.MAX_BATCH + 1):
+        assert f(1024, 256, batch, 0, ctypes.byref(h)) == -1 and not h.value
+        assert b"batch" in _lib.lib().spanqr_last_error()
+    assert f(100, 128, 4, 0, ctypes.byref(h)) == -1
+    assert f(1024, 256, 4, 0, None) == -1
+    # a null plan is refused by the batched call as by the single one
+    ptrs = (ctypes.c_void_p * 1)(None)
+    assert _lib.lib().spanqr_orth_batched_f32(None, 1, ptrs, 256, ptrs, 256, 5e-7, 1e-7, 1e-8, 2, None) == -1
+
+
 def test_orth_refuses_cpu_tensors():
     X = torch.randn(256, 128)
     with pytest.raises(TypeError):
@@ -68,6 +81,11 @@ def test_orth_refuses_cpu_tensors():
         spanqr_amd.kcholqr_f(X)
     with pytest.raises(TypeError):
         spanqr_amd.orth(X.double())
+    with pytest.raises(TypeError):
+        spanqr_amd.orth_many([X, X])
+    with pytest.raises(TypeError):
+        spanqr_amd.kcholqr_f_many([X])
+    assert spanqr_amd.orth_many([]) == [] and spanqr_amd.kcholqr_f_many([]) == []
 
 
 def test_missing_library_raises(monkeypatch, tmp_path):
@@ -80,3 +98,4 @@ def test_missing_library_raises(monkeypatch, tmp_path):
 def test_top_level_orth_is_the_package_orth():
     import orth as top
     assert top.orth is spanqr_amd.orth
+    assert top.orth_many is spanqr_amd.orth_many
