@@ -7,10 +7,12 @@ Workload (the reference's 0.8B TTF layer shapes): K x r in {1024x256, 2048x256, 
 resident on the GPU before timing. One step = one orth() call on each of the six inputs; every input has its own
 captured hipGraph. `value` = timed wall time / (steps x 6) in microseconds (lower is better).
 
-Also reported: per-shape back-to-back time; the 768x512 and 17408x256 shapes (the quoted targets); the batched
-layer set (12 x 768x512 + 12 x 2048x512, one hipGraph per shape group, against 24 single-call graphs); per kernel the
-average launch duration at each workload shape (HIP events around back-to-back launches on the call's stream) with
-its algorithmic flops and bytes; the roofline of the dominant kernel and of the whole call; the Cholesky's latency
+Also reported: per shape, back-to-back ("thr", 20 replays) and isolated synchronised ("lat") time per call, at the
+workload shapes and at 768x512, 2048x512, 5120x256, 6144x256 and 17408x256 (768x512 and 17408x256 are the quoted
+targets); the batched layer set (12 x 768x512 + 12 x 2048x512, one hipGraph per shape group, against 24
+single-call graphs); per kernel and shape the average launch duration (HIP events around back-to-back launches on
+the call's stream) with its algorithmic flops and bytes, as TFLOP/s and GB/s and as fractions of the MFMA and HBM
+peaks; the roofline of the dominant kernel and of the whole call; the Cholesky's latency
 per diagonal step; a CPU baseline on a bounded sample (the C restatement in oracle/, OpenMP, on the host, plus CPU
 torch.linalg.qr).
 """
@@ -35,6 +37,8 @@ METRIC = "µs per orth() call at K×r (median); max|QᵀQ−I|; % of HBM/MFMA ro
 WORKLOAD_SHAPES = [(1024, 256), (2048, 256), (3584, 256)]
 SEEDS = (0, 1)
 TARGET_SHAPES = [(768, 512), (17408, 256)]
+TARGET_US = {"768x512": 250.0, "17408x256": 350.0}
+OTHER_SHAPES = [(768, 512), (2048, 512), (5120, 256), (6144, 256), (17408, 256)]
 BATCH_GROUPS = [(768, 512, 12), (2048, 512, 12)]   # the 110M model's attention and down_proj layers
 PEAK_FP32_TFLOPS = 157.3     # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
@@ -191,6 +195,30 @@ def time_graph(g, n=20, reps=5):
     return statistics.median(out)
 
 
+def lat_us(g, n=20):
+    """isolated synchronised call: median host wall time of one replay followed by a device synchronisation"""
+    out = []
+    torch.cuda.synchronize()
+    for _ in range(n):
+        t0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        out.append((time.perf_counter() - t0) * 1e6)
+    return statistics.median(out)
+
+
+def kernels_at(X, reps):
+    """per kernel family at X's shape: average launch duration and its algorithmic rates"""
+    K, r = X.shape
+    out = {}
+    for fam, which, per_call in FAMILIES:
+        us = kernel_avg_us(X, which, reps)
+        fl, by = algorithmic(fam, K, r)
+        out[fam] = {"us": us, "per_call": per_call, "tflops": fl / us / 1e6, "gbs": by / us / 1e3,
+                    "mfma_frac": fl / us / 1e6 / PEAK_FP32_TFLOPS, "hbm_frac": by / us / 1e3 / PEAK_HBM_GBS}
+    return out
+
+
 def cpu_baseline(inputs, seconds):
     """the oracle (C restatement, OpenMP) and CPU torch.linalg.qr on the host, on a bounded sample"""
     import oracle
@@ -282,16 +310,24 @@ def main(argv=None):
     value = total_ms * 1000.0 / (a.steps * calls)
     orth_max = max(orth_error(q) for _g, q in graphs.values())
 
-    per_shape = {}
+    per_shape, per_shape_lat = {}, {}
     for (K, r, s), (g, _q) in graphs.items():
         per_shape.setdefault(f"{K}x{r}", []).append(time_graph(g))
+        per_shape_lat.setdefault(f"{K}x{r}", []).append(lat_us(g))
     per_shape = {k: statistics.mean(v) for k, v in per_shape.items()}
-    targets = {}
-    for K, r in TARGET_SHAPES:
+    per_shape_lat = {k: statistics.mean(v) for k, v in per_shape_lat.items()}
+    shapes = {}
+    for K, r in OTHER_SHAPES:
         X = gen.bench_input(K, r, seed=0).to(dev)
         g, q = capture(X) if not a.no_graph else (lambda d: (d, d.Q))(_Direct(X))
-        targets[f"{K}x{r}"] = {"us_per_call": time_graph(g), "orth": orth_error(q)}
-        del g
+        ks = kernels_at(X, a.kernel_reps)
+        shapes[f"{K}x{r}"] = {"thr_us": time_graph(g), "lat_us": lat_us(g), "orth": orth_error(q),
+                              "sum_of_kernels_us": sum(v["us"] * v["per_call"] for v in ks.values()),
+                              "kernels": ks}
+        del g, q, X
+        torch.cuda.synchronize()
+    targets = {k: {"us_per_call": shapes[k]["thr_us"], "lat_us": shapes[k]["lat_us"], "orth": shapes[k]["orth"],
+                   "target_us": TARGET_US[k]} for k in TARGET_US}
 
     batched = batched_layers(dev, max(1, min(a.steps, 20)))
 
@@ -299,16 +335,10 @@ def main(argv=None):
     kernels = {}
     call_us = {}
     for K, r in WORKLOAD_SHAPES:
-        X = inputs[(K, r, 0)]
-        tot = 0.0
-        for fam, which, per_call in FAMILIES:
-            us = kernel_avg_us(X, which, a.kernel_reps)
-            fl, by = algorithmic(fam, K, r)
-            kernels.setdefault(fam, {})[f"{K}x{r}"] = {
-                "us": us, "per_call": per_call, "tflops": fl / us / 1e6, "gbs": by / us / 1e3,
-                "mfma_frac": fl / us / 1e6 / PEAK_FP32_TFLOPS, "hbm_frac": by / us / 1e3 / PEAK_HBM_GBS}
-            tot += per_call * us
-        call_us[f"{K}x{r}"] = tot
+        ks = kernels_at(inputs[(K, r, 0)], a.kernel_reps)
+        for fam, v in ks.items():
+            kernels.setdefault(fam, {})[f"{K}x{r}"] = v
+        call_us[f"{K}x{r}"] = sum(v["us"] * v["per_call"] for v in ks.values())
     share = {fam: sum(v[s_]["us"] * v[s_]["per_call"] for s_ in v) / sum(call_us.values())
              for fam, v in kernels.items()}
     dom = max(share, key=share.get)
@@ -345,7 +375,8 @@ def main(argv=None):
         "config": {"workload": "0.8B TTF layers: orth() at 1024x256, 2048x256, 3584x256, 2 seeds each, one "
                                "hipGraph per input", "shapes": [f"{K}x{r}" for K, r in WORKLOAD_SHAPES],
                    "seeds": list(SEEDS), "calls_per_step": calls, "graphs": not a.no_graph},
-        "orth_max": orth_max, "per_shape_us": per_shape, "target_shapes": targets, "batched_layers": batched,
+        "orth_max": orth_max, "per_shape_us": per_shape, "per_shape_lat_us": per_shape_lat,
+        "target_shapes": targets, "shapes": shapes, "batched_layers": batched,
         "roofline": roofline, "call_roofline": call_roof, "kernels": kernels, "kernel_share": share,
         "sum_of_kernels_us": call_us, "cholesky": chol_info,
         "cpu_baseline": cpu,

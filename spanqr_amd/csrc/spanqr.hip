@@ -339,13 +339,19 @@ __device__ __forceinline__ void store_tile(float* dst, int ld, const Tile& src, 
     }
 }
 
-// transposed store: dst[c][r'] = src[r'][c] (the solve reads L^T and the Li blocks transposed, coalesced)
-__device__ __forceinline__ void store_tile_T(float* dst, int ld, const Tile& src, int t = -1, int nthr = 256) {
+// Solve operands: a factor block T (L(a, b), b < a, or Li_a for b = a) as the solve's MFMA B operands, 16 floats per
+// lane, contiguous: dst[16 lane + 8 cb + kk] = T[16 cb + (lane & 15)][4 kk + (lane >> 4)], at pair index
+// a (a + 1) / 2 + b of the packed factor (1024 floats per block).
+__device__ __forceinline__ int op_pair(int a, int b) { return a * (a + 1) / 2 + b; }
+__device__ __forceinline__ void store_tile_op(float* dst, const Tile& src, int t = -1, int nthr = 256) {
     for (int e = (t < 0 ? (int)threadIdx.x : t); e < 256; e += nthr) {
-        const int row = e >> 3, c4 = e & 7;
+        const int lane = e >> 2, h = e & 3, cb = h >> 1, kk0 = 4 * (h & 1), l16 = lane & 15, lk = lane >> 4;
         float4 v;
-        v.x = src[4 * c4 + 0][row]; v.y = src[4 * c4 + 1][row]; v.z = src[4 * c4 + 2][row]; v.w = src[4 * c4 + 3][row];
-        *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+        v.x = src[16 * cb + l16][4 * (kk0 + 0) + lk];
+        v.y = src[16 * cb + l16][4 * (kk0 + 1) + lk];
+        v.z = src[16 * cb + l16][4 * (kk0 + 2) + lk];
+        v.w = src[16 * cb + l16][4 * (kk0 + 3) + lk];
+        *reinterpret_cast<float4*>(dst + 4 * e) = v;
     }
 }
 
@@ -523,32 +529,36 @@ __device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Til
 // in at the end (a factor lane above the diagonal computes values that only its own dead upper-triangle registers
 // see). Then both halves run the same rank-1 update R[k] = fma(-own, l_k, R[k]) for k > c: the factor's trailing
 // update D_ik -= l_i l_k and the inverse's forward substitution acc_k -= L_kc x_c, each element's chain in column
-// order. Only the update of column c+1 is on the critical path: l_{c+1} comes by v_readlane and the next pivot is
-// formed right away; the other l_k are broadcast through LDS (bl) and their updates overlap the next pivot chain.
-// No lane-dependent selects: their masks would all be hoisted and spilled. Writes the factor to dl (the upper
-// triangle is left unspecified: publishers zero it) and the inverse to Li.
-__device__ __forceinline__ void factor_inv32(float* bl, float* pq, const Tile& id, const Tile& D, float tau, Tile& dl,
-                                             Tile& Li) {
+// order. Only lane c+1's diagonal is on the critical path: that lane forms its next pivot from its own l (the same
+// fma as the update) and takes the reciprocal square root itself; q crosses lanes once, by v_readlane. The other l_k
+// are broadcast through LDS, alternating between two buffers (bl0, bl1) so that no barrier is needed: the compiler
+// may interleave a column's update with the next pivot's chain. No lane-dependent selects: their masks would all be
+// hoisted and spilled. Writes the factor to dl (the upper triangle is left unspecified: publishers zero it) and the
+// inverse to Li.
+__device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, const Tile& id, const Tile& D,
+                                             float tau, Tile& dl, Tile& Li) {
     const int lane = threadIdx.x & 63, i = lane & 31;
     const bool fl = lane < 32;
     const float* src = fl ? &D[i][0] : &id[i][0];
     float R[CB];
 #pragma unroll
     for (int k = 0; k < CB; ++k) R[k] = src[k];
-    float piv = fmaxf(readlane(R[0], 0), tau);
-    float q = rsqrt_sw(piv);
+    const float pl = fmaxf(R[0], tau);         // lane 0's value is the first pivot
+    float q = readlane(rsqrt_sw(pl), 0);
+    float piv = readlane(pl, 0);
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
+        float* bl = (c & 1) ? bl1 : bl0;
         const float own = R[c] * q;
         pq[c] = piv * q;
         R[c] = own;
         if (c + 1 < CB) {
+            const float dn = __builtin_fmaf(-own, own, R[c + 1]);     // lane c+1: its diagonal after column c
+            const float pn = fmaxf(dn, tau);
+            const float qn = readlane(rsqrt_sw(pn), c + 1);
             R[c + 1] = __builtin_fmaf(-own, readlane(own, c + 1), R[c + 1]);
-            const float pn = fmaxf(readlane(R[c + 1], c + 1), tau);
-            const float qn = rsqrt_sw(pn);
             if (c + 2 < CB) {
                 bl[lane] = own;
-                __builtin_amdgcn_wave_barrier();
 #pragma unroll
                 for (int k0 = (c + 2) & ~3; k0 < CB; k0 += 4) {
                     const float4 l4 = *reinterpret_cast<const float4*>(&bl[k0]);
@@ -557,12 +567,12 @@ __device__ __forceinline__ void factor_inv32(float* bl, float* pq, const Tile& i
                     for (int t = 0; t < 4; ++t)
                         if (k0 + t > c + 1) R[k0 + t] = __builtin_fmaf(-own, lv[t], R[k0 + t]);
                 }
-                __builtin_amdgcn_wave_barrier();
             }
-            piv = pn;
+            piv = readlane(pn, c + 1);
             q = qn;
         }
     }
+    __builtin_amdgcn_wave_barrier();
     float* dst = fl ? &dl[i][0] : &Li[0][i];
     const int step = fl ? 1 : TS;
 #pragma unroll
@@ -640,7 +650,7 @@ size_t chol_lds_bytes(int r) {
     const int nb = r / CB;
     const int owner_tiles = 2 * nb;       // a tile row (up to nb tiles), the panels of one column block and Li_j
     const int tiles = owner_tiles > CH_WG0_TILES ? owner_tiles : CH_WG0_TILES;
-    return (size_t)tiles * sizeof(Tile) + 128 * sizeof(float);
+    return (size_t)tiles * sizeof(Tile) + 256 * sizeof(float);
 }
 
 // nb = r/32 tile rows; grid = max(1, nb - 3) workgroups. With nnp == 0 the shift is 0 and tau_rel is the absolute
@@ -652,7 +662,7 @@ size_t chol_lds_bytes(int r) {
 // start, 1 tile factored and row j+2 fetched, 2 look-ahead done; slot 0 is the kernel start, 1 + 4 nb the end.
 template <bool STAMP>
 __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
-                                              float tau_rel, float* L, float* Li, float* Lt, float* Lit, uint32_t* bar,
+                                              float tau_rel, float* L, float* Li, float* Lp, uint32_t* bar,
                                               uint32_t* flags, float* scal, uint64_t* stamps) {
     extern __shared__ float4 chol_lds[];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -661,9 +671,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         const size_t z = blockIdx.z;   // matrix of the batch
         A += z * r * r;
         L += z * r * r;
-        Lt += z * r * r;
         Li += z * r * CB;
-        Lit += z * r * CB;
+        Lp += z * (nb * (nb + 1) / 2) * CB * CB;
         npart += z * nnp;
         bar += z * BAR_STRIDE;
         flags += z * FLAG_STRIDE;
@@ -676,10 +685,10 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     bool dead = false;
     if (STAMP && b == 0 && tid == 0) stamps[0] = wall_clock64();
     const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
-    // misc: [0..2] nrm, shift, tau; [4..5] wave-group barrier counters; [32..95] tile-factor broadcast;
-    // [96..127] the tile factor's diagonal
+    // misc: [0..2] nrm, shift, tau; [4..5] wave-group barrier counters; [32..95] and [128..191] tile-factor
+    // broadcast buffers; [96..127] the tile factor's diagonal
     float* misc = reinterpret_cast<float*>(chol_lds);
-    Tile* tiles = reinterpret_cast<Tile*>(misc + 128);
+    Tile* tiles = reinterpret_cast<Tile*>(misc + 256);
     if (w == 0) {
         double s = 0.0;
         for (int p = lane; p < nnp; p += 64) s = s + npart[p];
@@ -701,7 +710,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     }
     __syncthreads();
     const float shift = misc[1], tau = misc[2];
-    float* bl = misc + 32;
+    float* bl0 = misc + 32;
+    float* bl1 = misc + 128;
     float* pq = misc + 96;
 
     if (b == 0) {
@@ -725,16 +735,15 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             const int q = j & 1;
             const size_t o = (size_t)CB * j;
             store_tile_lower(L + o * r + o, r, z.dl[q], false, lane, 64);
-            store_tile_lower(Lt + o * r + o, r, z.dl[q], true, lane, 64);
             store_tile(Li + o * CB, CB, z.li[q], lane, 64);
-            store_tile_T(Lit + o * CB, CB, z.li[q], lane, 64);
+            store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[q], lane, 64);
             if (j + 1 < nb) {
                 store_tile(L + (o + CB) * r + o, r, z.P1[q], lane, 64);
-                store_tile_T(Lt + o * r + o + CB, r, z.P1[q], lane, 64);
+                store_tile_op(Lp + (size_t)op_pair(j + 1, j) * CB * CB, z.P1[q], lane, 64);
             }
             if (j + 2 < nb) {
                 store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
-                store_tile_T(Lt + o * r + o + 2 * CB, r, z.P2[q], lane, 64);
+                store_tile_op(Lp + (size_t)op_pair(j + 2, j) * CB * CB, z.P2[q], lane, 64);
             }
             if (lane == 0) {
                 release();
@@ -747,7 +756,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             const int p = j & 1, pp = p ^ 1;
             if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
             if (w == 0) {
-                factor_inv32(bl, pq, z.id, z.D[p], tau, z.dl[p], z.li[p]);
+                factor_inv32(bl0, bl1, pq, z.id, z.D[p], tau, z.dl[p], z.li[p]);
             } else {
                 // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram). Waves 1-2 fetch it
                 // while wave 3 publishes the previous step; then L(j+2, j-1) (wave 1) and the block j-2 update of
@@ -789,7 +798,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
                         // the owners of rows j+4.. need L(j+2, j-1) for block j-1
                         const size_t o = (size_t)CB * (j - 1);
                         store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
-                        store_tile_T(Lt + o * r + o + 3 * CB, r, z.C2[p], lane, 64);
+                        store_tile_op(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], lane, 64);
                         if (lane == 0) publish_flag(flagL + (j + 2) * nb + j - 1, ep);
                     }
                 }
@@ -848,7 +857,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             __syncthreads();
             panel32(rt[j], rt[j], lij);
             store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j]);
-            store_tile_T(Lt + (size_t)CB * j * r + (size_t)CB * i, r, rt[j]);
+            store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j]);
             // publish L(i, j) before waiting on the other rows (so no row waits on a chain of rows)
             __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
             __syncthreads();
@@ -899,8 +908,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
 // m < 16 (c/16 + 1)), publishes it in LDS behind a flag, and every wave applies it to its later blocks:
 // acc_j -= Y_k L_jk^T (chain over the 32 columns of block k), so each element's chain runs over m = 0..32j-1 in
 // order. Waves synchronise only through those per-block flags (bounded waits); each wave prefetches the L and Li
-// operands of step k+1 into registers while it works on step k. The operands come from the transposed copies Lt = L^T
-// and Lit (each 32x32 block of Li transposed), which the Cholesky writes, so 16 lanes read 16 consecutive floats.
+// operands of step k+1 into registers while it works on step k. The operands come packed (store_tile_op), as the
+// Cholesky writes them: each lane reads its 16 values of a block with four 16-byte loads.
 // ---------------------------------------------------------------------------------------------------------------
 constexpr uint32_t FLAG_SPIN_LIMIT = 1u << 22;
 
@@ -909,45 +918,47 @@ struct TrsmOps {
     float l[Q][2][8];    // L_jk B operands: [owned block][column half][kk]
 };
 
-// Li_k B operands (block-lower: kk < 4 (cb + 1)) for the owner of block k
-__device__ __forceinline__ void trsm_fetch_li(float (&li)[2][8], const float* __restrict__ Lit, int nbc, int k, int l16,
-                                              int lk) {
+// the 16 B operands of one packed factor block for this lane: o[cb][kk] (4 x 16-byte loads)
+__device__ __forceinline__ void fetch_op(float (&o)[2][8], const float* __restrict__ Lp, int a, int b, int lane) {
+    const float4* src = reinterpret_cast<const float4*>(Lp + (size_t)op_pair(a, b) * CB * CB + 16 * lane);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const float4 v = src[h];
+        o[h >> 1][4 * (h & 1) + 0] = v.x;
+        o[h >> 1][4 * (h & 1) + 1] = v.y;
+        o[h >> 1][4 * (h & 1) + 2] = v.z;
+        o[h >> 1][4 * (h & 1) + 3] = v.w;
+    }
+}
+
+// Li_k B operands (block-lower: only kk < 4 (cb + 1) are used) for the owner of block k
+__device__ __forceinline__ void trsm_fetch_li(float (&li)[2][8], const float* __restrict__ Lp, int nbc, int k,
+                                              int lane) {
     if (k >= nbc) return;
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-            if (kk < 4 * (cb + 1)) li[cb][kk] = Lit[(size_t)(CB * k + 4 * kk + lk) * CB + 16 * cb + l16];
+    fetch_op(li, Lp, k, k, lane);
 }
 
 template <int Q>
-__device__ __forceinline__ void trsm_fetch(TrsmOps<Q>& o, const float* __restrict__ Lt, const float* __restrict__ Lit,
-                                           int r, int nbc, int k, int w, int l16, int lk) {
+__device__ __forceinline__ void trsm_fetch(TrsmOps<Q>& o, const float* __restrict__ Lp, int nbc, int k, int w,
+                                           int lane) {
     if (k >= nbc) return;
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         const int j = w + 4 * q;
-        if (j > k && j < nbc) {
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-                for (int kk = 0; kk < 8; ++kk)
-                    o.l[q][cb][kk] = Lt[(size_t)(CB * k + 4 * kk + lk) * r + CB * j + 16 * cb + l16];
-        }
+        if (j > k && j < nbc) fetch_op(o.l[q], Lp, j, k, lane);
     }
 }
 
 template <bool PASS1, int Q, int RB>
 __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, int r,
                                               const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
-                                              float eps, const float* __restrict__ Lt, const float* __restrict__ Lit,
-                                              const MatsOut Ys, long ldy, float* scal) {
+                                              float eps, const float* __restrict__ Lp, const MatsOut Ys, long ldy,
+                                              float* scal) {
     extern __shared__ float smem[];
     const float* __restrict__ A = As.p[blockIdx.z];
     float* __restrict__ Y = Ys.p[blockIdx.z];
     amax_part += (size_t)blockIdx.z * AMAX_BLOCKS;
-    Lt += (size_t)blockIdx.z * r * r;
-    Lit += (size_t)blockIdx.z * r * CB;
+    Lp += (size_t)blockIdx.z * (r / CB) * (r / CB + 1) / 2 * CB * CB;
     if (scal != nullptr) scal += (size_t)blockIdx.z * SCAL_STRIDE;
     const int ldsy = r + 4;
     float* sY = smem;                          // [16 RB][r + 4]: finished Y columns (MFMA A operands)
@@ -981,9 +992,9 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
                 }
         }
     TrsmOps<Q> cur, nxt;
-    trsm_fetch<Q>(cur, Lt, Lit, r, nbc, 0, w, l16, lk);
+    trsm_fetch<Q>(cur, Lp, nbc, 0, w, lane);
     float li[2][8];   // Li of this wave's next block to finish (fetched four steps ahead)
-    trsm_fetch_li(li, Lit, nbc, w, l16, lk);
+    trsm_fetch_li(li, Lp, nbc, w, lane);
     __syncthreads();   // flags cleared
     // finish block k (owner only): Y_k = acc_k Li_k^T into sY and Y, then raise its flag
     auto finish = [&](int k, int qk) {
@@ -1011,7 +1022,7 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
             __builtin_amdgcn_wave_barrier();
         }
         if (lane == 0) __hip_atomic_store(&sFlag[k], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        trsm_fetch_li(li, Lit, nbc, k + 4, l16, lk);
+        trsm_fetch_li(li, Lp, nbc, k + 4, lane);
     };
     // acc_j -= Y_k L_jk^T for owned block q
     auto apply = [&](int k, int q) {
@@ -1031,7 +1042,7 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
         for (int ow = 0; ow < 4; ++ow) {
             const int k = 4 * qk + ow;
             if (k < nbc) {
-                trsm_fetch<Q>(nxt, Lt, Lit, r, nbc, k + 1, w, l16, lk);
+                trsm_fetch<Q>(nxt, Lp, nbc, k + 1, w, lane);
                 if (w != ow) {
                     uint32_t n = 0;
                     while (__hip_atomic_load(&sFlag[k], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u) {
@@ -1063,19 +1074,146 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
     }
 }
 
-// Lt = L^T (lower tiles of L, r x r) and Lit = per-32-block transposes of Li (r x 32), for the stage entry point that
-// takes row-major L and Li.
-__global__ __launch_bounds__(256) void k_transpose_factors(const float* __restrict__ L, const float* __restrict__ Li,
-                                                           int r, float* __restrict__ Lt, float* __restrict__ Lit) {
+// Triangular solve with one wavefront per 16 rows (r = 32 NBC <= 256, tall X): the wave takes its rows through the
+// column blocks in order, left-looking: acc_j = A_j - sum_{k<j} Y_k L_jk^T (one MFMA chain per element, k and then m
+// ascending, the order of the blocked solve), then Y_j = acc_j Li_j^T. Its finished blocks stay in registers as MFMA
+// A operands, so waves never wait for each other. The packed L operands stream from L2 three blocks ahead of use
+// (scheduling barriers keep the loads where they are issued), and A one column block ahead. The arithmetic of every
+// element is that of k_trsm.
+template <bool PASS1, int NBC>
+__global__ __launch_bounds__(256) void k_trsm_rows(const MatsIn As, long lda, int K,
+                                                   const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
+                                                   float eps, const float* __restrict__ Lp, const MatsOut Ys,
+                                                   long ldy, float* scal) {
+    constexpr int r = NBC * CB;
+    constexpr int NSTEP = NBC * (NBC + 1) / 2;   // operand blocks in use order: L(j, 0..j-1), then Li_j, per j
+    constexpr int DIST = 3;                       // operand blocks in flight ahead of the one in use
+    __shared__ float sT[4][16][33];   // per-wave transpose of one 16 x 32 block
+    const int z = blockIdx.z;
+    const float* __restrict__ A = As.p[z];
+    float* __restrict__ Y = Ys.p[z];
+    amax_part += (size_t)z * AMAX_BLOCKS;
+    Lp += (size_t)z * NSTEP * CB * CB;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
+    float sc = 1.0f;
+    if (PASS1) {
+        sc = block_scale(amax_part);
+        if (blockIdx.x == 0 && tid == 0 && scal != nullptr) scal[(size_t)z * SCAL_STRIDE] = sc;
+    }
+    const int row0 = (blockIdx.x * 4 + w) * 16;
+    if (row0 >= K) return;           // no workgroup barrier follows
+    float(*st)[33] = sT[w];
+    // rows past K read row K-1 (in bounds) and are zeroed, so every load is unconditional
+    int rowc[4];
+    bool rin[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int row = row0 + 4 * lk + v;
+        rin[v] = row < K;
+        rowc[v] = rin[v] ? row : K - 1;
+    }
+    // packed operand blocks, in use order; block s is consumed at step s and fetched at step s - DIST
+    float ob[DIST + 1][2][8];
+    auto fetch_step = [&](int sidx) {
+        int j = 0;
+        while ((j + 1) * (j + 2) / 2 <= sidx) ++j;
+        const int k = sidx - j * (j + 1) / 2;
+        fetch_op(ob[sidx % (DIST + 1)], Lp, j, k, lane);
+        __builtin_amdgcn_sched_barrier(0);   // keep the prefetch where it is issued (the scheduler would sink it)
+    };
+    // A_j (and Z_j on pass 1) in C layout, one block ahead
+    float xa[2][2][4], za[2][2][4];
+    auto fetch_x = [&](int j, int buf) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int col = CB * j + 16 * cb + l16;
+                xa[buf][cb][v] = A[(size_t)rowc[v] * lda + col];
+                if (PASS1) za[buf][cb][v] = Z[(size_t)rowc[v] * r + col];
+            }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int q = 0; q < DIST; ++q)
+        if (q < NSTEP) fetch_step(q);
+    fetch_x(0, 0);
+    float ya[NBC][8];                 // ya[k][kk] = Y[row0 + l16][32 k + 4 kk + lk]
+    int sidx = 0;
+#pragma unroll
+    for (int j = 0; j < NBC; ++j) {
+        if (j + 1 < NBC) fetch_x(j + 1, (j + 1) & 1);
+        f32x4 acc[2];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                float x = xa[j & 1][cb][v];
+                if (PASS1) x = __builtin_fmaf(eps, za[j & 1][cb][v], sc * x);
+                acc[cb][v] = rin[v] ? x : 0.0f;
+            }
+#pragma unroll
+        for (int k = 0; k < j; ++k) {
+            if (sidx + DIST < NSTEP) fetch_step(sidx + DIST);
+            const float(&o)[2][8] = ob[sidx % (DIST + 1)];
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const float a = -ya[k][kk];
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) acc[cb] = mfma(a, o[cb][kk], acc[cb]);
+            }
+            ++sidx;
+        }
+        if (sidx + DIST < NSTEP) fetch_step(sidx + DIST);
+        const float(&li)[2][8] = ob[sidx % (DIST + 1)];
+        ++sidx;
+        // Y_j = acc_j Li_j^T, acc_j brought to the A-operand layout through LDS
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) st[4 * lk + v][16 * cb + l16] = acc[cb][v];
+        __builtin_amdgcn_wave_barrier();
+        float ar[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) ar[kk] = st[l16][4 * kk + lk];
+        __builtin_amdgcn_wave_barrier();
+        f32x4 y[2];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            y[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk)
+                if (kk < 4 * (cb + 1)) y[cb] = mfma(ar[kk], li[cb][kk], y[cb]);
+        }
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (rin[v]) Y[(size_t)(row0 + 4 * lk + v) * ldy + CB * j + 16 * cb + l16] = y[cb][v];
+                st[4 * lk + v][16 * cb + l16] = y[cb][v];
+            }
+        __builtin_amdgcn_wave_barrier();
+        if (j + 1 < NBC) {
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) ya[j][kk] = st[l16][4 * kk + lk];
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// The packed solve operands (store_tile_op's layout) from row-major L [r, r] and Li [r, 32], for the stage entry
+// point; one thread per packed element.
+__global__ __launch_bounds__(256) void k_pack_factors(const float* __restrict__ L, const float* __restrict__ Li, int r,
+                                                      float* __restrict__ Lp) {
+    const int nb = r / CB, npairs = nb * (nb + 1) / 2;
     const int e = blockIdx.x * 256 + threadIdx.x;
-    if (e < r * r) {
-        const int i = e / r, j = e - i * r;
-        Lt[(size_t)j * r + i] = L[e];
-    }
-    if (e < r * CB) {
-        const int i = e / CB, m = e - i * CB, blk = i / CB, c = i - blk * CB;
-        Lit[(size_t)(blk * CB + m) * CB + c] = Li[e];
-    }
+    if (e >= npairs * CB * CB) return;
+    const int pr = e >> 10, lane = (e >> 4) & 63, cb = (e >> 3) & 1, kk = e & 7;
+    int a = 0;
+    while (op_pair(a + 1, 0) <= pr) ++a;
+    const int b = pr - op_pair(a, 0);
+    const int row = 16 * cb + (lane & 15), col = 4 * kk + (lane >> 4);
+    Lp[e] = (a == b) ? Li[(size_t)(CB * a + row) * CB + col] : L[(size_t)(CB * a + row) * r + CB * b + col];
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1170,11 +1308,13 @@ inline uint64_t mix64(uint64_t z) {
 struct spanqr_plan {
     int K = 0, r = 0, device = 0;
     int batch = 1, chol_bmax = 1;   // matrices per call; matrices per Cholesky launch
+    size_t lp_stride = 0;           // floats of packed factor per matrix
     int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0, trsm_rb = 1;
+    bool trsm_rows = false;   // solve with one wavefront per 16 rows (k_trsm_rows) instead of k_trsm
     size_t bytes = 0;
     char* base = nullptr;
     float *Z = nullptr, *P = nullptr, *G = nullptr, *L = nullptr, *Li = nullptr, *Y0 = nullptr, *Y1 = nullptr;
-    float *Lt = nullptr, *Lit = nullptr;   // L^T and the per-block transposes of Li (solve operands)
+    float* Lp = nullptr;       // the factor as packed solve operands (store_tile_op's layout), per matrix
     float* scal = nullptr;     // s, nrm0, tau0, nrm1, tau1, nrm2, tau2, barrier error (as float bits)
     float* chscal = nullptr;   // per-launch Cholesky scalars (nrm, tau, err)
     double* npart = nullptr;
@@ -1260,19 +1400,16 @@ int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t
         float* A = p->G + z0 * r * r;
         const double* np = p->npart + (size_t)z0 * nnp;
         float* L = p->L + z0 * r * r;
-        float* Lt = p->Lt + z0 * r * r;
         float* Li = p->Li + z0 * r * CB;
-        float* Lit = p->Lit + z0 * r * CB;
+        float* Lp = p->Lp + z0 * p->lp_stride;
         uint32_t* bar = p->bar + (size_t)z0 * BAR_STRIDE;
         uint32_t* flags = p->flags + (size_t)z0 * FLAG_STRIDE;
         float* sc = scal ? scal + (size_t)z0 * SCAL_STRIDE : nullptr;
         const dim3 grid(p->chol_grid, 1, nz);
         if (stamp)
-            k_chol<true><<<grid, 256, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, flags, sc,
-                                                 p->stamps);
+            k_chol<true><<<grid, 256, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps);
         else
-            k_chol<false><<<grid, 256, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lt, Lit, bar, flags, sc,
-                                                  p->stamps);
+            k_chol<false><<<grid, 256, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps);
         HIPCHK(hipGetLastError());
     }
     return SPANQR_OK;
@@ -1304,34 +1441,52 @@ hipError_t trsm_set_lds_plan(int q, int rb, int r) {
 }
 
 template <int Q, int RB>
-void launch_trsm_t(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const float* L,
-                   const float* Li, const MatsOut& Y, long ldy, int n, hipStream_t st) {
+void launch_trsm_t(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const MatsOut& Y, long ldy,
+                   int n, hipStream_t st) {
     const dim3 grid((p->K + 16 * RB - 1) / (16 * RB), 1, n);
     const size_t lds = trsm_lds(p->r, RB);
-    if (pass1) k_trsm<true, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, L, Li, Y, ldy,
+    if (pass1) k_trsm<true, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, p->Lp, Y, ldy,
                                                            p->scal);
-    else k_trsm<false, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, L, Li, Y, ldy,
+    else k_trsm<false, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, p->Lp, Y, ldy,
                                                       p->scal);
 }
 
 template <int Q>
-void launch_trsm_q(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const float* L,
-                   const float* Li, const MatsOut& Y, long ldy, int n, hipStream_t st) {
+void launch_trsm_q(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const MatsOut& Y, long ldy,
+                   int n, hipStream_t st) {
     switch (p->trsm_rb) {
-        case 4: launch_trsm_t<Q, 4>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
-        case 2: launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
-        default: launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
+        case 4: launch_trsm_t<Q, 4>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+        case 2: launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+        default: launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
     }
 }
 
-// Y = A L^-T for the n matrices; L, Li are the plan's transposed factors of matrix 0 (stride r r and r 32)
-void launch_trsm(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const float* L,
-                 const float* Li, const MatsOut& Y, long ldy, int n, hipStream_t st) {
+template <int NBC>
+void launch_trsm_rows(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const MatsOut& Y,
+                      long ldy, int n, hipStream_t st) {
+    const dim3 grid((p->K + 63) / 64, 1, n);
+    if (pass1) k_trsm_rows<true, NBC><<<grid, 256, 0, st>>>(A, lda, p->K, p->amax_part, p->Z, eps, p->Lp, Y, ldy,
+                                                            p->scal);
+    else k_trsm_rows<false, NBC><<<grid, 256, 0, st>>>(A, lda, p->K, p->amax_part, p->Z, eps, p->Lp, Y, ldy, p->scal);
+}
+
+// Y = A L^-T for the n matrices, with the packed factors the plan's Cholesky left in p->Lp
+void launch_trsm(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const MatsOut& Y, long ldy,
+                 int n, hipStream_t st) {
+    if (p->trsm_rows) {
+        switch (p->r / CB) {
+            case 2: launch_trsm_rows<2>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+            case 4: launch_trsm_rows<4>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+            case 6: launch_trsm_rows<6>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+            default: launch_trsm_rows<8>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+        }
+        return;
+    }
     switch (p->trsm_q) {
-        case 1: launch_trsm_q<1>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
-        case 2: launch_trsm_q<2>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
-        case 3: launch_trsm_q<3>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
-        default: launch_trsm_q<4>(p, A, lda, pass1, eps, L, Li, Y, ldy, n, st); break;
+        case 1: launch_trsm_q<1>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+        case 2: launch_trsm_q<2>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+        case 3: launch_trsm_q<3>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+        default: launch_trsm_q<4>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
     }
 }
 
@@ -1369,7 +1524,7 @@ int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut
         if ((rc = mark())) return rc;
         if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U, n))) return rc;
         if ((rc = mark())) return rc;
-        launch_trsm(p, *in, ldin, pass == 0, eps, p->Lt, p->Lit, bout[cur], p->r, n, st);
+        launch_trsm(p, *in, ldin, pass == 0, eps, bout[cur], p->r, n, st);
         if ((rc = mark())) return rc;
         in = &bin[cur];
         ldin = p->r;
@@ -1464,6 +1619,9 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
     p->trsm_q = (r / CB + 3) / 4;
     // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU
     p->trsm_rb = ((K + 15) / 16 >= 2048) ? 4 : ((K + 15) / 16 >= 1024 ? 2 : 1);
+    // one wavefront per 16 rows once there are enough rows to occupy the SIMDs (its per-wave chain over r/32
+    // blocks is long); below that, k_trsm splits each row block's columns over four waves
+    p->trsm_rows = r <= 256 && K >= 4096;
     {
         const size_t need = trsm_lds(r, p->trsm_rb);
         int maxsh = 0;
@@ -1504,12 +1662,14 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
     const size_t nKr = (size_t)K * r * sizeof(float);
     const size_t sz_Z = al(nKr), sz_P = al(B * p->S * p->U * TB * TB * sizeof(float));
     const size_t sz_rr = al(B * r * r * sizeof(float)), sz_Li = al(B * r * CB * sizeof(float));
+    p->lp_stride = (size_t)(r / CB) * (r / CB + 1) / 2 * CB * CB;
+    const size_t sz_Lp = al(B * p->lp_stride * sizeof(float));
     const size_t sz_Y = al(B * nKr), sz_sc = al(B * SCAL_STRIDE * sizeof(float));
     const size_t sz_np = al(B * 16 * p->U * sizeof(double));
     const size_t sz_am = al(B * AMAX_BLOCKS * sizeof(uint32_t)), sz_bar = al(B * BAR_STRIDE * sizeof(uint32_t));
     const size_t sz_st = al(2 * (4 * (512 / CB) + 2) * sizeof(uint64_t));
     const size_t sz_fl = al(B * FLAG_STRIDE * sizeof(uint32_t));
-    p->bytes = sz_Z + sz_P + 3 * sz_rr + 2 * sz_Li + 2 * sz_Y + 2 * sz_sc + sz_np + sz_am + sz_bar + sz_st + sz_fl;
+    p->bytes = sz_Z + sz_P + 2 * sz_rr + sz_Li + sz_Lp + 2 * sz_Y + 2 * sz_sc + sz_np + sz_am + sz_bar + sz_st + sz_fl;
     if (hipMalloc((void**)&p->base, p->bytes) != hipSuccess) {
         const size_t nb = p->bytes;
         delete p;
@@ -1521,8 +1681,7 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
     p->G = (float*)c; c += sz_rr;
     p->L = (float*)c; c += sz_rr;
     p->Li = (float*)c; c += sz_Li;
-    p->Lt = (float*)c; c += sz_rr;
-    p->Lit = (float*)c; c += sz_Li;
+    p->Lp = (float*)c; c += sz_Lp;
     p->Y0 = (float*)c; c += sz_Y;
     p->Y1 = (float*)c; c += sz_Y;
     p->scal = (float*)c; c += sz_sc;
@@ -1536,7 +1695,7 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
     int rc = hz ? spanqr_dust_host(K, r, hz) : fail(SPANQR_ENOMEM, "host dust buffer");
     if (rc == SPANQR_OK) {
         if (hipMemcpy(p->Z, hz, nKr, hipMemcpyHostToDevice) != hipSuccess ||
-            hipMemset(p->L, 0, sz_rr) != hipSuccess || hipMemset(p->Lt, 0, sz_rr) != hipSuccess || hipMemset(p->scal, 0, 2 * sz_sc) != hipSuccess ||
+            hipMemset(p->L, 0, sz_rr) != hipSuccess || hipMemset(p->Lp, 0, sz_Lp) != hipSuccess || hipMemset(p->scal, 0, 2 * sz_sc) != hipSuccess ||
             hipMemset(p->bar, 0, sz_bar) != hipSuccess || hipMemset(p->flags, 0, sz_fl) != hipSuccess ||
             hipDeviceSynchronize() != hipSuccess)
             rc = fail(SPANQR_EHIP, "plan upload failed");
@@ -1650,8 +1809,8 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
             case SPANQR_K_GRAM: launch_gram(p, y0, r, 1, false, false, st); break;
             case SPANQR_K_REDUCE: launch_reduce(p, 0, p->G, 1, st); break;
             case SPANQR_K_CHOL: return launch_chol(p, 1e-7f, 1e-8f, p->scal + 1, st, 16 * p->U, 1);
-            case SPANQR_K_TRSM_PASS1: launch_trsm(p, y0, r, true, 5e-7f, p->Lt, p->Lit, y1, r, 1, st); break;
-            case SPANQR_K_TRSM: launch_trsm(p, y0, r, false, 0.0f, p->Lt, p->Lit, y1, r, 1, st); break;
+            case SPANQR_K_TRSM_PASS1: launch_trsm(p, y0, r, true, 5e-7f, y1, r, 1, st); break;
+            case SPANQR_K_TRSM: launch_trsm(p, y0, r, false, 0.0f, y1, r, 1, st); break;
             case SPANQR_K_NS_APPLY: launch_nsapply(p, y0, r, y1, r, 1, st); break;
         }
         return SPANQR_OK;
@@ -1723,8 +1882,8 @@ int spanqr_stage_trsm(spanqr_plan* p, const float* A, long lda, int pass1, float
     if ((rc = check_mat(p, Y, ldy, "Y"))) return rc;
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
-    k_transpose_factors<<<(p->r * p->r + 255) / 256, 256, 0, st>>>(L, Li, p->r, p->Lt, p->Lit);
-    launch_trsm(p, mats_in(&A, 1), lda, pass1 != 0, eps, p->Lt, p->Lit, mats_out(&Y, 1), ldy, 1, st);
+    k_pack_factors<<<(int)((p->lp_stride + 255) / 256), 256, 0, st>>>(L, Li, p->r, p->Lp);
+    launch_trsm(p, mats_in(&A, 1), lda, pass1 != 0, eps, mats_out(&Y, 1), ldy, 1, st);
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }

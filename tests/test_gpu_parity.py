@@ -102,7 +102,8 @@ def test_chol32_absolute(cuda, K, r):
     assert_bits(Li, Lio, "Li")
 
 
-@pytest.mark.parametrize("K,r", SHAPES + [(16384, 256), (32768, 64)])
+# K >= 4096 (r <= 256) takes the one-wavefront-per-16-rows solve, including ragged K
+@pytest.mark.parametrize("K,r", SHAPES + [(16384, 256), (32768, 64), (4100, 128), (4111, 192)])
 @pytest.mark.parametrize("pass1", [True, False])
 def test_trsm(cuda, K, r, pass1):
     print(f"trsm {K}x{r} pass1={pass1}", flush=True)
@@ -139,7 +140,7 @@ def test_ns_step(cuda, K, r, kahan):
 
 ORTH_CASES = [(256, 64, "mixed_c4"), (256, 128, "zero"), (384, 256, "rank_half"), (768, 512, "ttf_cu4_t1e-2"),
               (768, 512, "dup_cols"), (1024, 256, "huge_1e25"), (1024, 256, "tiny_1e-25"), (2048, 512, "mixed_c8"),
-              (17408, 256, "ttf_cu4_t1e-2")]
+              (17408, 256, "ttf_cu4_t1e-2"), (4100, 192, "mixed_c6")]
 
 
 @pytest.mark.parametrize("K,r,name", ORTH_CASES)
