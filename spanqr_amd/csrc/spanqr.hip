@@ -139,8 +139,8 @@ __global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, 
 
 // ---------------------------------------------------------------------------------------------------------------
 // Gram partials (tri.py:255-297, 324-375): workgroup (u, sp) computes upper 64x64 tile u = (ti, tj) of A^T A over
-// rows [sp*KS, min((sp+1)*KS, K)), in 32-row chunks (rows past the split read as 0). Wave w owns the 32x32 quadrant
-// (w >> 1, w & 1). KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one
+// rows [sp*KS, min((sp+1)*KS, K)), in 32-row chunks staged through LDS (rows past the split read as 0; the next
+// chunk is fetched into registers while this one is multiplied). Wave w owns the 32x32 quadrant (w >> 1, w & 1). KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one
 // chain runs over the whole split. SCALE: operands are s * a with the pass-1 power-of-2 scale.
 // ---------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
@@ -175,23 +175,39 @@ __global__ __launch_bounds__(256) void k_gram(const MatsIn As, long lda, int K, 
         }
     const int k0 = sp * KS;
     const int k1 = (k0 + KS < K) ? k0 + KS : K;
-    for (int kc = k0; kc < k1; kc += BK) {
+    // chunk kc + BK is loaded into registers while chunk kc is multiplied; rows past the split read row k1 - 1
+    // (in bounds) and are zeroed, so the loads are unconditional
+    float4 ra[2], rb[2];
+    auto gload = [&](int kc) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15, k = kc + row;
-            float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (k < k1) {
-                va = *reinterpret_cast<const float4*>(A + (size_t)k * lda + ti * TB + 4 * c4);
-                vb = *reinterpret_cast<const float4*>(A + (size_t)k * lda + tj * TB + 4 * c4);
-            }
+            const int kr = k < k1 ? k : k1 - 1;
+            ra[q] = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + ti * TB + 4 * c4);
+            rb[q] = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + tj * TB + 4 * c4);
+        }
+    };
+    gload(k0);
+    for (int kc = k0; kc < k1; kc += BK) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15;
+            const bool in = kc + row < k1;
+            float4 va = ra[q], vb = rb[q];
             if (SCALE) {
                 va.x = sc * va.x; va.y = sc * va.y; va.z = sc * va.z; va.w = sc * va.w;
                 vb.x = sc * vb.x; vb.y = sc * vb.y; vb.z = sc * vb.z; vb.w = sc * vb.w;
+            }
+            if (!in) {
+                va = make_float4(0.f, 0.f, 0.f, 0.f);
+                vb = make_float4(0.f, 0.f, 0.f, 0.f);
             }
             *reinterpret_cast<float4*>(&sA[row][4 * c4]) = va;
             *reinterpret_cast<float4*>(&sB[row][4 * c4]) = vb;
         }
         __syncthreads();
+        if (kc + BK < k1) gload(kc + BK);
+        __builtin_amdgcn_sched_barrier(0);   // the loads go out before the MFMAs
         f32x4 part[2][2];
 #pragma unroll
         for (int a = 0; a < 2; ++a)
