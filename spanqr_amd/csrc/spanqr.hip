@@ -9,12 +9,15 @@
 //   * the Gram is a split-K SYRK over upper 64x64 tiles with a fixed, shape-derived split count (no CU-count
 //     dependence), Kahan-compensated per 32-row chunk where the reference compensates, and reduced in fp64 in split
 //     order by a separate kernel that also emits fixed-order partials of ||G||_F^2;
-//   * the Cholesky is one persistent, grid-synchronised kernel stepping 64 columns (two 32-wide reference steps) per grid barrier:
-//     workgroup 0 factors the next 64x64 diagonal block (look-ahead) while the others update the trailing 64x64
-//     tiles; the 32x32 diagonal tiles are factored in one wavefront's registers (lane = row) and inverted (lane =
-//     column) as a by-product;
-//   * the triangular solve is row-block parallel (16 rows per workgroup) and right-looking inside the block: each
-//     wavefront owns every 4th 32-column block and applies a finished block to its later blocks with MFMA.
+//   * the Cholesky is one persistent kernel over 32x32 tiles synchronised by per-tile flags (no grid barriers):
+//     workgroup 0 runs the diagonal chain with a two-tile-row look-ahead, each other workgroup keeps one tile row in
+//     LDS; the 32x32 diagonal tiles are factored in one wavefront's registers (lane = row) and inverted (lanes
+//     32-63) in the same pass, and the factor is published both row-major and packed as the solve's MFMA operands;
+//   * the triangular solve is row-block parallel: for tall X one wavefront per 16 rows runs through all column
+//     blocks with its operands streamed ahead (k_trsm_rows); otherwise each of four wavefronts owns every 4th 32-column
+//     block of a row block and applies a finished block to its later blocks with MFMA (k_trsm);
+//   * every kernel takes its matrix of a batch from blockIdx.z (pointer tables passed by value), so a shape group of
+//     layers runs as one launch per stage.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -305,15 +308,17 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 // Clamped Cholesky (chol.cu:115-271): one persistent kernel over 32x32 tiles T(i, k), i >= k, nb = r / 32 tile rows,
 // synchronised by per-tile flags instead of grid barriers.
 //   * Workgroup 0 runs the critical chain. Step j: wave 0 factors T(j, j) and inverts the factor in one pass; at the
-//     same time wave 1 fetches tile row j+2 (T(j+2, j-1..j+2), handed over by its owner through column block j-2)
-//     and brings it through block j-1 (panel L(j+2, j-1) with the previous step's Li_{j-1}, L(j, j-1), L(j+1, j-1)
-//     still in LDS), and wave 2 publishes the previous step's L tiles and Li. Then all waves form the panels
-//     L(j+1, j), L(j+2, j) and apply column block j to T(j+1, j+1), T(j+2, j+1), T(j+2, j+2) (look-ahead over the
-//     next two tile rows).
+//     same time waves 1-2 fetch tile row j+2 (T(j+2, j-1..j+2), handed over by its owner through column block j-2,
+//     plus the owner's panel L(j+2, j-2)) while wave 3 publishes the previous step's L tiles and Li; then wave 1
+//     forms the panel L(j+2, j-1) (the previous step's Li_{j-1}, L(j, j-1), L(j+1, j-1) are still in LDS), wave 2
+//     applies the block j-2 update of T(j+2, j+1) that the owner leaves out, and the three waves apply block j-1 to
+//     T(j+2, j), T(j+2, j+1), T(j+2, j+2), wave 3 publishing L(j+2, j-1). Then all waves form the panels
+//     L(j+1, j), L(j+2, j) and apply column block j to T(j+1, j+1), T(j+2, j+1), T(j+2, j+2) in one phase
+//     (look-ahead over the next two tile rows).
 //   * Workgroup i-3 owns tile row i >= 4 for the whole factorisation, in LDS. For column block j = 0..i-4 in order:
 //     panel L(i, j) = T(i, j) Li_j^T (published), then T(i, k) -= L(i, j) L(k, j)^T for k = j+1..i with the other
-//     rows' panels of block j fetched together; after block i-4 it hands T(i, i-3..i) to workgroup 0, two steps
-//     before workgroup 0 needs them.
+//     rows' panels of block j fetched together (at its last block, j = i-4, T(i, i-1) is left to workgroup 0); after
+//     block i-4 it hands T(i, i-3..i) to workgroup 0, two steps before workgroup 0 factors T(i, i).
 // Every element keeps the reference order: updates by column block in increasing order, each one MFMA chain over the
 // block's 32 columns. A producer publishes with an agent-scope release after its stores; a consumer polls with
 // bounded waits (after SPIN_LIMIT polls it records an error and stops waiting, so the kernel always ends). Each
