@@ -757,21 +757,18 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             const size_t o = (size_t)CB * j;
             store_tile_lower(L + o * r + o, r, z.dl[q], false, lane, 64);
             store_tile(Li + o * CB, CB, z.li[q], lane, 64);
-            store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[q], lane, 64);
-            if (j + 1 < nb) {
-                store_tile(L + (o + CB) * r + o, r, z.P1[q], lane, 64);
-                store_tile_op(Lp + (size_t)op_pair(j + 1, j) * CB * CB, z.P1[q], lane, 64);
-            }
-            if (j + 2 < nb) {
-                store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
-                store_tile_op(Lp + (size_t)op_pair(j + 2, j) * CB * CB, z.P2[q], lane, 64);
-            }
+            if (j + 1 < nb) store_tile(L + (o + CB) * r + o, r, z.P1[q], lane, 64);
+            if (j + 2 < nb) store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
             if (lane == 0) {
                 release();
                 set_flag(flagL + j * nb + j, ep);
                 if (j + 1 < nb) set_flag(flagL + (j + 1) * nb + j, ep);
                 if (j + 2 < nb) set_flag(flagL + (j + 2) * nb + j, ep);
             }
+            // the solve's packed operands: read only by later kernels, so after the release
+            store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[q], lane, 64);
+            if (j + 1 < nb) store_tile_op(Lp + (size_t)op_pair(j + 1, j) * CB * CB, z.P1[q], lane, 64);
+            if (j + 2 < nb) store_tile_op(Lp + (size_t)op_pair(j + 2, j) * CB * CB, z.P2[q], lane, 64);
         };
         for (int j = 0; j < nb; ++j) {
             const int p = j & 1, pp = p ^ 1;
@@ -819,8 +816,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
                         // the owners of rows j+4.. need L(j+2, j-1) for block j-1
                         const size_t o = (size_t)CB * (j - 1);
                         store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
-                        store_tile_op(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], lane, 64);
                         if (lane == 0) publish_flag(flagL + (j + 2) * nb + j - 1, ep);
+                        store_tile_op(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], lane, 64);
                     }
                 }
             }
@@ -878,11 +875,11 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             __syncthreads();
             panel32(rt[j], rt[j], lij);
             store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j]);
-            store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j]);
             // publish L(i, j) before waiting on the other rows (so no row waits on a chain of rows)
             __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
             __syncthreads();
             if (tid == 0) publish_flag(flagL + i * nb + j, ep);
+            store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j]);   // for later kernels only
             // block j's panels of the rows between: L(k, j), k = j+1..i-1, all fetched before the updates. At the
             // last block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed.
             const int kend = (j + 4 == i) ? i - 1 : i;
