@@ -552,7 +552,8 @@ __device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Til
 // update D_ik -= l_i l_k and the inverse's forward substitution acc_k -= L_kc x_c, each element's chain in column
 // order. Only lane c+1's diagonal is on the critical path: that lane forms its next pivot from its own l (the same
 // fma as the update) and takes the reciprocal square root itself; q crosses lanes once, by v_readlane. The other l_k
-// are broadcast through LDS, alternating between two buffers (bl0, bl1) so that no barrier is needed: the compiler
+// are broadcast through LDS (96 floats each: lane i writes at 30 - c + i, so the l_k in use, k >= c + 2, start at the
+// aligned bl + 32), alternating between two buffers (bl0, bl1) so that no barrier is needed: the compiler
 // may interleave a column's update with the next pivot's chain. No lane-dependent selects: their masks would all be
 // hoisted and spilled. Writes the factor to dl (the upper triangle is left unspecified: publishers zero it) and the
 // inverse to Li.
@@ -579,14 +580,18 @@ __device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, 
             const float qn = readlane(rsqrt_sw(pn), c + 1);
             R[c + 1] = __builtin_fmaf(-own, readlane(own, c + 1), R[c + 1]);
             if (c + 2 < CB) {
-                bl[lane] = own;
+                // l_k lands at bl[32 + k - (c + 2)], so the values in use start 16-byte aligned at bl + 32
+                bl[30 - c + lane] = own;
+                const float* lk = bl + 32;
 #pragma unroll
-                for (int k0 = (c + 2) & ~3; k0 < CB; k0 += 4) {
-                    const float4 l4 = *reinterpret_cast<const float4*>(&bl[k0]);
+                for (int kq = 0; 4 * kq < CB - 2 - c; ++kq) {
+                    const float4 l4 = *reinterpret_cast<const float4*>(&lk[4 * kq]);
                     const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        if (k0 + t > c + 1) R[k0 + t] = __builtin_fmaf(-own, lv[t], R[k0 + t]);
+                    for (int t = 0; t < 4; ++t) {
+                        const int k = c + 2 + 4 * kq + t;
+                        if (k < CB) R[k] = __builtin_fmaf(-own, lv[t], R[k]);
+                    }
                 }
             }
             piv = readlane(pn, c + 1);
@@ -706,8 +711,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     bool dead = false;
     if (STAMP && b == 0 && tid == 0) stamps[0] = wall_clock64();
     const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
-    // misc: [0..2] nrm, shift, tau; [4..5] wave-group barrier counters; [32..95] and [128..191] tile-factor
-    // broadcast buffers; [96..127] the tile factor's diagonal
+    // misc: [0..2] nrm, shift, tau; [4..5] wave-group barrier counters; [32..63] the tile factor's diagonal;
+    // [64..159] and [160..255] tile-factor broadcast buffers
     float* misc = reinterpret_cast<float*>(chol_lds);
     Tile* tiles = reinterpret_cast<Tile*>(misc + 256);
     if (w == 0) {
@@ -731,9 +736,9 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     }
     __syncthreads();
     const float shift = misc[1], tau = misc[2];
-    float* bl0 = misc + 32;
-    float* bl1 = misc + 128;
-    float* pq = misc + 96;
+    float* pq = misc + 32;
+    float* bl0 = misc + 64;
+    float* bl1 = misc + 160;
 
     if (b == 0) {
         if (tid == 0 && scal != nullptr) {
