@@ -8,7 +8,8 @@
  * Conventions
  *   - Matrices are row-major fp32 in device memory; X and Q need 16-byte alignment and a leading dimension that is a
  *     multiple of 4 (the contiguous [K, r] case always qualifies). X is never written.
- *   - r must be a multiple of 64, 64 <= r <= 512, and K >= r.
+ *   - r must be a multiple of 64 with 64 <= r <= 512, or a multiple of 256 with 512 < r <= 4096 (the column-blocked
+ *     path: block Gram-Schmidt over 256-column blocks, as the reference's orth does above 512 columns); K >= r.
  *   - Every entry point that takes a stream only enqueues work on it: no host synchronisation, no allocation, so a
  *     call can be captured into a hipGraph. Plan creation allocates and synchronises.
  *   - Return value 0 means success; a negative value is an error whose message spanqr_last_error() returns (per
@@ -30,6 +31,9 @@ typedef struct spanqr_plan spanqr_plan;
 /* Most matrices one spanqr_orth_batched_f32 call takes. */
 #define SPANQR_MAX_BATCH 32
 
+/* Widest X a plan takes: above 512 columns (a multiple of 256) the plan is column-blocked (see spanqr_plan_create). */
+#define SPANQR_MAX_R 4096
+
 enum {
     SPANQR_OK = 0,
     SPANQR_EINVAL = -1,     /* bad argument (shape, alignment, null pointer) */
@@ -48,12 +52,16 @@ enum {
     SPANQR_Q_DEVICE = 6,
     SPANQR_Q_BATCH = 7,          /* matrices per call the plan holds workspace for */
     SPANQR_Q_CHOL_BATCH = 8,     /* matrices per Cholesky launch (all their workgroups fit on the device at once) */
+    SPANQR_Q_BLOCKS = 9,         /* 256-column blocks of a column-blocked plan (r > 512); 0 otherwise */
 };
 
 /* Create a plan for X [K, r] on HIP device `device` (allocates the workspace and uploads the dust matrix).
  * Replaces the per-call allocations and module-level caches of the reference: the dust cache _Z
  * (candidates/kcholqr.py:26, :83-89), chol32's G clone / L / Li / barrier (candidates/kchol.py:12-18, :40-42) and the
- * Gram partials (candidates/tri.py:371). */
+ * Gram partials (candidates/tri.py:371). For r > 512 the plan is column-blocked (borth, candidates/kbig.py:69-95,
+ * called from orth.py:18-19 with 256-column blocks): it holds the plan of one 256-column block, the K x r dust whose
+ * column slices the blocks use (_ZB, kbig.py:76-83) and the projection's buffers; such a plan runs spanqr_orth_f32
+ * only (the stage, profiling and batched entry points return SPANQR_EINVAL for it). */
 int spanqr_plan_create(int K, int r, int device, spanqr_plan** out);
 
 /* Plan for up to `batch` (1..SPANQR_MAX_BATCH) matrices [K, r] per call (spanqr_orth_batched_f32): one workspace
@@ -63,8 +71,11 @@ void spanqr_plan_destroy(spanqr_plan* plan);
 long spanqr_plan_query(const spanqr_plan* plan, int what);
 
 /* Q = orth(X) with the reference's keyword arguments (defaults eps 5e-7, alpha 1e-7, tau 1e-8, ns 2).
- * Replaces orth (orth.py:13-20, the r <= 512 branch) -> kcholqr_f (candidates/kcholqr.py:92-112). stream: a
- * hipStream_t (torch.cuda.current_stream().cuda_stream on ROCm), 0 for the null stream. */
+ * Replaces orth (orth.py:13-20): for r <= 512 kcholqr_f (candidates/kcholqr.py:92-112); on a column-blocked plan
+ * borth(X, 256) (candidates/kbig.py:69-95): per 256-column block, W = s X_blk (s of the whole X), twice
+ * W -= P (P^T W) against the finished columns P, the kcholf recipe on W with the block's dust slice (kbig.py:50-63),
+ * then once more W -= P (P^T W) and the recipe again. stream: a hipStream_t (torch.cuda.current_stream().cuda_stream
+ * on ROCm), 0 for the null stream. */
 int spanqr_orth_f32(spanqr_plan* plan, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
                     float tau, int ns, void* stream);
 

@@ -3,11 +3,9 @@
 TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, and
 only to check or time the CPU restatement; the product (spanqr_amd, orth.py) never imports it.
 
-Two restatements of candidates/kcholqr.py:92-112 live here:
-  * kcholf_oracle.c (loaded below through ctypes): the bit-exact restatement. It fixes the order of every
-    floating-point operation, and the HIP kernels follow the same order, so GPU results are compared bit for bit.
-  * torch_path.py: a vectorised pure-PyTorch CPU restatement (BLAS summation order, so it agrees with the C oracle
-    to rounding, not bitwise). It is the "pure-PyTorch CPU path" timed as a CPU baseline.
+kcholf_oracle.c (loaded below through ctypes) restates candidates/kcholqr.py:92-112 (kcholqr_f) and
+candidates/kbig.py:69-95 (borth, the r > 512 branch of orth.py:18-19) bit-exactly: it fixes the order of every
+floating-point operation, and the HIP kernels follow the same order, so GPU results are compared bit for bit.
 
 Arrays are numpy, row-major, float32 unless stated.
 """
@@ -58,6 +56,13 @@ def _bind(L):
     L.spqo_ns_apply.argtypes = [_f32p, c_long, c_int, c_int, _f32p, _f32p, c_long]
     L.spqo_orth.argtypes = [_f32p, c_long, c_int, c_int, c_int, c_float, c_float, c_float, c_int, _f32p, c_long,
                             _vp, _vp, _vp, _vp, _vp]
+    L.spqo_orth_dust.argtypes = [_f32p, c_long, c_int, c_int, c_int, c_float, c_float, c_float, c_int, _vp, c_long,
+                                 _f32p, c_long]
+    L.spqo_split_rows.argtypes = [c_int, c_int]
+    L.spqo_split_rows.restype = c_int
+    L.spqo_xgram.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, _f32p]
+    L.spqo_project.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, _f32p, c_long]
+    L.spqo_borth.argtypes = [_f32p, c_long, c_int, c_int, c_float, c_float, c_float, c_int, _f32p, c_long]
     return L
 
 
@@ -220,3 +225,54 @@ def orth(X, KS, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2, stages=False):
     if not stages:
         return Q
     return Q, dict(G=Gs, L=Ls, Li=Lis, Y=Ys, s=sc[0], nrm=sc[1::2].copy(), tau=sc[2::2].copy())
+
+
+def orth_dust(X, Z, KS, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
+    """kcholqr_f with the dust Z [K, r] given (kbig.py:48-63, _kf); Z may be a column slice of a wider dust"""
+    X = _c32(X)
+    K, r = X.shape
+    Z = np.asarray(Z, np.float32)
+    assert Z.shape == (K, r) and Z.strides[1] == 4
+    Q = np.empty((K, r), np.float32)
+    lib().spqo_orth_dust(X, r, K, r, KS, float(np.float32(eps)), float(np.float32(alpha)), float(np.float32(tau)), ns,
+                         Z.ctypes.data_as(ctypes.c_void_p), Z.strides[0] // 4, Q, r)
+    return Q
+
+
+# ---- column-blocked path (kbig.py:69-95) ----
+
+BW = 256   # borth block width (orth.py:19)
+
+
+def split_rows(K, U):
+    """rows per split of a split-K product with U 64x64 output tiles (the Gram's rule; a function of (K, U) only)"""
+    return lib().spqo_split_rows(K, U)
+
+
+def xgram(P, C, KS):
+    """T = P^T C for P [K, j], C [K, 256]: fp32 chains per split of KS rows, fp64 across splits"""
+    P, C = _c32(P), _c32(C)
+    K, j = P.shape
+    assert C.shape == (K, BW)
+    T = np.empty((j, BW), np.float32)
+    lib().spqo_xgram(_ptr(P), j, K, j, _ptr(C), BW, KS, T)
+    return T
+
+
+def project(P, C, KS):
+    """C - P (P^T C) (kbig.py:88-89)"""
+    P, C = _c32(P), _c32(C)
+    K, j = P.shape
+    Out = np.empty((K, BW), np.float32)
+    lib().spqo_project(_ptr(P), j, K, j, _ptr(C), BW, KS, Out, BW)
+    return Out
+
+
+def borth(X, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
+    """Q = borth(X, 256) with reorthogonalisation (kbig.py:69-95), r a multiple of 256"""
+    X = _c32(X)
+    K, r = X.shape
+    assert r % BW == 0
+    Q = np.empty((K, r), np.float32)
+    lib().spqo_borth(X, r, K, r, float(np.float32(eps)), float(np.float32(alpha)), float(np.float32(tau)), ns, Q, r)
+    return Q

@@ -5,7 +5,8 @@
  * __graft_entry__.py and the cpu_baseline leg of bench.py may load it. The product never links or calls it.
  *
  * What it restates (reference file:line):
- *   orth                        orth.py:13-20 (r <= 512 branch)
+ *   orth                        orth.py:13-20 (both branches)
+ *   borth                       candidates/kbig.py:69-95 (256-column blocks, orth.py:18-19), _kf at kbig.py:48-63
  *   kcholqr_f                   candidates/kcholqr.py:92-112
  *   _pow2_scale                 candidates/kcholqr.py:29-30  (with vector_norm(X, inf) at :102)
  *   _zdust                      candidates/kcholqr.py:83-89  (own generator, see spqo_dust)
@@ -27,6 +28,8 @@
  *     with a triangular tile inverse skip the 16-column groups above the diagonal block (exact zeros);
  *   - the pivot reciprocal square root is a software rsqrt (bit trick + 3 Newton steps) instead of CUDA's rsqrtf;
  *   - ||G||_F sums squares in fp64 in a fixed tree order;
+ *   - borth's projections P (P^T W) are a split product P^T W (fp32 fmaf chains per split of rows, fp64 across
+ *     splits in split order, the Gram's split rule) followed by one fmaf chain per element of P T, subtracted once;
  *   - the dust matrix comes from this project's own seeded counter-based generator (the reference's torch CUDA
  *     Philox stream cannot be reproduced off an NVIDIA GPU).
  */
@@ -338,8 +341,8 @@ void spqo_chol(float* A, int r, float tau, float* L, float* Li) {
 /* (tri.py:391-395). Block j: acc[c] = a[32j + c]; acc[c] = fmaf(-y[m], L[32j + c][m], acc[c]) for m = 0..32j-1  */
 /* in order; y[32j + c] = fmaf chain over m' < mend(c) from +0 of acc[m'] * Li[32j + c][m'] (tri.py:396-402).   */
 /* ------------------------------------------------------------------------------------------------------------ */
-void spqo_trsm(const float* X, long ldx, int K, int r, float s, int pass1, const float* Z, float eps,
-               const float* L, const float* Li, float* Y, long ldy) {
+static void trsm_z(const float* X, long ldx, int K, int r, float s, int pass1, const float* Z, long ldz, float eps,
+                   const float* L, const float* Li, float* Y, long ldy) {
     const int nb = r / CB;
     #pragma omp parallel for schedule(static)
     for (int k = 0; k < K; ++k) {
@@ -349,7 +352,7 @@ void spqo_trsm(const float* X, long ldx, int K, int r, float s, int pass1, const
         for (int j = 0; j < nb; ++j) {
             for (int c = 0; c < CB; ++c) {
                 float x = X[(size_t)k * ldx + j * CB + c];
-                acc[c] = pass1 ? fmaf(eps, Z[(size_t)k * r + j * CB + c], s * x) : x;
+                acc[c] = pass1 ? fmaf(eps, Z[(size_t)k * ldz + j * CB + c], s * x) : x;
             }
             for (int m = 0; m < j * CB; ++m) {
                 const float ym = -y[m];
@@ -364,6 +367,11 @@ void spqo_trsm(const float* X, long ldx, int K, int r, float s, int pass1, const
             }
         }
     }
+}
+
+void spqo_trsm(const float* X, long ldx, int K, int r, float s, int pass1, const float* Z, float eps,
+               const float* L, const float* Li, float* Y, long ldy) {
+    trsm_z(X, ldx, K, r, s, pass1, Z, r, eps, L, Li, Y, ldy);
 }
 
 /* ------------------------------------------------------------------------------------------------------------ */
@@ -397,8 +405,11 @@ void spqo_ns_apply(const float* Y, long ldy, int K, int r, const float* D, float
 /* Optional stage outputs (NULL to skip): Gs/Ls/Lis/Ys hold pass p at offset p*r*r, p*r*r, p*r*32, p*K*r;      */
 /* scal[0..] = s, then nrm and tau for passes 0..2.                                                          */
 /* ------------------------------------------------------------------------------------------------------------ */
-void spqo_orth(const float* X, long ldx, int K, int r, int KS, float eps, float alpha, float tau_rel, int ns,
-               float* Q, long ldq, float* Gs, float* Ls, float* Lis, float* Ys, float* scal) {
+/* Zx: the dust (row stride ldz) when given, else this shape's own (spqo_dust(K, r)) -- borth passes each block its
+ * column slice of a K x r dust (kbig.py:48-49, :80-82). */
+static void orth_z(const float* X, long ldx, int K, int r, int KS, float eps, float alpha, float tau_rel, int ns,
+                   float* Q, long ldq, float* Gs, float* Ls, float* Lis, float* Ys, float* scal, const float* Zx,
+                   long ldz) {
     fp_env();
     const int nt = r / TB, U = nt * (nt + 1) / 2;
     const float s = spqo_pow2_scale(spqo_amax(X, ldx, K, r));
@@ -409,7 +420,11 @@ void spqo_orth(const float* X, long ldx, int K, int r, int KS, float eps, float 
     float* Ya = (float*)malloc((size_t)K * r * sizeof(float));
     float* Yb = (float*)malloc((size_t)K * r * sizeof(float));
     double* np = (double*)malloc((size_t)U * 16 * sizeof(double));
-    spqo_dust(K, r, Z);
+    if (Zx == NULL) {
+        spqo_dust(K, r, Z);
+        Zx = Z;
+        ldz = r;
+    }
     if (scal) scal[0] = s;
     const float* in = X;
     long ldin = ldx;
@@ -423,7 +438,7 @@ void spqo_orth(const float* X, long ldx, int K, int r, int KS, float eps, float 
         spqo_chol(G, r, tau, L, Li);
         if (Ls) memcpy(Ls + (size_t)p * r * r, L, (size_t)r * r * sizeof(float));
         if (Lis) memcpy(Lis + (size_t)p * r * CB, Li, (size_t)r * CB * sizeof(float));
-        spqo_trsm(in, ldin, K, r, s, p == 0, Z, eps, L, Li, out, r);
+        trsm_z(in, ldin, K, r, s, p == 0, Zx, ldz, eps, L, Li, out, r);
         if (Ys) memcpy(Ys + (size_t)p * K * r, out, (size_t)K * r * sizeof(float));
         in = out; ldin = r;
         out = (out == Ya) ? Yb : Ya;
@@ -437,4 +452,112 @@ void spqo_orth(const float* X, long ldx, int K, int r, int KS, float eps, float 
     if (ns == 0)
         for (int k = 0; k < K; ++k) memcpy(Q + (size_t)k * ldq, in + (size_t)k * r, (size_t)r * sizeof(float));
     free(Z); free(G); free(L); free(Li); free(Ya); free(Yb); free(np);
+}
+
+void spqo_orth(const float* X, long ldx, int K, int r, int KS, float eps, float alpha, float tau_rel, int ns,
+               float* Q, long ldq, float* Gs, float* Ls, float* Lis, float* Ys, float* scal) {
+    orth_z(X, ldx, K, r, KS, eps, alpha, tau_rel, ns, Q, ldq, Gs, Ls, Lis, Ys, scal, NULL, 0);
+}
+
+/* kcholqr_f with the dust given (_kf, kbig.py:48-63): Z [K, r] with row stride ldz */
+void spqo_orth_dust(const float* X, long ldx, int K, int r, int KS, float eps, float alpha, float tau_rel, int ns,
+                    const float* Z, long ldz, float* Q, long ldq) {
+    orth_z(X, ldx, K, r, KS, eps, alpha, tau_rel, ns, Q, ldq, NULL, NULL, NULL, NULL, NULL, Z, ldz);
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* Gram split rule (the reference leaves it to tri.py's grid): for U output tiles, S = ceil(512 / U) splits,     */
+/* capped at ceil(K / 128) (at least 4 chunks of 32 rows each) and at least 1; KS = ceil(K / S) rounded up to a  */
+/* multiple of 32. Returns KS (the number of splits is then ceil(K / KS)). A function of (K, U) only.          */
+/* ------------------------------------------------------------------------------------------------------------ */
+int spqo_split_rows(int K, int U) {
+    int S = (512 + U - 1) / U;
+    const int cap = (K + 4 * BK - 1) / (4 * BK);
+    if (S > cap) S = cap;
+    if (S < 1) S = 1;
+    return ((K + S - 1) / S + BK - 1) / BK * BK;
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* borth's projection (kbig.py:88-89, :91): Out = C - P (P^T C) for P [K, j] and C [K, 256].                    */
+/* T = P^T C over 64x64 tiles: per split of KS rows, per element, an fmaf chain over the split's rows in order    */
+/* from +0 (rows past K read as 0); T[i][c] = fp32(((0.0 + T_0) + T_1) + ... ) in fp64, split order. Then        */
+/* Out[k][c] = C[k][c] - (fmaf chain over m = 0..j-1 from +0 of P[k][m] * T[m][c]). Out may be C.               */
+/* ------------------------------------------------------------------------------------------------------------ */
+#define BWID 256   /* borth block width (orth.py:19 calls borth(X, 256)) */
+
+void spqo_xgram(const float* P, long ldp, int K, int j, const float* C, long ldc, int KS, float* T) {
+    fp_env();
+    const int S = spqo_gram_splits(K, KS);
+    double* sum = (double*)calloc((size_t)j * BWID, sizeof(double));
+    float* part = (float*)malloc((size_t)j * BWID * sizeof(float));
+    for (int sp = 0; sp < S; ++sp) {
+        const int k0 = sp * KS, k1 = (k0 + KS < K) ? k0 + KS : K;
+        #pragma omp parallel for schedule(static)
+        for (int i = 0; i < j; ++i) {
+            fp_env();
+            float* a = part + (size_t)i * BWID;
+            for (int c = 0; c < BWID; ++c) a[c] = 0.0f;
+            for (int k = k0; k < k1; ++k) {
+                const float pk = P[(size_t)k * ldp + i];
+                for (int c = 0; c < BWID; ++c)
+                    a[c] = fmaf(pk, PLANTED(11) ? C[(size_t)k * ldc + i % BWID] : C[(size_t)k * ldc + c], a[c]);   /* 11 */
+            }
+            for (int c = 0; c < BWID; ++c) sum[(size_t)i * BWID + c] = sum[(size_t)i * BWID + c] + (double)a[c];
+        }
+    }
+    for (size_t e = 0; e < (size_t)j * BWID; ++e) T[e] = (float)sum[e];
+    free(sum); free(part);
+}
+
+void spqo_project(const float* P, long ldp, int K, int j, const float* C, long ldc, int KS, float* Out, long ldo) {
+    float* T = (float*)malloc((size_t)j * BWID * sizeof(float));
+    spqo_xgram(P, ldp, K, j, C, ldc, KS, T);
+    #pragma omp parallel for schedule(static)
+    for (int k = 0; k < K; ++k) {
+        fp_env();
+        float acc[BWID];
+        for (int c = 0; c < BWID; ++c) acc[c] = 0.0f;
+        for (int m = 0; m < j; ++m) {
+            const float pm = P[(size_t)k * ldp + m];
+            for (int c = 0; c < BWID; ++c) acc[c] = fmaf(pm, T[(size_t)m * BWID + c], acc[c]);
+        }
+        for (int c = 0; c < BWID; ++c)
+            Out[(size_t)k * ldo + c] = PLANTED(12) ? C[(size_t)k * ldc + c] + acc[c] : C[(size_t)k * ldc + c] - acc[c];   /* 12 */
+    }
+    free(T);
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* borth (kbig.py:69-95 with b = 256, reorth): s = _pow2_scale(max |X|) of the whole X (kbig.py:85); dust Zf =     */
+/* spqo_dust(K, r), block jb using columns 256 jb.. of it. Per block j: W = fp32(s * X[:, j:j+256]); for j > 0    */
+/* W = project(W) twice; Q_j = orth_z(W, dust slice) (_kf = kcholqr_f with the dust given, kbig.py:48-63); for    */
+/* j > 0 W = project(Q_j), Q_j = orth_z(W, dust slice). P = Q[:, :j], the finished blocks. Every orth_z uses the  */
+/* 256-column split rule; every projection the rule for its (j / 64) * 4 tiles.                                  */
+/* ------------------------------------------------------------------------------------------------------------ */
+void spqo_borth(const float* X, long ldx, int K, int r, float eps, float alpha, float tau_rel, int ns, float* Q,
+                long ldq) {
+    fp_env();
+    const float s = spqo_pow2_scale(spqo_amax(X, ldx, K, r));
+    float* Zf = (float*)malloc((size_t)K * r * sizeof(float));
+    float* W = (float*)malloc((size_t)K * BWID * sizeof(float));
+    spqo_dust(K, r, Zf);
+    const int KSb = spqo_split_rows(K, (BWID / TB) * (BWID / TB + 1) / 2);
+    for (int j = 0; j < r; j += BWID) {
+        const int KSp = j > 0 ? spqo_split_rows(K, (j / TB) * (BWID / TB)) : 0;
+        float* Qj = Q + j;
+        const float* Zj = Zf + (PLANTED(13) ? 0 : j);   /* 13: every block gets the first dust slice */
+        for (int k = 0; k < K; ++k)
+            for (int c = 0; c < BWID; ++c) W[(size_t)k * BWID + c] = s * X[(size_t)k * ldx + j + c];
+        if (j > 0) {
+            spqo_project(Q, ldq, K, j, W, BWID, KSp, W, BWID);
+            if (!PLANTED(14)) spqo_project(Q, ldq, K, j, W, BWID, KSp, W, BWID);   /* 14: projected once */
+        }
+        orth_z(W, BWID, K, BWID, KSb, eps, alpha, tau_rel, ns, Qj, ldq, NULL, NULL, NULL, NULL, NULL, Zj, r);
+        if (j > 0) {
+            spqo_project(Q, ldq, K, j, Qj, ldq, KSp, W, BWID);
+            orth_z(W, BWID, K, BWID, KSb, eps, alpha, tau_rel, ns, Qj, ldq, NULL, NULL, NULL, NULL, NULL, Zj, r);
+        }
+    }
+    free(Zf); free(W);
 }

@@ -18,8 +18,9 @@ HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 # plan queries (include/spanqr.h)
-Q_K, Q_R, Q_SPLITS, Q_SPLIT_ROWS, Q_CHOL_GRID, Q_WORKSPACE_MB, Q_DEVICE, Q_BATCH, Q_CHOL_BATCH = range(9)
+Q_K, Q_R, Q_SPLITS, Q_SPLIT_ROWS, Q_CHOL_GRID, Q_WORKSPACE_MB, Q_DEVICE, Q_BATCH, Q_CHOL_BATCH, Q_BLOCKS = range(10)
 MAX_BATCH = 32   # SPANQR_MAX_BATCH
+MAX_R = 4096     # SPANQR_MAX_R
 # kernels for spanqr_profile_kernel
 K_AMAX, K_GRAM_PASS1, K_GRAM, K_REDUCE, K_CHOL, K_TRSM_PASS1, K_TRSM, K_NS_APPLY = range(8)
 

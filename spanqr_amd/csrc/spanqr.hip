@@ -153,15 +153,25 @@ __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
     tj = t + rem;
 }
 
-template <bool KAHAN, bool SCALE>
+// CROSS: partials of A^T B instead (the block projection of the column-blocked path, kbig.py:88-89): every tile
+// u = ti * ntb + tj of the (columns of A) x (ntb * 64 columns of B) product, A's panel ti against B's panel tj.
+template <bool KAHAN, bool SCALE, bool CROSS = false>
 __global__ __launch_bounds__(256) void k_gram(const MatsIn As, long lda, int K, int nt, int KS,
-                                              const uint32_t* __restrict__ amax_part, float* __restrict__ P) {
+                                              const uint32_t* __restrict__ amax_part, float* __restrict__ P,
+                                              const float* __restrict__ Bx = nullptr, long ldb = 0, int ntb = 0) {
     const int u = blockIdx.x, sp = blockIdx.y, U = gridDim.x;
     const float* __restrict__ A = As.p[blockIdx.z];
     amax_part += (size_t)blockIdx.z * AMAX_BLOCKS;
     P += (size_t)blockIdx.z * gridDim.y * U * TB * TB;
     int ti, tj;
-    upper_tile(u, nt, ti, tj);
+    if (CROSS) {
+        ti = u / ntb;
+        tj = u - ti * ntb;
+    } else {
+        upper_tile(u, nt, ti, tj);
+    }
+    const float* __restrict__ B = CROSS ? Bx : A;
+    const long ldbb = CROSS ? ldb : lda;
     float sc = 1.0f;
     if (SCALE) sc = block_scale(amax_part);
     __shared__ float sA[BK][TB + 16];
@@ -187,7 +197,7 @@ __global__ __launch_bounds__(256) void k_gram(const MatsIn As, long lda, int K, 
             const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15, k = kc + row;
             const int kr = k < k1 ? k : k1 - 1;
             ra[q] = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + ti * TB + 4 * c4);
-            rb[q] = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + tj * TB + 4 * c4);
+            rb[q] = *reinterpret_cast<const float4*>(B + (size_t)kr * ldbb + tj * TB + 4 * c4);
         }
     };
     gload(k0);
@@ -260,15 +270,22 @@ __global__ __launch_bounds__(256) void k_gram(const MatsIn As, long lda, int K, 
 // shift-down tree, the four rows added in order, off-diagonal tiles doubled. MODE 1 writes D = fp32(I - G) * 0.5
 // for the Newton-Schulz step (kcholqr.py:21).
 // ---------------------------------------------------------------------------------------------------------------
+// MODE 2 (the block projection): tile u = ti * nt + tj of a full (not symmetric) product, written once into G with
+// row stride r; no norm partials.
 template <int MODE>
 __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int S, int nt, int r,
                                                 float* __restrict__ G, double* __restrict__ npart) {
     const int b = blockIdx.x, u = blockIdx.y, U = gridDim.y;
     P += (size_t)blockIdx.z * S * U * TB * TB;
     G += (size_t)blockIdx.z * r * r;
-    npart += (size_t)blockIdx.z * 16 * U;
+    if (MODE != 2) npart += (size_t)blockIdx.z * 16 * U;
     int ti, tj;
-    upper_tile(u, nt, ti, tj);
+    if (MODE == 2) {
+        ti = u / nt;
+        tj = u - ti * nt;
+    } else {
+        upper_tile(u, nt, ti, tj);
+    }
     const int t = threadIdx.x, row = 4 * b + (t >> 6), col = t & 63;
     const float* p = P + (size_t)u * TB * TB + row * TB + col;
     const size_t stride = (size_t)U * TB * TB;
@@ -297,10 +314,12 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
             const double tot = ((sw[0] + sw[1]) + sw[2]) + sw[3];
             npart[u * 16 + b] = (ti == tj) ? tot : 2.0 * tot;
         }
-    } else {
+    } else if (MODE == 1) {
         const float d = ((gi == gj ? 1.0f : 0.0f) - g) * 0.5f;
         G[(size_t)gi * r + gj] = d;
         if (ti != tj) G[(size_t)gj * r + gi] = d;
+    } else {
+        G[(size_t)gi * r + gj] = g;
     }
 }
 
@@ -975,7 +994,8 @@ __device__ __forceinline__ void trsm_fetch(TrsmOps<Q>& o, const float* __restric
 template <bool PASS1, int Q, int RB>
 __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, int r,
                                               const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
-                                              float eps, const float* __restrict__ Lp, const MatsOut Ys, long ldy,
+                                              long ldz, float eps, const float* __restrict__ Lp, const MatsOut Ys,
+                                              long ldy,
                                               float* scal) {
     extern __shared__ float smem[];
     const float* __restrict__ A = As.p[blockIdx.z];
@@ -1009,7 +1029,7 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
                     float x = 0.0f;
                     if (j < nbc && row < K) {
                         x = A[(size_t)row * lda + col];
-                        if (PASS1) x = __builtin_fmaf(eps, Z[(size_t)row * r + col], sc * x);
+                        if (PASS1) x = __builtin_fmaf(eps, Z[(size_t)row * ldz + col], sc * x);
                     }
                     acc[rb][q][cb][v] = x;
                 }
@@ -1106,7 +1126,7 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
 template <bool PASS1, int NBC>
 __global__ __launch_bounds__(256) void k_trsm_rows(const MatsIn As, long lda, int K,
                                                    const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
-                                                   float eps, const float* __restrict__ Lp, const MatsOut Ys,
+                                                   long ldz, float eps, const float* __restrict__ Lp, const MatsOut Ys,
                                                    long ldy, float* scal) {
     constexpr int r = NBC * CB;
     constexpr int NSTEP = NBC * (NBC + 1) / 2;   // operand blocks in use order: L(j, 0..j-1), then Li_j, per j
@@ -1153,7 +1173,7 @@ __global__ __launch_bounds__(256) void k_trsm_rows(const MatsIn As, long lda, in
             for (int v = 0; v < 4; ++v) {
                 const int col = CB * j + 16 * cb + l16;
                 xa[buf][cb][v] = A[(size_t)rowc[v] * lda + col];
-                if (PASS1) za[buf][cb][v] = Z[(size_t)rowc[v] * r + col];
+                if (PASS1) za[buf][cb][v] = Z[(size_t)rowc[v] * ldz + col];
             }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -1243,11 +1263,19 @@ __global__ __launch_bounds__(256) void k_pack_factors(const float* __restrict__ 
 // Newton-Schulz apply (kcholqr.py:22, addmm(Y, Y, D)): Out = Y + fp32(Y D), the product an MFMA chain over
 // m = 0..r-1 from 0 and added to Y once. 32x64 output tile per workgroup; wave w: rows 16(w >> 1), 2 column blocks.
 // ---------------------------------------------------------------------------------------------------------------
+// SUB (the block projection, kbig.py:88-89): Out = C - fp32(A B) with A [K, r] of another matrix and C its own input,
+// B [r, ncols] (row stride ldd); the chain and the single rounding are the same. The Newton-Schulz step is
+// A = C = Y, B = D.
+template <bool SUB = false>
 __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int K, int r, const float* __restrict__ D,
-                                                 const MatsOut Outs, long ldo) {
+                                                 const MatsOut Outs, long ldo, const float* __restrict__ Cx = nullptr,
+                                                 long ldc = 0, long ldd = 0) {
     const float* __restrict__ Yin = Ys.p[blockIdx.z];
     float* __restrict__ Out = Outs.p[blockIdx.z];
-    D += (size_t)blockIdx.z * r * r;
+    const long ldD = SUB ? ldd : r;
+    D += (size_t)blockIdx.z * r * ldD;
+    const float* __restrict__ Cin = SUB ? Cx : Yin;
+    const long ldC = SUB ? ldc : ldy;
     __shared__ float sY[32][33];
     __shared__ float sD[32][68];
     const int row0 = blockIdx.x * 32, col0 = blockIdx.y * 64;
@@ -1265,7 +1293,7 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
         for (int q = 0; q < 2; ++q) {
             const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15;
             *reinterpret_cast<float4*>(&sD[row][4 * c4]) =
-                *reinterpret_cast<const float4*>(D + (size_t)(m0 + row) * r + col0 + 4 * c4);
+                *reinterpret_cast<const float4*>(D + (size_t)(m0 + row) * ldD + col0 + 4 * c4);
         }
         __syncthreads();
 #pragma unroll
@@ -1281,8 +1309,28 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int row = row0 + 16 * rb + 4 * lk + v, col = col0 + 16 * (cbase + c) + l16;
-            if (row < K) Out[(size_t)row * ldo + col] = Yin[(size_t)row * ldy + col] + acc[c][v];
+            if (row < K) {
+                const float cv = Cin[(size_t)row * ldC + col];
+                Out[(size_t)row * ldo + col] = SUB ? cv - acc[c][v] : cv + acc[c][v];
+            }
         }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Column-blocked path (r > 512, kbig.py:69-95): W = s X[:, j:j+256] for one block, s the power-of-2 scale of all of
+// X (from the amax partials of the whole matrix). Exact: s is a power of 2.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int BW = 256;   // block width of the column-blocked path (orth.py:19, borth(X, 256))
+__global__ __launch_bounds__(256) void k_scale_block(const float* __restrict__ X, long ldx, int K,
+                                                     const uint32_t* __restrict__ amax_part, float* __restrict__ W) {
+    const float sc = block_scale(amax_part);
+    const int n4 = K * (BW / 4);
+    for (int e = blockIdx.x * 256 + threadIdx.x; e < n4; e += gridDim.x * 256) {
+        const int row = e / (BW / 4), c4 = e - row * (BW / 4);
+        float4 v = *reinterpret_cast<const float4*>(X + (size_t)row * ldx + 4 * c4);
+        v.x = sc * v.x; v.y = sc * v.y; v.z = sc * v.z; v.w = sc * v.w;
+        *reinterpret_cast<float4*>(W + (size_t)row * BW + 4 * c4) = v;
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1346,6 +1394,14 @@ struct spanqr_plan {
     uint64_t* stamps = nullptr;  // Cholesky phase stamps (profiling): start, then 4 per 32-column step
     uint32_t* flags = nullptr;   // Cholesky dataflow flags and per-workgroup call counters
     hipEvent_t ev[64] = {};    // profiling: one event before and after each kernel of a call
+    // column-blocked path (r > 512): the plan of one 256-column block, the K x r dust whose column slices the blocks
+    // use, the block buffer W [K, 256], the projection's split partials and its product T [r - 256, 256], the amax
+    // partials of the whole X
+    spanqr_plan* blk = nullptr;
+    int nblk = 0;
+    char* bbase = nullptr;
+    float *Zb = nullptr, *W = nullptr, *Tp = nullptr, *T = nullptr;
+    uint32_t* bamax = nullptr;
     int nev = 0;
 };
 
@@ -1463,53 +1519,60 @@ hipError_t trsm_set_lds_plan(int q, int rb, int r) {
 #undef TRSM_ATTR
 }
 
+// the dust the pass-1 solve adds: the plan's own Z [K, r], or a column slice of a wider one (row stride ldz)
+struct Dust {
+    const float* z;
+    long ldz;
+};
+
 template <int Q, int RB>
-void launch_trsm_t(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const MatsOut& Y, long ldy,
-                   int n, hipStream_t st) {
+void launch_trsm_t(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const Dust& dz,
+                   const MatsOut& Y, long ldy, int n, hipStream_t st) {
     const dim3 grid((p->K + 16 * RB - 1) / (16 * RB), 1, n);
     const size_t lds = trsm_lds(p->r, RB);
-    if (pass1) k_trsm<true, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, p->Lp, Y, ldy,
-                                                           p->scal);
-    else k_trsm<false, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, p->Z, eps, p->Lp, Y, ldy,
-                                                      p->scal);
+    if (pass1) k_trsm<true, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, dz.z, dz.ldz, eps, p->Lp,
+                                                           Y, ldy, p->scal);
+    else k_trsm<false, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, dz.z, dz.ldz, eps, p->Lp, Y,
+                                                      ldy, p->scal);
 }
 
 template <int Q>
-void launch_trsm_q(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const MatsOut& Y, long ldy,
-                   int n, hipStream_t st) {
+void launch_trsm_q(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const Dust& dz,
+                   const MatsOut& Y, long ldy, int n, hipStream_t st) {
     switch (p->trsm_rb) {
-        case 4: launch_trsm_t<Q, 4>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
-        case 2: launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
-        default: launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+        case 4: launch_trsm_t<Q, 4>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+        case 2: launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+        default: launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
     }
 }
 
 template <int NBC>
-void launch_trsm_rows(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const MatsOut& Y,
-                      long ldy, int n, hipStream_t st) {
+void launch_trsm_rows(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const Dust& dz,
+                      const MatsOut& Y, long ldy, int n, hipStream_t st) {
     const dim3 grid((p->K + 63) / 64, 1, n);
-    if (pass1) k_trsm_rows<true, NBC><<<grid, 256, 0, st>>>(A, lda, p->K, p->amax_part, p->Z, eps, p->Lp, Y, ldy,
-                                                            p->scal);
-    else k_trsm_rows<false, NBC><<<grid, 256, 0, st>>>(A, lda, p->K, p->amax_part, p->Z, eps, p->Lp, Y, ldy, p->scal);
+    if (pass1) k_trsm_rows<true, NBC><<<grid, 256, 0, st>>>(A, lda, p->K, p->amax_part, dz.z, dz.ldz, eps, p->Lp, Y,
+                                                            ldy, p->scal);
+    else k_trsm_rows<false, NBC><<<grid, 256, 0, st>>>(A, lda, p->K, p->amax_part, dz.z, dz.ldz, eps, p->Lp, Y, ldy,
+                                                       p->scal);
 }
 
 // Y = A L^-T for the n matrices, with the packed factors the plan's Cholesky left in p->Lp
-void launch_trsm(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const MatsOut& Y, long ldy,
-                 int n, hipStream_t st) {
+void launch_trsm(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const Dust& dz,
+                 const MatsOut& Y, long ldy, int n, hipStream_t st) {
     if (p->trsm_rows) {
         switch (p->r / CB) {
-            case 2: launch_trsm_rows<2>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
-            case 4: launch_trsm_rows<4>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
-            case 6: launch_trsm_rows<6>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
-            default: launch_trsm_rows<8>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+            case 2: launch_trsm_rows<2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+            case 4: launch_trsm_rows<4>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+            case 6: launch_trsm_rows<6>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+            default: launch_trsm_rows<8>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
         }
         return;
     }
     switch (p->trsm_q) {
-        case 1: launch_trsm_q<1>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
-        case 2: launch_trsm_q<2>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
-        case 3: launch_trsm_q<3>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
-        default: launch_trsm_q<4>(p, A, lda, pass1, eps, Y, ldy, n, st); break;
+        case 1: launch_trsm_q<1>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+        case 2: launch_trsm_q<2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+        case 3: launch_trsm_q<3>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+        default: launch_trsm_q<4>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
     }
 }
 
@@ -1524,7 +1587,8 @@ void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsO
 // each kernel launched once for all n (the Cholesky in groups of chol_bmax). With rec, an event is recorded after
 // every kernel (profiling).
 int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut& Q, long ldq, float eps, float alpha,
-                 float tau, int ns, hipStream_t st, bool rec) {
+                 float tau, int ns, hipStream_t st, bool rec, Dust dz = Dust{nullptr, 0}) {
+    if (dz.z == nullptr) dz = Dust{p->Z, p->r};
     int rc;
     auto mark = [&]() -> int {
         if (rec) {
@@ -1547,7 +1611,7 @@ int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut
         if ((rc = mark())) return rc;
         if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U, n))) return rc;
         if ((rc = mark())) return rc;
-        launch_trsm(p, *in, ldin, pass == 0, eps, bout[cur], p->r, n, st);
+        launch_trsm(p, *in, ldin, pass == 0, eps, dz, bout[cur], p->r, n, st);
         if ((rc = mark())) return rc;
         in = &bin[cur];
         ldin = p->r;
@@ -1605,12 +1669,117 @@ int spanqr_dust_host(int K, int r, float* Z) {
     return SPANQR_OK;
 }
 
-static int check_shape(int K, int r) {
-    if (r < 64 || r > 512 || (r % 64) != 0) return fail(SPANQR_EINVAL, "r = %d: must be a multiple of 64 in [64, 512]", r);
+static int check_shape(int K, int r, bool blocked_ok = false) {
+    const bool blocked = blocked_ok && r > 512 && r <= SPANQR_MAX_R && (r % BW) == 0;
+    if (!blocked && (r < 64 || r > 512 || (r % 64) != 0))
+        return fail(SPANQR_EINVAL, blocked_ok ? "r = %d: must be a multiple of 64 in [64, 512] or of 256 up to 4096"
+                                              : "r = %d: must be a multiple of 64 in [64, 512]", r);
     if (K < r) return fail(SPANQR_EINVAL, "K = %d < r = %d", K, r);
     if ((long)K * r >= (1L << 30)) return fail(SPANQR_EINVAL, "K * r too large");
     return SPANQR_OK;
 }
+
+namespace {
+
+// Column-blocked plan: a 256-column block plan plus the blocked path's own buffers (no Gram or Cholesky of its own).
+int create_blocked(int K, int r, int device, spanqr_plan** out) {
+    spanqr_plan* p = new spanqr_plan;
+    p->K = K; p->r = r; p->device = device; p->batch = 1; p->nblk = r / BW;
+    int rc = spanqr_plan_create_batched(K, BW, 1, device, &p->blk);
+    if (rc != SPANQR_OK) {
+        delete p;
+        return rc;
+    }
+    size_t maxp = 0;   // split partials of the largest projection (U = (j / 64) * 4 tiles for j = r - 256 columns)
+    for (int jb = 1; jb < p->nblk; ++jb) {
+        int S = 0, KS = 0;
+        const int U = (BW * jb / TB) * (BW / TB);
+        split_policy(K, U, &S, &KS);
+        if ((size_t)S * U > maxp) maxp = (size_t)S * U;
+    }
+    auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const size_t sz_Z = al((size_t)K * r * sizeof(float)), sz_W = al((size_t)K * BW * sizeof(float));
+    const size_t sz_Tp = al(maxp * TB * TB * sizeof(float)), sz_T = al((size_t)r * BW * sizeof(float));
+    const size_t sz_am = al(AMAX_BLOCKS * sizeof(uint32_t));
+    const size_t bytes = sz_Z + sz_W + sz_Tp + sz_T + sz_am;
+    DeviceGuard dg(device);
+    if (hipMalloc((void**)&p->bbase, bytes) != hipSuccess) {
+        spanqr_plan_destroy(p->blk);
+        delete p;
+        return fail(SPANQR_ENOMEM, "workspace allocation of %zu bytes failed", bytes);
+    }
+    p->bytes = bytes + p->blk->bytes;
+    char* c = p->bbase;
+    p->Zb = (float*)c; c += sz_Z;
+    p->W = (float*)c; c += sz_W;
+    p->Tp = (float*)c; c += sz_Tp;
+    p->T = (float*)c; c += sz_T;
+    p->bamax = (uint32_t*)c; c += sz_am;
+    float* hz = (float*)malloc((size_t)K * r * sizeof(float));
+    rc = hz ? spanqr_dust_host(K, r, hz) : fail(SPANQR_ENOMEM, "host dust buffer");
+    if (rc == SPANQR_OK && (hipMemcpy(p->Zb, hz, (size_t)K * r * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
+                            hipDeviceSynchronize() != hipSuccess))
+        rc = fail(SPANQR_EHIP, "plan upload failed");
+    free(hz);
+    if (rc != SPANQR_OK) {
+        (void)hipFree(p->bbase);
+        spanqr_plan_destroy(p->blk);
+        delete p;
+        return rc;
+    }
+    *out = p;
+    return SPANQR_OK;
+}
+
+// Out = Cin - P (P^T Cin) for P = the j leading columns of Q (row stride ldq) and Cin [K, 256] (row stride ldc): the
+// projection of kbig.py:88-89. P^T Cin is a split-K product (fp32 MFMA chains per split, fp64 across splits in split
+// order, tri.py's Gram rule for the split count), then one MFMA chain per element of P T, subtracted once.
+void project(const spanqr_plan* p, const float* Q, long ldq, int j, const float* Cin, long ldc, float* Out,
+             hipStream_t st) {
+    const int U = (j / TB) * (BW / TB);
+    int S = 0, KS = 0;
+    split_policy(p->K, U, &S, &KS);
+    const MatsIn P = mats_in(&Q, 1);
+    k_gram<false, false, true><<<dim3(U, S), 256, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, BW / TB);
+    k_reduce<2><<<dim3(16, U), 256, 0, st>>>(p->Tp, S, BW / TB, BW, p->T, nullptr);
+    k_nsapply<true><<<dim3((p->K + 31) / 32, BW / 64), 256, 0, st>>>(P, ldq, p->K, j, p->T, mats_out(&Out, 1), BW, Cin,
+                                                                    ldc, BW);
+}
+
+// borth (kbig.py:69-95, BCGS2 over 256-column blocks as orth.py:18-19 calls it): per block, W = s X_blk, projected
+// twice against the finished blocks, orthonormalised by the full kcholf call with the block's slice of the K x r dust;
+// then projected once more and orthonormalised again (reorth). Each block's result goes straight into its columns of Q.
+int enqueue_borth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, float eps, float alpha, float tau,
+                  int ns, hipStream_t st) {
+    const int K = p->K;
+    k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(mats_in(&X, 1), ldx, K, p->r, p->bamax);
+    const int sgrid = (K * (BW / 4) + 255) / 256 < 1024 ? (K * (BW / 4) + 255) / 256 : 1024;
+    int rc;
+    for (int jb = 0; jb < p->nblk; ++jb) {
+        const int j = BW * jb;
+        float* Qj = Q + j;
+        const float* Wc = p->W;
+        const Dust dz{p->Zb + j, p->r};
+        k_scale_block<<<sgrid, 256, 0, st>>>(X + j, ldx, K, p->bamax, p->W);
+        if (j > 0) {
+            project(p, Q, ldq, j, p->W, BW, p->W, st);
+            project(p, Q, ldq, j, p->W, BW, p->W, st);
+        }
+        if ((rc = enqueue_orth(p->blk, 1, mats_in(&Wc, 1), BW, mats_out(&Qj, 1), ldq, eps, alpha, tau, ns, st, false,
+                               dz)))
+            return rc;
+        if (j > 0) {
+            project(p, Q, ldq, j, Qj, ldq, p->W, st);
+            if ((rc = enqueue_orth(p->blk, 1, mats_in(&Wc, 1), BW, mats_out(&Qj, 1), ldq, eps, alpha, tau, ns, st,
+                                   false, dz)))
+                return rc;
+        }
+    }
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
+}  // namespace
 
 int spanqr_split_rows(int K, int r) {
     const int rc = check_shape(K, r);
@@ -1628,10 +1797,14 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
 int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan** out) {
     if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
     *out = nullptr;
-    const int shape_rc = check_shape(K, r);
+    const int shape_rc = check_shape(K, r, true);
     if (shape_rc != SPANQR_OK) return shape_rc;
     if (batch < 1 || batch > SPANQR_MAX_BATCH)
         return fail(SPANQR_EINVAL, "batch = %d: must be in [1, %d]", batch, SPANQR_MAX_BATCH);
+    if (r > 512) {
+        if (batch != 1) return fail(SPANQR_EINVAL, "r = %d > 512 (column-blocked path): batch must be 1", r);
+        return create_blocked(K, r, device, out);
+    }
     DeviceGuard dg(device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", device);
     spanqr_plan* p = new spanqr_plan;
@@ -1737,6 +1910,12 @@ void spanqr_plan_destroy(spanqr_plan* p) {
     if (!p) return;
     DeviceGuard dg(p->device);
     (void)hipDeviceSynchronize();
+    if (p->blk) {
+        spanqr_plan_destroy(p->blk);
+        (void)hipFree(p->bbase);
+        delete p;
+        return;
+    }
     for (int i = 0; i < 64; ++i)
         if (p->ev[i]) (void)hipEventDestroy(p->ev[i]);
     (void)hipFree(p->base);
@@ -1748,13 +1927,14 @@ long spanqr_plan_query(const spanqr_plan* p, int what) {
     switch (what) {
         case SPANQR_Q_K: return p->K;
         case SPANQR_Q_R: return p->r;
-        case SPANQR_Q_SPLITS: return p->S;
-        case SPANQR_Q_SPLIT_ROWS: return p->KS;
-        case SPANQR_Q_CHOL_GRID: return p->chol_grid;
+        case SPANQR_Q_SPLITS: return p->blk ? p->blk->S : p->S;
+        case SPANQR_Q_SPLIT_ROWS: return p->blk ? p->blk->KS : p->KS;
+        case SPANQR_Q_CHOL_GRID: return p->blk ? p->blk->chol_grid : p->chol_grid;
         case SPANQR_Q_WORKSPACE_MB: return (long)((p->bytes + (1u << 20) - 1) >> 20);
         case SPANQR_Q_DEVICE: return p->device;
         case SPANQR_Q_BATCH: return p->batch;
-        case SPANQR_Q_CHOL_BATCH: return p->chol_bmax;
+        case SPANQR_Q_CHOL_BATCH: return p->blk ? p->blk->chol_bmax : p->chol_bmax;
+        case SPANQR_Q_BLOCKS: return p->nblk;
         default: return -1;
     }
 }
@@ -1768,6 +1948,7 @@ int spanqr_orth_f32(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq
     if (ns < 0) return fail(SPANQR_EINVAL, "ns = %d < 0", ns);
     DeviceGuard dg(p->device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
+    if (p->blk) return enqueue_borth(p, X, ldx, Q, ldq, eps, alpha, tau, ns, (hipStream_t)stream);
     return enqueue_orth(p, 1, mats_in(&X, 1), ldx, mats_out(&Q, 1), ldq, eps, alpha, tau, ns, (hipStream_t)stream,
                         false);
 }
@@ -1775,6 +1956,7 @@ int spanqr_orth_f32(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq
 int spanqr_orth_batched_f32(spanqr_plan* p, int n, const float* const* X, long ldx, float* const* Q, long ldq,
                             float eps, float alpha, float tau, int ns, void* stream) {
     if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     if (n < 1 || n > p->batch) return fail(SPANQR_EINVAL, "n = %d: must be in [1, %d] (the plan's batch)", n, p->batch);
     if (!X || !Q) return fail(SPANQR_EINVAL, "pointer arrays must not be null");
     int rc;
@@ -1795,6 +1977,7 @@ int spanqr_orth_batched_f32(spanqr_plan* p, int n, const float* const* X, long l
 int spanqr_profile_orth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
                         float tau, int ns, void* stream, float* ms, int max_n, int* n_out) {
     if (!p || !ms || !n_out) return fail(SPANQR_EINVAL, "null argument");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     int rc = check_mat(p, X, ldx, "X");
     if (rc) return rc;
     if ((rc = check_mat(p, Q, ldq, "Q"))) return rc;
@@ -1815,6 +1998,7 @@ int spanqr_profile_orth(spanqr_plan* p, const float* X, long ldx, float* Q, long
 
 int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, void* stream) {
     if (!p || !avg_ms) return fail(SPANQR_EINVAL, "null argument");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     if (reps < 1 || reps > 100000) return fail(SPANQR_EINVAL, "reps = %d out of range", reps);
     if (which < SPANQR_K_AMAX || which > SPANQR_K_NS_APPLY) return fail(SPANQR_EINVAL, "unknown kernel %d", which);
     DeviceGuard dg(p->device);
@@ -1832,8 +2016,8 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
             case SPANQR_K_GRAM: launch_gram(p, y0, r, 1, false, false, st); break;
             case SPANQR_K_REDUCE: launch_reduce(p, 0, p->G, 1, st); break;
             case SPANQR_K_CHOL: return launch_chol(p, 1e-7f, 1e-8f, p->scal + 1, st, 16 * p->U, 1);
-            case SPANQR_K_TRSM_PASS1: launch_trsm(p, y0, r, true, 5e-7f, y1, r, 1, st); break;
-            case SPANQR_K_TRSM: launch_trsm(p, y0, r, false, 0.0f, y1, r, 1, st); break;
+            case SPANQR_K_TRSM_PASS1: launch_trsm(p, y0, r, true, 5e-7f, Dust{p->Z, r}, y1, r, 1, st); break;
+            case SPANQR_K_TRSM: launch_trsm(p, y0, r, false, 0.0f, Dust{p->Z, r}, y1, r, 1, st); break;
             case SPANQR_K_NS_APPLY: launch_nsapply(p, y0, r, y1, r, 1, st); break;
         }
         return SPANQR_OK;
@@ -1854,6 +2038,7 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
 
 int spanqr_stage_amax(spanqr_plan* p, const float* X, long ldx, void* stream) {
     if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     int rc = check_mat(p, X, ldx, "X");
     if (rc) return rc;
     DeviceGuard dg(p->device);
@@ -1865,6 +2050,7 @@ int spanqr_stage_amax(spanqr_plan* p, const float* X, long ldx, void* stream) {
 int spanqr_stage_gram(spanqr_plan* p, const float* A, long lda, int use_scale, int kahan, float* G, double* npart,
                       void* stream) {
     if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     int rc = check_mat(p, A, lda, "A");
     if (rc) return rc;
     if (!G) return fail(SPANQR_EINVAL, "G is null");
@@ -1881,6 +2067,7 @@ int spanqr_stage_gram(spanqr_plan* p, const float* A, long lda, int use_scale, i
 int spanqr_stage_chol(spanqr_plan* p, const float* G, const double* npart, float alpha, float tau, float* L,
                       float* Li, float* scal, void* stream) {
     if (!p || !G || !L || !Li) return fail(SPANQR_EINVAL, "null argument");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
@@ -1900,19 +2087,21 @@ int spanqr_stage_chol(spanqr_plan* p, const float* G, const double* npart, float
 int spanqr_stage_trsm(spanqr_plan* p, const float* A, long lda, int pass1, float eps, const float* L, const float* Li,
                       float* Y, long ldy, void* stream) {
     if (!p || !L || !Li) return fail(SPANQR_EINVAL, "null argument");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     int rc = check_mat(p, A, lda, "A");
     if (rc) return rc;
     if ((rc = check_mat(p, Y, ldy, "Y"))) return rc;
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
     k_pack_factors<<<(int)((p->lp_stride + 255) / 256), 256, 0, st>>>(L, Li, p->r, p->Lp);
-    launch_trsm(p, mats_in(&A, 1), lda, pass1 != 0, eps, mats_out(&Y, 1), ldy, 1, st);
+    launch_trsm(p, mats_in(&A, 1), lda, pass1 != 0, eps, Dust{p->Z, p->r}, mats_out(&Y, 1), ldy, 1, st);
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
 
 int spanqr_stage_ns(spanqr_plan* p, const float* Y, long ldy, int kahan, float* Yout, long ldo, void* stream) {
     if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     int rc = check_mat(p, Y, ldy, "Y");
     if (rc) return rc;
     if ((rc = check_mat(p, Yout, ldo, "Yout"))) return rc;
@@ -1928,6 +2117,7 @@ int spanqr_stage_ns(spanqr_plan* p, const float* Y, long ldy, int kahan, float* 
 int spanqr_profile_chol(spanqr_plan* p, const float* G, const double* npart, float alpha, float tau,
                         unsigned long long* stamps_out, double* tick_ns, void* stream) {
     if (!p || !G || !npart || !stamps_out || !tick_ns) return fail(SPANQR_EINVAL, "null argument");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
@@ -1945,6 +2135,7 @@ int spanqr_profile_chol(spanqr_plan* p, const float* G, const double* npart, flo
 
 int spanqr_plan_copy_dust(spanqr_plan* p, float* Z, void* stream) {
     if (!p || !Z) return fail(SPANQR_EINVAL, "null argument");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     DeviceGuard dg(p->device);
     HIPCHK(hipMemcpyAsync(Z, p->Z, (size_t)p->K * p->r * sizeof(float), hipMemcpyDeviceToDevice, (hipStream_t)stream));
     return SPANQR_OK;
@@ -1952,6 +2143,7 @@ int spanqr_plan_copy_dust(spanqr_plan* p, float* Z, void* stream) {
 
 int spanqr_plan_copy_scalars(spanqr_plan* p, float* scal8, void* stream) {
     if (!p || !scal8) return fail(SPANQR_EINVAL, "null argument");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(scal8, p->scal, 7 * sizeof(float), hipMemcpyDeviceToDevice, st));

@@ -12,6 +12,7 @@ from .plan import get_plan, stream_handle
 CB = 32          # Cholesky tile (chol.cu:15 TB = 32)
 TILE = 64        # the native kernels need r to be a multiple of this
 R_MAX = 512      # orth.py:18: wider X goes through block Gram-Schmidt in the reference
+BLOCK = 256      # its block width (orth.py:19, borth(X, 256))
 
 
 def _check_input(X):
@@ -104,19 +105,49 @@ def orth_many(Xs):
     return out
 
 
+def borth(X, b=BLOCK):
+    """Q for fp32 X [K, r], K >= r, by block Gram-Schmidt over b-column blocks (candidates/kbig.py:69-95, BCGS2 with
+    the reorthogonalisation): each block, scaled by the power of 2 of the whole X, has the finished blocks' span
+    removed twice, goes through the kcholf recipe with its own column slice of a K x r dust, then is projected and
+    orthonormalised once more. One native call for the whole X, no host synchronisation.
+
+    b = 256 is the width orth.py:19 uses and the only one implemented (the reference's default is 512). As in
+    kbig.py:77-78, r <= b or r not a multiple of b is one orth call at full width instead; r above 4096 raises.
+    """
+    _check_input(X)
+    if b != BLOCK:
+        raise ValueError(f"borth: only b = {BLOCK} is implemented (the width orth.py:19 uses)")
+    K, r = X.shape
+    if r <= b or r % b:
+        return orth(X)
+    if r > _lib.MAX_R or K < r:
+        raise ValueError(f"borth: shape [{K}, {r}] needs r <= {_lib.MAX_R} and K >= r")
+    X = _prepare(X)
+    dev = X.device
+    plan = get_plan(K, r, dev)
+    Q = torch.empty_like(X)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().spanqr_orth_f32(plan.handle, X.data_ptr(), r, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2,
+                                               stream_handle(dev)))
+    return Q
+
+
 def orth(X):
     """Orthonormal basis of the column span of X (fp32 GPU [K, r], K >= r), as orth.py:13-20: Q^T Q = I and
     span(Q) = span(X); rank-deficient or zero X is completed with orthonormal directions (never zero or NaN columns).
     Deterministic and free of host synchronisation.
 
-    Shapes outside the native kernels follow the reference's dispatch: r not a multiple of 32 (kcholqr.py:98-99)
-    and, here, r a multiple of 32 but not of 64, or K < r, go to torch.linalg.qr; r > 512 (the reference's block
-    Gram-Schmidt branch, orth.py:18-19) is not implemented yet and raises.
+    Dispatch as orth.py:18-20: r > 512 and a multiple of 256 goes through block Gram-Schmidt over 256-column blocks
+    (borth); r <= 512 through kcholqr_f. Shapes outside the native kernels -- r not a multiple of 32
+    (kcholqr.py:98-99) and, here, r a multiple of 32 but not of 64, K < r, r > 4096, or r > 512 and not a multiple of
+    256 (where the reference runs kcholqr_f at full width) -- go to torch.linalg.qr.
     """
     _check_input(X)
     K, r = X.shape
-    if r > R_MAX and r % 256 == 0:
-        raise NotImplementedError("orth: r > 512 (block Gram-Schmidt over 256-column blocks) is not implemented")
-    if r % TILE or K < r or r > R_MAX:
+    if r > R_MAX:
+        if r % BLOCK == 0 and r <= _lib.MAX_R and K >= r:
+            return borth(X)
+        return torch.linalg.qr(X)[0]
+    if r % TILE or K < r:
         return torch.linalg.qr(X)[0]
     return kcholqr_f(X)

@@ -347,5 +347,131 @@ def check_orth_small():
     return f
 
 
+# ---- column-blocked path (kbig.py:69-95) ----
+
+def check_split_rule():
+    """the split rule's own invariants: KS a multiple of 32, no empty split, at most ceil(512 / U) splits and at most
+    ceil(K / 128)"""
+    f = []
+    for K in (1, 31, 32, 127, 128, 129, 1000, 4096, 17408, 100000):
+        for U in (1, 4, 8, 10, 36, 136, 240):
+            KS = oracle.split_rows(K, U)
+            S = oracle.gram_splits(K, KS)
+            if KS % 32 or KS <= 0:
+                f.append(f"split_rows({K}, {U}) = {KS} not a positive multiple of 32")
+            elif S > max(1, -(-512 // U)) or S > max(1, -(-K // 128)) or (S - 1) * KS >= K:
+                f.append(f"split_rows({K}, {U}) = {KS}: {S} splits")
+    return f
+
+
+def check_xgram():
+    """P^T C against fp64 under the fp32 chain bound, exactly on integer data, and split-count independent on it"""
+    f = []
+    rng = np.random.default_rng(11)
+    for K, j, KS in ((300, 256, 128), (1000, 512, 256), (77, 256, 96)):
+        P = rng.standard_normal((K, j)).astype(np.float32)
+        C = rng.standard_normal((K, 256)).astype(np.float32)
+        T = oracle.xgram(P, C, KS).astype(np.float64)
+        T64 = P.astype(np.float64).T @ C
+        bound = (KS + 2) * U32 * (np.abs(P).astype(np.float64).T @ np.abs(C))
+        if not (np.abs(T - T64) <= bound).all():
+            f.append(f"xgram K={K} j={j}: not P^T C")
+        Pi = rng.integers(-8, 9, (K, j)).astype(np.float32)
+        Ci = rng.integers(-8, 9, (K, 256)).astype(np.float32)
+        Ti = Pi.astype(np.int64).T @ Ci.astype(np.int64)
+        for ks in (KS, 32):
+            if not np.array_equal(oracle.xgram(Pi, Ci, ks), Ti.astype(np.float32)):
+                f.append(f"xgram K={K} j={j} KS={ks}: integer product not exact")
+    return f
+
+
+def check_project():
+    """C - P P^T C: fp64 agreement, P^T Out ~ 0 for orthonormal P, a vector in span(P) removed, one orthogonal to
+    it kept"""
+    f = []
+    rng = np.random.default_rng(12)
+    K, j = 600, 512
+    P = np.linalg.qr(rng.standard_normal((K, j)))[0].astype(np.float32)
+    C = rng.standard_normal((K, 256)).astype(np.float32)
+    KS = oracle.split_rows(K, (j // 64) * 4)
+    Out = oracle.project(P, C, KS).astype(np.float64)
+    P64 = P.astype(np.float64)
+    ref = C - P64 @ (P64.T @ C)
+    if not np.abs(Out - ref).max() <= 1e-4:
+        f.append(f"project: not C - P P^T C ({np.abs(Out - ref).max():.2e})")
+    if not np.abs(P64.T @ Out).max() <= 1e-4:
+        f.append("project: result not orthogonal to P")
+    inside = (P64 @ rng.standard_normal((j, 256))).astype(np.float32)
+    if not np.abs(oracle.project(P, inside, KS)).max() <= 1e-4 * np.abs(inside).max():
+        f.append("project: a matrix in span(P) is not removed")
+    perp = (C.astype(np.float64) - P64 @ (P64.T @ C)).astype(np.float32)
+    if not np.abs(oracle.project(P, perp, KS) - perp).max() <= 1e-4 * np.abs(perp).max():
+        f.append("project: a matrix orthogonal to P is changed")
+    return f
+
+
+def _thin_q(X):
+    Qh, Rh = np.linalg.qr(X.astype(np.float64))
+    return Qh * np.sign(np.diag(Rh))
+
+
+def check_borth():
+    """borth on small shapes: on a well-conditioned X it is the thin-QR Q (BCGS with positive-diagonal block
+    factors gives X = Q R, R upper triangular with a positive diagonal, which fixes Q); X = 0 gives block j the span of
+    the dust's columns j.. with the earlier blocks removed; a repeated block is completed, never zero or NaN"""
+    f = []
+    rng = np.random.default_rng(13)
+    K, r = 1000, 768
+    X = rng.standard_normal((K, r)).astype(np.float32)
+    Q = oracle.borth(X).astype(np.float64)
+    if not np.abs(Q - _thin_q(X)).max() <= 1e-4:
+        f.append(f"borth: not the thin-QR Q on a well-conditioned X ({np.abs(Q - _thin_q(X)).max():.2e})")
+    for name, Xc in (("zero", np.zeros((K, r), np.float32)),
+                     ("repeated block", np.concatenate([X[:, :512], X[:, :256]], axis=1))):
+        Q = oracle.borth(Xc).astype(np.float64)
+        if not np.isfinite(Q).all() or not np.abs(Q.T @ Q - np.eye(r)).max() <= 1e-6:
+            f.append(f"borth {name}: Q not orthonormal")
+            continue
+        if name == "zero":
+            Z = oracle.dust(K, r).astype(np.float64)
+            for j in range(0, r, 256):
+                Zp = Z[:, j:j + 256] - Q[:, :j] @ (Q[:, :j].T @ Z[:, j:j + 256])
+                Qj = Q[:, j:j + 256]
+                if not np.abs(Zp - Qj @ (Qj.T @ Zp)).max() <= 1e-5 * np.abs(Zp).max():
+                    f.append(f"borth zero: block {j // 256} does not span its projected dust slice")
+        else:
+            Qh = _thin_q(Xc[:, :512])
+            if not np.abs(Q[:, :512] - Qh).max() <= 1e-4:
+                f.append("borth repeated block: leading blocks are not the thin-QR Q")
+    return f
+
+
+def check_borth_composition():
+    """kbig.py:85-93 step by step from the pieces pinned above: s from all of X, each block twice projected, _kf with
+    its dust slice, once more projected and _kf again"""
+    f = []
+    rng = np.random.default_rng(14)
+    K, r = 800, 768
+    X = (rng.standard_normal((K, r)) * np.exp(rng.uniform(-3, 3, r))).astype(np.float32)
+    Q = oracle.borth(X)
+    s = oracle.pow2_scale(oracle.amax(X))
+    Z = oracle.dust(K, r)
+    KSb = oracle.split_rows(K, 10)
+    R = np.empty_like(X)
+    for j in range(0, r, 256):
+        W = X[:, j:j + 256] * s
+        if j:
+            KSp = oracle.split_rows(K, (j // 64) * 4)
+            W = oracle.project(R[:, :j], oracle.project(R[:, :j], W, KSp), KSp)
+        W = oracle.orth_dust(W, Z[:, j:j + 256], KSb)
+        if j:
+            W = oracle.orth_dust(oracle.project(R[:, :j], W, KSp), Z[:, j:j + 256], KSb)
+        R[:, j:j + 256] = W
+    if not np.array_equal(Q.view(np.uint32), R.view(np.uint32)):
+        f.append("borth is not kbig.py's composition of scale, projections and _kf")
+    return f
+
+
 ALL = [check_scale, check_scale_rounding_margin, check_rsqrt, check_dust, check_gram, check_shift, check_chol,
-       check_trsm, check_ns, check_orth_small]
+       check_trsm, check_ns, check_orth_small, check_split_rule, check_xgram, check_project, check_borth,
+       check_borth_composition]

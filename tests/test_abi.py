@@ -40,9 +40,33 @@ def test_split_policy():
         KS = 32 * -(-(-(-K // S)) // 32)
         assert f(K, r) == KS, (K, r)
         assert KS % 32 == 0 and -(-K // KS) <= S
-    for K, r in [(100, 128), (1024, 96), (1024, 576), (1024, 0)]:
+    for K, r in [(100, 128), (1024, 96), (1024, 576), (1024, 0), (2048, 768)]:
         assert f(K, r) == -1
         assert _lib.lib().spanqr_last_error()
+
+
+def test_split_policy_is_the_oracle_rule():
+    """the library's split rule (every Gram and block projection) is the one the oracle restates"""
+    f = _lib.lib().spanqr_split_rows
+    for K in (64, 100, 513, 1024, 3000, 17408, 65536):
+        for r in range(64, 513, 64):
+            if K >= r:
+                nt = r // 64
+                assert f(K, r) == oracle.split_rows(K, nt * (nt + 1) // 2), (K, r)
+
+
+def test_column_blocked_shapes_checked_before_any_device_work():
+    h = ctypes.c_void_p()
+    f = _lib.lib().spanqr_plan_create_batched
+    for K, r in [(1024, 640), (1024, 800), (512, 768), (8192, 4352), (1 << 19, 4096)]:
+        assert f(K, r, 1, 0, ctypes.byref(h)) == -1 and not h.value, (K, r)
+    assert f(2048, 768, 2, 0, ctypes.byref(h)) == -1 and b"batch" in _lib.lib().spanqr_last_error()
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")
+def test_column_blocked_plan_without_gpu_fails_cleanly():
+    h = ctypes.c_void_p()
+    assert _lib.lib().spanqr_plan_create(2048, 768, 0, ctypes.byref(h)) == -2 and not h.value
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")
@@ -85,6 +109,8 @@ def test_orth_refuses_cpu_tensors():
         spanqr_amd.orth_many([X, X])
     with pytest.raises(TypeError):
         spanqr_amd.kcholqr_f_many([X])
+    with pytest.raises(TypeError):
+        spanqr_amd.borth(torch.randn(1024, 768))
     assert spanqr_amd.orth_many([]) == [] and spanqr_amd.kcholqr_f_many([]) == []
 
 
@@ -99,3 +125,4 @@ def test_top_level_orth_is_the_package_orth():
     import orth as top
     assert top.orth is spanqr_amd.orth
     assert top.orth_many is spanqr_amd.orth_many
+    assert top.borth is spanqr_amd.borth and top.kcholqr_f is spanqr_amd.kcholqr_f

@@ -16,6 +16,10 @@ DEFECTS = {
     8: "pivot clamp with fminf instead of fmaxf",
     9: "dust columns not normalised",
     10: "power-of-2 scale rounds up instead of to nearest",
+    11: "block projection product reads the wrong column of C",
+    12: "block projection adds P P^T C instead of subtracting it",
+    13: "every block gets the first dust slice",
+    14: "blocks projected once before orthonormalisation instead of twice",
 }
 
 
