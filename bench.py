@@ -9,7 +9,8 @@ captured hipGraph. `value` = timed wall time / (steps x 6) in microseconds (lowe
 
 Also reported: per shape, back-to-back ("thr", 20 replays) and isolated synchronised ("lat") time per call, at the
 workload shapes and at 768x512, 2048x512, 5120x256, 6144x256 and 17408x256 (768x512 and 17408x256 are the quoted
-targets); the batched layer set (12 x 768x512 + 12 x 2048x512, one hipGraph per shape group, against 24
+targets); the 27B layers wider than 512 (5120x1024, 17408x1024, 17408x2048: block Gram-Schmidt over 256-column
+blocks); the batched layer set (12 x 768x512 + 12 x 2048x512, one hipGraph per shape group, against 24
 single-call graphs); per kernel and shape the average launch duration (HIP events around back-to-back launches on
 the call's stream) with its algorithmic flops and bytes, as TFLOP/s and GB/s and as fractions of the MFMA and HBM
 peaks; the roofline of the dominant kernel and of the whole call; the Cholesky's latency
@@ -29,7 +30,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from spanqr_amd import _lib, kcholqr_f, kcholqr_f_many, stages  # noqa: E402
+from spanqr_amd import _lib, kcholqr_f, kcholqr_f_many, orth, stages  # noqa: E402
 from spanqr_amd.plan import get_plan, stream_handle  # noqa: E402
 from spanqr_amd.qrbench import gen  # noqa: E402
 
@@ -39,6 +40,8 @@ SEEDS = (0, 1)
 TARGET_SHAPES = [(768, 512), (17408, 256)]
 TARGET_US = {"768x512": 250.0, "17408x256": 350.0}
 OTHER_SHAPES = [(768, 512), (2048, 512), (5120, 256), (6144, 256), (17408, 256)]
+# 27B layers wider than 512 (orth.py:18-19: block Gram-Schmidt over 256-column blocks, candidates/kbig.py:69-95)
+BLOCKED_SHAPES = [(5120, 1024), (17408, 1024), (17408, 2048)]
 BATCH_GROUPS = [(768, 512, 12), (2048, 512, 12)]   # the 110M model's attention and down_proj layers
 PEAK_FP32_TFLOPS = 157.3     # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
@@ -103,16 +106,17 @@ def traffic_bytes(family):
     return None if rec is None else rec.get("bytes_per_launch")
 
 
-def capture(X):
+def capture(X, fn=None):
     """(graph, Q): one orth() call on X captured into a hipGraph on a side stream (plan created beforehand)"""
+    fn = fn or kcholqr_f
     st = torch.cuda.Stream(X.device)
     st.wait_stream(torch.cuda.current_stream(X.device))
     with torch.cuda.stream(st):
-        kcholqr_f(X)               # creates the plan for this stream and warms up
+        fn(X)                      # creates the plan for this stream and warms up
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=st):
-        Q = kcholqr_f(X)
+        Q = fn(X)
     torch.cuda.synchronize()
     return g, Q
 
@@ -326,6 +330,14 @@ def main(argv=None):
                               "kernels": ks}
         del g, q, X
         torch.cuda.synchronize()
+    blocked = {}
+    for K, r in BLOCKED_SHAPES:
+        X = gen.bench_input(K, r, seed=0).to(dev)
+        g, q = capture(X, orth)
+        blocked[f"{K}x{r}"] = {"thr_us": time_graph(g, n=5), "lat_us": lat_us(g, n=5), "orth": orth_error(q),
+                               "blocks": r // 256, "orth_calls_per_call": 2 * (r // 256) - 1}
+        del g, q, X
+        torch.cuda.synchronize()
     targets = {k: {"us_per_call": shapes[k]["thr_us"], "lat_us": shapes[k]["lat_us"], "orth": shapes[k]["orth"],
                    "target_us": TARGET_US[k]} for k in TARGET_US}
 
@@ -376,7 +388,7 @@ def main(argv=None):
                                "hipGraph per input", "shapes": [f"{K}x{r}" for K, r in WORKLOAD_SHAPES],
                    "seeds": list(SEEDS), "calls_per_step": calls, "graphs": not a.no_graph},
         "orth_max": orth_max, "per_shape_us": per_shape, "per_shape_lat_us": per_shape_lat,
-        "target_shapes": targets, "shapes": shapes, "batched_layers": batched,
+        "target_shapes": targets, "shapes": shapes, "blocked_shapes": blocked, "batched_layers": batched,
         "roofline": roofline, "call_roofline": call_roof, "kernels": kernels, "kernel_share": share,
         "sum_of_kernels_us": call_us, "cholesky": chol_info,
         "cpu_baseline": cpu,

@@ -330,14 +330,16 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 //     same time waves 1-2 fetch tile row j+2 (T(j+2, j-1..j+2), handed over by its owner through column block j-2,
 //     plus the owner's panel L(j+2, j-2)) while wave 3 publishes the previous step's L tiles and Li; then wave 1
 //     forms the panel L(j+2, j-1) (the previous step's Li_{j-1}, L(j, j-1), L(j+1, j-1) are still in LDS), wave 2
-//     applies the block j-2 update of T(j+2, j+1) that the owner leaves out, and the three waves apply block j-1 to
-//     T(j+2, j), T(j+2, j+1), T(j+2, j+2), wave 3 publishing L(j+2, j-1). Then all waves form the panels
-//     L(j+1, j), L(j+2, j) and apply column block j to T(j+1, j+1), T(j+2, j+1), T(j+2, j+2) in one phase
-//     (look-ahead over the next two tile rows).
+//     applies the block j-2 update of T(j+2, j+1) that the owner leaves out, and the two waves apply block j-1 to
+//     T(j+2, j), T(j+2, j+2) (wave 1) and T(j+2, j+1) (wave 2); wave 3, after publishing, applies block j-1 to
+//     T(j+1, j) and T(j+1, j+1). Then all waves form the panels L(j+1, j), L(j+2, j) and apply column block j to
+//     T(j+1, j+1), the tile the next step factors (look-ahead over the next two tile rows; block j on the rest of
+//     row j+2 is wave 3's work in the next step).
 //   * Workgroup i-3 owns tile row i >= 4 for the whole factorisation, in LDS. For column block j = 0..i-4 in order:
 //     panel L(i, j) = T(i, j) Li_j^T (published), then T(i, k) -= L(i, j) L(k, j)^T for k = j+1..i with the other
 //     rows' panels of block j fetched together (at its last block, j = i-4, T(i, i-1) is left to workgroup 0); after
-//     block i-4 it hands T(i, i-3..i) to workgroup 0, two steps before workgroup 0 factors T(i, i).
+//     block i-4 it hands T(i, i-3..i) to workgroup 0, two steps before workgroup 0 factors T(i, i). The panel
+//     L(j+3, j) of the row just handed over it forms itself from the handed-over T(j+3, j).
 // Every element keeps the reference order: updates by column block in increasing order, each one MFMA chain over the
 // block's 32 columns. A producer publishes with an agent-scope release after its stores; a consumer polls with
 // bounded waits (after SPIN_LIMIT polls it records an error and stops waiting, so the kernel always ends). Each
@@ -460,6 +462,7 @@ __device__ __forceinline__ void panel32(Tile& out, const Tile& in, const Tile& l
 }
 
 // dst = C - Pi Pk^T (chain over m = 0..31 starting from C); lower: skip the upper 16x16 block. dst may alias C.
+// Every wave's global stores have completed when it returns (they are covered by a release made after it).
 __device__ __forceinline__ void update32(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk, bool lower) {
     WAVE_COORDS;
     if (!(lower && bi == 0 && bj == 1)) {
@@ -472,6 +475,7 @@ __device__ __forceinline__ void update32(Tile& dst, const Tile& C, const Tile& P
 #pragma unroll
         for (int v = 0; v < 4; ++v) dst[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
 }
 
@@ -496,6 +500,32 @@ __device__ __forceinline__ void panel32x2(Tile& outA, const Tile& inA, Tile& out
     for (int v = 0; v < 4; ++v) {
         outA[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
         outB[16 * bi + 4 * lk + v][16 * bj + l16] = c[v];
+    }
+    __syncthreads();
+}
+
+// Two panels in place: A = A Li^T, B = B Li^T (every operand is read before the first write)
+__device__ __forceinline__ void panel32x2_inplace(Tile& A, Tile& B, const Tile& li) {
+    WAVE_COORDS;
+    float xa[8], xb[8], lv[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+        xa[kk] = A[16 * bi + l16][4 * kk + lk];
+        xb[kk] = B[16 * bi + l16][4 * kk + lk];
+        lv[kk] = li[16 * bj + l16][4 * kk + lk];
+    }
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+        if (kk < 4 * (bj + 1)) {
+            a = mfma(xa[kk], lv[kk], a);
+            c = mfma(xb[kk], lv[kk], c);
+        }
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        A[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
+        B[16 * bi + 4 * lk + v][16 * bj + l16] = c[v];
     }
     __syncthreads();
 }
@@ -528,10 +558,10 @@ __device__ __forceinline__ void panel32_wave(Tile& out, const Tile& in, const Ti
     __builtin_amdgcn_wave_barrier();
 }
 
-// One wave, a whole 32x32 tile: C -= Pi Pk^T in place (LOWER: the upper 16x16 block is left alone); operands read
-// once, the quadrants' chains (over m = 0..31 from C) interleaved.
+// One wave, a whole 32x32 tile: dst = C - Pi Pk^T (LOWER: the upper 16x16 block is left alone; dst may alias C);
+// operands read once, the quadrants' chains (over m = 0..31 from C) interleaved.
 template <bool LOWER>
-__device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Tile& Pk) {
+__device__ __forceinline__ void update32_wave_to(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk) {
     const int lane = threadIdx.x & 63, l16 = lane & 15, lk = lane >> 4;
     float a[2][8], b[2][8];
 #pragma unroll
@@ -555,9 +585,14 @@ __device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Til
     for (int qd = 0; qd < 4; ++qd)
         if (!(LOWER && qd == 1))
 #pragma unroll
-            for (int v = 0; v < 4; ++v) C[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16] = acc[qd][v];
+            for (int v = 0; v < 4; ++v) dst[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16] = acc[qd][v];
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();
+}
+
+template <bool LOWER>
+__device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Tile& Pk) {
+    update32_wave_to<LOWER>(C, C, Pi, Pk);
 }
 
 // Wave 0 only: factor the 32x32 tile D (lower part) and invert the factor in one pass (chol.cu:131-168).
@@ -575,9 +610,9 @@ __device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Til
 // aligned bl + 32), alternating between two buffers (bl0, bl1) so that no barrier is needed: the compiler
 // may interleave a column's update with the next pivot's chain. No lane-dependent selects: their masks would all be
 // hoisted and spilled. Writes the factor to dl (the upper triangle is left unspecified: publishers zero it) and the
-// inverse to Li.
+// inverse to Li, and the inverse also to global memory at gli (row stride ldg; the stores are left in flight).
 __device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, const Tile& id, const Tile& D,
-                                             float tau, Tile& dl, Tile& Li) {
+                                             float tau, Tile& dl, Tile& Li, float* gli, int ldg) {
     const int lane = threadIdx.x & 63, i = lane & 31;
     const bool fl = lane < 32;
     const float* src = fl ? &D[i][0] : &id[i][0];
@@ -618,6 +653,10 @@ __device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, 
         }
     }
     __builtin_amdgcn_wave_barrier();
+    if (!fl) {   // the inverse, row-major from its column lanes, to gli (row stride ldg) for the other workgroups
+#pragma unroll
+        for (int k = 0; k < CB; ++k) gli[(size_t)k * ldg + i] = R[k];
+    }
     float* dst = fl ? &dl[i][0] : &Li[0][i];
     const int step = fl ? 1 : TS;
 #pragma unroll
@@ -634,6 +673,25 @@ __device__ __forceinline__ void wait_flag(const uint32_t* f, uint32_t ep, uint32
     while (!dead && __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != ep) {
         if (++n > SPIN_LIMIT) {
             __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            dead = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// Poll up to 64 agent-scope flags at once, each lane watching its own (`mine`; nullptr: nothing to wait for), until
+// all hold `ep` (bounded), then acquire. Called by a whole wavefront; costs one round trip after the last publication
+// instead of one per flag.
+__device__ __forceinline__ void wait_flags_wave(const uint32_t* mine, uint32_t ep, uint32_t* err, bool& dead) {
+    const int lane = threadIdx.x & 63;
+    uint32_t polls = 0;
+    while (!dead) {
+        const bool ok = mine == nullptr || __hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ep;
+        if (__all(ok)) break;
+        if (++polls > SPIN_LIMIT) {
+            if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             dead = true;
             break;
         }
@@ -676,13 +734,13 @@ __device__ __forceinline__ void wave_group_barrier(uint32_t* ctr, uint32_t targe
 }
 
 constexpr int CH_MAXROW = 16;      // tiles in a tile row at most (r <= 512)
-constexpr int CH_WG0_TILES = 19;   // workgroup 0: D[2], X1, R2[5], dl[2], li[2], P1[2], P2[2], C2[2], id
+constexpr int CH_WG0_TILES = 24;   // workgroup 0: D[2], X1, R2[2][5], dl[2], li[2], P1[2], P2[2], C2[2], id
 
 struct CholWG0 {
     Tile D[2];      // D[j & 1]: T(j, j) through block j-1 (factored at step j); D[(j+1) & 1]: T(j+1, j+1)
     Tile X1;        // T(j+1, j) through block j-1 (its panel is L(j+1, j))
-    Tile R2[5];     // tile row j+2: T(j+2, j-1..j+2) as handed over (through block j-2), then through block j-1;
-                    // R2[4] = L(j+2, j-2): the owner's last panel of row j+2
+    Tile R2[2][5];  // R2[j & 1]: tile row j+2: T(j+2, j-1..j+2) as handed over (through block j-2), then through
+                    // block j-1; [4] = L(j+2, j-2): the owner's last panel of row j+2. Read again at step j+1.
     Tile dl[2];     // L(j, j)
     Tile li[2];     // Li_j
     Tile P1[2];     // L(j+1, j)
@@ -730,7 +788,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     bool dead = false;
     if (STAMP && b == 0 && tid == 0) stamps[0] = wall_clock64();
     const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
-    // misc: [0..2] nrm, shift, tau; [4..5] wave-group barrier counters; [32..63] the tile factor's diagonal;
+    // misc: [0..2] nrm, shift, tau; [4] the waves 1-2 barrier counter; [32..63] the tile factor's diagonal;
     // [64..159] and [160..255] tile-factor broadcast buffers
     float* misc = reinterpret_cast<float*>(chol_lds);
     Tile* tiles = reinterpret_cast<Tile*>(misc + 256);
@@ -740,7 +798,6 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_down(s, off);
         if (lane == 0) {
             reinterpret_cast<uint32_t*>(misc)[4] = 0u;
-            reinterpret_cast<uint32_t*>(misc)[5] = 0u;
             if (nnp > 0) {
                 const float nrm = sqrtf((float)s);
                 misc[0] = nrm;
@@ -765,9 +822,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             scal[1] = tau;
         }
         CholWG0& z = *reinterpret_cast<CholWG0*>(tiles);
-        uint32_t* bar12 = reinterpret_cast<uint32_t*>(misc + 4);    // waves 1-2 barrier counter (zeroed below)
-        uint32_t* bar123 = reinterpret_cast<uint32_t*>(misc + 5);   // waves 1-3 barrier counter
-        uint32_t n12 = 0, n123 = 0;
+        uint32_t* bar12 = reinterpret_cast<uint32_t*>(misc + 4);    // waves 1-2 barrier counter (zeroed above)
+        uint32_t n12 = 0;
         for (int e = tid; e < CB * CB; e += 256) z.id[e >> 5][e & 31] = ((e >> 5) == (e & 31)) ? 1.0f : 0.0f;
         load_tile(z.D[0], A, r, true, shift);
         if (nb > 1) {
@@ -776,20 +832,20 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         }
         __syncthreads();
         // wave 3: publish L(j, j), Li_j, L(j+1, j), L(j+2, j) of step j (parity q = j & 1)
+        // What the owners need for column block j -- Li_j, T(j+1, j) and T(j+2, j) through block j-1 -- goes into
+        // the slots (j..j+2, j) of A, which nothing reads any more (row j was fetched at step j-2, rows j+1 and j+2
+        // at steps j-1 and j; rows 1 and 2 are still the Gram's there at step 0), each stored by the wave that
+        // finishes it during step j (wave 0: Li_j; wave 3: T(j+1, j); wave 1: T(j+2, j)) and completed before the
+        // look-ahead's last barrier. Wave 3, at the start of step j+1: release them, then the outputs of step j
+        // (L(j, j), Li_j, L(j+1, j), L(j+2, j) and their packed forms), which only later kernels read.
         auto publish = [&](int j) {
             const int q = j & 1;
             const size_t o = (size_t)CB * j;
+            if (lane == 0) publish_flag(flagL + j * nb + j, ep);
             store_tile_lower(L + o * r + o, r, z.dl[q], false, lane, 64);
             store_tile(Li + o * CB, CB, z.li[q], lane, 64);
             if (j + 1 < nb) store_tile(L + (o + CB) * r + o, r, z.P1[q], lane, 64);
             if (j + 2 < nb) store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
-            if (lane == 0) {
-                release();
-                set_flag(flagL + j * nb + j, ep);
-                if (j + 1 < nb) set_flag(flagL + (j + 1) * nb + j, ep);
-                if (j + 2 < nb) set_flag(flagL + (j + 2) * nb + j, ep);
-            }
-            // the solve's packed operands: read only by later kernels, so after the release
             store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[q], lane, 64);
             if (j + 1 < nb) store_tile_op(Lp + (size_t)op_pair(j + 1, j) * CB * CB, z.P1[q], lane, 64);
             if (j + 2 < nb) store_tile_op(Lp + (size_t)op_pair(j + 2, j) * CB * CB, z.P2[q], lane, 64);
@@ -798,83 +854,66 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             const int p = j & 1, pp = p ^ 1;
             if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
             if (w == 0) {
-                factor_inv32(bl0, bl1, pq, z.id, z.D[p], tau, z.dl[p], z.li[p]);
+                factor_inv32(bl0, bl1, pq, z.id, z.D[p], tau, z.dl[p], z.li[p], A + (size_t)CB * j * r + CB * j, r);
             } else {
-                // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram). Waves 1-2 fetch it
-                // while wave 3 publishes the previous step; then L(j+2, j-1) (wave 1) and the block j-2 update of
-                // T(j+2, j+1) that its owner left (wave 2); then block j-1 on T(j+2, j) (wave 1), T(j+2, j+1)
-                // (wave 2) and T(j+2, j+2) (wave 3, which then publishes L(j+2, j-1)).
+                // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p]. Wave 3
+                // publishes the previous step, then applies the part of the previous step's look-ahead that this
+                // step's factor does not need: block j-1 on T(j+1, j) (into X1) and T(j+1, j+1) (into D[pp]), from
+                // row j+1 as R2[pp] holds it. Waves 1-2 fetch row j+2; then L(j+2, j-1) (wave 1) and the block j-2
+                // update of T(j+2, j+1) that its owner left (wave 2); then block j-1 on T(j+2, j) and T(j+2, j+2)
+                // (wave 1) and on T(j+2, j+1) (wave 2).
+                Tile* R2 = z.R2[p];
                 const bool row2 = j + 2 < nb;
                 if (w == 3) {
                     if (j >= 1) publish(j - 1);
+                    if (j >= 1 && j + 1 < nb) {
+                        const Tile* R1 = z.R2[pp];
+                        update32_wave_to<false>(z.X1, R1[2], z.P2[pp], z.P1[pp]);      // T(j+1, j)
+                        store_tile(A + (size_t)CB * (j + 1) * r + CB * j, r, z.X1, lane, 64);
+                        update32_wave_to<true>(z.D[pp], R1[3], z.P2[pp], z.P2[pp]);    // T(j+1, j+1)
+                    }
                 } else if (row2) {
                     const int i2 = j + 2, wl = (w - 1) * 64 + lane;
                     const float* rowp = A + (size_t)CB * i2 * r;
                     if (j <= 1) {
                         const int t0 = (j == 0) ? 1 : 0;     // row 2: T(2, 0..2) into R2[1..3]; row 3: T(3, 0..3)
-                        load_tiles<4, 128>(&z.R2[t0], 4 - t0, r, 1u << (3 - t0), shift, wl,
+                        load_tiles<4, 128>(&R2[t0], 4 - t0, r, 1u << (3 - t0), shift, wl,
                                            [&](int q) { return rowp + CB * (j - 1 + t0 + q); });
                     } else {
                         if (lane == 0) wait_flag(flagT + i2, ep, err, dead);
                         __builtin_amdgcn_wave_barrier();
                         const float* hp = L + (size_t)CB * i2 * r + (size_t)CB * (j - 2);     // into R2[4] = H
-                        load_tiles<5, 128>(&z.R2[0], 5, r, 0u, 0.f, wl,
+                        load_tiles<5, 128>(&R2[0], 5, r, 0u, 0.f, wl,
                                            [&](int q) { return q < 4 ? rowp + CB * (j - 1 + q) : hp; });
                     }
                     wave_group_barrier(bar12, 2 * ++n12, err, dead);
                     if (j >= 1) {
                         if (w == 1)
-                            panel32_wave(z.C2[p], z.R2[0], z.li[pp]);                  // L(j+2, j-1)
+                            panel32_wave(z.C2[p], R2[0], z.li[pp]);                    // L(j+2, j-1)
                         else if (j >= 2)
-                            update32_wave<false>(z.R2[2], z.R2[4], z.C2[pp]);  // T(j+2, j+1), block j-2 (owner skips it)
-                    }
-                }
-                if (row2 && j >= 1) {
-                    wave_group_barrier(bar123, 3 * ++n123, err, dead);
-                    if (w == 1) {
-                        update32_wave<false>(z.R2[1], z.C2[p], z.P1[pp]);              // T(j+2, j), block j-1
-                    } else if (w == 2) {
-                        update32_wave<false>(z.R2[2], z.C2[p], z.P2[pp]);              // T(j+2, j+1)
-                    } else {
-                        update32_wave<true>(z.R2[3], z.C2[p], z.C2[p]);                // T(j+2, j+2)
-                        // the owners of rows j+4.. need L(j+2, j-1) for block j-1
-                        const size_t o = (size_t)CB * (j - 1);
-                        store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
-                        if (lane == 0) publish_flag(flagL + (j + 2) * nb + j - 1, ep);
-                        store_tile_op(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], lane, 64);
+                            update32_wave<false>(R2[2], R2[4], z.C2[pp]);      // T(j+2, j+1), block j-2 (owner skips it)
+                        wave_group_barrier(bar12, 2 * ++n12, err, dead);
+                        if (w == 1) {
+                            update32_wave<false>(R2[1], z.C2[p], z.P1[pp]);            // T(j+2, j), block j-1
+                            store_tile(A + (size_t)CB * (j + 2) * r + CB * j, r, R2[1], lane, 64);
+                            update32_wave<true>(R2[3], z.C2[p], z.C2[p]);              // T(j+2, j+2)
+                        } else {
+                            update32_wave<false>(R2[2], z.C2[p], z.P2[pp]);            // T(j+2, j+1)
+                            // L(j+2, j-1) for the output and the later kernels (the owners form their own copy)
+                            const size_t o = (size_t)CB * (j - 1);
+                            store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
+                            store_tile_op(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], lane, 64);
+                        }
                     }
                 }
             }
             __syncthreads();
             if (STAMP && tid == 0) stamps[2 + 4 * j] = wall_clock64();
+            // look-ahead, the part the next factor needs: L(j+1, j) (and L(j+2, j), in the same phase), then block j
+            // on T(j+1, j+1); block j on tile row j+2 is left to wave 3 of the next step
             if (j + 2 < nb) {
-                panel32x2(z.P1[p], z.X1, z.P2[p], z.R2[1], z.li[p]);            // L(j+1, j), L(j+2, j)
-                {
-                    WAVE_COORDS;   // the three updates of block j, one phase
-                    f32x4 a1, a2, a3;
-                    const bool up = (bi == 0 && bj == 1);
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        a1[v] = z.D[pp][16 * bi + 4 * lk + v][16 * bj + l16];
-                        a2[v] = z.R2[2][16 * bi + 4 * lk + v][16 * bj + l16];
-                        a3[v] = z.R2[3][16 * bi + 4 * lk + v][16 * bj + l16];
-                    }
-#pragma unroll
-                    for (int kk = 0; kk < 8; ++kk) {
-                        const float p1i = z.P1[p][16 * bi + l16][4 * kk + lk], p1k = z.P1[p][16 * bj + l16][4 * kk + lk];
-                        const float p2i = z.P2[p][16 * bi + l16][4 * kk + lk], p2k = z.P2[p][16 * bj + l16][4 * kk + lk];
-                        a1 = mfma(-p1i, p1k, a1);      // T(j+1, j+1) -= L(j+1, j) L(j+1, j)^T
-                        a2 = mfma(-p2i, p1k, a2);      // T(j+2, j+1) -= L(j+2, j) L(j+1, j)^T
-                        a3 = mfma(-p2i, p2k, a3);      // T(j+2, j+2) -= L(j+2, j) L(j+2, j)^T
-                    }
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        if (!up) z.D[pp][16 * bi + 4 * lk + v][16 * bj + l16] = a1[v];
-                        z.X1[16 * bi + 4 * lk + v][16 * bj + l16] = a2[v];
-                        if (!up) z.D[p][16 * bi + 4 * lk + v][16 * bj + l16] = a3[v];
-                    }
-                    __syncthreads();
-                }
+                panel32x2(z.P1[p], z.X1, z.P2[p], z.R2[p][1], z.li[p]);        // L(j+1, j), L(j+2, j)
+                update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true);
             } else if (j + 1 < nb) {
                 panel32(z.P1[p], z.X1, z.li[p]);
                 update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true);
@@ -888,44 +927,82 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         const int i = b + 3;
         Tile* rt = tiles;
         Tile* op = tiles + nb;
-        Tile& lij = op[nb - 1];              // Li_j (op[k] is used for k < i <= nb - 1 only)
         load_tiles<CH_MAXROW, 256>(rt, i + 1, r, 1u << i, shift, tid,
                                    [&](int q) { return A + (size_t)CB * i * r + (size_t)CB * q; });
         for (int j = 0; j + 4 <= i; ++j) {
-            // panel L(i, j) = T(i, j) Li_j^T
+            // workgroup 0's block j: Li_j into op[j], T(j+1, j) and T(j+2, j) (through block j-1) into op[j+1..j+2]
             if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead);
             __syncthreads();
-            load_tile(lij, Li + (size_t)CB * j * CB, CB, false, 0.f);
+            load_tiles<3, 256>(&op[j], 3, r, 0u, 0.f, tid,
+                               [&](int q) { return A + (size_t)CB * (j + q) * r + (size_t)CB * j; });
             __syncthreads();
+            const Tile& lij = op[j];
+            // panel L(i, j) = T(i, j) Li_j^T, published before anything else (so no row waits on a chain of rows)
             panel32(rt[j], rt[j], lij);
             store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j]);
-            // publish L(i, j) before waiting on the other rows (so no row waits on a chain of rows)
             __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
             __syncthreads();
             if (tid == 0) publish_flag(flagL + i * nb + j, ep);
             store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j]);   // for later kernels only
-            // block j's panels of the rows between: L(k, j), k = j+1..i-1, all fetched before the updates. At the
-            // last block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed.
+            // block j's panels of the rows between: L(k, j), k = j+1..i-1, all in LDS before the updates. At the
+            // last block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed. Rows j+1 and j+2
+            // are workgroup 0's: their panels are formed here, as workgroup 0 forms them. Row j+3 has just been
+            // handed to workgroup 0 (before block j; row 3 never had an owner): its panel too is formed here, from
+            // the handed-over T(j+3, j). Rows j+4.. publish their own.
+            panel32x2_inplace(op[j + 1], op[j + 2], lij);                 // L(j+1, j), L(j+2, j)
             const int kend = (j + 4 == i) ? i - 1 : i;
-            if (tid == 0)
-                for (int k = j + 1; k < kend; ++k) wait_flag(flagL + k * nb + j, ep, err, dead);
+            const bool own3 = j + 3 < kend;
+            if (w == 0) {
+                const int k = j + 3 + lane;
+                const uint32_t* f = nullptr;
+                if (k < kend) f = (k != j + 3) ? flagL + k * nb + j : (k >= 4 ? flagT + k : nullptr);
+                wait_flags_wave(f, ep, err, dead);
+            }
             __syncthreads();
-            load_tiles<CH_MAXROW, 256>(&op[j + 1], kend - j - 1, r, 0u, 0.f, tid,
-                                       [&](int q) { return L + (size_t)CB * (j + 1 + q) * r + (size_t)CB * j; });
+            load_tiles<CH_MAXROW, 256>(&op[j + 3], kend - j - 3, r, 0u, 0.f, tid, [&](int q) {
+                const int k = j + 3 + q;
+                return (k == j + 3 ? A : L) + (size_t)CB * k * r + (size_t)CB * j;
+            });
             __syncthreads();
+            if (own3) panel32(op[j + 3], op[j + 3], lij);     // L(j+3, j)
             {
-                WAVE_COORDS;   // every tile's quadrant (bi, bj) in one phase: the tiles are independent
-                for (int k = j + 1; k <= i; ++k) {
-                    if ((j + 4 == i && k == i - 1) || (k == i && bi == 0 && bj == 1)) continue;
+                // every tile's quadrant (bi, bj) in one phase (the tiles are independent): the panel's A operands stay
+                // in registers, and the next tile's B operands and accumulator are read while this tile's chain runs
+                WAVE_COORDS;
+                float an[8];
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) an[kk] = -rt[j][16 * bi + l16][4 * kk + lk];
+                const bool upq = (bi == 0 && bj == 1);
+                auto next_k = [&](int k) {
+                    ++k;
+                    if (j + 4 == i && k == i - 1) ++k;
+                    if (k == i && upq) ++k;
+                    return k;
+                };
+                auto fetch = [&](int k, float (&bv)[8], f32x4& acc) {
                     const Tile& Pk = (k == i) ? rt[j] : op[k];
-                    f32x4 acc;
+#pragma unroll
+                    for (int kk = 0; kk < 8; ++kk) bv[kk] = Pk[16 * bj + l16][4 * kk + lk];
 #pragma unroll
                     for (int v = 0; v < 4; ++v) acc[v] = rt[k][16 * bi + 4 * lk + v][16 * bj + l16];
+                };
+                int k = next_k(j);
+                float bv[8];
+                f32x4 acc;
+                if (k <= i) fetch(k, bv, acc);
+                while (k <= i) {
+                    const int kn = next_k(k);
+                    float bn[8];
+                    f32x4 accn;
+                    if (kn <= i) fetch(kn, bn, accn);
 #pragma unroll
-                    for (int kk = 0; kk < 8; ++kk)
-                        acc = mfma(-rt[j][16 * bi + l16][4 * kk + lk], Pk[16 * bj + l16][4 * kk + lk], acc);
+                    for (int kk = 0; kk < 8; ++kk) acc = mfma(an[kk], bv[kk], acc);
 #pragma unroll
                     for (int v = 0; v < 4; ++v) rt[k][16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+                    k = kn;
+#pragma unroll
+                    for (int kk = 0; kk < 8; ++kk) bv[kk] = bn[kk];
+                    acc = accn;
                 }
                 __syncthreads();
             }
