@@ -428,6 +428,32 @@ __device__ __forceinline__ void load_tiles(Tile* dst, int n, int ld, uint32_t di
             }
 }
 
+// As load_tiles, without diagonal shifts, tile q from srcf(q) with row stride ldf(q)
+template <int NMAX, int NTHR, class SrcF, class LdF>
+__device__ __forceinline__ void load_tiles_ld(Tile* dst, int n, int t, SrcF srcf, LdF ldf) {
+    constexpr int PER = 256 / NTHR;
+    float4 v[NMAX][PER];
+#pragma unroll
+    for (int q = 0; q < NMAX; ++q)
+        if (q < n)
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const int e = t + u * NTHR, row = e >> 3, c4 = e & 7;
+                v[q][u] = *reinterpret_cast<const float4*>(srcf(q) + (size_t)row * ldf(q) + 4 * c4);
+            }
+#pragma unroll
+    for (int q = 0; q < NMAX; ++q)
+        if (q < n)
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const int e = t + u * NTHR, row = e >> 3, c4 = e & 7;
+                dst[q][row][4 * c4 + 0] = v[q][u].x;
+                dst[q][row][4 * c4 + 1] = v[q][u].y;
+                dst[q][row][4 * c4 + 2] = v[q][u].z;
+                dst[q][row][4 * c4 + 3] = v[q][u].w;
+            }
+}
+
 // the lower triangle of a diagonal tile (zeros above the diagonal), straight and transposed
 __device__ __forceinline__ void store_tile_lower(float* dst, int ld, const Tile& src, bool transpose, int t, int nthr) {
     for (int e = t; e < 256; e += nthr) {
@@ -610,9 +636,9 @@ __device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Til
 // aligned bl + 32), alternating between two buffers (bl0, bl1) so that no barrier is needed: the compiler
 // may interleave a column's update with the next pivot's chain. No lane-dependent selects: their masks would all be
 // hoisted and spilled. Writes the factor to dl (the upper triangle is left unspecified: publishers zero it) and the
-// inverse to Li, and the inverse also to global memory at gli (row stride ldg; the stores are left in flight).
+// inverse to Li, and the inverse also to global memory at gli (row stride 32; the stores are left in flight).
 __device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, const Tile& id, const Tile& D,
-                                             float tau, Tile& dl, Tile& Li, float* gli, int ldg) {
+                                             float tau, Tile& dl, Tile& Li, float* gli) {
     const int lane = threadIdx.x & 63, i = lane & 31;
     const bool fl = lane < 32;
     const float* src = fl ? &D[i][0] : &id[i][0];
@@ -653,9 +679,9 @@ __device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, 
         }
     }
     __builtin_amdgcn_wave_barrier();
-    if (!fl) {   // the inverse, row-major from its column lanes, to gli (row stride ldg) for the other workgroups
+    if (!fl) {   // the inverse, row-major (row stride 32) from its column lanes, to gli for the other workgroups
 #pragma unroll
-        for (int k = 0; k < CB; ++k) gli[(size_t)k * ldg + i] = R[k];
+        for (int k = 0; k < CB; ++k) gli[k * CB + i] = R[k];
     }
     float* dst = fl ? &dl[i][0] : &Li[0][i];
     const int step = fl ? 1 : TS;
@@ -832,18 +858,17 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         }
         __syncthreads();
         // wave 3: publish L(j, j), Li_j, L(j+1, j), L(j+2, j) of step j (parity q = j & 1)
-        // What the owners need for column block j -- Li_j, T(j+1, j) and T(j+2, j) through block j-1 -- goes into
-        // the slots (j..j+2, j) of A, which nothing reads any more (row j was fetched at step j-2, rows j+1 and j+2
-        // at steps j-1 and j; rows 1 and 2 are still the Gram's there at step 0), each stored by the wave that
+        // What the owners need for column block j -- Li_j (into its place in Li), T(j+1, j) and T(j+2, j) through
+        // block j-1 (into the slots (j+1..j+2, j) of A, which nothing reads any more: rows j+1 and j+2 were fetched
+        // at steps j-1 and j; rows 1 and 2 are still the Gram's there at step 0) -- is stored by the wave that
         // finishes it during step j (wave 0: Li_j; wave 3: T(j+1, j); wave 1: T(j+2, j)) and completed before the
         // look-ahead's last barrier. Wave 3, at the start of step j+1: release them, then the outputs of step j
-        // (L(j, j), Li_j, L(j+1, j), L(j+2, j) and their packed forms), which only later kernels read.
+        // (L(j, j), L(j+1, j), L(j+2, j) and the packed forms), which only later kernels read.
         auto publish = [&](int j) {
             const int q = j & 1;
             const size_t o = (size_t)CB * j;
             if (lane == 0) publish_flag(flagL + j * nb + j, ep);
             store_tile_lower(L + o * r + o, r, z.dl[q], false, lane, 64);
-            store_tile(Li + o * CB, CB, z.li[q], lane, 64);
             if (j + 1 < nb) store_tile(L + (o + CB) * r + o, r, z.P1[q], lane, 64);
             if (j + 2 < nb) store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
             store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[q], lane, 64);
@@ -854,7 +879,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             const int p = j & 1, pp = p ^ 1;
             if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
             if (w == 0) {
-                factor_inv32(bl0, bl1, pq, z.id, z.D[p], tau, z.dl[p], z.li[p], A + (size_t)CB * j * r + CB * j, r);
+                factor_inv32(bl0, bl1, pq, z.id, z.D[p], tau, z.dl[p], z.li[p], Li + (size_t)CB * j * CB);
             } else {
                 // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p]. Wave 3
                 // publishes the previous step, then applies the part of the previous step's look-ahead that this
@@ -933,8 +958,12 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             // workgroup 0's block j: Li_j into op[j], T(j+1, j) and T(j+2, j) (through block j-1) into op[j+1..j+2]
             if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead);
             __syncthreads();
-            load_tiles<3, 256>(&op[j], 3, r, 0u, 0.f, tid,
-                               [&](int q) { return A + (size_t)CB * (j + q) * r + (size_t)CB * j; });
+            load_tiles_ld<3, 256>(&op[j], 3, tid,
+                                  [&](int q) {
+                                      return q == 0 ? Li + (size_t)CB * j * CB
+                                                    : A + (size_t)CB * (j + q) * r + (size_t)CB * j;
+                                  },
+                                  [&](int q) { return q == 0 ? CB : r; });
             __syncthreads();
             const Tile& lij = op[j];
             // panel L(i, j) = T(i, j) Li_j^T, published before anything else (so no row waits on a chain of rows)
