@@ -13,6 +13,7 @@ All builders return CPU tensors; the caller moves them to the device.
 """
 import math
 from dataclasses import dataclass, field
+from pathlib import Path
 
 import torch
 
@@ -219,3 +220,21 @@ def adversarial(K, r, seed=0):
     out["cond1e8_x1e-25"] = _finish(base * 1e-25)
     out["cond1e8_x1e25"] = _finish(base * 1e25)
     return out
+
+
+# ---- matrices dumped from a training run (qrbench/gen.py:185-194) ----
+
+def real_cases(dump_dir="dumps", shape=None):
+    """Case per *.pt file under dump_dir (recursively, sorted), as written by spanqr_amd.qrbench.dump or the
+    reference's qrbench.dump: a dict with 'X' and optionally 'V' (the previous basis, kept in ctx), or a bare tensor.
+    shape: only files whose X is [K, r] = shape. Loaded with torch.load(weights_only=True); CPU fp32 tensors."""
+    root = Path(dump_dir)
+    for p in sorted(root.rglob("*.pt")):
+        d = torch.load(p, map_location="cpu", weights_only=True)
+        X = d["X"] if isinstance(d, dict) else d
+        if shape is not None and tuple(X.shape) != tuple(shape):
+            continue
+        ctx = {}
+        if isinstance(d, dict) and d.get("V") is not None:
+            ctx["V"] = d["V"].float().contiguous()
+        yield Case(f"real/{p.relative_to(root).with_suffix('')}", X.float().contiguous(), ctx, True)
