@@ -118,13 +118,30 @@ __global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, 
     uint32_t m = 0;
     const int r4 = r >> 2;
     const int n4 = K * r4;
-    for (int e = blockIdx.x * 256 + threadIdx.x; e < n4; e += gridDim.x * 256) {
-        const int row = e / r4, c4 = e - row * r4;
-        const float4 v = *reinterpret_cast<const float4*>(X + (size_t)row * ldx + 4 * c4);
+    const int stride = gridDim.x * 256;
+    auto amax4 = [](const float4 v) {
         const uint32_t a = __float_as_uint(v.x) & 0x7fffffffu, b = __float_as_uint(v.y) & 0x7fffffffu;
         const uint32_t c = __float_as_uint(v.z) & 0x7fffffffu, d = __float_as_uint(v.w) & 0x7fffffffu;
-        const uint32_t ab = a > b ? a : b, cd = c > d ? c : d, abcd = ab > cd ? ab : cd;
-        m = abcd > m ? abcd : m;
+        const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
+        return ab > cd ? ab : cd;
+    };
+    // four independent loads in flight per thread (one memory latency per four strides, not one per stride)
+    for (int e0 = blockIdx.x * 256 + threadIdx.x; e0 < n4; e0 += 4 * stride) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = e0 + u * stride;
+            v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (e < n4) {
+                const int row = e / r4, c4 = e - row * r4;
+                v[u] = *reinterpret_cast<const float4*>(X + (size_t)row * ldx + 4 * c4);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t a = amax4(v[u]);
+            m = a > m ? a : m;
+        }
     }
     for (int off = 32; off >= 1; off >>= 1) {
         const uint32_t o = (uint32_t)__shfl_xor((int)m, off);
@@ -331,10 +348,10 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 //     plus the owner's panel L(j+2, j-2)) while wave 3 publishes the previous step's L tiles and Li; then wave 1
 //     forms the panel L(j+2, j-1) (the previous step's Li_{j-1}, L(j, j-1), L(j+1, j-1) are still in LDS), wave 2
 //     applies the block j-2 update of T(j+2, j+1) that the owner leaves out, and the two waves apply block j-1 to
-//     T(j+2, j), T(j+2, j+2) (wave 1) and T(j+2, j+1) (wave 2); wave 3, after publishing, applies block j-1 to
-//     T(j+1, j) and T(j+1, j+1). Then all waves form the panels L(j+1, j), L(j+2, j) and apply column block j to
-//     T(j+1, j+1), the tile the next step factors (look-ahead over the next two tile rows; block j on the rest of
-//     row j+2 is wave 3's work in the next step).
+//     T(j+2, j) and the lower half of T(j+2, j+2) (wave 1), T(j+2, j+1) and the rest (wave 2); wave 3, after
+//     publishing, applies block j-1 to T(j+1, j) and T(j+1, j+1). Then all waves form the panels L(j+1, j),
+//     L(j+2, j) and apply column block j to T(j+1, j+1), the tile the next step factors (look-ahead over the next two
+//     tile rows; block j on the rest of row j+2 is wave 3's work in the next step).
 //   * Workgroup i-3 owns tile row i >= 4 for the whole factorisation, in LDS. For column block j = 0..i-4 in order:
 //     panel L(i, j) = T(i, j) Li_j^T (published), then T(i, k) -= L(i, j) L(k, j)^T for k = j+1..i with the other
 //     rows' panels of block j fetched together (at its last block, j = i-4, T(i, i-1) is left to workgroup 0); after
@@ -584,10 +601,10 @@ __device__ __forceinline__ void panel32_wave(Tile& out, const Tile& in, const Ti
     __builtin_amdgcn_wave_barrier();
 }
 
-// One wave, a whole 32x32 tile: dst = C - Pi Pk^T (LOWER: the upper 16x16 block is left alone; dst may alias C);
+// One wave: dst = C - Pi Pk^T on the 16x16 quadrants qd = 2 bi + bj whose bit is set in QM (dst may alias C);
 // operands read once, the quadrants' chains (over m = 0..31 from C) interleaved.
-template <bool LOWER>
-__device__ __forceinline__ void update32_wave_to(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk) {
+template <int QM>
+__device__ __forceinline__ void update32_wave_q(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk) {
     const int lane = threadIdx.x & 63, l16 = lane & 15, lk = lane >> 4;
     float a[2][8], b[2][8];
 #pragma unroll
@@ -606,19 +623,24 @@ __device__ __forceinline__ void update32_wave_to(Tile& dst, const Tile& C, const
     for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd)
-            if (!(LOWER && qd == 1)) acc[qd] = mfma(a[qd >> 1][kk], b[qd & 1][kk], acc[qd]);
+            if ((QM >> qd) & 1) acc[qd] = mfma(a[qd >> 1][kk], b[qd & 1][kk], acc[qd]);
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd)
-        if (!(LOWER && qd == 1))
+        if ((QM >> qd) & 1)
 #pragma unroll
             for (int v = 0; v < 4; ++v) dst[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16] = acc[qd][v];
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();
 }
 
+// whole tile (LOWER: without the upper 16x16 block), in place or to dst
+template <bool LOWER>
+__device__ __forceinline__ void update32_wave_to(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk) {
+    update32_wave_q<LOWER ? 0xD : 0xF>(dst, C, Pi, Pk);
+}
 template <bool LOWER>
 __device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Tile& Pk) {
-    update32_wave_to<LOWER>(C, C, Pi, Pk);
+    update32_wave_q<LOWER ? 0xD : 0xF>(C, C, Pi, Pk);
 }
 
 // Wave 0 only: factor the 32x32 tile D (lower part) and invert the factor in one pass (chol.cu:131-168).
@@ -764,7 +786,7 @@ constexpr int CH_WG0_TILES = 24;   // workgroup 0: D[2], X1, R2[2][5], dl[2], li
 
 struct CholWG0 {
     Tile D[2];      // D[j & 1]: T(j, j) through block j-1 (factored at step j); D[(j+1) & 1]: T(j+1, j+1)
-    Tile X1;        // T(j+1, j) through block j-1 (its panel is L(j+1, j))
+    Tile X1;        // T(j+1, j) through block j-1 (its panel is L(j+1, j)); D[0], D[1], X1 are loaded as one batch
     Tile R2[2][5];  // R2[j & 1]: tile row j+2: T(j+2, j-1..j+2) as handed over (through block j-2), then through
                     // block j-1; [4] = L(j+2, j-2): the owner's last panel of row j+2. Read again at step j+1.
     Tile dl[2];     // L(j, j)
@@ -785,7 +807,7 @@ size_t chol_lds_bytes(int r) {
 // nb = r/32 tile rows; grid = max(1, nb - 3) workgroups. With nnp == 0 the shift is 0 and tau_rel is the absolute
 // pivot floor (chol32's contract); otherwise ||G||_F comes from the nnp fp64 partials: lane l of wave 0 sums
 // npart[l], npart[l + 64], ... in order, then a shift-down tree over the 64 lane sums; nrm = sqrtf(fp32(sum)),
-// shift = alpha * nrm added to the diagonal on first load, tau = tau_rel * nrm + 1e-30 (kcholqr.py:107-109).
+// shift = alpha * nrm added to the diagonal after the first load, tau = tau_rel * nrm + 1e-30 (kcholqr.py:107-109).
 // flags: [nb * nb] panel flags (L(i, j) published; (j, j): L(j, j) and Li_j), [nb] hand-over flags (tile row i),
 // [64] per-workgroup call counters. STAMP: workgroup 0 records wall_clock64() at 1 + 4j + s for step j: s = 0 step
 // start, 1 tile factored and row j+2 fetched, 2 look-ahead done; slot 0 is the kernel start, 1 + 4 nb the end.
@@ -818,9 +840,34 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     // [64..159] and [160..255] tile-factor broadcast buffers
     float* misc = reinterpret_cast<float*>(chol_lds);
     Tile* tiles = reinterpret_cast<Tile*>(misc + 256);
+    // Waves 1-2 load the workgroup's first tiles (workgroup 0: T(0, 0), T(1, 1), T(1, 0) into D[0], D[1], X1; an
+    // owner: its tile row) while wave 0 sums the norm partials; the diagonal shift is added once it is known (the same
+    // single addition as on a shifted load).
+    if (w == 1 || w == 2) {
+        if (b == 0) {
+            load_tiles<3, 128>(tiles, nb > 1 ? 3 : 1, r, 0u, 0.f, tid - 64, [&](int q) {
+                return A + (q == 0 ? (size_t)0 : (size_t)CB * r + (q == 1 ? CB : 0));
+            });
+        } else {
+            load_tiles<CH_MAXROW, 128>(tiles, b + 4, r, 0u, 0.f, tid - 64,
+                                       [&](int q) { return A + (size_t)CB * (b + 3) * r + (size_t)CB * q; });
+        }
+    }
+    if (w == 3 && b == 0) {
+        Tile& id = reinterpret_cast<CholWG0*>(tiles)->id;
+        for (int e = lane; e < CB * CB; e += 64) id[e >> 5][e & 31] = ((e >> 5) == (e & 31)) ? 1.0f : 0.0f;
+    }
     if (w == 0) {
+        // lane sums in index order, the partials loaded eight at a time (one memory latency per eight)
         double s = 0.0;
-        for (int p = lane; p < nnp; p += 64) s = s + npart[p];
+        for (int p0 = lane; p0 < nnp; p0 += 8 * 64) {
+            double v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = (p0 + 64 * u < nnp) ? npart[p0 + 64 * u] : 0.0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (p0 + 64 * u < nnp) s = s + v[u];
+        }
         for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_down(s, off);
         if (lane == 0) {
             reinterpret_cast<uint32_t*>(misc)[4] = 0u;
@@ -838,6 +885,15 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
     }
     __syncthreads();
     const float shift = misc[1], tau = misc[2];
+    if (tid < CB) {
+        if (b == 0) {
+            tiles[0][tid][tid] = tiles[0][tid][tid] + shift;
+            if (nb > 1) tiles[1][tid][tid] = tiles[1][tid][tid] + shift;
+        } else {
+            tiles[b + 3][tid][tid] = tiles[b + 3][tid][tid] + shift;
+        }
+    }
+    __syncthreads();
     float* pq = misc + 32;
     float* bl0 = misc + 64;
     float* bl1 = misc + 160;
@@ -850,13 +906,6 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         CholWG0& z = *reinterpret_cast<CholWG0*>(tiles);
         uint32_t* bar12 = reinterpret_cast<uint32_t*>(misc + 4);    // waves 1-2 barrier counter (zeroed above)
         uint32_t n12 = 0;
-        for (int e = tid; e < CB * CB; e += 256) z.id[e >> 5][e & 31] = ((e >> 5) == (e & 31)) ? 1.0f : 0.0f;
-        load_tile(z.D[0], A, r, true, shift);
-        if (nb > 1) {
-            load_tile(z.X1, A + (size_t)CB * r, r, false, 0.f);
-            load_tile(z.D[1], A + (size_t)CB * r + CB, r, true, shift);
-        }
-        __syncthreads();
         // wave 3: publish L(j, j), Li_j, L(j+1, j), L(j+2, j) of step j (parity q = j & 1)
         // What the owners need for column block j -- Li_j (into its place in Li), T(j+1, j) and T(j+2, j) through
         // block j-1 (into the slots (j+1..j+2, j) of A, which nothing reads any more: rows j+1 and j+2 were fetched
@@ -885,8 +934,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
                 // publishes the previous step, then applies the part of the previous step's look-ahead that this
                 // step's factor does not need: block j-1 on T(j+1, j) (into X1) and T(j+1, j+1) (into D[pp]), from
                 // row j+1 as R2[pp] holds it. Waves 1-2 fetch row j+2; then L(j+2, j-1) (wave 1) and the block j-2
-                // update of T(j+2, j+1) that its owner left (wave 2); then block j-1 on T(j+2, j) and T(j+2, j+2)
-                // (wave 1) and on T(j+2, j+1) (wave 2).
+                // update of T(j+2, j+1) that its owner left (wave 2); then block j-1 on T(j+2, j) and the lower
+                // half of T(j+2, j+2) (wave 1) and on T(j+2, j+1) and T(j+2, j+2)'s quadrant (0, 0) (wave 2).
                 Tile* R2 = z.R2[p];
                 const bool row2 = j + 2 < nb;
                 if (w == 3) {
@@ -921,9 +970,10 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
                         if (w == 1) {
                             update32_wave<false>(R2[1], z.C2[p], z.P1[pp]);            // T(j+2, j), block j-1
                             store_tile(A + (size_t)CB * (j + 2) * r + CB * j, r, R2[1], lane, 64);
-                            update32_wave<true>(R2[3], z.C2[p], z.C2[p]);              // T(j+2, j+2)
+                            update32_wave_q<0xC>(R2[3], R2[3], z.C2[p], z.C2[p]);      // T(j+2, j+2), lower half
                         } else {
                             update32_wave<false>(R2[2], z.C2[p], z.P2[pp]);            // T(j+2, j+1)
+                            update32_wave_q<0x1>(R2[3], R2[3], z.C2[p], z.C2[p]);      // T(j+2, j+2), quadrant (0, 0)
                             // L(j+2, j-1) for the output and the later kernels (the owners form their own copy)
                             const size_t o = (size_t)CB * (j - 1);
                             store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
@@ -952,8 +1002,6 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         const int i = b + 3;
         Tile* rt = tiles;
         Tile* op = tiles + nb;
-        load_tiles<CH_MAXROW, 256>(rt, i + 1, r, 1u << i, shift, tid,
-                                   [&](int q) { return A + (size_t)CB * i * r + (size_t)CB * q; });
         for (int j = 0; j + 4 <= i; ++j) {
             // workgroup 0's block j: Li_j into op[j], T(j+1, j) and T(j+2, j) (through block j-1) into op[j+1..j+2]
             if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead);
