@@ -30,7 +30,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from spanqr_amd import _lib, kcholqr_f, kcholqr_f_many, orth, stages  # noqa: E402
+from spanqr_amd import _lib, kchol, kcholqr_f, kcholqr_f_many, orth, stages  # noqa: E402
 from spanqr_amd.plan import get_plan, stream_handle  # noqa: E402
 from spanqr_amd.qrbench import gen  # noqa: E402
 
@@ -338,6 +338,21 @@ def main(argv=None):
                                "blocks": r // 256, "orth_calls_per_call": 2 * (r // 256) - 1}
         del g, q, X
         torch.cuda.synchronize()
+    # fp64 clamped Cholesky with fp32 copies (kchol.chol64; not on orth's path): HIP events around back-to-back calls
+    chol64 = {}
+    for n in (256, 512):
+        Xd = torch.randn(n + 64, n, device=dev, dtype=torch.float64, generator=torch.Generator(dev).manual_seed(n))
+        G64 = Xd.T @ Xd
+        for _ in range(2):
+            kchol.chol64(G64, 1e-12)
+        s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_.record()
+        for _ in range(10):
+            kchol.chol64(G64, 1e-12)
+        e_.record()
+        torch.cuda.synchronize()
+        chol64[str(n)] = {"us": s_.elapsed_time(e_) * 100.0}
+        del Xd, G64
     targets = {k: {"us_per_call": shapes[k]["thr_us"], "lat_us": shapes[k]["lat_us"], "orth": shapes[k]["orth"],
                    "target_us": TARGET_US[k]} for k in TARGET_US}
 
@@ -389,6 +404,7 @@ def main(argv=None):
                    "seeds": list(SEEDS), "calls_per_step": calls, "graphs": not a.no_graph},
         "orth_max": orth_max, "per_shape_us": per_shape, "per_shape_lat_us": per_shape_lat,
         "target_shapes": targets, "shapes": shapes, "blocked_shapes": blocked, "batched_layers": batched,
+        "chol64": chol64,
         "roofline": roofline, "call_roofline": call_roof, "kernels": kernels, "kernel_share": share,
         "sum_of_kernels_us": call_us, "cholesky": chol_info,
         "cpu_baseline": cpu,

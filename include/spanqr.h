@@ -169,6 +169,20 @@ int spanqr_stage_ns(spanqr_plan* plan, const float* Y, long ldy, int kahan, floa
 int spanqr_plan_copy_dust(spanqr_plan* plan, float* Z, void* stream);
 int spanqr_plan_copy_scalars(spanqr_plan* plan, float* scal8, void* stream);
 
+/* ---- fp64 clamped Cholesky (kchol.chol64, candidates/kchol.py:47-57 -> chol_f64, candidates/cuk/chol.cu:278-281) ----
+ * A plan holds the flag words of one n x n factorisation (n a multiple of 32 up to 1024); one plan per concurrent
+ * stream. spanqr_chol64: G [n, n] fp64 (lower tiles read, row stride ldg, even), tau a device pointer to the fp64
+ * pivot floor (as the reference passes it, no host synchronisation); writes L [n, n] fp64 (zeros above the
+ * diagonal), Li [n, 32] fp64 (inverses of the 32x32 diagonal tiles) and their fp32 copies Lf [n, n], Lif [n, 32].
+ * Pivots below tau (or NaN) are clamped to tau. spanqr_chol64_status synchronises the stream and reports a wait
+ * that gave up (which can only happen if not every workgroup of the launch was resident). */
+typedef struct spanqr_chol64_plan spanqr_chol64_plan;
+int spanqr_chol64_plan_create(int n, int device, spanqr_chol64_plan** out);
+void spanqr_chol64_plan_destroy(spanqr_chol64_plan* plan);
+int spanqr_chol64(spanqr_chol64_plan* plan, const double* G, long ldg, const double* tau, double* L, double* Li,
+                  float* Lf, float* Lif, void* stream);
+int spanqr_chol64_status(spanqr_chol64_plan* plan, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,6 +63,10 @@ def _bind(L):
     L.spqo_xgram.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, _f32p]
     L.spqo_project.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, _f32p, c_long]
     L.spqo_borth.argtypes = [_f32p, c_long, c_int, c_int, c_float, c_float, c_float, c_int, _f32p, c_long]
+    L.spqo_rsqrt64.argtypes = [ctypes.c_double]
+    L.spqo_rsqrt64.restype = ctypes.c_double
+    L.spqo_diag_factor64.argtypes = [_f64p, c_long, ctypes.c_double, _f64p, c_long, _f64p]
+    L.spqo_chol64.argtypes = [_f64p, c_int, ctypes.c_double, _f64p, _f64p, _f32p, _f32p]
     return L
 
 
@@ -276,3 +280,21 @@ def borth(X, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
     Q = np.empty((K, r), np.float32)
     lib().spqo_borth(X, r, K, r, float(np.float32(eps)), float(np.float32(alpha)), float(np.float32(tau)), ns, Q, r)
     return Q
+
+
+# ---- fp64 clamped Cholesky (kchol.py:47-57, chol.cu:278-281) ----
+
+def rsqrt64(x):
+    return float(lib().spqo_rsqrt64(float(x)))
+
+
+def chol64(G, tau):
+    """(L [r, r] fp64, Li [r, 32] fp64, Lf, Lif fp32 copies) of the clamped factorisation of fp64 G"""
+    A = np.ascontiguousarray(G, np.float64).copy()
+    r = A.shape[0]
+    L = np.zeros((r, r), np.float64)
+    Li = np.zeros((r, CB), np.float64)
+    Lf = np.zeros((r, r), np.float32)
+    Lif = np.zeros((r, CB), np.float32)
+    lib().spqo_chol64(A, r, float(tau), L, Li, Lf, Lif)
+    return L, Li, Lf, Lif

@@ -16,6 +16,7 @@
  *   chol32 / chol_f32           candidates/kchol.py:35-44, candidates/cuk/chol.cu:115-271
  *   trsm_f                      candidates/tri.py:378-412
  *   _ns_mm                      candidates/kcholqr.py:16-23
+ *   chol64 / chol_f64           candidates/kchol.py:47-57, candidates/cuk/chol.cu:115-281 (the fp64 instantiation)
  *
  * Arithmetic contract. Every floating-point operation is written out: fmaf() where a fused multiply-add is meant,
  * separate operations elsewhere (built with -ffp-contract=off, no -ffast-math). Each output element is produced by
@@ -560,4 +561,93 @@ void spqo_borth(const float* X, long ldx, int K, int r, float eps, float alpha, 
         }
     }
     free(Zf); free(W);
+}
+
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* fp64 clamped Cholesky (kchol.chol64, kchol.py:47-57 -> chol_f64, chol.cu:278-281): the same tile algorithm as  */
+/* spqo_chol in double -- 32-wide diagonal tiles, pivots fmax(D_cc, tau) (NaN -> tau), tile inverses by forward */
+/* substitution, panels A Li^T over m < mend(b), trailing updates as fma chains over the block's 32 columns from */
+/* A -- plus fp32 copies of L and Li (chol.cu:175-176, 215, 255: (float) of each fp64 value). The reciprocal     */
+/* square root (CUDA's rsqrt in the reference) is this project's own: start 0x5FE6EB50C7B537A9 - (bits >> 1),    */
+/* then four Newton steps y <- y * (1.5 - (0.5x * y) * y), the bracket as one fma.                              */
+/* ------------------------------------------------------------------------------------------------------------ */
+static inline uint64_t d2u(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
+static inline double u2d(uint64_t u) { double d; memcpy(&d, &u, 8); return d; }
+
+double spqo_rsqrt64(double x) {
+    double y = u2d(0x5FE6EB50C7B537A9ull - (d2u(x) >> 1));
+    const double h = 0.5 * x;
+    for (int it = 0; it < 4; ++it) {
+        double t = h * y;
+        t = fma(-t, y, 1.5);
+        y = y * t;
+    }
+    return y;
+}
+
+void spqo_diag_factor64(double* D, long ld, double tau, double* L, long ldl, double* Li) {
+    double rd[CB], lc[CB];
+    for (int c = 0; c < CB; ++c) {
+        double piv = fmax(D[(size_t)c * ld + c], tau);
+        double q = spqo_rsqrt64(piv);
+        rd[c] = q;
+        lc[c] = piv * q;
+        for (int i = c + 1; i < CB; ++i) lc[i] = D[(size_t)i * ld + c] * q;
+        for (int i = 0; i < CB; ++i) L[(size_t)i * ldl + c] = (i >= c) ? lc[i] : 0.0;
+        for (int k = c + 1; k < CB; ++k)
+            for (int i = k; i < CB; ++i) D[(size_t)i * ld + k] = fma(-lc[i], lc[k], D[(size_t)i * ld + k]);
+    }
+    for (int kk = 0; kk < CB; ++kk) {
+        double x[CB];
+        for (int i = 0; i < CB; ++i) {
+            double acc = (i == kk) ? 1.0 : 0.0;
+            for (int m = 0; m < i; ++m) acc = fma(-L[(size_t)i * ldl + m], x[m], acc);
+            x[i] = (i < kk) ? 0.0 : acc * rd[i];
+        }
+        for (int i = 0; i < CB; ++i) Li[i * CB + kk] = x[i];
+    }
+}
+
+/* A: r x r (lower tiles read; destroyed). L: r x r fp64 (upper triangle zero), Li: r x 32; Lf, Lif their fp32 copies */
+void spqo_chol64(double* A, int r, double tau, double* L, double* Li, float* Lf, float* Lif) {
+    fp_env();
+    const int nb = r / CB;
+    memset(L, 0, (size_t)r * r * sizeof(double));
+    double* P = (double*)malloc((size_t)r * CB * sizeof(double));
+    for (int j = 0; j < nb; ++j) {
+        double* Dj = A + (size_t)(j * CB) * r + j * CB;
+        double* Lj = L + (size_t)(j * CB) * r + j * CB;
+        double* Lij = Li + (size_t)(j * CB) * CB;
+        spqo_diag_factor64(Dj, r, tau, Lj, r, Lij);
+        #pragma omp parallel for schedule(static)
+        for (int i = j + 1; i < nb; ++i) {
+            fp_env();
+            for (int a = 0; a < CB; ++a)
+                for (int b = 0; b < CB; ++b) {
+                    double acc = 0.0;
+                    for (int m = 0; m < mend(b); ++m)
+                        acc = fma(A[(size_t)(i * CB + a) * r + j * CB + m], Lij[b * CB + m], acc);
+                    P[(size_t)(i * CB + a) * CB + b] = acc;
+                    L[(size_t)(i * CB + a) * r + j * CB + b] = acc;
+                }
+        }
+        #pragma omp parallel for schedule(dynamic, 1)
+        for (int i = j + 1; i < nb; ++i) {
+            fp_env();
+            for (int k = j + 1; k <= i; ++k)
+                for (int a = 0; a < CB; ++a)
+                    for (int b = 0; b < CB; ++b) {
+                        if (i == k && b > a) continue;
+                        double acc = A[(size_t)(i * CB + a) * r + k * CB + b];
+                        for (int m = 0; m < CB; ++m)
+                            acc = fma(PLANTED(15) ? P[(size_t)(i * CB + a) * CB + m] : -P[(size_t)(i * CB + a) * CB + m],
+                                      P[(size_t)(k * CB + b) * CB + m], acc);   /* 15: update sign */
+                        A[(size_t)(i * CB + a) * r + k * CB + b] = acc;
+                    }
+        }
+    }
+    for (size_t e = 0; e < (size_t)r * r; ++e) Lf[e] = (float)L[e];
+    for (size_t e = 0; e < (size_t)r * CB; ++e) Lif[e] = (float)Li[e];
+    free(P);
 }

@@ -2306,3 +2306,280 @@ int spanqr_plan_copy_scalars(spanqr_plan* p, float* scal8, void* stream) {
 }
 
 }  // extern "C"
+
+// ===============================================================================================================
+// fp64 clamped Cholesky (kchol.chol64, kchol.py:47-57 -> chol_f64, chol.cu:115-281 instantiated for double): the
+// tile algorithm of the fp32 factorisation in double, plus fp32 copies of L and Li (chol.cu:175-176, 215, 255).
+// Every workgroup owns one lower 32x32 tile (i, k) for the whole factorisation: it applies column blocks j < k in
+// order, each as soon as the panels L(i, j) and L(k, j) are published (fma chains over the block's 32 columns, two
+// rows x two columns per thread); then the diagonal owner factors and inverts its tile in one wavefront (the fp32
+// kernel's per-column scheme in double: the pivot from lane c's register, column broadcast through LDS), and an
+// off-diagonal owner forms its panel L(i, k) = T(i, k) Li_k^T (chain over the non-zero 16-column groups of Li_k)
+// once Li_k is published. Publication: stores, wait for them, one agent-scope release, a flag; waits are bounded
+// (an error word records a wait that gave up). Each tile waits only on tiles of earlier columns or its own column's
+// diagonal tile, so with every workgroup resident (checked when the plan is made) nothing deadlocks.
+// ===============================================================================================================
+namespace {
+
+constexpr int C64_TS = CB + 1;
+typedef double TileD[CB][C64_TS];
+
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// reciprocal square root for the fp64 pivots (CUDA's rsqrt in the reference): start 0x5FE6EB50C7B537A9 - (bits >> 1),
+// then four Newton steps y <- y * (1.5 - (0.5x * y) * y), the bracket as one fma
+__device__ __forceinline__ double rsqrt64_sw(double x) {
+#pragma clang fp contract(off)
+    double y = __longlong_as_double((long long)(0x5FE6EB50C7B537A9ull - ((uint64_t)__double_as_longlong(x) >> 1)));
+    const double h = 0.5 * x;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        double t = h * y;
+        t = __builtin_fma(-t, y, 1.5);
+        y = y * t;
+    }
+    return y;
+}
+
+// global 32x32 double tile (row stride ld) <-> LDS, all 256 threads, two doubles per access
+__device__ __forceinline__ void load_tile_d(TileD& dst, const double* src, long ld) {
+    for (int e = threadIdx.x; e < CB * CB / 2; e += 256) {
+        const int row = e >> 4, c2 = e & 15;
+        const double2 v = *reinterpret_cast<const double2*>(src + (size_t)row * ld + 2 * c2);
+        dst[row][2 * c2] = v.x;
+        dst[row][2 * c2 + 1] = v.y;
+    }
+}
+// to dst (fp64) and dstf (fp32 copy), both row stride ld; lower: zeros above the diagonal
+__device__ __forceinline__ void store_tile_d(double* dst, float* dstf, long ld, const TileD& src, bool lower) {
+    for (int e = threadIdx.x; e < CB * CB / 2; e += 256) {
+        const int row = e >> 4, c2 = e & 15;
+        double2 v;
+        v.x = (lower && 2 * c2 > row) ? 0.0 : src[row][2 * c2];
+        v.y = (lower && 2 * c2 + 1 > row) ? 0.0 : src[row][2 * c2 + 1];
+        *reinterpret_cast<double2*>(dst + (size_t)row * ld + 2 * c2) = v;
+        *reinterpret_cast<float2*>(dstf + (size_t)row * ld + 2 * c2) = make_float2((float)v.x, (float)v.y);
+    }
+}
+
+// T -= Pa Pb^T (chain over m = 0..31 from T); lower: elements above the diagonal are left (never read)
+__device__ __forceinline__ void update_d(TileD& T, const TileD& Pa, const TileD& Pb, bool lower) {
+#pragma clang fp contract(off)
+    const int r0 = 2 * (threadIdx.x >> 4), c0 = 2 * (threadIdx.x & 15);
+    double acc[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int v = 0; v < 2; ++v) acc[u][v] = T[r0 + u][c0 + v];
+#pragma unroll 4
+    for (int m = 0; m < CB; ++m) {
+        const double a0 = Pa[r0][m], a1 = Pa[r0 + 1][m], b0 = Pb[c0][m], b1 = Pb[c0 + 1][m];
+        acc[0][0] = __builtin_fma(-a0, b0, acc[0][0]);
+        acc[0][1] = __builtin_fma(-a0, b1, acc[0][1]);
+        acc[1][0] = __builtin_fma(-a1, b0, acc[1][0]);
+        acc[1][1] = __builtin_fma(-a1, b1, acc[1][1]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int v = 0; v < 2; ++v)
+            if (!(lower && c0 + v > r0 + u)) T[r0 + u][c0 + v] = acc[u][v];
+    __syncthreads();
+}
+
+// Out = T Li^T (chain over m < 16 (b / 16 + 1) from +0); Out may alias T
+__device__ __forceinline__ void panel_d(TileD& Out, const TileD& T, const TileD& Li) {
+#pragma clang fp contract(off)
+    const int r0 = 2 * (threadIdx.x >> 4), c0 = 2 * (threadIdx.x & 15);
+    const int mend = 16 * (c0 / 16 + 1);
+    double acc[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+#pragma unroll 4
+    for (int m = 0; m < mend; ++m) {
+        const double a0 = T[r0][m], a1 = T[r0 + 1][m], b0 = Li[c0][m], b1 = Li[c0 + 1][m];
+        acc[0][0] = __builtin_fma(a0, b0, acc[0][0]);
+        acc[0][1] = __builtin_fma(a0, b1, acc[0][1]);
+        acc[1][0] = __builtin_fma(a1, b0, acc[1][0]);
+        acc[1][1] = __builtin_fma(a1, b1, acc[1][1]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int v = 0; v < 2; ++v) Out[r0 + u][c0 + v] = acc[u][v];
+    __syncthreads();
+}
+
+// Wave 0: factor the lower part of D and invert the factor (chol.cu:131-168 in double). Lanes 0..31 hold row i of D,
+// lanes 32..63 column i of the identity, which becomes column i of the inverse; column c: piv = fmax(D_cc, tau)
+// (NaN -> tau) from lane c, q = rsqrt(piv), own = R[c] q (l_i on a factor lane, x_c on an inverse lane, exactly 0
+// above its diagonal), then R[k] = fma(-own, l_k, R[k]) for k > c with l_k broadcast through LDS. The column loop
+// is a real loop (the row stays in registers, updated under k > c), which keeps the register count low. The factor's
+// diagonal entry is piv q. Writes the factor (upper triangle unspecified) to dl and the inverse to Li.
+__device__ __forceinline__ void factor_inv32_d(const TileD& D, double tau, TileD& dl, TileD& Li, double* bl, double* pq) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63, i = lane & 31;
+    const bool fl = lane < 32;
+    double R[CB];
+#pragma unroll
+    for (int k = 0; k < CB; ++k) R[k] = fl ? D[i][k] : (i == k ? 1.0 : 0.0);
+#pragma nounroll
+    for (int c = 0; c < CB; ++c) {
+        double rc = 0.0;
+#pragma unroll
+        for (int k = 0; k < CB; ++k)
+            if (k == c) rc = R[k];
+        const double piv = fmax(readlane_d(rc, c), tau);
+        const double q = rsqrt64_sw(piv);
+        const double own = (!fl && c < i) ? 0.0 : rc * q;
+        if (lane == 0) pq[c] = piv * q;
+        if (fl) bl[i] = own;
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int k = 0; k < CB; ++k) {
+            if (k == c) R[k] = own;
+            else if (k > c) R[k] = __builtin_fma(-own, bl[k], R[k]);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int k = 0; k < CB; ++k) {
+        if (fl) dl[i][k] = (k == i) ? pq[i] : R[k];
+        else Li[k][i] = R[k];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_c64_fill(uint32_t* flags, int nf, double* L, float* Lf, int n) {
+    const size_t nn = (size_t)n * n;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < nn; e += (size_t)gridDim.x * 256) {
+        L[e] = 0.0;
+        Lf[e] = 0.0f;
+        if (e < (size_t)nf) flags[e] = 0u;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_chol64(const double* __restrict__ G, long ldg, int n,
+                                                const double* __restrict__ taup, double* L, double* Li, float* Lf,
+                                                float* Lif, uint32_t* flags) {
+    extern __shared__ double c64_lds[];
+    TileD* tl = reinterpret_cast<TileD*>(c64_lds);
+    TileD& T = tl[0];
+    TileD& Pa = tl[1];
+    TileD& Pb = tl[2];
+    TileD& X = tl[3];
+    double* bl = c64_lds + 4 * CB * C64_TS;
+    double* pq = bl + CB;
+    const int u = blockIdx.x, nb = n / CB, nt = nb * (nb + 1) / 2;
+    int i = 0;
+    while ((i + 1) * (i + 2) / 2 <= u) ++i;
+    const int k = u - i * (i + 1) / 2;
+    uint32_t* err = flags + nt;
+    auto fidx = [](int a, int b) { return a * (a + 1) / 2 + b; };
+    bool dead = false;
+    const double tau = *taup;
+    load_tile_d(T, G + (size_t)CB * i * ldg + CB * k, ldg);
+    __syncthreads();
+    for (int j = 0; j < k; ++j) {
+        if (threadIdx.x == 0) {
+            wait_flag(flags + fidx(i, j), 1u, err, dead);
+            if (i != k) wait_flag(flags + fidx(k, j), 1u, err, dead);
+        }
+        __syncthreads();
+        load_tile_d(Pa, L + (size_t)CB * i * n + CB * j, n);
+        if (i != k) load_tile_d(Pb, L + (size_t)CB * k * n + CB * j, n);
+        __syncthreads();
+        update_d(T, Pa, i == k ? Pa : Pb, i == k);
+    }
+    if (i == k) {
+        if (threadIdx.x < 64) factor_inv32_d(T, tau, X, Pa, bl, pq);
+        __syncthreads();
+        store_tile_d(L + (size_t)CB * k * n + CB * k, Lf + (size_t)CB * k * n + CB * k, n, X, true);
+        store_tile_d(Li + (size_t)CB * k * CB, Lif + (size_t)CB * k * CB, CB, Pa, false);
+    } else {
+        if (threadIdx.x == 0) wait_flag(flags + fidx(k, k), 1u, err, dead);
+        __syncthreads();
+        load_tile_d(Pb, Li + (size_t)CB * k * CB, CB);
+        __syncthreads();
+        panel_d(T, T, Pb);
+        store_tile_d(L + (size_t)CB * i * n + CB * k, Lf + (size_t)CB * i * n + CB * k, n, T, false);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    if (threadIdx.x == 0) publish_flag(flags + fidx(i, k), 1u);
+}
+
+size_t chol64_lds_bytes() { return 4 * sizeof(TileD) + 2 * CB * sizeof(double); }
+
+}  // namespace
+
+struct spanqr_chol64_plan {
+    int n = 0, device = 0, nt = 0;
+    uint32_t* flags = nullptr;   // nt tile flags + the wait-error word
+};
+
+extern "C" {
+
+int spanqr_chol64_plan_create(int n, int device, spanqr_chol64_plan** out) {
+    if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
+    *out = nullptr;
+    if (n < CB || n > 1024 || n % CB) return fail(SPANQR_EINVAL, "n = %d: must be a multiple of 32 in [32, 1024]", n);
+    DeviceGuard dg(device);
+    if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", device);
+    const int nb = n / CB, nt = nb * (nb + 1) / 2;
+    int occ = 0, cus = 0;
+    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol64, 256, chol64_lds_bytes()));
+    HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+    if ((long)occ * cus < nt)
+        return fail(SPANQR_EHIP, "the fp64 Cholesky needs %d resident workgroups, the device holds %d", nt, occ * cus);
+    spanqr_chol64_plan* p = new spanqr_chol64_plan;
+    p->n = n; p->device = device; p->nt = nt;
+    if (hipMalloc((void**)&p->flags, (size_t)(nt + 1) * sizeof(uint32_t)) != hipSuccess) {
+        delete p;
+        return fail(SPANQR_ENOMEM, "flag allocation failed");
+    }
+    *out = p;
+    return SPANQR_OK;
+}
+
+void spanqr_chol64_plan_destroy(spanqr_chol64_plan* p) {
+    if (!p) return;
+    DeviceGuard dg(p->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(p->flags);
+    delete p;
+}
+
+int spanqr_chol64(spanqr_chol64_plan* p, const double* G, long ldg, const double* tau, double* L, double* Li,
+                  float* Lf, float* Lif, void* stream) {
+    if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    if (!G || !tau || !L || !Li || !Lf || !Lif) return fail(SPANQR_EINVAL, "null argument");
+    if (!aligned16(G) || !aligned16(L) || !aligned16(Li) || ((uintptr_t)Lf & 7) || ((uintptr_t)Lif & 7))
+        return fail(SPANQR_EINVAL, "G, L, Li must be 16-byte and Lf, Lif 8-byte aligned");
+    if (ldg < p->n || (ldg & 1)) return fail(SPANQR_EINVAL, "ldg = %ld: must be >= n and even", ldg);
+    DeviceGuard dg(p->device);
+    if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
+    hipStream_t st = (hipStream_t)stream;
+    k_c64_fill<<<256, 256, 0, st>>>(p->flags, p->nt + 1, L, Lf, p->n);
+    k_chol64<<<p->nt, 256, chol64_lds_bytes(), st>>>(G, ldg, p->n, tau, L, Li, Lf, Lif, p->flags);
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
+int spanqr_chol64_status(spanqr_chol64_plan* p, void* stream) {
+    if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    DeviceGuard dg(p->device);
+    uint32_t e = 0;
+    HIPCHK(hipMemcpyAsync(&e, p->flags + p->nt, sizeof(uint32_t), hipMemcpyDeviceToHost, (hipStream_t)stream));
+    HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+    if (e) return fail(SPANQR_EHIP, "fp64 Cholesky: a wait exceeded its bound (not every workgroup was resident)");
+    return SPANQR_OK;
+}
+
+}  // extern "C"

@@ -472,6 +472,57 @@ def check_borth_composition():
     return f
 
 
+# ---- fp64 Cholesky (kchol.py:47-57, chol.cu:278-281) ----
+
+def check_rsqrt64():
+    """the fp64 pivot reciprocal square root within 3 ulp of 1/sqrt in extended precision over 1e-300..1e300"""
+    x = np.logspace(-300, 300, 4001)
+    y = np.array([oracle.rsqrt64(v) for v in x])
+    ref = (1 / np.sqrt(x.astype(np.longdouble))).astype(np.float64)
+    ulp = np.abs(y - ref) / np.spacing(ref)
+    return [] if ulp.max() <= 3 else [f"rsqrt64 off by {ulp.max():.1f} ulp"]
+
+
+def check_chol64():
+    """fp64 LAPACK Cholesky (clamp inactive), residual, Li L_jj = I, zero G -> sqrt(tau) I, NaN pivot -> tau,
+    rank deficiency clamped, fp32 copies the rounded fp64 values"""
+    f = []
+    rng = np.random.default_rng(15)
+    for r in (64, 256):
+        X = rng.standard_normal((r + 40, r))
+        G = X.T @ X
+        L, Li, Lf, Lif = oracle.chol64(G, 1e-12)
+        L0 = np.linalg.cholesky(G)
+        if not np.abs(L - L0).max() <= 1e-12 * np.abs(L0).max():
+            f.append(f"chol64 r={r}: not LAPACK's factor ({np.abs(L - L0).max():.2e})")
+        if not np.abs(L @ L.T - G).max() <= 1e-13 * np.abs(G).max():
+            f.append(f"chol64 r={r}: residual")
+        for j in range(r // 32):
+            Ljj = L[32 * j:32 * j + 32, 32 * j:32 * j + 32]
+            if not np.abs(Li[32 * j:32 * j + 32] @ Ljj - np.eye(32)).max() <= 1e-12 * max(1.0, np.abs(Li).max()):
+                f.append(f"chol64 r={r}: Li is not the diagonal tile's inverse")
+                break
+        if not (np.array_equal(Lf, L.astype(np.float32)) and np.array_equal(Lif, Li.astype(np.float32))):
+            f.append("chol64: fp32 copies are not the rounded fp64 values")
+        if not np.all(np.triu(L, 1) == 0):
+            f.append("chol64: upper triangle not zero")
+    tau = 1e-20
+    L, Li, _, _ = oracle.chol64(np.zeros((64, 64)), tau)
+    if not np.allclose(L, np.sqrt(tau) * np.eye(64), rtol=1e-15, atol=0):
+        f.append("chol64: zero G does not give sqrt(tau) I")
+    G = rng.standard_normal((96, 64))
+    G = G.T @ G
+    G[5, 5] = np.nan
+    L, _, _, _ = oracle.chol64(G, 1e-3)
+    if not abs(L[5, 5] - np.sqrt(1e-3)) <= 1e-15 or not np.isfinite(L[:5, :5]).all():
+        f.append("chol64: a NaN pivot is not clamped to tau")
+    B = rng.standard_normal((64, 16))
+    L, _, _, _ = oracle.chol64(B @ B.T, 1e-10)
+    if not (np.diag(L)[16:] <= 2 * np.sqrt(1e-10)).all():
+        f.append("chol64: rank-deficient pivots are not clamped")
+    return f
+
+
 ALL = [check_scale, check_scale_rounding_margin, check_rsqrt, check_dust, check_gram, check_shift, check_chol,
        check_trsm, check_ns, check_orth_small, check_split_rule, check_xgram, check_project, check_borth,
-       check_borth_composition]
+       check_borth_composition, check_rsqrt64, check_chol64]

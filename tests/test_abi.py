@@ -126,3 +126,15 @@ def test_top_level_orth_is_the_package_orth():
     assert top.orth is spanqr_amd.orth
     assert top.orth_many is spanqr_amd.orth_many
     assert top.borth is spanqr_amd.borth and top.kcholqr_f is spanqr_amd.kcholqr_f
+
+
+def test_chol64_arguments_checked_before_any_device_work():
+    h = ctypes.c_void_p()
+    f = _lib.lib().spanqr_chol64_plan_create
+    for n in (0, 16, 48, 1056):
+        assert f(n, 0, ctypes.byref(h)) == -1 and not h.value
+    assert f(64, 0, None) == -1
+    assert _lib.lib().spanqr_chol64(None, None, 64, None, None, None, None, None, None) == -1
+    from spanqr_amd import kchol
+    with pytest.raises(TypeError):
+        kchol.chol64(torch.zeros(64, 64, dtype=torch.float64), 1e-9)

@@ -20,6 +20,7 @@ DEFECTS = {
     12: "block projection adds P P^T C instead of subtracting it",
     13: "every block gets the first dust slice",
     14: "blocks projected once before orthonormalisation instead of twice",
+    15: "fp64 trailing update with the wrong sign",
 }
 
 
