@@ -1193,7 +1193,9 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
     float li[2][8];   // Li of this wave's next block to finish (fetched four steps ahead)
     trsm_fetch_li(li, Lp, nbc, w, lane);
     __syncthreads();   // flags cleared
-    // finish block k (owner only): Y_k = acc_k Li_k^T into sY and Y, then raise its flag
+    const bool full = row0 + 16 * RB <= K;   // every row of the workgroup exists: stores need no bounds check
+    // finish block k (owner only): Y_k = acc_k Li_k^T into sY and Y, then raise its flag. The accumulator goes
+    // through LDS into the MFMA A layout; both 16-column halves' chains run interleaved before any store.
     auto finish = [&](int k, int qk) {
         float* sa = sAcc + w * 16 * 33;
 #pragma unroll
@@ -1203,19 +1205,24 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
 #pragma unroll
                 for (int v = 0; v < 4; ++v) sa[(4 * lk + v) * 33 + 16 * cb + l16] = acc[rb][qk][cb][v];
             __builtin_amdgcn_wave_barrier();
+            float av[8];
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                f32x4 y = {0.f, 0.f, 0.f, 0.f};
+            for (int kk = 0; kk < 8; ++kk) av[kk] = sa[l16 * 33 + 4 * kk + lk];
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 y[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-                for (int kk = 0; kk < 8; ++kk)
-                    if (kk < 4 * (cb + 1)) y = mfma(sa[l16 * 33 + 4 * kk + lk], li[cb][kk], y);
+            for (int kk = 0; kk < 8; ++kk) {
+                if (kk < 4) y[0] = mfma(av[kk], li[0][kk], y[0]);
+                y[1] = mfma(av[kk], li[1][kk], y[1]);
+            }
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int rl = 16 * rb + 4 * lk + v, col = CB * k + 16 * cb + l16;
-                    sY[rl * ldsy + col] = y[v];
-                    if (row0 + rl < K) Y[(size_t)(row0 + rl) * ldy + col] = y[v];
+                    sY[rl * ldsy + col] = y[cb][v];
+                    if (full || row0 + rl < K) Y[(size_t)(row0 + rl) * ldy + col] = y[cb][v];
                 }
-            }
             __builtin_amdgcn_wave_barrier();
         }
         if (lane == 0) __hip_atomic_store(&sFlag[k], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1224,13 +1231,16 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
     // acc_j -= Y_k L_jk^T for owned block q
     auto apply = [&](int k, int q) {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb) {
+            float av[8];   // the A operands read together, then both halves' chains interleaved
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const float a = -sY[(16 * rb + l16) * ldsy + CB * k + 4 * kk + lk];
+            for (int kk = 0; kk < 8; ++kk) av[kk] = -sY[(16 * rb + l16) * ldsy + CB * k + 4 * kk + lk];
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int cb = 0; cb < 2; ++cb) acc[rb][q][cb] = mfma(a, cur.l[q][cb][kk], acc[rb][q][cb]);
-            }
+            for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) acc[rb][q][cb] = mfma(av[kk], cur.l[q][cb][kk], acc[rb][q][cb]);
+        }
     };
     if (w == 0) finish(0, 0);
 #pragma unroll
