@@ -367,7 +367,7 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 
 // wave w computes the 16x16 block (w >> 1, w & 1) of a 32x32 tile; lane (l16, lk) holds rows 16bi + 4lk + v
 #define WAVE_COORDS                                                                  \
-    const int w_ = threadIdx.x >> 6, lane_ = threadIdx.x & 63;                       \
+    const int w_ = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane_ = threadIdx.x & 63; \
     const int bi = w_ >> 1, bj = w_ & 1, l16 = lane_ & 15, lk = lane_ >> 4;          \
     (void)bi; (void)bj; (void)l16; (void)lk
 
@@ -494,6 +494,7 @@ __device__ __forceinline__ void panel32(Tile& out, const Tile& in, const Tile& l
         a[kk] = in[16 * bi + l16][4 * kk + lk];
         b[kk] = li[16 * bj + l16][4 * kk + lk];
     }
+    __builtin_amdgcn_sched_barrier(0);   // every operand read issued before the chain
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
@@ -510,11 +511,17 @@ __device__ __forceinline__ void update32(Tile& dst, const Tile& C, const Tile& P
     WAVE_COORDS;
     if (!(lower && bi == 0 && bj == 1)) {
         f32x4 acc;
+        float a[8], b[8];
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[v] = C[16 * bi + 4 * lk + v][16 * bj + l16];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-            acc = mfma(-Pi[16 * bi + l16][4 * kk + lk], Pk[16 * bj + l16][4 * kk + lk], acc);
+        for (int kk = 0; kk < 8; ++kk) {
+            a[kk] = Pi[16 * bi + l16][4 * kk + lk];
+            b[kk] = Pk[16 * bj + l16][4 * kk + lk];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) acc = mfma(-a[kk], b[kk], acc);
 #pragma unroll
         for (int v = 0; v < 4; ++v) dst[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
     }
@@ -532,6 +539,7 @@ __device__ __forceinline__ void panel32x2(Tile& outA, const Tile& inA, Tile& out
         xb[kk] = inB[16 * bi + l16][4 * kk + lk];
         lv[kk] = li[16 * bj + l16][4 * kk + lk];
     }
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
@@ -557,6 +565,7 @@ __device__ __forceinline__ void panel32x2_inplace(Tile& A, Tile& B, const Tile& 
         xb[kk] = B[16 * bi + l16][4 * kk + lk];
         lv[kk] = li[16 * bj + l16][4 * kk + lk];
     }
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
@@ -585,6 +594,7 @@ __device__ __forceinline__ void panel32_wave(Tile& out, const Tile& in, const Ti
             a[h][kk] = in[16 * h + l16][4 * kk + lk];
             b[h][kk] = (kk < 4 * (h + 1)) ? li[16 * h + l16][4 * kk + lk] : 0.0f;
         }
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
@@ -619,6 +629,7 @@ __device__ __forceinline__ void update32_wave_q(Tile& dst, const Tile& C, const 
     for (int qd = 0; qd < 4; ++qd)
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[qd][v] = C[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
@@ -650,15 +661,19 @@ __device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Til
 // (exactly +0 while c < kk: those registers stay +0). The factor's diagonal entry is piv q, which differs from
 // R[c] q only when the pivot was clamped; it is used nowhere but the output, so it is recorded in pq[c] and patched
 // in at the end (a factor lane above the diagonal computes values that only its own dead upper-triangle registers
-// see). Then both halves run the same rank-1 update R[k] = fma(-own, l_k, R[k]) for k > c: the factor's trailing
-// update D_ik -= l_i l_k and the inverse's forward substitution acc_k -= L_kc x_c, each element's chain in column
-// order. Only lane c+1's diagonal is on the critical path: that lane forms its next pivot from its own l (the same
-// fma as the update) and takes the reciprocal square root itself; q crosses lanes once, by v_readlane. The other l_k
-// are broadcast through LDS (96 floats each: lane i writes at 30 - c + i, so the l_k in use, k >= c + 2, start at the
-// aligned bl + 32), alternating between two buffers (bl0, bl1) so that no barrier is needed: the compiler
-// may interleave a column's update with the next pivot's chain. No lane-dependent selects: their masks would all be
-// hoisted and spilled. Writes the factor to dl (the upper triangle is left unspecified: publishers zero it) and the
-// inverse to Li, and the inverse also to global memory at gli (row stride 32; the stores are left in flight).
+// see). Both halves run the same rank-1 updates R[k] = fma(-own_c, l_k, R[k]), k > c: the factor's trailing update
+// D_ik -= l_i l_k and the inverse's forward substitution acc_k -= L_kc x_c, each element's chain in column order.
+//
+// Schedule (a single wavefront issues in order, so the work that does not feed the next pivot is placed in the gaps
+// of the pivot chain): each lane keeps its diagonal element also in dg (the same fmas as R[lane]: l_lane is the lane's
+// own value), so the pivot chain dn = fma(-own, own, dg) -> fmaxf -> rsqrt -> v_readlane touches no memory. Column
+// c's values reach the other lanes through LDS (96 floats per column: lane i writes at 28 - c + i, so l_{c+4} lands
+// on the aligned bl + 32, alternating between bl0 and bl1), are read back during column c+1 and applied during column
+// c+2 to the elements k >= c+5, interleaved with that column's pivot chain. Elements c+1 and c+2 are needed within two
+// columns; at column c, element c+2 takes column c-2's update (from the same LDS values), then column c-1's and
+// column c's through v_readlane, and element c+1 column c's; so every element still gets its updates in column order.
+// Writes the factor to dl (the upper triangle is left unspecified: publishers zero it) and the inverse to Li, and the
+// inverse also to global memory at gli (row stride 32; the stores are left in flight).
 __device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, const Tile& id, const Tile& D,
                                              float tau, Tile& dl, Tile& Li, float* gli) {
     const int lane = threadIdx.x & 63, i = lane & 31;
@@ -667,38 +682,96 @@ __device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, 
     float R[CB];
 #pragma unroll
     for (int k = 0; k < CB; ++k) R[k] = src[k];
+    float dg = src[i];
     const float pl = fmaxf(R[0], tau);         // lane 0's value is the first pivot
     float q = readlane(rsqrt_sw(pl), 0);
     float piv = readlane(pl, 0);
+    float own_m1 = 0.0f, own_m2 = 0.0f;        // own of columns c-1 and c-2
+    float rl_m1 = 0.0f;                        // l_{c+2} of column c-1 (v_readlane of lane c+2)
+    float lbA[CB], lbB[CB];                    // LDS values of columns c-2 (in use) and c-1 (being read), by parity
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-        float* bl = (c & 1) ? bl1 : bl0;
+        float* lb = (c & 1) ? lbB : lbA;       // column c-2's l_k at lb[k - c - 2]
+        float* lbn = (c & 1) ? lbA : lbB;      // column c-1's l_k at lbn[k - c - 3]
         const float own = R[c] * q;
         pq[c] = piv * q;
         R[c] = own;
-        if (c + 1 < CB) {
-            const float dn = __builtin_fmaf(-own, own, R[c + 1]);     // lane c+1: its diagonal after column c
-            const float pn = fmaxf(dn, tau);
-            const float qn = readlane(rsqrt_sw(pn), c + 1);
-            R[c + 1] = __builtin_fmaf(-own, readlane(own, c + 1), R[c + 1]);
-            if (c + 2 < CB) {
-                // l_k lands at bl[32 + k - (c + 2)], so the values in use start 16-byte aligned at bl + 32
-                bl[30 - c + lane] = own;
-                const float* lk = bl + 32;
+        if (c >= 1 && c + 3 < CB) {            // read column c-1's values (k >= c+3) back; used at column c+1
+            const float* src4 = ((c - 1) & 1 ? bl1 : bl0) + 32;
 #pragma unroll
-                for (int kq = 0; 4 * kq < CB - 2 - c; ++kq) {
-                    const float4 l4 = *reinterpret_cast<const float4*>(&lk[4 * kq]);
-                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+            for (int kq = 0; 4 * kq < CB - 3 - c; ++kq) {
+                const float4 l4 = *reinterpret_cast<const float4*>(&src4[4 * kq]);
+                lbn[4 * kq + 0] = l4.x;
+                lbn[4 * kq + 1] = l4.y;
+                lbn[4 * kq + 2] = l4.z;
+                lbn[4 * kq + 3] = l4.w;
+            }
+        }
+        // bulk: column c-2's update of the elements k >= c+3, spread over the pivot chain's steps
+        constexpr int NSTEP = 14;
+        auto bulk = [&](int g) {
+            if (c >= 2) {
+                const int nbk = CB - 3 - c;
+                const int per = (nbk + NSTEP - 1) / NSTEP;
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const int k = c + 2 + 4 * kq + t;
-                        if (k < CB) R[k] = __builtin_fmaf(-own, lv[t], R[k]);
+                for (int u = 0; u < 4; ++u) {
+                    const int t = g * per + u;
+                    if (u < per && t < nbk) {
+                        const int k = c + 3 + t;
+                        R[k] = __builtin_fmaf(-own_m2, lb[k - c - 2], R[k]);
                     }
                 }
             }
-            piv = readlane(pn, c + 1);
-            q = qn;
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        float qn = 0.0f, pivn = 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
+        if (c + 1 < CB) {
+            // the pivot chain of column c+1, written out step by step (rsqrt_sw's operations in its order)
+            const float dn = __builtin_fmaf(-own, own, dg);
+            __builtin_amdgcn_sched_barrier(0);
+            bulk(0);
+            const float pn = fmaxf(dn, tau);
+            __builtin_amdgcn_sched_barrier(0);
+            bulk(1);
+            float y = __uint_as_float(0x5f375a86u - (__float_as_uint(pn) >> 1));
+            const float h = 0.5f * pn;
+            __builtin_amdgcn_sched_barrier(0);
+            bulk(2);
+#pragma unroll
+            for (int it = 0; it < 3; ++it) {
+                float t = h * y;
+                __builtin_amdgcn_sched_barrier(0);
+                bulk(3 + 3 * it);
+                t = __builtin_fmaf(-t, y, 1.5f);
+                __builtin_amdgcn_sched_barrier(0);
+                bulk(4 + 3 * it);
+                y = y * t;
+                __builtin_amdgcn_sched_barrier(0);
+                bulk(5 + 3 * it);
+            }
+            qn = readlane(y, c + 1);
+            pivn = readlane(pn, c + 1);
+            dg = dn;
+            __builtin_amdgcn_sched_barrier(0);
+            bulk(12);
+            bulk(13);
+        } else {
+            bulk(0);
         }
+        // element c+2: columns c-2, c-1 and c; element c+1: column c
+        if (c + 2 < CB) {
+            if (c >= 2) R[c + 2] = __builtin_fmaf(-own_m2, lb[0], R[c + 2]);
+            if (c >= 1) R[c + 2] = __builtin_fmaf(-own_m1, rl_m1, R[c + 2]);
+            R[c + 2] = __builtin_fmaf(-own, readlane(own, c + 2), R[c + 2]);
+        }
+        if (c + 1 < CB) R[c + 1] = __builtin_fmaf(-own, readlane(own, c + 1), R[c + 1]);
+        if (c + 3 < CB) rl_m1 = readlane(own, c + 3);
+        if (c + 4 < CB) ((c & 1) ? bl1 : bl0)[28 - c + lane] = own;
+        own_m2 = own_m1;
+        own_m1 = own;
+        piv = pivn;
+        q = qn;
     }
     __builtin_amdgcn_wave_barrier();
     if (!fl) {   // the inverse, row-major (row stride 32) from its column lanes, to gli for the other workgroups
@@ -816,7 +889,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
                                               float tau_rel, float* L, float* Li, float* Lp, uint32_t* bar,
                                               uint32_t* flags, float* scal, uint64_t* stamps) {
     extern __shared__ float4 chol_lds[];
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int b = blockIdx.x, nb = r / CB;
     {
         const size_t z = blockIdx.z;   // matrix of the batch
@@ -1063,23 +1136,41 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
 #pragma unroll
                     for (int v = 0; v < 4; ++v) acc[v] = rt[k][16 * bi + 4 * lk + v][16 * bj + l16];
                 };
-                int k = next_k(j);
-                float bv[8];
-                f32x4 acc;
-                if (k <= i) fetch(k, bv, acc);
-                while (k <= i) {
-                    const int kn = next_k(k);
-                    float bn[8];
-                    f32x4 accn;
-                    if (kn <= i) fetch(kn, bn, accn);
+                // two operand sets in turn: tile k's chain runs while tile kn's operands are in flight
+                auto chain = [&](int k, const float (&bv)[8], f32x4 acc) {
 #pragma unroll
                     for (int kk = 0; kk < 8; ++kk) acc = mfma(an[kk], bv[kk], acc);
 #pragma unroll
                     for (int v = 0; v < 4; ++v) rt[k][16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
-                    k = kn;
+                };
+                int k = next_k(j);
+                float b0[8], b1[8];
+                f32x4 c0, c1;
+                if (k <= i) fetch(k, b0, c0);
+                // the prefetch is unconditional (past the last tile it reads tile k again, unused), so the wait before
+                // a chain only ever covers the previous prefetch
+                // In-order issue: the next tile's reads go between the chain's first MFMAs (two after each), where they
+                // issue while the previous MFMA runs and complete before the chain ends.
+                auto interleave = [&]() {
 #pragma unroll
-                    for (int kk = 0; kk < 8; ++kk) bv[kk] = bn[kk];
-                    acc = accn;
+                    for (int g = 0; g < 3; ++g) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS reads
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
+                };
+                while (k <= i) {
+                    int kn = next_k(k);
+                    fetch(kn <= i ? kn : k, b1, c1);
+                    chain(k, b0, c0);
+                    interleave();
+                    k = kn;
+                    if (k > i) break;
+                    kn = next_k(k);
+                    fetch(kn <= i ? kn : k, b0, c0);
+                    chain(k, b1, c1);
+                    interleave();
+                    k = kn;
                 }
                 __syncthreads();
             }
@@ -1161,7 +1252,7 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
     float* sY = smem;                          // [16 RB][r + 4]: finished Y columns (MFMA A operands)
     float* sAcc = sY + 16 * RB * ldsy;         // [4][16][33]: per-wave transpose of the block being finished
     uint32_t* sFlag = reinterpret_cast<uint32_t*>(sAcc + 4 * 16 * 33);   // [nbc]
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
     const int row0 = blockIdx.x * 16 * RB, nbc = r / CB;
     float sc = 1.0f;
     if (PASS1) {
