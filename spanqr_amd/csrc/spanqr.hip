@@ -2071,8 +2071,9 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
     // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU
     p->trsm_rb = ((K + 15) / 16 >= 2048) ? 4 : ((K + 15) / 16 >= 1024 ? 2 : 1);
     // one wavefront per 16 rows once there are enough rows to occupy the SIMDs (its per-wave chain over r/32
-    // blocks is long); below that, k_trsm splits each row block's columns over four waves
-    p->trsm_rows = r <= 256 && K >= 4096;
+    // blocks is long; the measured crossover at r = 256 lies between K = 8192 and 10240); below that, k_trsm
+    // splits each row block's columns over four waves
+    p->trsm_rows = r <= 256 && K >= 9216;
     {
         const size_t need = trsm_lds(r, p->trsm_rb);
         int maxsh = 0;
