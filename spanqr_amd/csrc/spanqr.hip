@@ -13,9 +13,10 @@
 //     workgroup 0 runs the diagonal chain with a two-tile-row look-ahead, each other workgroup keeps one tile row in
 //     LDS; the 32x32 diagonal tiles are factored in one wavefront's registers (lane = row) and inverted (lanes
 //     32-63) in the same pass, and the factor is published both row-major and packed as the solve's MFMA operands;
-//   * the triangular solve is row-block parallel: for tall X one wavefront per 16 rows runs through all column
-//     blocks with its operands streamed ahead (k_trsm_rows); otherwise each of four wavefronts owns every 4th 32-column
-//     block of a row block and applies a finished block to its later blocks with MFMA (k_trsm);
+//   * the triangular solve is row-block parallel: for tall X a pair of wavefronts per 16 rows runs through all column
+//     blocks, one 16-column half of each, with its operands streamed ahead (k_trsm_rows); otherwise each of four
+//     wavefronts owns every 4th 32-column block of a row block and applies a finished block to its later blocks with
+//     MFMA (k_trsm);
 //   * every kernel takes its matrix of a batch from blockIdx.z (pointer tables passed by value), so a shape group of
 //     layers runs as one launch per stage.
 #include <hip/hip_runtime.h>
@@ -90,6 +91,22 @@ __device__ float block_scale(const uint32_t* __restrict__ part) {
     __syncthreads();
     uint32_t t = sm[0];
     for (int i = 1; i < 4; ++i) t = sm[i] > t ? sm[i] : t;
+    __syncthreads();
+    return pow2_scale_bits(t);
+}
+
+// As block_scale, for a 128-thread workgroup (each thread takes two of the partial maxima; the maximum is exact)
+__device__ float block_scale128(const uint32_t* __restrict__ part) {
+    __shared__ uint32_t sm[2];
+    const uint32_t a = part[threadIdx.x], b = part[threadIdx.x + 128];
+    uint32_t m = a > b ? a : b;
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)m, off);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    const uint32_t t = sm[0] > sm[1] ? sm[0] : sm[1];
     __syncthreads();
     return pow2_scale_bits(t);
 }
@@ -1372,35 +1389,36 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
     }
 }
 
-// Triangular solve with one wavefront per 16 rows (r = 32 NBC <= 256, tall X): the wave takes its rows through the
-// column blocks in order, left-looking: acc_j = A_j - sum_{k<j} Y_k L_jk^T (one MFMA chain per element, k and then m
-// ascending, the order of the blocked solve), then Y_j = acc_j Li_j^T. Its finished blocks stay in registers as MFMA
-// A operands, so waves never wait for each other. The packed L operands stream from L2 three blocks ahead of use
+// Triangular solve with a workgroup of two wavefronts per 16 rows (r = 32 NBC <= 256, tall X): wavefront h takes the
+// 16-column half h of every column block, in order, left-looking: acc_j = A_j - sum_{k<j} Y_k L_jk^T (one MFMA chain
+// per element, k and then m ascending, the order of the blocked solve), then Y_j = acc_j Li_j^T. The product's A
+// operand spans the block's 32 columns, so the pair swaps its accumulator halves through LDS, and then Y_j, which
+// both keep in registers as the later blocks' MFMA A operands (one workgroup barrier each). Two wavefronts per row
+// tile halve each chain, and the resulting ~2 wavefronts per SIMD at the tall shapes overlap one's LDS traffic with
+// the other's MFMAs. The packed L operands (each wavefront its half) stream from L2 three blocks ahead of use
 // (scheduling barriers keep the loads where they are issued), and A one column block ahead. The arithmetic of every
 // element is that of k_trsm.
 template <bool PASS1, int NBC>
-__global__ __launch_bounds__(256) void k_trsm_rows(const MatsIn As, long lda, int K,
+__global__ __launch_bounds__(128) void k_trsm_rows(const MatsIn As, long lda, int K,
                                                    const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
                                                    long ldz, float eps, const float* __restrict__ Lp, const MatsOut Ys,
                                                    long ldy, float* scal) {
-    constexpr int r = NBC * CB;
     constexpr int NSTEP = NBC * (NBC + 1) / 2;   // operand blocks in use order: L(j, 0..j-1), then Li_j, per j
     constexpr int DIST = 3;                       // operand blocks in flight ahead of the one in use
-    __shared__ float sT[4][16][33];   // per-wave transpose of one 16 x 32 block
+    __shared__ float sT[2][16][33];               // the pair's exchange: [0] acc_j, [1] Y_j (16 rows x 32 columns)
     const int z = blockIdx.z;
     const float* __restrict__ A = As.p[z];
     float* __restrict__ Y = Ys.p[z];
     amax_part += (size_t)z * AMAX_BLOCKS;
     Lp += (size_t)z * NSTEP * CB * CB;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
+    const int tid = threadIdx.x, h = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, l16 = lane & 15,
+              lk = lane >> 4;
     float sc = 1.0f;
     if (PASS1) {
-        sc = block_scale(amax_part);
+        sc = block_scale128(amax_part);
         if (blockIdx.x == 0 && tid == 0 && scal != nullptr) scal[(size_t)z * SCAL_STRIDE] = sc;
     }
-    const int row0 = (blockIdx.x * 4 + w) * 16;
-    if (row0 >= K) return;           // no workgroup barrier follows
-    float(*st)[33] = sT[w];
+    const int row0 = blockIdx.x * 16;   // < K: the grid is ceil(K / 16)
     // rows past K read row K-1 (in bounds) and are zeroed, so every load is unconditional
     int rowc[4];
     bool rin[4];
@@ -1410,92 +1428,84 @@ __global__ __launch_bounds__(256) void k_trsm_rows(const MatsIn As, long lda, in
         rin[v] = row < K;
         rowc[v] = rin[v] ? row : K - 1;
     }
-    // packed operand blocks, in use order; block s is consumed at step s and fetched at step s - DIST
-    float ob[DIST + 1][2][8];
+    // this wavefront's half of the packed operand blocks, in use order; block s is consumed at step s and fetched at
+    // step s - DIST (packed layout: 16 floats per lane, the half h at 8 h)
+    float ob[DIST + 1][8];
     auto fetch_step = [&](int sidx) {
         int j = 0;
         while ((j + 1) * (j + 2) / 2 <= sidx) ++j;
         const int k = sidx - j * (j + 1) / 2;
-        fetch_op(ob[sidx % (DIST + 1)], Lp, j, k, lane);
+        const float4* src = reinterpret_cast<const float4*>(Lp + (size_t)op_pair(j, k) * CB * CB + 16 * lane + 8 * h);
+        float(&o)[8] = ob[sidx % (DIST + 1)];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float4 v = src[q];
+            o[4 * q + 0] = v.x;
+            o[4 * q + 1] = v.y;
+            o[4 * q + 2] = v.z;
+            o[4 * q + 3] = v.w;
+        }
         __builtin_amdgcn_sched_barrier(0);   // keep the prefetch where it is issued (the scheduler would sink it)
     };
-    // A_j (and Z_j on pass 1) in C layout, one block ahead
-    float xa[2][2][4], za[2][2][4];
+    // this wavefront's half of A_j (and Z_j on pass 1) in C layout, one block ahead
+    float xa[2][4], za[2][4];
     auto fetch_x = [&](int j, int buf) {
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int col = CB * j + 16 * cb + l16;
-                xa[buf][cb][v] = A[(size_t)rowc[v] * lda + col];
-                if (PASS1) za[buf][cb][v] = Z[(size_t)rowc[v] * ldz + col];
-            }
+        for (int v = 0; v < 4; ++v) {
+            const int col = CB * j + 16 * h + l16;
+            xa[buf][v] = A[(size_t)rowc[v] * lda + col];
+            if (PASS1) za[buf][v] = Z[(size_t)rowc[v] * ldz + col];
+        }
         __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
     for (int q = 0; q < DIST; ++q)
         if (q < NSTEP) fetch_step(q);
     fetch_x(0, 0);
-    float ya[NBC][8];                 // ya[k][kk] = Y[row0 + l16][32 k + 4 kk + lk]
+    float ya[NBC][8];                 // ya[k][kk] = Y[row0 + l16][32 k + 4 kk + lk], both halves
     int sidx = 0;
 #pragma unroll
     for (int j = 0; j < NBC; ++j) {
         if (j + 1 < NBC) fetch_x(j + 1, (j + 1) & 1);
-        f32x4 acc[2];
+        f32x4 acc;
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                float x = xa[j & 1][cb][v];
-                if (PASS1) x = __builtin_fmaf(eps, za[j & 1][cb][v], sc * x);
-                acc[cb][v] = rin[v] ? x : 0.0f;
-            }
+        for (int v = 0; v < 4; ++v) {
+            float x = xa[j & 1][v];
+            if (PASS1) x = __builtin_fmaf(eps, za[j & 1][v], sc * x);
+            acc[v] = rin[v] ? x : 0.0f;
+        }
 #pragma unroll
         for (int k = 0; k < j; ++k) {
             if (sidx + DIST < NSTEP) fetch_step(sidx + DIST);
-            const float(&o)[2][8] = ob[sidx % (DIST + 1)];
+            const float(&o)[8] = ob[sidx % (DIST + 1)];
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const float a = -ya[k][kk];
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb) acc[cb] = mfma(a, o[cb][kk], acc[cb]);
-            }
+            for (int kk = 0; kk < 8; ++kk) acc = mfma(-ya[k][kk], o[kk], acc);
             ++sidx;
         }
         if (sidx + DIST < NSTEP) fetch_step(sidx + DIST);
-        const float(&li)[2][8] = ob[sidx % (DIST + 1)];
+        const float(&li)[8] = ob[sidx % (DIST + 1)];
         ++sidx;
-        // Y_j = acc_j Li_j^T, acc_j brought to the A-operand layout through LDS
+        // Y_j = acc_j Li_j^T: the product's A operand is acc_j over the block's 32 columns, from both wavefronts
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) st[4 * lk + v][16 * cb + l16] = acc[cb][v];
-        __builtin_amdgcn_wave_barrier();
+        for (int v = 0; v < 4; ++v) sT[0][4 * lk + v][16 * h + l16] = acc[v];
+        __syncthreads();
         float ar[8];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) ar[kk] = st[l16][4 * kk + lk];
-        __builtin_amdgcn_wave_barrier();
-        f32x4 y[2];
+        for (int kk = 0; kk < 8; ++kk) ar[kk] = sT[0][l16][4 * kk + lk];
+        f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            y[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < 8; ++kk)
+            if (kk < 4 * (h + 1)) y = mfma(ar[kk], li[kk], y);
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk)
-                if (kk < 4 * (cb + 1)) y[cb] = mfma(ar[kk], li[cb][kk], y[cb]);
+        for (int v = 0; v < 4; ++v) {
+            if (rin[v]) Y[(size_t)(row0 + 4 * lk + v) * ldy + CB * j + 16 * h + l16] = y[v];
+            sT[1][4 * lk + v][16 * h + l16] = y[v];
         }
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                if (rin[v]) Y[(size_t)(row0 + 4 * lk + v) * ldy + CB * j + 16 * cb + l16] = y[cb][v];
-                st[4 * lk + v][16 * cb + l16] = y[cb][v];
-            }
-        __builtin_amdgcn_wave_barrier();
+        __syncthreads();
         if (j + 1 < NBC) {
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) ya[j][kk] = st[l16][4 * kk + lk];
+            for (int kk = 0; kk < 8; ++kk) ya[j][kk] = sT[1][l16][4 * kk + lk];
         }
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -1531,8 +1541,10 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
     D += (size_t)blockIdx.z * r * ldD;
     const float* __restrict__ Cin = SUB ? Cx : Yin;
     const long ldC = SUB ? ldc : ldy;
-    __shared__ float sY[32][33];
-    __shared__ float sD[32][68];
+    // row strides 34 and 80: each half-wavefront's operand reads (A: rows l16, columns 4kk + lk; B: rows 4kk + lk,
+    // columns l16) fall on 32 distinct banks
+    __shared__ float sY[32][34];
+    __shared__ float sD[32][80];
     const int row0 = blockIdx.x * 32, col0 = blockIdx.y * 64;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
     const int rb = w >> 1, cbase = (w & 1) * 2;
@@ -1636,7 +1648,7 @@ struct spanqr_plan {
     int batch = 1, chol_bmax = 1;   // matrices per call; matrices per Cholesky launch
     size_t lp_stride = 0;           // floats of packed factor per matrix
     int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0, trsm_rb = 1;
-    bool trsm_rows = false;   // solve with one wavefront per 16 rows (k_trsm_rows) instead of k_trsm
+    bool trsm_rows = false;   // solve with a wavefront pair per 16 rows (k_trsm_rows) instead of k_trsm
     size_t bytes = 0;
     char* base = nullptr;
     float *Z = nullptr, *P = nullptr, *G = nullptr, *L = nullptr, *Li = nullptr, *Y0 = nullptr, *Y1 = nullptr;
@@ -1804,10 +1816,10 @@ void launch_trsm_q(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, 
 template <int NBC>
 void launch_trsm_rows(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const Dust& dz,
                       const MatsOut& Y, long ldy, int n, hipStream_t st) {
-    const dim3 grid((p->K + 63) / 64, 1, n);
-    if (pass1) k_trsm_rows<true, NBC><<<grid, 256, 0, st>>>(A, lda, p->K, p->amax_part, dz.z, dz.ldz, eps, p->Lp, Y,
+    const dim3 grid((p->K + 15) / 16, 1, n);
+    if (pass1) k_trsm_rows<true, NBC><<<grid, 128, 0, st>>>(A, lda, p->K, p->amax_part, dz.z, dz.ldz, eps, p->Lp, Y,
                                                             ldy, p->scal);
-    else k_trsm_rows<false, NBC><<<grid, 256, 0, st>>>(A, lda, p->K, p->amax_part, dz.z, dz.ldz, eps, p->Lp, Y, ldy,
+    else k_trsm_rows<false, NBC><<<grid, 128, 0, st>>>(A, lda, p->K, p->amax_part, dz.z, dz.ldz, eps, p->Lp, Y, ldy,
                                                        p->scal);
 }
 
