@@ -502,31 +502,39 @@ __device__ __forceinline__ void store_tile_lower(float* dst, int ld, const Tile&
     }
 }
 
+// The four-quadrant tile helpers below are called by every wavefront of the workgroup (they contain workgroup
+// barriers); the work is done by waves 0-3 (one 16x16 quadrant each) when `on` is set, the others only pass the
+// barriers.
+
 // out = in Li^T; chain over m < 16 (bj + 1) (Li is lower triangular, chol.cu panel). out may alias in.
-__device__ __forceinline__ void panel32(Tile& out, const Tile& in, const Tile& li) {
+__device__ __forceinline__ void panel32(Tile& out, const Tile& in, const Tile& li, bool on = true) {
     WAVE_COORDS;
-    float a[8], b[8];
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-        a[kk] = in[16 * bi + l16][4 * kk + lk];
-        b[kk] = li[16 * bj + l16][4 * kk + lk];
-    }
-    __builtin_amdgcn_sched_barrier(0);   // every operand read issued before the chain
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (on) {
+        float a[8], b[8];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-        if (kk < 4 * (bj + 1)) acc = mfma(a[kk], b[kk], acc);
+        for (int kk = 0; kk < 8; ++kk) {
+            a[kk] = in[16 * bi + l16][4 * kk + lk];
+            b[kk] = li[16 * bj + l16][4 * kk + lk];
+        }
+        __builtin_amdgcn_sched_barrier(0);   // every operand read issued before the chain
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            if (kk < 4 * (bj + 1)) acc = mfma(a[kk], b[kk], acc);
+    }
     __syncthreads();
+    if (on)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) out[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+        for (int v = 0; v < 4; ++v) out[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
     __syncthreads();
 }
 
 // dst = C - Pi Pk^T (chain over m = 0..31 starting from C); lower: skip the upper 16x16 block. dst may alias C.
 // Every wave's global stores have completed when it returns (they are covered by a release made after it).
-__device__ __forceinline__ void update32(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk, bool lower) {
+__device__ __forceinline__ void update32(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk, bool lower,
+                                         bool on = true) {
     WAVE_COORDS;
-    if (!(lower && bi == 0 && bj == 1)) {
+    if (on && !(lower && bi == 0 && bj == 1)) {
         f32x4 acc;
         float a[8], b[8];
 #pragma unroll
@@ -547,55 +555,61 @@ __device__ __forceinline__ void update32(Tile& dst, const Tile& C, const Tile& P
 }
 
 // Two panels in one phase: outA = inA Li^T, outB = inB Li^T (outputs must not alias the inputs)
-__device__ __forceinline__ void panel32x2(Tile& outA, const Tile& inA, Tile& outB, const Tile& inB, const Tile& li) {
+__device__ __forceinline__ void panel32x2(Tile& outA, const Tile& inA, Tile& outB, const Tile& inB, const Tile& li,
+                                          bool on = true) {
     WAVE_COORDS;
-    float xa[8], xb[8], lv[8];
+    if (on) {
+        float xa[8], xb[8], lv[8];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-        xa[kk] = inA[16 * bi + l16][4 * kk + lk];
-        xb[kk] = inB[16 * bi + l16][4 * kk + lk];
-        lv[kk] = li[16 * bj + l16][4 * kk + lk];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-        if (kk < 4 * (bj + 1)) {
-            a = mfma(xa[kk], lv[kk], a);
-            c = mfma(xb[kk], lv[kk], c);
+        for (int kk = 0; kk < 8; ++kk) {
+            xa[kk] = inA[16 * bi + l16][4 * kk + lk];
+            xb[kk] = inB[16 * bi + l16][4 * kk + lk];
+            lv[kk] = li[16 * bj + l16][4 * kk + lk];
         }
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        outA[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
-        outB[16 * bi + 4 * lk + v][16 * bj + l16] = c[v];
+        for (int kk = 0; kk < 8; ++kk)
+            if (kk < 4 * (bj + 1)) {
+                a = mfma(xa[kk], lv[kk], a);
+                c = mfma(xb[kk], lv[kk], c);
+            }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            outA[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
+            outB[16 * bi + 4 * lk + v][16 * bj + l16] = c[v];
+        }
     }
     __syncthreads();
 }
 
 // Two panels in place: A = A Li^T, B = B Li^T (every operand is read before the first write)
-__device__ __forceinline__ void panel32x2_inplace(Tile& A, Tile& B, const Tile& li) {
+__device__ __forceinline__ void panel32x2_inplace(Tile& A, Tile& B, const Tile& li, bool on = true) {
     WAVE_COORDS;
-    float xa[8], xb[8], lv[8];
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-        xa[kk] = A[16 * bi + l16][4 * kk + lk];
-        xb[kk] = B[16 * bi + l16][4 * kk + lk];
-        lv[kk] = li[16 * bj + l16][4 * kk + lk];
-    }
-    __builtin_amdgcn_sched_barrier(0);
     f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
+    if (on) {
+        float xa[8], xb[8], lv[8];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-        if (kk < 4 * (bj + 1)) {
-            a = mfma(xa[kk], lv[kk], a);
-            c = mfma(xb[kk], lv[kk], c);
+        for (int kk = 0; kk < 8; ++kk) {
+            xa[kk] = A[16 * bi + l16][4 * kk + lk];
+            xb[kk] = B[16 * bi + l16][4 * kk + lk];
+            lv[kk] = li[16 * bj + l16][4 * kk + lk];
         }
-    __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        A[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
-        B[16 * bi + 4 * lk + v][16 * bj + l16] = c[v];
+        for (int kk = 0; kk < 8; ++kk)
+            if (kk < 4 * (bj + 1)) {
+                a = mfma(xa[kk], lv[kk], a);
+                c = mfma(xb[kk], lv[kk], c);
+            }
     }
+    __syncthreads();
+    if (on)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            A[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
+            B[16 * bi + 4 * lk + v][16 * bj + l16] = c[v];
+        }
     __syncthreads();
 }
 
@@ -901,8 +915,11 @@ size_t chol_lds_bytes(int r) {
 // flags: [nb * nb] panel flags (L(i, j) published; (j, j): L(j, j) and Li_j), [nb] hand-over flags (tile row i),
 // [64] per-workgroup call counters. STAMP: workgroup 0 records wall_clock64() at 1 + 4j + s for step j: s = 0 step
 // start, 1 tile factored and row j+2 fetched, 2 look-ahead done; slot 0 is the kernel start, 1 + 4 nb the end.
+// Workgroups of eight wavefronts: waves 0-3 do all the work described here; waves 4-7 share the owners' row update
+// with them (two wavefronts per SIMD there, so one's LDS traffic overlaps the other's MFMA chain) and otherwise only
+// pass the same workgroup barriers.
 template <bool STAMP>
-__global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
+__global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
                                               float tau_rel, float* L, float* Li, float* Lp, uint32_t* bar,
                                               uint32_t* flags, float* scal, uint64_t* stamps) {
     extern __shared__ float4 chol_lds[];
@@ -1019,7 +1036,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
             if (w == 0) {
                 factor_inv32(bl0, bl1, pq, z.id, z.D[p], tau, z.dl[p], z.li[p], Li + (size_t)CB * j * CB);
-            } else {
+            } else if (w < 4) {
                 // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p]. Wave 3
                 // publishes the previous step, then applies the part of the previous step's look-ahead that this
                 // step's factor does not need: block j-1 on T(j+1, j) (into X1) and T(j+1, j+1) (into D[pp]), from
@@ -1076,12 +1093,13 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             if (STAMP && tid == 0) stamps[2 + 4 * j] = wall_clock64();
             // look-ahead, the part the next factor needs: L(j+1, j) (and L(j+2, j), in the same phase), then block j
             // on T(j+1, j+1); block j on tile row j+2 is left to wave 3 of the next step
+            const bool q4 = w < 4;
             if (j + 2 < nb) {
-                panel32x2(z.P1[p], z.X1, z.P2[p], z.R2[p][1], z.li[p]);        // L(j+1, j), L(j+2, j)
-                update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true);
+                panel32x2(z.P1[p], z.X1, z.P2[p], z.R2[p][1], z.li[p], q4);    // L(j+1, j), L(j+2, j)
+                update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true, q4);
             } else if (j + 1 < nb) {
-                panel32(z.P1[p], z.X1, z.li[p]);
-                update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true);
+                panel32(z.P1[p], z.X1, z.li[p], q4);
+                update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true, q4);
             }
             if (STAMP && tid == 0) stamps[3 + 4 * j] = wall_clock64();
         }
@@ -1094,9 +1112,11 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
         Tile* op = tiles + nb;
         for (int j = 0; j + 4 <= i; ++j) {
             // workgroup 0's block j: Li_j into op[j], T(j+1, j) and T(j+2, j) (through block j-1) into op[j+1..j+2]
+            const bool q4 = w < 4;
             if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead);
             __syncthreads();
-            load_tiles_ld<3, 256>(&op[j], 3, tid,
+            if (q4)
+                load_tiles_ld<3, 256>(&op[j], 3, tid,
                                   [&](int q) {
                                       return q == 0 ? Li + (size_t)CB * j * CB
                                                     : A + (size_t)CB * (j + q) * r + (size_t)CB * j;
@@ -1105,8 +1125,8 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             __syncthreads();
             const Tile& lij = op[j];
             // panel L(i, j) = T(i, j) Li_j^T, published before anything else (so no row waits on a chain of rows)
-            panel32(rt[j], rt[j], lij);
-            store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j]);
+            panel32(rt[j], rt[j], lij, q4);
+            store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j]);   // threads 0-255
             __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
             __syncthreads();
             if (tid == 0) publish_flag(flagL + i * nb + j, ep);
@@ -1116,7 +1136,7 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
             // are workgroup 0's: their panels are formed here, as workgroup 0 forms them. Row j+3 has just been
             // handed to workgroup 0 (before block j; row 3 never had an owner): its panel too is formed here, from
             // the handed-over T(j+3, j). Rows j+4.. publish their own.
-            panel32x2_inplace(op[j + 1], op[j + 2], lij);                 // L(j+1, j), L(j+2, j)
+            panel32x2_inplace(op[j + 1], op[j + 2], lij, q4);             // L(j+1, j), L(j+2, j)
             const int kend = (j + 4 == i) ? i - 1 : i;
             const bool own3 = j + 3 < kend;
             if (w == 0) {
@@ -1126,24 +1146,27 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
                 wait_flags_wave(f, ep, err, dead);
             }
             __syncthreads();
-            load_tiles<CH_MAXROW, 256>(&op[j + 3], kend - j - 3, r, 0u, 0.f, tid, [&](int q) {
-                const int k = j + 3 + q;
-                return (k == j + 3 ? A : L) + (size_t)CB * k * r + (size_t)CB * j;
-            });
+            if (q4)
+                load_tiles<CH_MAXROW, 256>(&op[j + 3], kend - j - 3, r, 0u, 0.f, tid, [&](int q) {
+                    const int k = j + 3 + q;
+                    return (k == j + 3 ? A : L) + (size_t)CB * k * r + (size_t)CB * j;
+                });
             __syncthreads();
-            if (own3) panel32(op[j + 3], op[j + 3], lij);     // L(j+3, j)
+            if (own3) panel32(op[j + 3], op[j + 3], lij, q4);     // L(j+3, j)
             {
-                // every tile's quadrant (bi, bj) in one phase (the tiles are independent): the panel's A operands stay
-                // in registers, and the next tile's B operands and accumulator are read while this tile's chain runs
-                WAVE_COORDS;
+                // every tile's quadrant in one phase (the tiles are independent): waves w and w + 4 take quadrant
+                // (bi, bj) = (w & 3) of alternate tiles of the row (the tiles k = j+1..i in order, without T(i, i-1)
+                // at the last block and without the upper quadrant of T(i, i)); the panel's A operands stay in
+                // registers, and the next tile's B operands and accumulator are read while this tile's chain runs
+                const int l16 = lane & 15, lk = lane >> 4, qd = w & 3, bi = qd >> 1, bj = qd & 1;
                 float an[8];
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk) an[kk] = -rt[j][16 * bi + l16][4 * kk + lk];
                 const bool upq = (bi == 0 && bj == 1);
-                auto next_k = [&](int k) {
-                    ++k;
-                    if (j + 4 == i && k == i - 1) ++k;
-                    if (k == i && upq) ++k;
+                const int n = i - j - (j + 4 == i ? 1 : 0) - (upq ? 1 : 0);   // tiles in this quadrant's sequence
+                auto kof = [&](int t) {                                       // tile t of the sequence, t < n
+                    int k = j + 1 + t;
+                    if (j + 4 == i && k >= i - 1) ++k;
                     return k;
                 };
                 auto fetch = [&](int k, float (&bv)[8], f32x4& acc) {
@@ -1153,19 +1176,15 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
 #pragma unroll
                     for (int v = 0; v < 4; ++v) acc[v] = rt[k][16 * bi + 4 * lk + v][16 * bj + l16];
                 };
-                // two operand sets in turn: tile k's chain runs while tile kn's operands are in flight
+                // two operand sets in turn: tile t's chain runs while the operands of this wave's next tile are in
+                // flight; the prefetch is unconditional (past the last tile it reads tile t again, unused), so the
+                // wait before a chain only ever covers the previous prefetch
                 auto chain = [&](int k, const float (&bv)[8], f32x4 acc) {
 #pragma unroll
                     for (int kk = 0; kk < 8; ++kk) acc = mfma(an[kk], bv[kk], acc);
 #pragma unroll
                     for (int v = 0; v < 4; ++v) rt[k][16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
                 };
-                int k = next_k(j);
-                float b0[8], b1[8];
-                f32x4 c0, c1;
-                if (k <= i) fetch(k, b0, c0);
-                // the prefetch is unconditional (past the last tile it reads tile k again, unused), so the wait before
-                // a chain only ever covers the previous prefetch
                 // In-order issue: the next tile's reads go between the chain's first MFMAs (two after each), where they
                 // issue while the previous MFMA runs and complete before the chain ends.
                 auto interleave = [&]() {
@@ -1176,18 +1195,22 @@ __global__ __launch_bounds__(256) void k_chol(float* A, int r, const double* __r
                     }
                     __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
                 };
-                while (k <= i) {
-                    int kn = next_k(k);
-                    fetch(kn <= i ? kn : k, b1, c1);
-                    chain(k, b0, c0);
+                int t = w >> 2;                 // this wave's tiles: t, t + 2, ...
+                float b0[8], b1[8];
+                f32x4 c0, c1;
+                if (t < n) fetch(kof(t), b0, c0);
+                while (t < n) {
+                    int tn = t + 2;
+                    fetch(kof(tn < n ? tn : t), b1, c1);
+                    chain(kof(t), b0, c0);
                     interleave();
-                    k = kn;
-                    if (k > i) break;
-                    kn = next_k(k);
-                    fetch(kn <= i ? kn : k, b0, c0);
-                    chain(k, b1, c1);
+                    t = tn;
+                    if (t >= n) break;
+                    tn = t + 2;
+                    fetch(kof(tn < n ? tn : t), b0, c0);
+                    chain(kof(t), b1, c1);
                     interleave();
-                    k = kn;
+                    t = tn;
                 }
                 __syncthreads();
             }
@@ -1753,9 +1776,9 @@ int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t
         float* sc = scal ? scal + (size_t)z0 * SCAL_STRIDE : nullptr;
         const dim3 grid(p->chol_grid, 1, nz);
         if (stamp)
-            k_chol<true><<<grid, 256, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps);
+            k_chol<true><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps);
         else
-            k_chol<false><<<grid, 256, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps);
+            k_chol<false><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps);
         HIPCHK(hipGetLastError());
     }
     return SPANQR_OK;
@@ -2111,7 +2134,7 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
             return fail(SPANQR_EHIP, "setting the Cholesky's LDS size (%d bytes) failed: %s", need, hipGetErrorString(e));
         }
     }
-    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol<true>, 256, chol_lds_bytes(r)));
+    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol<true>, 512, chol_lds_bytes(r)));
     HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
     if (occ * cus < p->chol_grid) {
         const int need = p->chol_grid;
