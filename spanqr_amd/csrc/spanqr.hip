@@ -95,6 +95,22 @@ __device__ float block_scale(const uint32_t* __restrict__ part) {
     return pow2_scale_bits(t);
 }
 
+// As block_scale, for a 512-thread workgroup (threads 256-511 contribute 0, the identity of the maximum of patterns)
+__device__ float block_scale512(const uint32_t* __restrict__ part) {
+    __shared__ uint32_t sm[8];
+    uint32_t m = threadIdx.x < 256 ? part[threadIdx.x] : 0u;
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)m, off);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    uint32_t t = sm[0];
+    for (int i = 1; i < 8; ++i) t = sm[i] > t ? sm[i] : t;
+    __syncthreads();
+    return pow2_scale_bits(t);
+}
+
 // As block_scale, for a 128-thread workgroup (each thread takes two of the partial maxima; the maximum is exact)
 __device__ float block_scale128(const uint32_t* __restrict__ part) {
     __shared__ uint32_t sm[2];
@@ -190,7 +206,7 @@ __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
 // CROSS: partials of A^T B instead (the block projection of the column-blocked path, kbig.py:88-89): every tile
 // u = ti * ntb + tj of the (columns of A) x (ntb * 64 columns of B) product, A's panel ti against B's panel tj.
 template <bool KAHAN, bool SCALE, bool CROSS = false>
-__global__ __launch_bounds__(256) void k_gram(const MatsIn As, long lda, int K, int nt, int KS,
+__global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, int nt, int KS,
                                               const uint32_t* __restrict__ amax_part, float* __restrict__ P,
                                               const float* __restrict__ Bx = nullptr, long ldb = 0, int ntb = 0) {
     const int u = blockIdx.x, sp = blockIdx.y, U = gridDim.x;
@@ -207,40 +223,36 @@ __global__ __launch_bounds__(256) void k_gram(const MatsIn As, long lda, int K, 
     const float* __restrict__ B = CROSS ? Bx : A;
     const long ldbb = CROSS ? ldb : lda;
     float sc = 1.0f;
-    if (SCALE) sc = block_scale(amax_part);
+    if (SCALE) sc = block_scale512(amax_part);
     __shared__ float sA[BK][TB + 16];
     __shared__ float sB[BK][TB + 16];
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int qi = w >> 1, qj = w & 1, l16 = lane & 15, lk = lane >> 4;
-    f32x4 acc[2][2], comp[2][2];
+    // eight wavefronts: wave w computes rows 32 qi + 16 a (a = 0, 1) x columns 32 qj + 16 hb of the 64x64 tile, with
+    // qi = (w >> 1) & 1, qj = w & 1, hb = w >> 2 (two per SIMD, so one's LDS traffic overlaps the other's MFMAs)
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int qi = (w >> 1) & 1, qj = w & 1, hb = w >> 2, l16 = lane & 15, lk = lane >> 4;
+    f32x4 acc[2], comp[2];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-            comp[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+    for (int a = 0; a < 2; ++a) {
+        acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+        comp[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     const int k0 = sp * KS;
     const int k1 = (k0 + KS < K) ? k0 + KS : K;
     // chunk kc + BK is loaded into registers while chunk kc is multiplied; rows past the split read row k1 - 1
     // (in bounds) and are zeroed, so the loads are unconditional
-    float4 ra[2], rb[2];
+    float4 ra, rb;
+    const int grow = tid >> 4, gc4 = tid & 15;   // this thread's float4 of each 32 x 64 chunk
     auto gload = [&](int kc) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15, k = kc + row;
-            const int kr = k < k1 ? k : k1 - 1;
-            ra[q] = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + ti * TB + 4 * c4);
-            rb[q] = *reinterpret_cast<const float4*>(B + (size_t)kr * ldbb + tj * TB + 4 * c4);
-        }
+        const int k = kc + grow;
+        const int kr = k < k1 ? k : k1 - 1;
+        ra = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + ti * TB + 4 * gc4);
+        rb = *reinterpret_cast<const float4*>(B + (size_t)kr * ldbb + tj * TB + 4 * gc4);
     };
     gload(k0);
     for (int kc = k0; kc < k1; kc += BK) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15;
-            const bool in = kc + row < k1;
-            float4 va = ra[q], vb = rb[q];
+        {
+            const bool in = kc + grow < k1;
+            float4 va = ra, vb = rb;
             if (SCALE) {
                 va.x = sc * va.x; va.y = sc * va.y; va.z = sc * va.z; va.w = sc * va.w;
                 vb.x = sc * vb.x; vb.y = sc * vb.y; vb.z = sc * vb.z; vb.w = sc * vb.w;
@@ -249,53 +261,44 @@ __global__ __launch_bounds__(256) void k_gram(const MatsIn As, long lda, int K, 
                 va = make_float4(0.f, 0.f, 0.f, 0.f);
                 vb = make_float4(0.f, 0.f, 0.f, 0.f);
             }
-            *reinterpret_cast<float4*>(&sA[row][4 * c4]) = va;
-            *reinterpret_cast<float4*>(&sB[row][4 * c4]) = vb;
+            *reinterpret_cast<float4*>(&sA[grow][4 * gc4]) = va;
+            *reinterpret_cast<float4*>(&sB[grow][4 * gc4]) = vb;
         }
         __syncthreads();
         if (kc + BK < k1) gload(kc + BK);
         __builtin_amdgcn_sched_barrier(0);   // the loads go out before the MFMAs
-        f32x4 part[2][2];
+        f32x4 part[2];
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int b = 0; b < 2; ++b) part[a][b] = KAHAN ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[a][b];
+        for (int a = 0; a < 2; ++a) part[a] = KAHAN ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[a];
 #pragma unroll
         for (int kk = 0; kk < BK / 4; ++kk) {
             const int kr = 4 * kk + lk;
             const float a0 = sA[kr][qi * 32 + l16], a1 = sA[kr][qi * 32 + 16 + l16];
-            const float b0 = sB[kr][qj * 32 + l16], b1 = sB[kr][qj * 32 + 16 + l16];
-            part[0][0] = mfma(a0, b0, part[0][0]);
-            part[0][1] = mfma(a0, b1, part[0][1]);
-            part[1][0] = mfma(a1, b0, part[1][0]);
-            part[1][1] = mfma(a1, b1, part[1][1]);
+            const float b0 = sB[kr][qj * 32 + 16 * hb + l16];
+            part[0] = mfma(a0, b0, part[0]);
+            part[1] = mfma(a1, b0, part[1]);
         }
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int a = 0; a < 2; ++a) {
+            if (KAHAN) {
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                if (KAHAN) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const float y = part[a][b][v] - comp[a][b][v];
-                        const float t = acc[a][b][v] + y;
-                        comp[a][b][v] = (t - acc[a][b][v]) - y;
-                        acc[a][b][v] = t;
-                    }
-                } else {
-                    acc[a][b] = part[a][b];
+                for (int v = 0; v < 4; ++v) {
+                    const float y = part[a][v] - comp[a][v];
+                    const float t = acc[a][v] + y;
+                    comp[a][v] = (t - acc[a][v]) - y;
+                    acc[a][v] = t;
                 }
+            } else {
+                acc[a] = part[a];
             }
+        }
         __syncthreads();
     }
     float* Pt = P + ((size_t)sp * U + u) * TB * TB;
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                Pt[(qi * 32 + a * 16 + 4 * lk + v) * TB + qj * 32 + b * 16 + l16] = acc[a][b][v];
+        for (int v = 0; v < 4; ++v) Pt[(qi * 32 + a * 16 + 4 * lk + v) * TB + qj * 32 + hb * 16 + l16] = acc[a][v];
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1745,10 +1748,10 @@ MatsOut buf_out(const spanqr_plan* p, float* base) {
 
 void launch_gram(const spanqr_plan* p, const MatsIn& A, long lda, int n, bool scale, bool kahan, hipStream_t st) {
     const dim3 grid(p->U, p->S, n);
-    if (kahan && scale) k_gram<true, true><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
-    else if (kahan) k_gram<true, false><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
-    else if (scale) k_gram<false, true><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
-    else k_gram<false, false><<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    if (kahan && scale) k_gram<true, true><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    else if (kahan) k_gram<true, false><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    else if (scale) k_gram<false, true><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    else k_gram<false, false><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
 }
 
 void launch_reduce(const spanqr_plan* p, int mode, float* out, int n, hipStream_t st) {
@@ -2030,7 +2033,7 @@ void project(const spanqr_plan* p, const float* Q, long ldq, int j, const float*
     int S = 0, KS = 0;
     split_policy(p->K, U, &S, &KS);
     const MatsIn P = mats_in(&Q, 1);
-    k_gram<false, false, true><<<dim3(U, S), 256, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, BW / TB);
+    k_gram<false, false, true><<<dim3(U, S), 512, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, BW / TB);
     k_reduce<2><<<dim3(16, U), 256, 0, st>>>(p->Tp, S, BW / TB, BW, p->T, nullptr);
     k_nsapply<true><<<dim3((p->K + 31) / 32, BW / 64), 256, 0, st>>>(P, ldq, p->K, j, p->T, mats_out(&Out, 1), BW, Cin,
                                                                     ldc, BW);
