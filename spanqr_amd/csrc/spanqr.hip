@@ -14,8 +14,8 @@
 //     LDS; the 32x32 diagonal tiles are factored in one wavefront's registers (lane = row) and inverted (lanes
 //     32-63) in the same pass, and the factor is published both row-major and packed as the solve's MFMA operands;
 //   * the triangular solve is row-block parallel: for tall X a pair of wavefronts per 16 rows runs through all column
-//     blocks, one 16-column half of each, with its operands streamed ahead (k_trsm_rows); otherwise each of four
-//     wavefronts owns every 4th 32-column block of a row block and applies a finished block to its later blocks with
+//     blocks, one 16-column half of each, with its operands streamed ahead (k_trsm_rows); otherwise each of eight
+//     wavefronts owns every 8th 32-column block of a row block and applies a finished block to its later blocks with
 //     MFMA (k_trsm);
 //   * every kernel takes its matrix of a batch from blockIdx.z (pointer tables passed by value), so a shape group of
 //     layers runs as one launch per stage.
@@ -1232,8 +1232,8 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Triangular solve Y = A L^-T (tri.py:378-412). A workgroup takes RB blocks of 16 rows; wave w owns the 32-column
-// blocks j = w, w+4, ... of all of them and keeps their accumulators (acc_j starts at a_j; pass 1:
+// Triangular solve Y = A L^-T (tri.py:378-412). A workgroup of eight wavefronts takes RB blocks of 16 rows; wave w
+// owns the 32-column blocks j = w, w+8, ... of all of them and keeps their accumulators (acc_j starts at a_j; pass 1:
 // fmaf(eps, z, s * x)). For k = 0..nbc-1 the owner of block k forms Y_k = acc_k Li_k^T (chain over
 // m < 16 (c/16 + 1)), publishes it in LDS behind a flag, and every wave applies it to its later blocks:
 // acc_j -= Y_k L_jk^T (chain over the 32 columns of block k), so each element's chain runs over m = 0..32j-1 in
@@ -1268,19 +1268,21 @@ __device__ __forceinline__ void trsm_fetch_li(float (&li)[2][8], const float* __
     fetch_op(li, Lp, k, k, lane);
 }
 
+constexpr int TRSM_NW = 8;   // wavefronts per k_trsm workgroup; wave w owns the column blocks w + TRSM_NW q
+
 template <int Q>
 __device__ __forceinline__ void trsm_fetch(TrsmOps<Q>& o, const float* __restrict__ Lp, int nbc, int k, int w,
                                            int lane) {
     if (k >= nbc) return;
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
-        const int j = w + 4 * q;
+        const int j = w + TRSM_NW * q;
         if (j > k && j < nbc) fetch_op(o.l[q], Lp, j, k, lane);
     }
 }
 
 template <bool PASS1, int Q, int RB>
-__global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, int r,
+__global__ __launch_bounds__(64 * TRSM_NW) void k_trsm(const MatsIn As, long lda, int K, int r,
                                               const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
                                               long ldz, float eps, const float* __restrict__ Lp, const MatsOut Ys,
                                               long ldy,
@@ -1293,22 +1295,22 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
     if (scal != nullptr) scal += (size_t)blockIdx.z * SCAL_STRIDE;
     const int ldsy = r + 4;
     float* sY = smem;                          // [16 RB][r + 4]: finished Y columns (MFMA A operands)
-    float* sAcc = sY + 16 * RB * ldsy;         // [4][16][33]: per-wave transpose of the block being finished
-    uint32_t* sFlag = reinterpret_cast<uint32_t*>(sAcc + 4 * 16 * 33);   // [nbc]
+    float* sAcc = sY + 16 * RB * ldsy;         // [TRSM_NW][16][33]: per-wave transpose of the block being finished
+    uint32_t* sFlag = reinterpret_cast<uint32_t*>(sAcc + TRSM_NW * 16 * 33);   // [nbc]
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
     const int row0 = blockIdx.x * 16 * RB, nbc = r / CB;
     float sc = 1.0f;
     if (PASS1) {
-        sc = block_scale(amax_part);
+        sc = block_scale512(amax_part);
         if (blockIdx.x == 0 && tid == 0 && scal != nullptr) scal[0] = sc;
     }
-    for (int k = tid; k < nbc; k += 256) sFlag[k] = 0u;
+    for (int k = tid; k < nbc; k += 64 * TRSM_NW) sFlag[k] = 0u;
     f32x4 acc[RB][Q][2];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
-            const int j = w + 4 * q;
+            const int j = w + TRSM_NW * q;
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
@@ -1324,7 +1326,7 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
         }
     TrsmOps<Q> cur, nxt;
     trsm_fetch<Q>(cur, Lp, nbc, 0, w, lane);
-    float li[2][8];   // Li of this wave's next block to finish (fetched four steps ahead)
+    float li[2][8];   // Li of this wave's next block to finish (fetched TRSM_NW steps ahead)
     trsm_fetch_li(li, Lp, nbc, w, lane);
     __syncthreads();   // flags cleared
     const bool full = row0 + 16 * RB <= K;   // every row of the workgroup exists: stores need no bounds check
@@ -1360,7 +1362,7 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
             __builtin_amdgcn_wave_barrier();
         }
         if (lane == 0) __hip_atomic_store(&sFlag[k], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        trsm_fetch_li(li, Lp, nbc, k + 4, lane);
+        trsm_fetch_li(li, Lp, nbc, k + TRSM_NW, lane);
     };
     // acc_j -= Y_k L_jk^T for owned block q
     auto apply = [&](int k, int q) {
@@ -1380,8 +1382,8 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
 #pragma unroll
     for (int qk = 0; qk < Q; ++qk) {
 #pragma unroll
-        for (int ow = 0; ow < 4; ++ow) {
-            const int k = 4 * qk + ow;
+        for (int ow = 0; ow < TRSM_NW; ++ow) {
+            const int k = TRSM_NW * qk + ow;
             if (k < nbc) {
                 trsm_fetch<Q>(nxt, Lp, nbc, k + 1, w, lane);
                 if (w != ow) {
@@ -1392,21 +1394,20 @@ __global__ __launch_bounds__(256) void k_trsm(const MatsIn As, long lda, int K, 
                     }
                 }
                 // the owner of block k+1 brings it up to date and publishes it before its other updates
-                const int kn = k + 1, qn = kn >> 2;
+                const int kn = k + 1;
 #pragma unroll
                 for (int q = 0; q < Q; ++q) {
-                    const int j = w + 4 * q;
+                    const int j = w + TRSM_NW * q;
                     if (j == kn && j < nbc) apply(k, q);
                 }
 #pragma unroll
                 for (int q = 0; q < Q; ++q) {
-                    const int j = w + 4 * q;
+                    const int j = w + TRSM_NW * q;
                     if (j == kn && j < nbc) finish(kn, q);
                 }
-                (void)qn;
 #pragma unroll
                 for (int q = 0; q < Q; ++q) {
-                    const int j = w + 4 * q;
+                    const int j = w + TRSM_NW * q;
                     if (j > kn && j < nbc) apply(k, q);
                 }
                 cur = nxt;
@@ -1722,7 +1723,7 @@ int check_mat(const spanqr_plan* p, const float* M, long ld, const char* name) {
     return SPANQR_OK;
 }
 
-size_t trsm_lds(int r, int rb) { return (size_t)(16 * rb * (r + 4) + 4 * 16 * 33 + r / CB) * sizeof(float); }
+size_t trsm_lds(int r, int rb) { return (size_t)(16 * rb * (r + 4) + TRSM_NW * 16 * 33 + r / CB) * sizeof(float); }
 
 MatsIn mats_in(const float* const* X, int n) {
     MatsIn m{};
@@ -1797,19 +1798,8 @@ hipError_t trsm_set_lds(int r) {
 }
 
 hipError_t trsm_set_lds_plan(int q, int rb, int r) {
-#define TRSM_ATTR(QQ)                                         \
-    case QQ:                                                  \
-        if (rb == 4) return trsm_set_lds<QQ, 4>(r);           \
-        if (rb == 2) return trsm_set_lds<QQ, 2>(r);           \
-        return trsm_set_lds<QQ, 1>(r);
-    switch (q) {
-        TRSM_ATTR(1)
-        TRSM_ATTR(2)
-        TRSM_ATTR(3)
-        default:
-        TRSM_ATTR(4)
-    }
-#undef TRSM_ATTR
+    if (q == 1) return rb == 2 ? trsm_set_lds<1, 2>(r) : trsm_set_lds<1, 1>(r);
+    return rb == 2 ? trsm_set_lds<2, 2>(r) : trsm_set_lds<2, 1>(r);
 }
 
 // the dust the pass-1 solve adds: the plan's own Z [K, r], or a column slice of a wider one (row stride ldz)
@@ -1823,20 +1813,17 @@ void launch_trsm_t(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, 
                    const MatsOut& Y, long ldy, int n, hipStream_t st) {
     const dim3 grid((p->K + 16 * RB - 1) / (16 * RB), 1, n);
     const size_t lds = trsm_lds(p->r, RB);
-    if (pass1) k_trsm<true, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, dz.z, dz.ldz, eps, p->Lp,
+    if (pass1) k_trsm<true, Q, RB><<<grid, 64 * TRSM_NW, lds, st>>>(A, lda, p->K, p->r, p->amax_part, dz.z, dz.ldz, eps, p->Lp,
                                                            Y, ldy, p->scal);
-    else k_trsm<false, Q, RB><<<grid, 256, lds, st>>>(A, lda, p->K, p->r, p->amax_part, dz.z, dz.ldz, eps, p->Lp, Y,
+    else k_trsm<false, Q, RB><<<grid, 64 * TRSM_NW, lds, st>>>(A, lda, p->K, p->r, p->amax_part, dz.z, dz.ldz, eps, p->Lp, Y,
                                                       ldy, p->scal);
 }
 
 template <int Q>
 void launch_trsm_q(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const Dust& dz,
                    const MatsOut& Y, long ldy, int n, hipStream_t st) {
-    switch (p->trsm_rb) {
-        case 4: launch_trsm_t<Q, 4>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
-        case 2: launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
-        default: launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
-    }
+    if (p->trsm_rb == 2) launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st);
+    else launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, dz, Y, ldy, n, st);
 }
 
 template <int NBC>
@@ -1861,11 +1848,9 @@ void launch_trsm(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, fl
         }
         return;
     }
-    switch (p->trsm_q) {
+    switch (p->trsm_q) {   // r <= 512: at most two column blocks per wavefront
         case 1: launch_trsm_q<1>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
-        case 2: launch_trsm_q<2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
-        case 3: launch_trsm_q<3>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
-        default: launch_trsm_q<4>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+        default: launch_trsm_q<2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
     }
 }
 
@@ -2105,12 +2090,12 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
     p->nt = r / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / 64;
     split_policy(K, p->U, &p->S, &p->KS);
     p->chol_grid = (r / CB > 4) ? r / CB - 3 : 1;     // workgroup 0 + one per tile row 4..r/32-1
-    p->trsm_q = (r / CB + 3) / 4;
+    p->trsm_q = (r / CB + TRSM_NW - 1) / TRSM_NW;
     // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU
-    p->trsm_rb = ((K + 15) / 16 >= 2048) ? 4 : ((K + 15) / 16 >= 1024 ? 2 : 1);
-    // one wavefront per 16 rows once there are enough rows to occupy the SIMDs (its per-wave chain over r/32
-    // blocks is long; the measured crossover at r = 256 lies between K = 8192 and 10240); below that, k_trsm
-    // splits each row block's columns over four waves
+    p->trsm_rb = ((K + 15) / 16 >= 1024) ? 2 : 1;
+    // a wavefront pair per 16 rows once there are enough rows to occupy the SIMDs (the chain over r/32 blocks is
+    // long; the measured crossover at r = 256 lies near K = 8192-10240); below that, k_trsm splits each row block's
+    // columns over eight waves
     p->trsm_rows = r <= 256 && K >= 9216;
     {
         const size_t need = trsm_lds(r, p->trsm_rb);
