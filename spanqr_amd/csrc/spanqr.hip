@@ -1798,7 +1798,8 @@ hipError_t trsm_set_lds(int r) {
 }
 
 hipError_t trsm_set_lds_plan(int q, int rb, int r) {
-    if (q == 1) return rb == 2 ? trsm_set_lds<1, 2>(r) : trsm_set_lds<1, 1>(r);
+    // two row blocks only with two column blocks per wave (r > 256, K >= 16384; taller r <= 256 takes k_trsm_rows)
+    if (q == 1) return trsm_set_lds<1, 1>(r);
     return rb == 2 ? trsm_set_lds<2, 2>(r) : trsm_set_lds<2, 1>(r);
 }
 
@@ -1822,8 +1823,13 @@ void launch_trsm_t(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, 
 template <int Q>
 void launch_trsm_q(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, float eps, const Dust& dz,
                    const MatsOut& Y, long ldy, int n, hipStream_t st) {
-    if (p->trsm_rb == 2) launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st);
-    else launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, dz, Y, ldy, n, st);
+    if constexpr (Q == 2) {
+        if (p->trsm_rb == 2) {
+            launch_trsm_t<Q, 2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st);
+            return;
+        }
+    }
+    launch_trsm_t<Q, 1>(p, A, lda, pass1, eps, dz, Y, ldy, n, st);
 }
 
 template <int NBC>

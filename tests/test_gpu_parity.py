@@ -102,9 +102,10 @@ def test_chol32_absolute(cuda, K, r):
     assert_bits(Li, Lio, "Li")
 
 
-# K >= 9216 (r <= 256) takes the one-wavefront-per-16-rows solve, below it the column-blocked one; ragged K on both
+# K >= 9216 (r <= 256) takes the row-blocked solve (a wavefront pair per 16 rows), below it the column-blocked one
+# (16400 x 384: two column blocks per wave and two row blocks per workgroup, the last one past K); ragged K on all
 @pytest.mark.parametrize("K,r", SHAPES + [(16384, 256), (32768, 64), (4100, 128), (4111, 192), (9230, 192),
-                                          (16400, 256), (16425, 128)])
+                                          (16400, 256), (16425, 128), (16400, 384)])
 @pytest.mark.parametrize("pass1", [True, False])
 def test_trsm(cuda, K, r, pass1):
     print(f"trsm {K}x{r} pass1={pass1}", flush=True)
