@@ -393,22 +393,6 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 
 typedef float Tile[CB][TS];
 
-// global 32x32 tile (row stride ld) -> LDS tile by threads t0, t0 + nthr, ... of the workgroup; adds `shift` to the
-// diagonal when diag is set
-__device__ __forceinline__ void load_tile(Tile& dst, const float* src, int ld, bool diag, float shift, int t = -1,
-                                          int nthr = 256) {
-    for (int e = (t < 0 ? (int)threadIdx.x : t); e < 256; e += nthr) {
-        const int row = e >> 3, c4 = e & 7;
-        const float4 v = *reinterpret_cast<const float4*>(src + (size_t)row * ld + 4 * c4);
-        float x[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if (diag && row == 4 * c4 + q) x[q] = x[q] + shift;
-            dst[row][4 * c4 + q] = x[q];
-        }
-    }
-}
-
 __device__ __forceinline__ void store_tile(float* dst, int ld, const Tile& src, int t = -1, int nthr = 256) {
     for (int e = (t < 0 ? (int)threadIdx.x : t); e < 256; e += nthr) {
         const int row = e >> 3, c4 = e & 7;
