@@ -192,8 +192,8 @@ __global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, 
 
 // ---------------------------------------------------------------------------------------------------------------
 // Gram partials (tri.py:255-297, 324-375): workgroup (u, sp) computes upper 64x64 tile u = (ti, tj) of A^T A over
-// rows [sp*KS, min((sp+1)*KS, K)), in 32-row chunks staged through LDS (rows past the split read as 0; the next
-// chunk is fetched into registers while this one is multiplied). Wave w owns the 32x32 quadrant (w >> 1, w & 1). KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one
+// rows [sp*KS, min((sp+1)*KS, K)), in 32-row chunks staged through LDS two at a time (rows past the split read as 0;
+// the next two chunks are fetched into registers while these are multiplied). Wave w owns the 32x32 quadrant (w >> 1, w & 1). KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one
 // chain runs over the whole split. SCALE: operands are s * a with the pass-1 power-of-2 scale.
 // ---------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
@@ -224,8 +224,8 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
     const long ldbb = CROSS ? ldb : lda;
     float sc = 1.0f;
     if (SCALE) sc = block_scale512(amax_part);
-    __shared__ float sA[BK][TB + 16];
-    __shared__ float sB[BK][TB + 16];
+    __shared__ float sA[2 * BK][TB + 16];
+    __shared__ float sB[2 * BK][TB + 16];
     // eight wavefronts: wave w computes rows 32 qi + 16 a (a = 0, 1) x columns 32 qj + 16 hb of the 64x64 tile, with
     // qi = (w >> 1) & 1, qj = w & 1, hb = w >> 2 (two per SIMD, so one's LDS traffic overlaps the other's MFMAs)
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -238,21 +238,25 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
     }
     const int k0 = sp * KS;
     const int k1 = (k0 + KS < K) ? k0 + KS : K;
-    // chunk kc + BK is loaded into registers while chunk kc is multiplied; rows past the split read row k1 - 1
-    // (in bounds) and are zeroed, so the loads are unconditional
-    float4 ra, rb;
+    // stages of two BK-row chunks: stage kc + 2 BK is loaded into registers while the chunks of stage kc are
+    // multiplied; rows past the split read row k1 - 1 (in bounds) and are zeroed, so the loads are unconditional
+    float4 ra[2], rb[2];
     const int grow = tid >> 4, gc4 = tid & 15;   // this thread's float4 of each 32 x 64 chunk
     auto gload = [&](int kc) {
-        const int k = kc + grow;
-        const int kr = k < k1 ? k : k1 - 1;
-        ra = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + ti * TB + 4 * gc4);
-        rb = *reinterpret_cast<const float4*>(B + (size_t)kr * ldbb + tj * TB + 4 * gc4);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = kc + h * BK + grow;
+            const int kr = k < k1 ? k : k1 - 1;
+            ra[h] = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + ti * TB + 4 * gc4);
+            rb[h] = *reinterpret_cast<const float4*>(B + (size_t)kr * ldbb + tj * TB + 4 * gc4);
+        }
     };
     gload(k0);
-    for (int kc = k0; kc < k1; kc += BK) {
-        {
-            const bool in = kc + grow < k1;
-            float4 va = ra, vb = rb;
+    for (int kc = k0; kc < k1; kc += 2 * BK) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const bool in = kc + h * BK + grow < k1;
+            float4 va = ra[h], vb = rb[h];
             if (SCALE) {
                 va.x = sc * va.x; va.y = sc * va.y; va.z = sc * va.z; va.w = sc * va.w;
                 vb.x = sc * vb.x; vb.y = sc * vb.y; vb.z = sc * vb.z; vb.w = sc * vb.w;
@@ -261,35 +265,39 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
                 va = make_float4(0.f, 0.f, 0.f, 0.f);
                 vb = make_float4(0.f, 0.f, 0.f, 0.f);
             }
-            *reinterpret_cast<float4*>(&sA[grow][4 * gc4]) = va;
-            *reinterpret_cast<float4*>(&sB[grow][4 * gc4]) = vb;
+            *reinterpret_cast<float4*>(&sA[h * BK + grow][4 * gc4]) = va;
+            *reinterpret_cast<float4*>(&sB[h * BK + grow][4 * gc4]) = vb;
         }
         __syncthreads();
-        if (kc + BK < k1) gload(kc + BK);
+        if (kc + 2 * BK < k1) gload(kc + 2 * BK);
         __builtin_amdgcn_sched_barrier(0);   // the loads go out before the MFMAs
-        f32x4 part[2];
 #pragma unroll
-        for (int a = 0; a < 2; ++a) part[a] = KAHAN ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[a];
+        for (int h = 0; h < 2; ++h) {
+            if (kc + h * BK >= k1) break;    // a chunk wholly past the split is not part of the sum
+            f32x4 part[2];
 #pragma unroll
-        for (int kk = 0; kk < BK / 4; ++kk) {
-            const int kr = 4 * kk + lk;
-            const float a0 = sA[kr][qi * 32 + l16], a1 = sA[kr][qi * 32 + 16 + l16];
-            const float b0 = sB[kr][qj * 32 + 16 * hb + l16];
-            part[0] = mfma(a0, b0, part[0]);
-            part[1] = mfma(a1, b0, part[1]);
-        }
+            for (int a = 0; a < 2; ++a) part[a] = KAHAN ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[a];
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-            if (KAHAN) {
+            for (int kk = 0; kk < BK / 4; ++kk) {
+                const int kr = h * BK + 4 * kk + lk;
+                const float a0 = sA[kr][qi * 32 + l16], a1 = sA[kr][qi * 32 + 16 + l16];
+                const float b0 = sB[kr][qj * 32 + 16 * hb + l16];
+                part[0] = mfma(a0, b0, part[0]);
+                part[1] = mfma(a1, b0, part[1]);
+            }
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const float y = part[a][v] - comp[a][v];
-                    const float t = acc[a][v] + y;
-                    comp[a][v] = (t - acc[a][v]) - y;
-                    acc[a][v] = t;
+            for (int a = 0; a < 2; ++a) {
+                if (KAHAN) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float y = part[a][v] - comp[a][v];
+                        const float t = acc[a][v] + y;
+                        comp[a][v] = (t - acc[a][v]) - y;
+                        acc[a][v] = t;
+                    }
+                } else {
+                    acc[a] = part[a];
                 }
-            } else {
-                acc[a] = part[a];
             }
         }
         __syncthreads();
