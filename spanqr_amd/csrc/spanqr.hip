@@ -192,8 +192,8 @@ __global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, 
 
 // ---------------------------------------------------------------------------------------------------------------
 // Gram partials (tri.py:255-297, 324-375): workgroup (u, sp) computes upper 64x64 tile u = (ti, tj) of A^T A over
-// rows [sp*KS, min((sp+1)*KS, K)), in 32-row chunks staged through LDS two at a time (rows past the split read as 0;
-// the next two chunks are fetched into registers while these are multiplied). Wave w owns the 32x32 quadrant (w >> 1, w & 1). KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one
+// rows [sp*KS, min((sp+1)*KS, K)), in 32-row chunks staged through LDS NCH at a time (rows past the split read as 0;
+// the next NCH chunks are fetched into registers while these are multiplied). Wave w owns the 32x32 quadrant (w >> 1, w & 1). KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one
 // chain runs over the whole split. SCALE: operands are s * a with the pass-1 power-of-2 scale.
 // ---------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
@@ -205,7 +205,7 @@ __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
 
 // CROSS: partials of A^T B instead (the block projection of the column-blocked path, kbig.py:88-89): every tile
 // u = ti * ntb + tj of the (columns of A) x (ntb * 64 columns of B) product, A's panel ti against B's panel tj.
-template <bool KAHAN, bool SCALE, bool CROSS = false>
+template <bool KAHAN, bool SCALE, bool CROSS = false, int NCH = 1>
 __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, int nt, int KS,
                                               const uint32_t* __restrict__ amax_part, float* __restrict__ P,
                                               const float* __restrict__ Bx = nullptr, long ldb = 0, int ntb = 0) {
@@ -224,8 +224,8 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
     const long ldbb = CROSS ? ldb : lda;
     float sc = 1.0f;
     if (SCALE) sc = block_scale512(amax_part);
-    __shared__ float sA[2 * BK][TB + 16];
-    __shared__ float sB[2 * BK][TB + 16];
+    __shared__ float sA[NCH * BK][TB + 16];
+    __shared__ float sB[NCH * BK][TB + 16];
     // eight wavefronts: wave w computes rows 32 qi + 16 a (a = 0, 1) x columns 32 qj + 16 hb of the 64x64 tile, with
     // qi = (w >> 1) & 1, qj = w & 1, hb = w >> 2 (two per SIMD, so one's LDS traffic overlaps the other's MFMAs)
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -238,13 +238,13 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
     }
     const int k0 = sp * KS;
     const int k1 = (k0 + KS < K) ? k0 + KS : K;
-    // stages of two BK-row chunks: stage kc + 2 BK is loaded into registers while the chunks of stage kc are
+    // stages of NCH BK-row chunks: stage kc + NCH BK is loaded into registers while the chunks of stage kc are
     // multiplied; rows past the split read row k1 - 1 (in bounds) and are zeroed, so the loads are unconditional
-    float4 ra[2], rb[2];
+    float4 ra[NCH], rb[NCH];
     const int grow = tid >> 4, gc4 = tid & 15;   // this thread's float4 of each 32 x 64 chunk
     auto gload = [&](int kc) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NCH; ++h) {
             const int k = kc + h * BK + grow;
             const int kr = k < k1 ? k : k1 - 1;
             ra[h] = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + ti * TB + 4 * gc4);
@@ -252,9 +252,9 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
         }
     };
     gload(k0);
-    for (int kc = k0; kc < k1; kc += 2 * BK) {
+    for (int kc = k0; kc < k1; kc += NCH * BK) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NCH; ++h) {
             const bool in = kc + h * BK + grow < k1;
             float4 va = ra[h], vb = rb[h];
             if (SCALE) {
@@ -269,10 +269,10 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
             *reinterpret_cast<float4*>(&sB[h * BK + grow][4 * gc4]) = vb;
         }
         __syncthreads();
-        if (kc + 2 * BK < k1) gload(kc + 2 * BK);
+        if (kc + NCH * BK < k1) gload(kc + NCH * BK);
         __builtin_amdgcn_sched_barrier(0);   // the loads go out before the MFMAs
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NCH; ++h) {
             if (kc + h * BK >= k1) break;    // a chunk wholly past the split is not part of the sum
             f32x4 part[2];
 #pragma unroll
@@ -334,8 +334,16 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
     const int t = threadIdx.x, row = 4 * b + (t >> 6), col = t & 63;
     const float* p = P + (size_t)u * TB * TB + row * TB + col;
     const size_t stride = (size_t)U * TB * TB;
+    // the partials in order of s, loaded eight (then four) at a time: one memory latency per batch
     double sum = 0.0;
     int s = 0;
+    for (; s + 8 <= S; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = p[(size_t)(s + e) * stride];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum = sum + (double)v[e];
+    }
     for (; s + 4 <= S; s += 4) {
         const float p0 = p[(size_t)s * stride], p1 = p[(size_t)(s + 1) * stride];
         const float p2 = p[(size_t)(s + 2) * stride], p3 = p[(size_t)(s + 3) * stride];
@@ -1739,12 +1747,24 @@ MatsOut buf_out(const spanqr_plan* p, float* base) {
     return m;
 }
 
+// Chunks per Gram stage: two for splits of at most GRAM_DEEP_KS rows (more loads in flight: 0.2-0.5 us faster at
+// 128-row splits), one for longer splits (the two-chunk stage measured ~1 us slower at 352-row splits).
+constexpr int GRAM_DEEP_KS = 8 * BK;
+
+template <int NCH>
+void launch_gram_n(const spanqr_plan* p, const MatsIn& A, long lda, dim3 grid, bool scale, bool kahan, hipStream_t st) {
+    if (kahan && scale) k_gram<true, true, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    else if (kahan) k_gram<true, false, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    else if (scale) k_gram<false, true, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    else k_gram<false, false, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+}
+
 void launch_gram(const spanqr_plan* p, const MatsIn& A, long lda, int n, bool scale, bool kahan, hipStream_t st) {
     const dim3 grid(p->U, p->S, n);
-    if (kahan && scale) k_gram<true, true><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
-    else if (kahan) k_gram<true, false><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
-    else if (scale) k_gram<false, true><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
-    else k_gram<false, false><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    if (p->KS <= GRAM_DEEP_KS)
+        launch_gram_n<2>(p, A, lda, grid, scale, kahan, st);
+    else
+        launch_gram_n<1>(p, A, lda, grid, scale, kahan, st);
 }
 
 void launch_reduce(const spanqr_plan* p, int mode, float* out, int n, hipStream_t st) {
@@ -2016,7 +2036,10 @@ void project(const spanqr_plan* p, const float* Q, long ldq, int j, const float*
     int S = 0, KS = 0;
     split_policy(p->K, U, &S, &KS);
     const MatsIn P = mats_in(&Q, 1);
-    k_gram<false, false, true><<<dim3(U, S), 512, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, BW / TB);
+    if (KS <= GRAM_DEEP_KS)
+        k_gram<false, false, true, 2><<<dim3(U, S), 512, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, BW / TB);
+    else
+        k_gram<false, false, true, 1><<<dim3(U, S), 512, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, BW / TB);
     k_reduce<2><<<dim3(16, U), 256, 0, st>>>(p->Tp, S, BW / TB, BW, p->T, nullptr);
     k_nsapply<true><<<dim3((p->K + 31) / 32, BW / 64), 256, 0, st>>>(P, ldq, p->K, j, p->T, mats_out(&Out, 1), BW, Cin,
                                                                     ldc, BW);
