@@ -193,8 +193,9 @@ __global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, 
 // ---------------------------------------------------------------------------------------------------------------
 // Gram partials (tri.py:255-297, 324-375): workgroup (u, sp) computes upper 64x64 tile u = (ti, tj) of A^T A over
 // rows [sp*KS, min((sp+1)*KS, K)), in 32-row chunks staged through LDS NCH at a time (rows past the split read as 0;
-// the next NCH chunks are fetched into registers while these are multiplied). Wave w owns the 32x32 quadrant (w >> 1, w & 1). KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one
-// chain runs over the whole split. SCALE: operands are s * a with the pass-1 power-of-2 scale.
+// the next NCH chunks are fetched into registers while these are multiplied). Eight wavefronts, each a 32x16 piece of
+// the tile. KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one chain
+// runs over the whole split. SCALE: operands are s * a with the pass-1 power-of-2 scale.
 // ---------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
     int t = 0, rem = u;
