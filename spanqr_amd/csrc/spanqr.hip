@@ -1555,11 +1555,12 @@ __global__ __launch_bounds__(256) void k_pack_factors(const float* __restrict__ 
 // ---------------------------------------------------------------------------------------------------------------
 // Newton-Schulz apply (kcholqr.py:22, addmm(Y, Y, D)): Out = Y + fp32(Y D), the product an MFMA chain over
 // m = 0..r-1 from 0 and added to Y once. 32x64 output tile per workgroup; wave w: rows 16(w >> 1), 2 column blocks.
+// MS columns of Y (rows of D) per step through LDS (32 or 64).
 // ---------------------------------------------------------------------------------------------------------------
 // SUB (the block projection, kbig.py:88-89): Out = C - fp32(A B) with A [K, r] of another matrix and C its own input,
 // B [r, ncols] (row stride ldd); the chain and the single rounding are the same. The Newton-Schulz step is
 // A = C = Y, B = D.
-template <bool SUB = false>
+template <bool SUB = false, int MS = 32>
 __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int K, int r, const float* __restrict__ D,
                                                  const MatsOut Outs, long ldo, const float* __restrict__ Cx = nullptr,
                                                  long ldc = 0, long ldd = 0) {
@@ -1571,28 +1572,29 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
     const long ldC = SUB ? ldc : ldy;
     // row strides 34 and 80: each half-wavefront's operand reads (A: rows l16, columns 4kk + lk; B: rows 4kk + lk,
     // columns l16) fall on 32 distinct banks
-    __shared__ float sY[32][34];
-    __shared__ float sD[32][80];
+    __shared__ float sY[32][MS + 2];
+    __shared__ float sD[MS][80];
     const int row0 = blockIdx.x * 32, col0 = blockIdx.y * 64;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
     const int rb = w >> 1, cbase = (w & 1) * 2;
     f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    for (int m0 = 0; m0 < r; m0 += 32) {
-        {
-            const int row = tid >> 3, c4 = tid & 7;
+    for (int m0 = 0; m0 < r; m0 += MS) {
+#pragma unroll
+        for (int q = 0; q < MS / 32; ++q) {
+            const int idx = tid + 256 * q, row = idx / (MS / 4), c4 = idx % (MS / 4);
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (row0 + row < K) v = *reinterpret_cast<const float4*>(Yin + (size_t)(row0 + row) * ldy + m0 + 4 * c4);
             sY[row][4 * c4 + 0] = v.x; sY[row][4 * c4 + 1] = v.y; sY[row][4 * c4 + 2] = v.z; sY[row][4 * c4 + 3] = v.w;
         }
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < MS / 16; ++q) {
             const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15;
             *reinterpret_cast<float4*>(&sD[row][4 * c4]) =
                 *reinterpret_cast<const float4*>(D + (size_t)(m0 + row) * ldD + col0 + 4 * c4);
         }
         __syncthreads();
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
+        for (int kk = 0; kk < MS / 4; ++kk) {
             const float a = sY[16 * rb + l16][4 * kk + lk];
 #pragma unroll
             for (int c = 0; c < 2; ++c) acc[c] = mfma(a, sD[4 * kk + lk][16 * (cbase + c) + l16], acc[c]);
@@ -1875,8 +1877,10 @@ void launch_trsm(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, fl
 
 void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsOut& Out, long ldo, int n,
                     hipStream_t st) {
+    // 64-column steps: half the load-then-multiply steps of each workgroup's chain (1-1.5 us faster at 17408x256
+    // and 768x512 than 32-column steps, level elsewhere)
     const dim3 grid((p->K + 31) / 32, p->r / 64, n);
-    k_nsapply<<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo);
+    k_nsapply<false, 64><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo);
 }
 
 
