@@ -2046,7 +2046,7 @@ void project(const spanqr_plan* p, const float* Q, long ldq, int j, const float*
     else
         k_gram<false, false, true, 1><<<dim3(U, S), 512, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, BW / TB);
     k_reduce<2><<<dim3(16, U), 256, 0, st>>>(p->Tp, S, BW / TB, BW, p->T, nullptr);
-    k_nsapply<true><<<dim3((p->K + 31) / 32, BW / 64), 256, 0, st>>>(P, ldq, p->K, j, p->T, mats_out(&Out, 1), BW, Cin,
+    k_nsapply<true, 64><<<dim3((p->K + 31) / 32, BW / 64), 256, 0, st>>>(P, ldq, p->K, j, p->T, mats_out(&Out, 1), BW, Cin,
                                                                     ldc, BW);
 }
 
