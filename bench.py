@@ -1,21 +1,27 @@
 """Benchmark of orth(X) on one MI355X: microseconds per orth() call, max|Q^T Q - I|, and the roofline of each kernel.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S] [--no-cpu] [--no-graph]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S] [--no-cpu] [--no-graph] [--headline-only]
 
-Workload (the reference's 0.8B TTF layer shapes): K x r in {1024x256, 2048x256, 3584x256}, two seeds each, X = V (U^T U)
-+ u^T U with N = K (U's singular values log-uniform over [1, 1e4], u unit-RMS Gaussian), generated on the CPU and
-resident on the GPU before timing. One step = one orth() call on each of the six inputs; every input has its own
-captured hipGraph. `value` = timed wall time / (steps x 6) in microseconds (lower is better).
+Workload (the quoted target shapes): one orth() call at 768x512 (the 110M attention layer: X = V (U^T U) + u^T U with
+N = 768, U's singular values log-uniform over [1, 1e4], u unit-RMS Gaussian, seed 0) and one at 17408x256 (the 27B
+down_proj layer, same generator with N = 5120), generated on the CPU and resident on the GPU before timing. Each
+input has its own captured hipGraph; one step replays both. `value` = timed wall time / (steps x 2) in microseconds
+per call (lower is better); the per-shape figures are in `targets` at the end of the line.
 
-Also reported: per shape, back-to-back ("thr", 20 replays) and isolated synchronised ("lat") time per call, at the
-workload shapes and at 768x512, 2048x512, 5120x256, 6144x256 and 17408x256 (768x512 and 17408x256 are the quoted
-targets); the 27B layers wider than 512 (5120x1024, 17408x1024, 17408x2048: block Gram-Schmidt over 256-column
-blocks); the batched layer set (12 x 768x512 + 12 x 2048x512, one hipGraph per shape group, against 24
-single-call graphs); per kernel and shape the average launch duration (HIP events around back-to-back launches on
-the call's stream) with its algorithmic flops and bytes, as TFLOP/s and GB/s and as fractions of the MFMA and HBM
-peaks; the roofline of the dominant kernel and of the whole call; the Cholesky's latency
-per diagonal step; a CPU baseline on a bounded sample (the C restatement in oracle/, OpenMP, on the host, plus CPU
-torch.linalg.qr).
+Per headline shape, as the reference's qrbench/bench.py:28-53 measures: "thr" (median of 5 bursts of 20
+back-to-back replays), "lat" (one replay between two events after a synchronisation, median of 20) and "lat_flush"
+(the same after overwriting a 512 MiB buffer, which evicts the L2s and the 256 MiB MALL), plus every kernel's average
+launch duration (HIP events around back-to-back launches on the call's stream) with its algorithmic flops and bytes
+as fractions of the MFMA and HBM peaks, the roofline of the dominant kernel, the Cholesky's per-step critical path
+(device wall clock) and the gap between the graph replay and the summed kernel times.
+
+Secondary lines: the 0.8B layer shapes (1024x256, 2048x256, 3584x256, two seeds each), 2048x512, 5120x256,
+6144x256, the 27B layers wider than 512 (block Gram-Schmidt), the batched layer set (12 x 768x512 + 12 x 2048x512,
+one hipGraph per shape group, against 24 single-call graphs) and a CPU baseline on a bounded sample at the two
+headline shapes (the C restatement in oracle/ with OpenMP on the host, and CPU torch.linalg.qr).
+
+--headline-only runs the timed region alone and prints its line (the command the rocprofv3 summaries in profiles/
+come from). --detail PATH also writes every measured figure to PATH as JSON.
 """
 import argparse
 import ctypes
@@ -30,21 +36,23 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from spanqr_amd import _lib, kchol, kcholqr_f, kcholqr_f_many, orth, stages  # noqa: E402
+from spanqr_amd import _lib, kcholqr_f, kcholqr_f_many, orth, stages  # noqa: E402
 from spanqr_amd.plan import get_plan, stream_handle  # noqa: E402
 from spanqr_amd.qrbench import gen  # noqa: E402
 
 METRIC = "µs per orth() call at K×r (median); max|QᵀQ−I|; % of HBM/MFMA roofline"
-WORKLOAD_SHAPES = [(1024, 256), (2048, 256), (3584, 256)]
-SEEDS = (0, 1)
-TARGET_SHAPES = [(768, 512), (17408, 256)]
+# (name, K, r, generator arguments): the two shapes the targets are quoted at
+HEADLINE = [("768x512", 768, 512, {"N": 768, "seed": 0}), ("17408x256", 17408, 256, {"N": 5120, "seed": 0})]
 TARGET_US = {"768x512": 250.0, "17408x256": 350.0}
-OTHER_SHAPES = [(768, 512), (2048, 512), (5120, 256), (6144, 256), (17408, 256)]
+WORKLOAD_08B = [(1024, 256), (2048, 256), (3584, 256)]
+SEEDS_08B = (0, 1)
+OTHER_SHAPES = [(2048, 512), (5120, 256), (6144, 256)]
 # 27B layers wider than 512 (orth.py:18-19: block Gram-Schmidt over 256-column blocks, candidates/kbig.py:69-95)
 BLOCKED_SHAPES = [(5120, 1024), (17408, 1024), (17408, 2048)]
 BATCH_GROUPS = [(768, 512, 12), (2048, 512, 12)]   # the 110M model's attention and down_proj layers
 PEAK_FP32_TFLOPS = 157.3     # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+FLUSH_BYTES = 512 << 20      # more than the 256 MiB MALL plus every XCD's L2
 
 
 # kernel families of one call: (name, spanqr_profile_kernel id, launches per call)
@@ -81,7 +89,7 @@ def kernel_avg_us(X, which, reps):
 
 def chol_steps_us(X):
     """per 32-column diagonal step of the Cholesky: the device wall clock stamped by workgroup 0 of an instrumented
-    copy of the kernel (spanqr_profile_chol): list of (step us, of which tile factor + next-row wait us)"""
+    copy of the kernel (spanqr_profile_chol): (list of step us, factorisation us)"""
     K, r = X.shape
     kcholqr_f(X)
     plan = get_plan(K, r, X.device)
@@ -92,16 +100,16 @@ def chol_steps_us(X):
     _lib.check(_lib.lib().spanqr_profile_chol(plan.handle, G.data_ptr(), npart.data_ptr(), 1e-7, 1e-8, stamps,
                                               ctypes.byref(tick), stream_handle(X.device)))
     us = lambda a, b: (stamps[b] - stamps[a]) * tick.value / 1000.0
-    return [(us(1 + 4 * j, 1 + 4 * (j + 1)), us(1 + 4 * j, 2 + 4 * j)) for j in range(nb)]
+    return [round(us(1 + 4 * j, 1 + 4 * (j + 1)), 2) for j in range(nb)], round(us(0, 1 + 4 * nb), 2)
 
 
-def traffic_bytes(family):
-    """HBM bytes per launch of a kernel family at the workload, from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
-    recorded in profiles/traffic.json (None if that kernel has no record)"""
+def traffic_bytes(family, shape):
+    """HBM bytes per launch of a kernel family at a shape, from the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
+    recorded in profiles/traffic.json (None if there is no record)"""
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
-            rec = json.load(f).get(family)
-    except (OSError, ValueError):
+            rec = json.load(f).get(shape, {}).get(family)
+    except (OSError, ValueError, AttributeError):
         return None
     return None if rec is None else rec.get("bytes_per_launch")
 
@@ -121,6 +129,24 @@ def capture(X, fn=None):
     return g, Q
 
 
+class _Direct:
+    """direct launches in place of a graph (--no-graph)"""
+
+    def __init__(self, X, fn=None):
+        self.X, self.fn = X, fn or kcholqr_f
+        self.Q = self.fn(X)
+
+    def replay(self):
+        self.Q = self.fn(self.X)
+
+
+def runner(X, graphs, fn=None):
+    if graphs:
+        return capture(X, fn)
+    d = _Direct(X, fn)
+    return d, d.Q
+
+
 def capture_many(Xs):
     """(graph, [Q]): one batched call on the same-shape list Xs captured into a hipGraph on a side stream"""
     st = torch.cuda.Stream(Xs[0].device)
@@ -135,7 +161,7 @@ def capture_many(Xs):
     return g, Qs
 
 
-def time_replays(graphs, steps, reps=5):
+def time_rounds(graphs, steps, reps=5):
     """median over `reps` of the time of `steps` rounds of replaying every graph once, microseconds per round"""
     out = []
     for _ in range(reps):
@@ -151,64 +177,31 @@ def time_replays(graphs, steps, reps=5):
     return statistics.median(out)
 
 
-def batched_layers(dev, steps):
-    """the batched layer set: per training step, orth of 12 layers at 768x512 and 12 at 2048x512 (independent
-    inputs of the cond-1e8 generator, seeds 100 + i), as two batched graphs (one per shape group) and as 24
-    single-call graphs; Q of the two forms compared bit for bit"""
-    groups = []
-    for gi, (K, r, n) in enumerate(BATCH_GROUPS):
-        groups.append([gen.ttf_uu(K, r, N=K, seed=100 + 12 * gi + i).to(dev) for i in range(n)])
-    single = [capture(X) for grp in groups for X in grp]
-    batched = [capture_many(grp) for grp in groups]
-    for g, _q in single + batched:
+def thr_us(g, n=20, reps=5):
+    """back-to-back: median over `reps` bursts of n replays, microseconds per replay (qrbench/bench.py:44-52)"""
+    return time_rounds([g], n, reps)
+
+
+def lat_us(g, n=20, flush=None):
+    """isolated call: one replay between two events after a synchronisation, median of n (qrbench/bench.py:36-43);
+    with `flush` (a device buffer) overwritten before each sample so that no cache holds the inputs"""
+    out = []
+    for _ in range(n):
+        if flush is not None:
+            flush.zero_()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
         g.replay()
-    torch.cuda.synchronize()
-    q_single = [q for _g, q in single]
-    q_batched = [q for _g, qs in batched for q in qs]
-    same = all(torch.equal(a.view(torch.int32), b.view(torch.int32)) for a, b in zip(q_single, q_batched))
-    t_single = time_replays([g for g, _q in single], steps)
-    t_batched = time_replays([g for g, _q in batched], steps)
-    res = {"layers": sum(n for _k, _r, n in BATCH_GROUPS),
-           "groups": [f"{n} x {K}x{r}" for K, r, n in BATCH_GROUPS],
-           "us_per_step_batched": t_batched, "us_per_step_sequential": t_single,
-           "speedup": t_single / t_batched, "bitwise_equal_to_single_calls": same,
-           "orth_max": max(orth_error(q) for q in q_batched),
-           "chol_per_launch": {f"{K}x{r}": get_plan(K, r, dev, n).chol_batch for K, r, n in BATCH_GROUPS}}
-    del single, batched
-    torch.cuda.synchronize()
-    return res
+        e.record()
+        torch.cuda.synchronize()
+        out.append(s.elapsed_time(e) * 1000.0)
+    return statistics.median(out)
 
 
 def orth_error(Q):
     Qd = Q.detach().double().cpu()
     return float((Qd.T @ Qd - torch.eye(Q.shape[1], dtype=torch.float64)).abs().max())
-
-
-def time_graph(g, n=20, reps=5):
-    """median over `reps` bursts of n back-to-back replays, microseconds per replay"""
-    out = []
-    for _ in range(reps):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        s.record()
-        for _ in range(n):
-            g.replay()
-        e.record()
-        torch.cuda.synchronize()
-        out.append(s.elapsed_time(e) * 1000.0 / n)
-    return statistics.median(out)
-
-
-def lat_us(g, n=20):
-    """isolated synchronised call: median host wall time of one replay followed by a device synchronisation"""
-    out = []
-    torch.cuda.synchronize()
-    for _ in range(n):
-        t0 = time.perf_counter()
-        g.replay()
-        torch.cuda.synchronize()
-        out.append((time.perf_counter() - t0) * 1e6)
-    return statistics.median(out)
 
 
 def kernels_at(X, reps):
@@ -218,9 +211,30 @@ def kernels_at(X, reps):
     for fam, which, per_call in FAMILIES:
         us = kernel_avg_us(X, which, reps)
         fl, by = algorithmic(fam, K, r)
-        out[fam] = {"us": us, "per_call": per_call, "tflops": fl / us / 1e6, "gbs": by / us / 1e3,
-                    "mfma_frac": fl / us / 1e6 / PEAK_FP32_TFLOPS, "hbm_frac": by / us / 1e3 / PEAK_HBM_GBS}
+        out[fam] = {"us": round(us, 3), "per_call": per_call, "tflops": round(fl / us / 1e6, 3),
+                    "gbs": round(by / us / 1e3, 1), "mfma_frac": round(fl / us / 1e6 / PEAK_FP32_TFLOPS, 5),
+                    "hbm_frac": round(by / us / 1e3 / PEAK_HBM_GBS, 5)}
     return out
+
+
+def roofline_of(kern, shapes):
+    """roofline of the kernel family with the largest share of the summed kernel time over the headline shapes:
+    achieved = mean algorithmic work per launch / mean launch duration (both over one launch at each shape, as a
+    trace of the timed region averages them)"""
+    tot = {fam: sum(kern[s][fam]["us"] * kern[s][fam]["per_call"] for s in shapes) for fam in kern[shapes[0]]}
+    dom = max(tot, key=tot.get)
+    dims = {name: (K, r) for name, K, r, _ in HEADLINE}
+    fl = statistics.mean(algorithmic(dom, *dims[s])[0] for s in shapes)
+    by = statistics.mean(algorithmic(dom, *dims[s])[1] for s in shapes)
+    us = statistics.mean(kern[s][dom]["us"] for s in shapes)
+    bound = "mfma" if fl / PEAK_FP32_TFLOPS >= by / PEAK_HBM_GBS * 1e-3 else "hbm"
+    achieved = fl / us / 1e6 if bound == "mfma" else by / us / 1e3
+    peak = PEAK_FP32_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
+    traffic = [traffic_bytes(dom, s) for s in shapes]
+    return {"bound": bound, "achieved": achieved, "peak": peak, "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+            "frac": achieved / peak, "traffic": statistics.mean(traffic) if None not in traffic else None,
+            "kernel": dom, "avg_launch_us": us, "work_per_launch": fl if bound == "mfma" else by,
+            "share_of_kernel_time": tot[dom] / sum(tot.values())}
 
 
 def cpu_baseline(inputs, seconds):
@@ -230,7 +244,8 @@ def cpu_baseline(inputs, seconds):
     torch.set_num_threads(threads)
     per_shape, hh = {}, {}
     budget = seconds / max(1, len(inputs))
-    for (K, r), X in inputs.items():
+    for name, X in inputs.items():
+        K, r = X.shape
         Xn = X.cpu().numpy()
         KS = get_plan(K, r, X.device).split_rows
         oracle.orth(Xn, KS)                                  # warm-up
@@ -239,7 +254,7 @@ def cpu_baseline(inputs, seconds):
             t0 = time.perf_counter()
             oracle.orth(Xn, KS)
             times.append(time.perf_counter() - t0)
-        per_shape[f"{K}x{r}"] = statistics.median(times) * 1e6
+        per_shape[name] = round(statistics.median(times) * 1e6, 1)
         Xc = X.cpu()
         torch.linalg.qr(Xc)
         ht = []
@@ -247,7 +262,7 @@ def cpu_baseline(inputs, seconds):
             t0 = time.perf_counter()
             torch.linalg.qr(Xc)
             ht.append(time.perf_counter() - t0)
-        hh[f"{K}x{r}"] = statistics.median(ht) * 1e6
+        hh[name] = round(statistics.median(ht) * 1e6, 1)
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -256,7 +271,8 @@ def cpu_baseline(inputs, seconds):
         pass
     return {
         "value": statistics.mean(per_shape.values()), "unit": "us/call", "cores": threads, "kind": "port",
-        "sample": f"oracle/kcholf_oracle.c orth() on seed 0 of each workload shape, >= {budget:.1f} s each, median",
+        "sample": f"oracle/kcholf_oracle.c orth() of the headline inputs ({', '.join(inputs)}), median over "
+                  f">= {budget:.1f} s each (OpenMP, {threads} threads)",
         "per_shape_us": per_shape, "torch_linalg_qr_us": hh, "cpu_model": model, "cpu_count": os.cpu_count(),
     }
 
@@ -270,6 +286,8 @@ def main(argv=None):
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="direct launches instead of one hipGraph per input")
     p.add_argument("--kernel-reps", type=int, default=100, help="launches per kernel timing")
+    p.add_argument("--headline-only", action="store_true", help="only the timed region (for profiling runs)")
+    p.add_argument("--detail", default=None, help="also write every figure to this JSON file")
     a = p.parse_args(argv)
     if a.gpus != 1:
         print(f"bench.py measures one GPU: orth() of one matrix runs on a single MI355X and this build has no "
@@ -277,141 +295,120 @@ def main(argv=None):
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    graphs = not a.no_graph
 
-    inputs = {}
-    for K, r in WORKLOAD_SHAPES:
-        for s in SEEDS:
-            inputs[(K, r, s)] = gen.ttf_uu(K, r, N=K, seed=s).to(dev)
-    if a.no_graph:
-        class _Direct:
-            def __init__(self, X):
-                self.X = X
-                self.Q = kcholqr_f(X)
-
-            def replay(self):
-                self.Q = kcholqr_f(self.X)
-
-        graphs = {}
-        for key, X in inputs.items():
-            d = _Direct(X)
-            graphs[key] = (d, d.Q)
-    else:
-        graphs = {key: capture(X) for key, X in inputs.items()}
+    inputs = {name: gen.ttf_uu(K, r, **kw).to(dev) for name, K, r, kw in HEADLINE}
+    runs = {name: runner(X, graphs) for name, X in inputs.items()}
     for _ in range(a.warmup):
-        for g, _q in graphs.values():
+        for g, _q in runs.values():
             g.replay()
     torch.cuda.synchronize()
-    calls = len(graphs)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
     for _ in range(a.steps):
-        for g, _q in graphs.values():
+        for g, _q in runs.values():
             g.replay()
     end.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
-    value = total_ms * 1000.0 / (a.steps * calls)
-    orth_max = max(orth_error(q) for _g, q in graphs.values())
-
-    per_shape, per_shape_lat = {}, {}
-    for (K, r, s), (g, _q) in graphs.items():
-        per_shape.setdefault(f"{K}x{r}", []).append(time_graph(g))
-        per_shape_lat.setdefault(f"{K}x{r}", []).append(lat_us(g))
-    per_shape = {k: statistics.mean(v) for k, v in per_shape.items()}
-    per_shape_lat = {k: statistics.mean(v) for k, v in per_shape_lat.items()}
-    shapes = {}
-    for K, r in OTHER_SHAPES:
-        X = gen.bench_input(K, r, seed=0).to(dev)
-        g, q = capture(X) if not a.no_graph else (lambda d: (d, d.Q))(_Direct(X))
-        ks = kernels_at(X, a.kernel_reps)
-        shapes[f"{K}x{r}"] = {"thr_us": time_graph(g), "lat_us": lat_us(g), "orth": orth_error(q),
-                              "sum_of_kernels_us": sum(v["us"] * v["per_call"] for v in ks.values()),
-                              "kernels": ks}
-        del g, q, X
-        torch.cuda.synchronize()
-    blocked = {}
-    for K, r in BLOCKED_SHAPES:
-        X = gen.bench_input(K, r, seed=0).to(dev)
-        g, q = capture(X, orth)
-        blocked[f"{K}x{r}"] = {"thr_us": time_graph(g, n=5), "lat_us": lat_us(g, n=5), "orth": orth_error(q),
-                               "blocks": r // 256, "orth_calls_per_call": 2 * (r // 256) - 1}
-        del g, q, X
-        torch.cuda.synchronize()
-    # fp64 clamped Cholesky with fp32 copies (kchol.chol64; not on orth's path): HIP events around back-to-back calls
-    chol64 = {}
-    for n in (256, 512):
-        Xd = torch.randn(n + 64, n, device=dev, dtype=torch.float64, generator=torch.Generator(dev).manual_seed(n))
-        G64 = Xd.T @ Xd
-        for _ in range(2):
-            kchol.chol64(G64, 1e-12)
-        s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s_.record()
-        for _ in range(10):
-            kchol.chol64(G64, 1e-12)
-        e_.record()
-        torch.cuda.synchronize()
-        chol64[str(n)] = {"us": s_.elapsed_time(e_) * 100.0}
-        del Xd, G64
-    targets = {k: {"us_per_call": shapes[k]["thr_us"], "lat_us": shapes[k]["lat_us"], "orth": shapes[k]["orth"],
-                   "target_us": TARGET_US[k]} for k in TARGET_US}
-
-    batched = batched_layers(dev, max(1, min(a.steps, 20)))
-
-    # per kernel: average launch duration at each workload shape (HIP events around back-to-back launches)
-    kernels = {}
-    call_us = {}
-    for K, r in WORKLOAD_SHAPES:
-        ks = kernels_at(inputs[(K, r, 0)], a.kernel_reps)
-        for fam, v in ks.items():
-            kernels.setdefault(fam, {})[f"{K}x{r}"] = v
-        call_us[f"{K}x{r}"] = sum(v["us"] * v["per_call"] for v in ks.values())
-    share = {fam: sum(v[s_]["us"] * v[s_]["per_call"] for s_ in v) / sum(call_us.values())
-             for fam, v in kernels.items()}
-    dom = max(share, key=share.get)
-    dk = kernels[dom]
-    avg_us = statistics.mean(v["us"] for v in dk.values())
-    fl = statistics.mean(algorithmic(dom, K, r)[0] for K, r in WORKLOAD_SHAPES)
-    by = statistics.mean(algorithmic(dom, K, r)[1] for K, r in WORKLOAD_SHAPES)
-    bound = "mfma" if fl / PEAK_FP32_TFLOPS >= by / PEAK_HBM_GBS * 1e-3 else "hbm"
-    achieved = fl / avg_us / 1e6 if bound == "mfma" else by / avg_us / 1e3
-    peak = PEAK_FP32_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
-    roofline = {"bound": bound, "kernel": dom, "achieved": achieved, "peak": peak,
-                "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "frac": achieved / peak,
-                "traffic": traffic_bytes(dom), "avg_launch_us": avg_us, "share_of_call": share[dom],
-                "note": "algorithmic work per launch / average launch duration (HIP events around back-to-back "
-                        "launches on the call's stream); the Cholesky is latency-bound (its critical path is a chain "
-                        "of r pivots), so its roofline fraction is small by construction"}
-    call_roof = {}
-    for K, r in WORKLOAD_SHAPES:
-        F, B = call_work(K, r)
-        t = per_shape[f"{K}x{r}"] * 1e-6
-        call_roof[f"{K}x{r}"] = {"tflops": F / t / 1e12, "mfma_frac": F / t / 1e12 / PEAK_FP32_TFLOPS,
-                                 "gbs": B / t / 1e9, "hbm_frac": B / t / 1e9 / PEAK_HBM_GBS}
-    steps = chol_steps_us(inputs[(WORKLOAD_SHAPES[0][0], WORKLOAD_SHAPES[0][1], 0)])
-    chol_info = {"r": WORKLOAD_SHAPES[0][1], "us_per_32col_step": [round(a, 2) for a, _ in steps],
-                 "us_factor_and_wait": [round(b, 2) for _, b in steps],
-                 "us_per_32col_diag_step": statistics.mean(a for a, _ in steps),
-                 "note": "device wall clock stamped by workgroup 0 of an instrumented copy of the kernel"}
-
-    cpu = None if a.no_cpu else cpu_baseline({(K, r): inputs[(K, r, 0)] for K, r in WORKLOAD_SHAPES}, a.cpu_seconds)
+    value = total_ms * 1000.0 / (a.steps * len(runs))
+    orth_max = max(orth_error(q) for _g, q in runs.values())
     line = {
         "metric": METRIC, "value": value, "unit": "us/call", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": total_ms / a.steps, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "0.8B TTF layers: orth() at 1024x256, 2048x256, 3584x256, 2 seeds each, one "
-                               "hipGraph per input", "shapes": [f"{K}x{r}" for K, r in WORKLOAD_SHAPES],
-                   "seeds": list(SEEDS), "calls_per_step": calls, "graphs": not a.no_graph},
-        "orth_max": orth_max, "per_shape_us": per_shape, "per_shape_lat_us": per_shape_lat,
-        "target_shapes": targets, "shapes": shapes, "blocked_shapes": blocked, "batched_layers": batched,
-        "chol64": chol64,
-        "roofline": roofline, "call_roofline": call_roof, "kernels": kernels, "kernel_share": share,
-        "sum_of_kernels_us": call_us, "cholesky": chol_info,
-        "cpu_baseline": cpu,
-        "device": torch.cuda.get_device_name(dev),
+        "config": {"workload": "orth() at 768x512 (110M attention layer, N=768) and 17408x256 (27B down_proj "
+                               "layer, N=5120), cond(U^T U) ~1e8 generator, seed 0, one hipGraph per input, both "
+                               "per step", "shapes": list(runs), "calls_per_step": len(runs), "graphs": graphs},
+        "orth_max": orth_max,
     }
+    if a.headline_only:
+        print(json.dumps(line), flush=True)
+        return 0
+
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    head, kern = {}, {}
+    for name, K, r, _kw in HEADLINE:
+        g, q = runs[name]
+        ks = kernels_at(inputs[name], a.kernel_reps)
+        kern[name] = ks
+        t = thr_us(g)
+        summed = sum(v["us"] * v["per_call"] for v in ks.values())
+        F, B = call_work(K, r)
+        steps, chol_us = chol_steps_us(inputs[name])
+        head[name] = {"thr_us": round(t, 2), "lat_us": round(lat_us(g), 2), "lat_flush_us": round(lat_us(g, flush=flush), 2),
+                      "orth": orth_error(q), "sum_of_kernels_us": round(summed, 2), "gap_us": round(t - summed, 2),
+                      "call_mfma_frac": round(F / (t * 1e-6) / 1e12 / PEAK_FP32_TFLOPS, 4),
+                      "call_hbm_frac": round(B / (t * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                      "chol_us": chol_us, "chol_step_us": steps,
+                      "kernels_us": {fam: v["us"] for fam, v in ks.items()}}
+    del flush
+    roofline = roofline_of(kern, list(head))
+
+    w08 = {}
+    for K, r in WORKLOAD_08B:
+        ts = []
+        for s in SEEDS_08B:
+            g, _q = runner(gen.ttf_uu(K, r, N=K, seed=s).to(dev), graphs)
+            ts.append(thr_us(g))
+        w08[f"{K}x{r}"] = round(statistics.mean(ts), 2)
+    others = {}
+    for K, r in OTHER_SHAPES:
+        X = gen.bench_input(K, r, seed=0).to(dev)
+        g, q = runner(X, graphs)
+        others[f"{K}x{r}"] = {"thr_us": round(thr_us(g), 2), "lat_us": round(lat_us(g), 2), "orth": orth_error(q)}
+        del g, q, X
+    blocked = {}
+    for K, r in BLOCKED_SHAPES:
+        X = gen.bench_input(K, r, seed=0).to(dev)
+        g, q = runner(X, graphs, orth)
+        blocked[f"{K}x{r}"] = {"thr_us": round(thr_us(g, n=5), 1), "lat_us": round(lat_us(g, n=5), 1),
+                               "orth": orth_error(q), "blocks": r // 256}
+        del g, q, X
+    torch.cuda.synchronize()
+    batched = batched_layers(dev, max(1, min(a.steps, 20)))
+
+    cpu = None if a.no_cpu else cpu_baseline(inputs, a.cpu_seconds)
+    targets = {name: {"us_per_call": head[name]["thr_us"], "target_us": TARGET_US[name],
+                      "met": head[name]["thr_us"] <= TARGET_US[name], "lat_us": head[name]["lat_us"],
+                      "orth": head[name]["orth"], "chol_us": head[name]["chol_us"]} for name in head}
+    line.update({
+        "roofline": roofline, "cpu_baseline": cpu, "headline": head,
+        "shapes_0.8b_thr_us": w08, "shapes": others, "blocked_shapes": blocked, "batched_layers": batched,
+        "device": torch.cuda.get_device_name(dev), "targets": targets,
+    })
+    if a.detail:
+        with open(a.detail, "w") as f:
+            json.dump({"line": line, "kernels": kern}, f, indent=1)
     print(json.dumps(line), flush=True)
     return 0
+
+
+def batched_layers(dev, steps):
+    """the batched layer set: per training step, orth of 12 layers at 768x512 and 12 at 2048x512 (independent
+    inputs of the cond-1e8 generator, seeds 100 + 12 g + i), as two batched graphs (one per shape group) and as 24
+    single-call graphs; Q of the two forms compared bit for bit"""
+    groups = []
+    for gi, (K, r, n) in enumerate(BATCH_GROUPS):
+        groups.append([gen.ttf_uu(K, r, N=K, seed=100 + 12 * gi + i).to(dev) for i in range(n)])
+    single = [capture(X) for grp in groups for X in grp]
+    batched = [capture_many(grp) for grp in groups]
+    for g, _q in single + batched:
+        g.replay()
+    torch.cuda.synchronize()
+    q_single = [q for _g, q in single]
+    q_batched = [q for _g, qs in batched for q in qs]
+    same = all(torch.equal(a.view(torch.int32), b.view(torch.int32)) for a, b in zip(q_single, q_batched))
+    t_single = time_rounds([g for g, _q in single], steps)
+    t_batched = time_rounds([g for g, _q in batched], steps)
+    res = {"groups": [f"{n} x {K}x{r}" for K, r, n in BATCH_GROUPS],
+           "us_per_step_batched": round(t_batched, 1), "us_per_step_sequential": round(t_single, 1),
+           "speedup": round(t_single / t_batched, 2), "bitwise_equal_to_single_calls": same,
+           "orth_max": max(orth_error(q) for q in q_batched)}
+    del single, batched
+    torch.cuda.synchronize()
+    return res
 
 
 if __name__ == "__main__":

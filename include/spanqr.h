@@ -165,9 +165,17 @@ int spanqr_stage_trsm(spanqr_plan* plan, const float* A, long lda, int pass1, fl
 int spanqr_stage_ns(spanqr_plan* plan, const float* Y, long ldy, int kahan, float* Yout, long ldo, void* stream);
 
 /* Copy the plan's dust matrix (device) and the scalars of the last call's first matrix {s, nrm0, tau0, nrm1, tau1,
- * nrm2, tau2, wait error} (device, 8 floats; the last is nonzero if a bounded wait of the Cholesky timed out). */
+ * nrm2, tau2, wait error} (device, 8 floats; the last is nonzero if a bounded wait of that call's Cholesky gave up:
+ * every call clears it first, and such a call's Q is NaN). */
 int spanqr_plan_copy_dust(spanqr_plan* plan, float* Z, void* stream);
 int spanqr_plan_copy_scalars(spanqr_plan* plan, float* scal8, void* stream);
+
+/* Testing only (no counterpart in the reference): polls one bounded wait of the Cholesky makes before it gives up
+ * (default 2^20, about a second). Lowered to 0, a wait gives up unless its flag is already set, so the tests can
+ * exercise the failure path with every kernel still ending normally: the wait-error word is set and the call's Q
+ * comes out NaN. Applies to launches made after the call (a captured graph keeps the value it was captured with).
+ * Not thread-safe with concurrent launches; restore the default (1048576) afterwards. */
+int spanqr_debug_spin_limit(unsigned polls);
 
 /* ---- fp64 clamped Cholesky (kchol.chol64, candidates/kchol.py:47-57 -> chol_f64, candidates/cuk/chol.cu:278-281) ----
  * A plan holds the flag words of one n x n factorisation (n a multiple of 32 up to 1024); one plan per concurrent

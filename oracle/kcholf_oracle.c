@@ -65,12 +65,18 @@ static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
  * of |x| wins, and NaN patterns sort above +inf. */
 float spqo_amax(const float* X, long ldx, int K, int r) {
     uint32_t m = 0;
+    float sm = -INFINITY;
     for (int k = 0; k < K; ++k)
         for (int c = 0; c < r; ++c) {
-            uint32_t u = f2u(X[(size_t)k * ldx + c]) & 0x7fffffffu;
+            const float x = X[(size_t)k * ldx + c];
+            if (PLANTED(16)) {   /* 16: signed maximum (the absolute value dropped) */
+                if (x > sm) sm = x;
+                continue;
+            }
+            uint32_t u = f2u(x) & 0x7fffffffu;
             if (u > m) m = u;
         }
-    return u2f(m);
+    return PLANTED(16) ? sm : u2f(m);
 }
 
 /* _pow2_scale (kcholqr.py:29-30): s = 2^-round(log2(max(m, 1e-38))) with torch's fp32 log2 and round half to even;

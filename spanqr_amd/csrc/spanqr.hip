@@ -143,11 +143,14 @@ __device__ __forceinline__ float rsqrt_sw(float x) {
 
 // ---------------------------------------------------------------------------------------------------------------
 // max|x| partials (torch.linalg.vector_norm(X, inf), kcholqr.py:102): the largest bit pattern of |x| per workgroup;
-// NaN patterns sort above +inf, so NaN propagates as in torch.
+// NaN patterns sort above +inf, so NaN propagates as in torch. As the first kernel of a call it also clears the
+// matrix's wait-error word (bar[2], set by a bounded wait of this call's Cholesky that gave up).
 // ---------------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, int r, uint32_t* __restrict__ part) {
+__global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, int r, uint32_t* __restrict__ part,
+                                              uint32_t* bar = nullptr) {
     const float* __restrict__ X = Xs.p[blockIdx.z];
     part += (size_t)blockIdx.z * AMAX_BLOCKS;
+    if (bar != nullptr && blockIdx.x == 0 && threadIdx.x == 0) bar[(size_t)blockIdx.z * BAR_STRIDE + 2] = 0u;
     uint32_t m = 0;
     const int r4 = r >> 2;
     const int n4 = K * r4;
@@ -396,7 +399,7 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 //     L(j+3, j) of the row just handed over it forms itself from the handed-over T(j+3, j).
 // Every element keeps the reference order: updates by column block in increasing order, each one MFMA chain over the
 // block's 32 columns. A producer publishes with an agent-scope release after its stores; a consumer polls with
-// bounded waits (after SPIN_LIMIT polls it records an error and stops waiting, so the kernel always ends). Each
+// bounded waits (after `lim` polls it records an error and stops waiting, so the kernel always ends). Each
 // workgroup waits only on work earlier in the (column block, panel before update) order, which with all
 // workgroups resident (checked at plan creation) rules out deadlock. Flags hold the call number of the workgroup's
 // own counter, so nothing is reset between calls.
@@ -824,10 +827,11 @@ __device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, 
 }
 
 // Poll an agent-scope flag until it holds `ep` (bounded), then acquire. Called by one lane.
-__device__ __forceinline__ void wait_flag(const uint32_t* f, uint32_t ep, uint32_t* err, bool& dead) {
+__device__ __forceinline__ void wait_flag(const uint32_t* f, uint32_t ep, uint32_t* err, bool& dead,
+                                          uint32_t lim = SPIN_LIMIT) {
     uint32_t n = 0;
     while (!dead && __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != ep) {
-        if (++n > SPIN_LIMIT) {
+        if (++n > lim) {
             __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             dead = true;
             break;
@@ -840,13 +844,14 @@ __device__ __forceinline__ void wait_flag(const uint32_t* f, uint32_t ep, uint32
 // Poll up to 64 agent-scope flags at once, each lane watching its own (`mine`; nullptr: nothing to wait for), until
 // all hold `ep` (bounded), then acquire. Called by a whole wavefront; costs one round trip after the last publication
 // instead of one per flag.
-__device__ __forceinline__ void wait_flags_wave(const uint32_t* mine, uint32_t ep, uint32_t* err, bool& dead) {
+__device__ __forceinline__ void wait_flags_wave(const uint32_t* mine, uint32_t ep, uint32_t* err, bool& dead,
+                                                uint32_t lim) {
     const int lane = threadIdx.x & 63;
     uint32_t polls = 0;
     while (!dead) {
         const bool ok = mine == nullptr || __hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ep;
         if (__all(ok)) break;
-        if (++polls > SPIN_LIMIT) {
+        if (++polls > lim) {
             if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             dead = true;
             break;
@@ -871,14 +876,15 @@ __device__ __forceinline__ void publish_flag(uint32_t* f, uint32_t ep) {
 // Barrier of some waves of a workgroup while the others keep running: an LDS counter that each participating
 // wave's lane 0 bumps after its own LDS writes have completed, then waits for (bounded) until it reaches `target`
 // (the number of participants times the number of times this barrier has been passed).
-__device__ __forceinline__ void wave_group_barrier(uint32_t* ctr, uint32_t target, uint32_t* err, bool& dead) {
+__device__ __forceinline__ void wave_group_barrier(uint32_t* ctr, uint32_t target, uint32_t* err, bool& dead,
+                                                   uint32_t lim) {
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
     if ((threadIdx.x & 63) == 0) {
         __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         uint32_t n = 0;
         while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
-            if (++n > SPIN_LIMIT) {
+            if (++n > lim) {
                 __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 dead = true;
                 break;
@@ -925,7 +931,7 @@ size_t chol_lds_bytes(int r) {
 template <bool STAMP>
 __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
                                               float tau_rel, float* L, float* Li, float* Lp, uint32_t* bar,
-                                              uint32_t* flags, float* scal, uint64_t* stamps) {
+                                              uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim) {
     extern __shared__ float4 chol_lds[];
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int b = blockIdx.x, nb = r / CB;
@@ -1065,19 +1071,19 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
                         load_tiles<4, 128>(&R2[t0], 4 - t0, r, 1u << (3 - t0), shift, wl,
                                            [&](int q) { return rowp + CB * (j - 1 + t0 + q); });
                     } else {
-                        if (lane == 0) wait_flag(flagT + i2, ep, err, dead);
+                        if (lane == 0) wait_flag(flagT + i2, ep, err, dead, lim);
                         __builtin_amdgcn_wave_barrier();
                         const float* hp = L + (size_t)CB * i2 * r + (size_t)CB * (j - 2);     // into R2[4] = H
                         load_tiles<5, 128>(&R2[0], 5, r, 0u, 0.f, wl,
                                            [&](int q) { return q < 4 ? rowp + CB * (j - 1 + q) : hp; });
                     }
-                    wave_group_barrier(bar12, 2 * ++n12, err, dead);
+                    wave_group_barrier(bar12, 2 * ++n12, err, dead, lim);
                     if (j >= 1) {
                         if (w == 1)
                             panel32_wave(z.C2[p], R2[0], z.li[pp]);                    // L(j+2, j-1)
                         else if (j >= 2)
                             update32_wave<false>(R2[2], R2[4], z.C2[pp]);      // T(j+2, j+1), block j-2 (owner skips it)
-                        wave_group_barrier(bar12, 2 * ++n12, err, dead);
+                        wave_group_barrier(bar12, 2 * ++n12, err, dead, lim);
                         if (w == 1) {
                             update32_wave<false>(R2[1], z.C2[p], z.P1[pp]);            // T(j+2, j), block j-1
                             store_tile(A + (size_t)CB * (j + 2) * r + CB * j, r, R2[1], lane, 64);
@@ -1117,7 +1123,7 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
         for (int j = 0; j + 4 <= i; ++j) {
             // workgroup 0's block j: Li_j into op[j], T(j+1, j) and T(j+2, j) (through block j-1) into op[j+1..j+2]
             const bool q4 = w < 4;
-            if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead);
+            if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead, lim);
             __syncthreads();
             if (q4)
                 load_tiles_ld<3, 256>(&op[j], 3, tid,
@@ -1147,7 +1153,7 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
                 const int k = j + 3 + lane;
                 const uint32_t* f = nullptr;
                 if (k < kend) f = (k != j + 3) ? flagL + k * nb + j : (k >= 4 ? flagT + k : nullptr);
-                wait_flags_wave(f, ep, err, dead);
+                wait_flags_wave(f, ep, err, dead, lim);
             }
             __syncthreads();
             if (q4)
@@ -1560,15 +1566,19 @@ __global__ __launch_bounds__(256) void k_pack_factors(const float* __restrict__ 
 // SUB (the block projection, kbig.py:88-89): Out = C - fp32(A B) with A [K, r] of another matrix and C its own input,
 // B [r, ncols] (row stride ldd); the chain and the single rounding are the same. The Newton-Schulz step is
 // A = C = Y, B = D.
+// err (Newton-Schulz only; may be null): the matrix's wait-error word; when a bounded wait of the call's Cholesky
+// gave up, the output is NaN, so the failure shows in Q without a host synchronisation. Out may alias Cin (the
+// projection updates its block in place; each element is read before it is written, by the same thread).
 template <bool SUB = false, int MS = 32>
 __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int K, int r, const float* __restrict__ D,
-                                                 const MatsOut Outs, long ldo, const float* __restrict__ Cx = nullptr,
-                                                 long ldc = 0, long ldd = 0) {
+                                                 const MatsOut Outs, long ldo, const float* Cx = nullptr,
+                                                 long ldc = 0, long ldd = 0, const uint32_t* err = nullptr) {
     const float* __restrict__ Yin = Ys.p[blockIdx.z];
-    float* __restrict__ Out = Outs.p[blockIdx.z];
+    float* Out = Outs.p[blockIdx.z];
     const long ldD = SUB ? ldd : r;
     D += (size_t)blockIdx.z * r * ldD;
-    const float* __restrict__ Cin = SUB ? Cx : Yin;
+    const bool failed = err != nullptr && err[(size_t)blockIdx.z * BAR_STRIDE + 2] != 0u;
+    const float* Cin = SUB ? Cx : Yin;
     const long ldC = SUB ? ldc : ldy;
     // row strides 34 and 80: each half-wavefront's operand reads (A: rows l16, columns 4kk + lk; B: rows 4kk + lk,
     // columns l16) fall on 32 distinct banks
@@ -1608,9 +1618,29 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
             const int row = row0 + 16 * rb + 4 * lk + v, col = col0 + 16 * (cbase + c) + l16;
             if (row < K) {
                 const float cv = Cin[(size_t)row * ldC + col];
-                Out[(size_t)row * ldo + col] = SUB ? cv - acc[c][v] : cv + acc[c][v];
+                Out[(size_t)row * ldo + col] = failed ? __builtin_nanf("") : SUB ? cv - acc[c][v] : cv + acc[c][v];
             }
         }
+}
+
+// word[i * stride] = 0 for i < n (clears wait-error words where no k_amax runs first)
+__global__ void k_clear_words(uint32_t* word, int n, int stride) {
+    if ((int)threadIdx.x < n) word[(size_t)threadIdx.x * stride] = 0u;
+}
+
+// Q = Y for a call without polish steps (ns = 0), NaN when the call's Cholesky gave up a wait (as k_nsapply)
+__global__ __launch_bounds__(256) void k_copy_out(const MatsIn Ys, long ldy, int K, int r, const MatsOut Outs, long ldo,
+                                                  const uint32_t* err) {
+    const float* __restrict__ Y = Ys.p[blockIdx.z];
+    float* __restrict__ Out = Outs.p[blockIdx.z];
+    const bool failed = err[(size_t)blockIdx.z * BAR_STRIDE + 2] != 0u;
+    const int r4 = r >> 2;
+    for (int e = blockIdx.x * 256 + threadIdx.x; e < K * r4; e += gridDim.x * 256) {
+        const int row = e / r4, c4 = e - row * r4;
+        float4 v = *reinterpret_cast<const float4*>(Y + (size_t)row * ldy + 4 * c4);
+        if (failed) v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+        *reinterpret_cast<float4*>(Out + (size_t)row * ldo + 4 * c4) = v;
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1634,6 +1664,9 @@ __global__ __launch_bounds__(256) void k_scale_block(const float* __restrict__ X
 // host side
 // ---------------------------------------------------------------------------------------------------------------
 thread_local std::string g_err;
+// polls of one bounded wait before the Cholesky gives up on it (spanqr_debug_spin_limit lowers it for the tests of
+// the failure path)
+uint32_t g_spin_limit = SPIN_LIMIT;
 
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char* fmt, ...) {
@@ -1795,9 +1828,11 @@ int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t
         float* sc = scal ? scal + (size_t)z0 * SCAL_STRIDE : nullptr;
         const dim3 grid(p->chol_grid, 1, nz);
         if (stamp)
-            k_chol<true><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps);
+            k_chol<true><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps,
+                                                 g_spin_limit);
         else
-            k_chol<false><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps);
+            k_chol<false><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps,
+                                                  g_spin_limit);
         HIPCHK(hipGetLastError());
     }
     return SPANQR_OK;
@@ -1880,7 +1915,7 @@ void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsO
     // 64-column steps: half the load-then-multiply steps of each workgroup's chain (1-1.5 us faster at 17408x256
     // and 768x512 than 32-column steps, level elsewhere)
     const dim3 grid((p->K + 31) / 32, p->r / 64, n);
-    k_nsapply<false, 64><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo);
+    k_nsapply<false, 64><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, nullptr, 0, 0, p->bar);
 }
 
 
@@ -1898,7 +1933,7 @@ int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut
         }
         return SPANQR_OK;
     };
-    k_amax<<<dim3(AMAX_BLOCKS, 1, n), 256, 0, st>>>(X, ldx, p->K, p->r, p->amax_part);
+    k_amax<<<dim3(AMAX_BLOCKS, 1, n), 256, 0, st>>>(X, ldx, p->K, p->r, p->amax_part, p->bar);
     if ((rc = mark())) return rc;
     const MatsIn bin[2] = {buf_in(p, p->Y0), buf_in(p, p->Y1)};
     const MatsOut bout[2] = {buf_out(p, p->Y0), buf_out(p, p->Y1)};
@@ -1932,10 +1967,10 @@ int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut
         }
         if ((rc = mark())) return rc;
     }
-    if (ns == 0)
-        for (int z = 0; z < n; ++z)
-            HIPCHK(hipMemcpy2DAsync(Q.p[z], ldq * sizeof(float), in->p[z], ldin * sizeof(float), p->r * sizeof(float),
-                                    p->K, hipMemcpyDeviceToDevice, st));
+    if (ns == 0) {
+        const int blocks = (p->K * (p->r / 4) + 255) / 256 < 1024 ? (p->K * (p->r / 4) + 255) / 256 : 1024;
+        k_copy_out<<<dim3(blocks, 1, n), 256, 0, st>>>(*in, ldin, p->K, p->r, Q, ldq, p->bar);
+    }
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
@@ -2156,7 +2191,10 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
         return fail(SPANQR_EHIP, "the Cholesky needs %d co-resident workgroups, device holds %d", need,
                     occ * cus);
     }
-    p->chol_bmax = (occ * cus) / p->chol_grid;
+    // a batch's launch takes at most three quarters of the device's resident capacity: the flag waits need every
+    // workgroup of a launch resident at once, and the margin leaves room for work of other streams
+    p->chol_bmax = (occ * cus * 3 / 4) / p->chol_grid;
+    if (p->chol_bmax < 1) p->chol_bmax = 1;
     if (p->chol_bmax > batch) p->chol_bmax = batch;
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
     const size_t B = (size_t)batch;
@@ -2377,6 +2415,7 @@ int spanqr_stage_chol(spanqr_plan* p, const float* G, const double* npart, float
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
     if (npart) HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
+    k_clear_words<<<1, 64, 0, st>>>(p->bar + 2, 1, BAR_STRIDE);
     int rc = launch_chol(p, alpha, tau, p->chscal, st, npart ? 16 * p->U : 0, 1);
     if (rc) return rc;
     HIPCHK(hipMemcpyAsync(L, p->L, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
@@ -2435,6 +2474,11 @@ int spanqr_profile_chol(spanqr_plan* p, const float* G, const double* npart, flo
     int khz = 0;
     HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, p->device));
     *tick_ns = khz > 0 ? 1e6 / khz : 0.0;
+    return SPANQR_OK;
+}
+
+int spanqr_debug_spin_limit(unsigned polls) {
+    g_spin_limit = polls;
     return SPANQR_OK;
 }
 

@@ -81,6 +81,46 @@ def check_scale_rounding_margin():
     return [] if worst > 64 else [f"double log2 within {worst} double ulps of an fp32 rounding boundary"]
 
 
+def check_amax():
+    """max|x| (torch.linalg.vector_norm(X, ord=inf) at candidates/kcholqr.py:102) against torch's own CPU evaluation
+    of that expression: the largest magnitude carried by a negative entry, +-inf, NaN (propagates), all -0.0,
+    subnormal-only, and a row stride wider than r (columns past r are not part of X)"""
+    f = []
+    rng = np.random.default_rng(11)
+    cases = {}
+    X = rng.standard_normal((37, 24)).astype(np.float32)
+    cases["random"] = X
+    Y = X.copy()
+    Y[5, 7] = -50.0
+    cases["negative maximum"] = Y
+    Y = X.copy()
+    Y[0, 0] = -np.inf
+    cases["-inf"] = Y
+    Y = X.copy()
+    Y[36, 23] = np.inf
+    cases["+inf"] = Y
+    Y = X.copy()
+    Y[3, 2] = np.nan
+    Y[4, 4] = np.inf
+    cases["nan"] = Y
+    cases["all -0"] = np.full((8, 16), -0.0, np.float32)
+    cases["subnormal"] = (rng.standard_normal((16, 8)) * 1e-40).astype(np.float32)
+    for name, A in cases.items():
+        want = float(torch.linalg.vector_norm(torch.from_numpy(A), ord=float("inf")))
+        got = float(oracle.amax(A))
+        same = (math.isnan(want) and math.isnan(got)) or (want == got and math.copysign(1, want) == math.copysign(1, got))
+        if not same:
+            f.append(f"amax({name}) = {got!r}, torch.linalg.vector_norm(inf) = {want!r}")
+    W = np.zeros((20, 12), np.float32)
+    W[:, :8] = rng.standard_normal((20, 8))
+    W[:, 8:] = -1e9                                   # outside the 8 columns of X
+    got = float(oracle.lib().spqo_amax(W, 12, 20, 8))
+    want = float(torch.linalg.vector_norm(torch.from_numpy(W[:, :8].copy()), ord=float("inf")))
+    if got != want:
+        f.append(f"amax with a row stride wider than r reads past the columns: {got} vs {want}")
+    return f
+
+
 # ---- pivot reciprocal square root (chol.cu:45 uses rsqrtf) ----
 
 def check_rsqrt():
@@ -523,6 +563,6 @@ def check_chol64():
     return f
 
 
-ALL = [check_scale, check_scale_rounding_margin, check_rsqrt, check_dust, check_gram, check_shift, check_chol,
+ALL = [check_amax, check_scale, check_scale_rounding_margin, check_rsqrt, check_dust, check_gram, check_shift, check_chol,
        check_trsm, check_ns, check_orth_small, check_split_rule, check_xgram, check_project, check_borth,
        check_borth_composition, check_rsqrt64, check_chol64]

@@ -99,3 +99,18 @@ def test_batched_abi_rejects_bad_operands(cuda):
     assert b"Q[1]" in _lib.lib().spanqr_last_error()
     assert f(plan.handle, 2, None, r, good_q, r, 5e-7, 1e-7, 1e-8, 2, st) == -1
     assert f(plan.handle, 2, good_x, r, good_q, r, 5e-7, 1e-7, 1e-8, 2, st) == 0
+
+
+def test_batched_layer_set(cuda):
+    """the batched layer set of one training step: 12 layers at 768x512 and 12 at 2048x512 (attention and down_proj
+    of the 110M model), independent cond-1e8 inputs (seeds 100 + 12 g + i), through orth_many: every Q bit-identical
+    to its single call and to the oracle, and through the spec's gates"""
+    groups = [(768, 512, 12), (2048, 512, 12)]
+    Xs = [gen.ttf_uu(K, r, N=K, seed=100 + 12 * gi + i) for gi, (K, r, n) in enumerate(groups) for i in range(n)]
+    print(f"batched layer set: {[f'{n} x {K}x{r}' for K, r, n in groups]}", flush=True)
+    Qs = orth_many([X.to(cuda) for X in Xs])
+    for i, (X, Q) in enumerate(zip(Xs, Qs)):
+        K, r = X.shape
+        assert_bits(Q, orth(X.to(cuda)), f"layer {i} ({K}x{r}) vs its single call")
+        assert_bits(Q, oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows), f"layer {i} ({K}x{r}) vs oracle")
+        gate(X, Q, f"layer {i} ({K}x{r})")

@@ -21,6 +21,7 @@ DEFECTS = {
     13: "every block gets the first dust slice",
     14: "blocks projected once before orthonormalisation instead of twice",
     15: "fp64 trailing update with the wrong sign",
+    16: "max|x| as a signed maximum (absolute value dropped)",
 }
 
 
