@@ -88,6 +88,19 @@ int spanqr_orth_f32(spanqr_plan* plan, const float* X, long ldx, float* Q, long 
 int spanqr_orth_batched_f32(spanqr_plan* plan, int n, const float* const* X, long ldx, float* const* Q, long ldq,
                             float eps, float alpha, float tau, int ns, void* stream);
 
+/* Allocation-free form of spanqr_orth_f32. No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc). Q = orth(X) for
+ * X [K, r] on the current device, bit-identical to spanqr_orth_f32 on a plan for (K, r), but without a plan: the
+ * workspace lives in a fixed 64 MiB device array of the library (each GPU the library runs on holds its own copy
+ * until the process ends), and nothing is allocated or synchronised. Limits: r a multiple of 64 in [64, 512] (no
+ * column-blocked path), K >= r, and the workspace of (K, r) within 64 MiB (17408 x 256 fits; 32768 x 512 does
+ * not): larger shapes return SPANQR_EINVAL. The dust is generated on the device and kept with a shape tag, so a call
+ * after one of another shape regenerates it (a few extra kernels). Every call on one GPU shares the array, which
+ * keeps the last call's contents: calls that overlap in time on one GPU (other streams or threads) race, and the
+ * caller must order them. */
+int spanqr_orth_f32_noalloc(int K, int r, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
+                            float tau, int ns, void* stream);
+
 /* Profiling form of spanqr_orth_f32: the same kernels on the same stream with a HIP event after each, then waits
  * for the stream (host synchronisation: not for the hot path). ms[i] receives the time of kernel i in launch order
  * (amax; per pass gram, reduce, chol, trsm; per polish step gram, reduce, apply); *n_out their number.

@@ -33,6 +33,7 @@ SIGNATURES = {
     "spanqr_plan_query": (_L, [_P, _I]),
     "spanqr_orth_f32": (_I, [_P, _P, _L, _P, _L, _F, _F, _F, _I, _P]),
     "spanqr_orth_batched_f32": (_I, [_P, _I, _P, _L, _P, _L, _F, _F, _F, _I, _P]),
+    "spanqr_orth_f32_noalloc": (_I, [_I, _I, _P, _L, _P, _L, _F, _F, _F, _I, _P]),
     "spanqr_profile_orth": (_I, [_P, _P, _L, _P, _L, _F, _F, _F, _I, _P, _P, _I, ctypes.POINTER(ctypes.c_int)]),
     "spanqr_profile_chol": (_I, [_P, _P, _P, _F, _F, _P, ctypes.POINTER(ctypes.c_double), _P]),
     "spanqr_profile_kernel": (_I, [_P, _I, _I, ctypes.POINTER(ctypes.c_float), _P]),

@@ -2017,6 +2017,95 @@ static int check_shape(int K, int r, bool blocked_ok = false) {
 
 namespace {
 
+size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Shape-derived fields of a kcholf plan (r <= 512): the Gram's split rule, the Cholesky's grid, the solve variant.
+void plan_shape(spanqr_plan* p, int K, int r, int batch) {
+    p->K = K; p->r = r; p->batch = batch;
+    p->nt = r / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / 64;
+    split_policy(K, p->U, &p->S, &p->KS);
+    p->chol_grid = (r / CB > 4) ? r / CB - 3 : 1;     // workgroup 0 + one per tile row 4..r/32-1
+    p->trsm_q = (r / CB + TRSM_NW - 1) / TRSM_NW;
+    // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU
+    p->trsm_rb = ((K + 15) / 16 >= 1024) ? 2 : 1;
+    // a wavefront pair per 16 rows once there are enough rows to occupy the SIMDs (the chain over r/32 blocks is
+    // long; the measured crossover at r = 256 lies near K = 8192-10240); below that, k_trsm splits each row block's
+    // columns over eight waves
+    p->trsm_rows = r <= 256 && K >= 9216;
+    p->lp_stride = (size_t)(r / CB) * (r / CB + 1) / 2 * CB * CB;
+}
+
+// Per-device set-up of a kcholf plan's kernels: the dynamic LDS limits of the solve and the Cholesky, and the
+// co-residency check that the Cholesky's flag waits rely on; sets chol_bmax (at most batch).
+int plan_device_setup(spanqr_plan* p, int device) {
+    const int r = p->r;
+    {
+        const size_t need = trsm_lds(r, p->trsm_rb);
+        int maxsh = 0;
+        HIPCHK(hipDeviceGetAttribute(&maxsh, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+        if ((size_t)maxsh < need)
+            return fail(SPANQR_EHIP, "the solve needs %zu bytes of LDS per workgroup, device allows %d", need, maxsh);
+        const hipError_t e = trsm_set_lds_plan(p->trsm_q, p->trsm_rb, r);
+        if (e != hipSuccess) return fail(SPANQR_EHIP, "setting the solve's LDS size failed: %s", hipGetErrorString(e));
+    }
+    int occ = 0, cus = 0;
+    {
+        const int need = (int)chol_lds_bytes(r);
+        hipError_t e = hipFuncSetAttribute((const void*)k_chol<true>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)k_chol<false>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
+        if (e != hipSuccess)
+            return fail(SPANQR_EHIP, "setting the Cholesky's LDS size (%d bytes) failed: %s", need, hipGetErrorString(e));
+    }
+    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol<true>, 512, chol_lds_bytes(r)));
+    HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+    if (occ * cus < p->chol_grid)
+        return fail(SPANQR_EHIP, "the Cholesky needs %d co-resident workgroups, device holds %d", p->chol_grid, occ * cus);
+    // a batch's launch takes at most three quarters of the device's resident capacity: the flag waits need every
+    // workgroup of a launch resident at once, and the margin leaves room for work of other streams
+    p->chol_bmax = (occ * cus * 3 / 4) / p->chol_grid;
+    if (p->chol_bmax < 1) p->chol_bmax = 1;
+    if (p->chol_bmax > p->batch) p->chol_bmax = p->batch;
+    return SPANQR_OK;
+}
+
+// Workspace of a kcholf plan, 256-byte aligned buffers in this order: Z first (the dust: uploaded or generated; the
+// rest starts zeroed), then the Gram partials, G, L, Li, Lp, Y0, Y1, scalars, Cholesky scalars, norm partials, amax
+// partials, error words, stamps, flags. Assigns the pointers from base (nullptr: sizes only); returns the bytes.
+size_t plan_layout(spanqr_plan* p, char* base) {
+    const size_t B = (size_t)p->batch, K = p->K, r = p->r;
+    const size_t nKr = K * r * sizeof(float);
+    const size_t sz[] = {
+        al256(nKr),                                             // Z
+        al256(B * p->S * p->U * TB * TB * sizeof(float)),       // P
+        al256(B * r * r * sizeof(float)),                       // G
+        al256(B * r * r * sizeof(float)),                       // L
+        al256(B * r * CB * sizeof(float)),                      // Li
+        al256(B * p->lp_stride * sizeof(float)),                // Lp
+        al256(B * nKr), al256(B * nKr),                         // Y0, Y1
+        al256(B * SCAL_STRIDE * sizeof(float)),                 // scal
+        al256(B * SCAL_STRIDE * sizeof(float)),                 // chscal
+        al256(B * 16 * p->U * sizeof(double)),                  // npart
+        al256(B * AMAX_BLOCKS * sizeof(uint32_t)),              // amax_part
+        al256(B * BAR_STRIDE * sizeof(uint32_t)),               // bar
+        al256(2 * (4 * (512 / CB) + 2) * sizeof(uint64_t)),     // stamps
+        al256(B * FLAG_STRIDE * sizeof(uint32_t)),              // flags
+    };
+    void** ptrs[] = {(void**)&p->Z, (void**)&p->P, (void**)&p->G, (void**)&p->L, (void**)&p->Li, (void**)&p->Lp,
+                     (void**)&p->Y0, (void**)&p->Y1, (void**)&p->scal, (void**)&p->chscal, (void**)&p->npart,
+                     (void**)&p->amax_part, (void**)&p->bar, (void**)&p->stamps, (void**)&p->flags};
+    size_t off = 0;
+    for (size_t i = 0; i < sizeof(sz) / sizeof(sz[0]); ++i) {
+        if (base) *ptrs[i] = base + off;
+        off += sz[i];
+    }
+    return off;
+}
+
+}  // namespace
+
+namespace {
+
 // Column-blocked plan: a 256-column block plan plus the blocked path's own buffers (no Gram or Cholesky of its own).
 int create_blocked(int K, int r, int device, spanqr_plan** out) {
     spanqr_plan* p = new spanqr_plan;
@@ -2147,95 +2236,26 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
     DeviceGuard dg(device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", device);
     spanqr_plan* p = new spanqr_plan;
-    p->K = K; p->r = r; p->device = device; p->batch = batch;
-    p->nt = r / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / 64;
-    split_policy(K, p->U, &p->S, &p->KS);
-    p->chol_grid = (r / CB > 4) ? r / CB - 3 : 1;     // workgroup 0 + one per tile row 4..r/32-1
-    p->trsm_q = (r / CB + TRSM_NW - 1) / TRSM_NW;
-    // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU
-    p->trsm_rb = ((K + 15) / 16 >= 1024) ? 2 : 1;
-    // a wavefront pair per 16 rows once there are enough rows to occupy the SIMDs (the chain over r/32 blocks is
-    // long; the measured crossover at r = 256 lies near K = 8192-10240); below that, k_trsm splits each row block's
-    // columns over eight waves
-    p->trsm_rows = r <= 256 && K >= 9216;
-    {
-        const size_t need = trsm_lds(r, p->trsm_rb);
-        int maxsh = 0;
-        HIPCHK(hipDeviceGetAttribute(&maxsh, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
-        if ((size_t)maxsh < need) {
-            delete p;
-            return fail(SPANQR_EHIP, "the solve needs %zu bytes of LDS per workgroup, device allows %d", need, maxsh);
-        }
-        const hipError_t e = trsm_set_lds_plan(p->trsm_q, p->trsm_rb, r);
-        if (e != hipSuccess) {
-            delete p;
-            return fail(SPANQR_EHIP, "setting the solve's LDS size failed: %s", hipGetErrorString(e));
-        }
-    }
-    int occ = 0, cus = 0;
-    {
-        const int need = (int)chol_lds_bytes(r);
-        hipError_t e = hipFuncSetAttribute((const void*)k_chol<true>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)k_chol<false>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
-        if (e != hipSuccess) {
-            delete p;
-            return fail(SPANQR_EHIP, "setting the Cholesky's LDS size (%d bytes) failed: %s", need, hipGetErrorString(e));
-        }
-    }
-    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol<true>, 512, chol_lds_bytes(r)));
-    HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
-    if (occ * cus < p->chol_grid) {
-        const int need = p->chol_grid;
+    p->device = device;
+    plan_shape(p, K, r, batch);
+    int rc = plan_device_setup(p, device);
+    if (rc != SPANQR_OK) {
         delete p;
-        return fail(SPANQR_EHIP, "the Cholesky needs %d co-resident workgroups, device holds %d", need,
-                    occ * cus);
+        return rc;
     }
-    // a batch's launch takes at most three quarters of the device's resident capacity: the flag waits need every
-    // workgroup of a launch resident at once, and the margin leaves room for work of other streams
-    p->chol_bmax = (occ * cus * 3 / 4) / p->chol_grid;
-    if (p->chol_bmax < 1) p->chol_bmax = 1;
-    if (p->chol_bmax > batch) p->chol_bmax = batch;
-    auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
-    const size_t B = (size_t)batch;
-    const size_t nKr = (size_t)K * r * sizeof(float);
-    const size_t sz_Z = al(nKr), sz_P = al(B * p->S * p->U * TB * TB * sizeof(float));
-    const size_t sz_rr = al(B * r * r * sizeof(float)), sz_Li = al(B * r * CB * sizeof(float));
-    p->lp_stride = (size_t)(r / CB) * (r / CB + 1) / 2 * CB * CB;
-    const size_t sz_Lp = al(B * p->lp_stride * sizeof(float));
-    const size_t sz_Y = al(B * nKr), sz_sc = al(B * SCAL_STRIDE * sizeof(float));
-    const size_t sz_np = al(B * 16 * p->U * sizeof(double));
-    const size_t sz_am = al(B * AMAX_BLOCKS * sizeof(uint32_t)), sz_bar = al(B * BAR_STRIDE * sizeof(uint32_t));
-    const size_t sz_st = al(2 * (4 * (512 / CB) + 2) * sizeof(uint64_t));
-    const size_t sz_fl = al(B * FLAG_STRIDE * sizeof(uint32_t));
-    p->bytes = sz_Z + sz_P + 2 * sz_rr + sz_Li + sz_Lp + 2 * sz_Y + 2 * sz_sc + sz_np + sz_am + sz_bar + sz_st + sz_fl;
+    p->bytes = plan_layout(p, nullptr);
     if (hipMalloc((void**)&p->base, p->bytes) != hipSuccess) {
         const size_t nb = p->bytes;
         delete p;
         return fail(SPANQR_ENOMEM, "workspace allocation of %zu bytes failed", nb);
     }
-    char* c = p->base;
-    p->Z = (float*)c; c += sz_Z;
-    p->P = (float*)c; c += sz_P;
-    p->G = (float*)c; c += sz_rr;
-    p->L = (float*)c; c += sz_rr;
-    p->Li = (float*)c; c += sz_Li;
-    p->Lp = (float*)c; c += sz_Lp;
-    p->Y0 = (float*)c; c += sz_Y;
-    p->Y1 = (float*)c; c += sz_Y;
-    p->scal = (float*)c; c += sz_sc;
-    p->chscal = (float*)c; c += sz_sc;
-    p->npart = (double*)c; c += sz_np;
-    p->amax_part = (uint32_t*)c; c += sz_am;
-    p->bar = (uint32_t*)c; c += sz_bar;
-    p->stamps = (uint64_t*)c; c += sz_st;
-    p->flags = (uint32_t*)c; c += sz_fl;
+    plan_layout(p, p->base);
+    const size_t nKr = (size_t)K * r * sizeof(float);
     float* hz = (float*)malloc(nKr);
-    int rc = hz ? spanqr_dust_host(K, r, hz) : fail(SPANQR_ENOMEM, "host dust buffer");
+    rc = hz ? spanqr_dust_host(K, r, hz) : fail(SPANQR_ENOMEM, "host dust buffer");
     if (rc == SPANQR_OK) {
         if (hipMemcpy(p->Z, hz, nKr, hipMemcpyHostToDevice) != hipSuccess ||
-            hipMemset(p->L, 0, sz_rr) != hipSuccess || hipMemset(p->Lp, 0, sz_Lp) != hipSuccess || hipMemset(p->scal, 0, 2 * sz_sc) != hipSuccess ||
-            hipMemset(p->bar, 0, sz_bar) != hipSuccess || hipMemset(p->flags, 0, sz_fl) != hipSuccess ||
+            hipMemset(p->base + al256(nKr), 0, p->bytes - al256(nKr)) != hipSuccess ||   // all but Z
             hipDeviceSynchronize() != hipSuccess)
             rc = fail(SPANQR_EHIP, "plan upload failed");
     }
@@ -2498,6 +2518,132 @@ int spanqr_plan_copy_scalars(spanqr_plan* p, float* scal8, void* stream) {
     HIPCHK(hipMemcpyAsync(scal8, p->scal, 7 * sizeof(float), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipMemcpyAsync(scal8 + 7, p->bar + 2, sizeof(float), hipMemcpyDeviceToDevice, st));
     return SPANQR_OK;
+}
+
+}  // extern "C"
+
+// ===============================================================================================================
+// Allocation-free orth: spanqr_orth_f32's kernels on a workspace carved out of a fixed device array instead of a
+// plan's hipMalloc. No counterpart in the reference; for callers that cannot allocate (code under graph capture,
+// serving loops). The dust is generated on the device, bit-identical to spanqr_dust_host, and kept in the array with
+// a shape tag, so a call regenerates it only after a call of another shape.
+// ===============================================================================================================
+constexpr size_t SCRATCH_BYTES = (size_t)64 << 20;   // the largest workspace the entry point takes
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+
+__device__ __forceinline__ uint64_t mix64_dev(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// raw draws of spanqr_dust_host: element e = k r + c, six splitmix64 outputs, their twelve halves summed, centred,
+// scaled by 2^-32 and rounded to fp32
+__global__ __launch_bounds__(256) void k_dust_raw(float* Z, int K, int r, const uint64_t* tag, uint64_t want) {
+    if (*tag == want) return;
+    const uint64_t key = mix64_dev(20261018ull);
+    const size_t n = (size_t)K * r;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) {
+        uint64_t S = 0;
+        for (uint64_t j = 0; j < 6; ++j) {
+            const uint64_t wv = mix64_dev(key + (6 * (uint64_t)e + j + 1) * 0x9E3779B97F4A7C15ull);
+            S += (wv & 0xffffffffull) + (wv >> 32);
+        }
+        Z[e] = (float)ldexp((double)((int64_t)S - (int64_t)6 * 4294967295ll), -32);
+    }
+}
+
+// column norms of the raw draws: sqrt of the squares summed in double in ascending k (one thread per column)
+__global__ __launch_bounds__(256) void k_dust_norm(const float* Z, int K, int r, double* nrm, const uint64_t* tag,
+                                                   uint64_t want) {
+    if (*tag == want) return;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= r) return;
+    double acc = 0.0;
+    for (int k = 0; k < K; ++k) {
+        const double z = (double)Z[(size_t)k * r + c];
+        acc += z * z;
+    }
+    nrm[c] = sqrt(acc);
+}
+
+__global__ __launch_bounds__(256) void k_dust_scale(float* Z, int K, int r, const double* nrm, const uint64_t* tag,
+                                                    uint64_t want) {
+    if (*tag == want) return;
+    const size_t n = (size_t)K * r;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256)
+        Z[e] = (float)((double)Z[e] / nrm[e % r]);
+}
+
+// every call: the Cholesky's flags and call counters start from zero (the previous call may have had another shape,
+// hence another workgroup count), and the dust now held is tagged
+__global__ __launch_bounds__(256) void k_noalloc_prep(uint32_t* flags, int nflags, uint64_t* tag, uint64_t want) {
+    for (int e = threadIdx.x; e < nflags; e += 256) flags[e] = 0u;
+    if (threadIdx.x == 0) *tag = want;
+}
+
+std::mutex g_na_mu;
+char* g_na_base[MAX_DEVICES] = {};   // the array's device address on each device (hipGetSymbolAddress)
+
+// The array: the dust's shape tag and column norms at fixed offsets (every call finds the tag of the dust the array
+// holds at the same place, whatever the shape of the call that wrote it), then a plan's workspace.
+constexpr size_t NA_TAG = 0, NA_NRM = 256, NA_WS = NA_NRM + 512 * sizeof(double);
+
+size_t noalloc_bytes(int K, int r) {
+    spanqr_plan p;
+    plan_shape(&p, K, r, 1);
+    return NA_WS + plan_layout(&p, nullptr);
+}
+
+}  // namespace
+
+extern "C" {
+
+int spanqr_orth_f32_noalloc(int K, int r, const float* X, long ldx, float* Q, long ldq, float eps, float alpha,
+                            float tau, int ns, void* stream) {
+    int rc = check_shape(K, r);
+    if (rc != SPANQR_OK) return rc;
+    const size_t need = noalloc_bytes(K, r);
+    if (need > SCRATCH_BYTES)
+        return fail(SPANQR_EINVAL, "noalloc: X [%d, %d] needs %zu bytes of workspace, more than the fixed %zu "
+                                   "(use a plan)", K, r, need, SCRATCH_BYTES);
+    if (ns < 0) return fail(SPANQR_EINVAL, "ns = %d < 0", ns);
+    spanqr_plan p;
+    plan_shape(&p, K, r, 1);
+    if ((rc = check_mat(&p, X, ldx, "X"))) return rc;
+    if ((rc = check_mat(&p, Q, ldq, "Q"))) return rc;
+    int dev = -1;
+    HIPCHK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEVICES) return fail(SPANQR_EINVAL, "noalloc: device %d out of range", dev);
+    char* base = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_na_mu);
+        if (g_na_base[dev] == nullptr) {
+            void* ptr = nullptr;
+            HIPCHK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+            if (ptr == nullptr) return fail(SPANQR_EHIP, "noalloc: no device address for the workspace array");
+            g_na_base[dev] = (char*)ptr;
+        }
+        base = g_na_base[dev];
+    }
+    p.device = dev;
+    if ((rc = plan_device_setup(&p, dev))) return rc;
+    plan_layout(&p, base + NA_WS);
+    uint64_t* tag = (uint64_t*)(base + NA_TAG);
+    double* nrm = (double*)(base + NA_NRM);
+    const uint64_t want = ((uint64_t)(uint32_t)K << 32) | (uint32_t)r;
+    hipStream_t st = (hipStream_t)stream;
+    const int eblocks = (int)(((size_t)K * r + 255) / 256 < 2048 ? ((size_t)K * r + 255) / 256 : 2048);
+    k_dust_raw<<<eblocks, 256, 0, st>>>(p.Z, K, r, tag, want);
+    k_dust_norm<<<(r + 255) / 256, 256, 0, st>>>(p.Z, K, r, nrm, tag, want);
+    k_dust_scale<<<eblocks, 256, 0, st>>>(p.Z, K, r, nrm, tag, want);
+    k_noalloc_prep<<<1, 256, 0, st>>>(p.flags, FLAG_STRIDE, tag, want);
+    HIPCHK(hipGetLastError());
+    return enqueue_orth(&p, 1, mats_in(&X, 1), ldx, mats_out(&Q, 1), ldq, eps, alpha, tau, ns, st, false);
 }
 
 }  // extern "C"
