@@ -55,10 +55,14 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 FLUSH_BYTES = 512 << 20      # more than the 256 MiB MALL plus every XCD's L2
 
 
-# kernel families of one call: (name, spanqr_profile_kernel id, launches per call)
+# kernel families of one call: (name, spanqr_profile_kernel id, launches per call); a plan whose solve runs in the
+# Cholesky's launch has chol_solve families in place of chol and trsm
 FAMILIES = [("amax", _lib.K_AMAX, 1), ("gram_pass1", _lib.K_GRAM_PASS1, 1), ("gram", _lib.K_GRAM, 4),
             ("reduce", _lib.K_REDUCE, 5), ("chol", _lib.K_CHOL, 3), ("trsm_pass1", _lib.K_TRSM_PASS1, 1),
             ("trsm", _lib.K_TRSM, 2), ("ns_apply", _lib.K_NS_APPLY, 2)]
+FUSED_FAMILIES = [("amax", _lib.K_AMAX, 1), ("gram_pass1", _lib.K_GRAM_PASS1, 1), ("gram", _lib.K_GRAM, 4),
+                  ("reduce", _lib.K_REDUCE, 5), ("chol_solve_pass1", _lib.K_CHOL_SOLVE_PASS1, 1),
+                  ("chol_solve", _lib.K_CHOL_SOLVE, 2), ("ns_apply", _lib.K_NS_APPLY, 2)]
 
 
 def algorithmic(family, K, r):
@@ -68,7 +72,9 @@ def algorithmic(family, K, r):
     kr = 4.0 * K * r
     return {"amax": (0.0, kr), "gram_pass1": (K * r * (r + 1.0), kr), "gram": (K * r * (r + 1.0), kr),
             "reduce": (0.0, 0.0), "chol": (r ** 3 / 3.0, 0.0), "trsm_pass1": (K * r * (r + 1.0), 3 * kr),
-            "trsm": (K * r * (r + 1.0), 2 * kr), "ns_apply": (2.0 * K * r * r, 2 * kr)}[family]
+            "trsm": (K * r * (r + 1.0), 2 * kr), "ns_apply": (2.0 * K * r * r, 2 * kr),
+            "chol_solve_pass1": (r ** 3 / 3.0 + K * r * (r + 1.0), 3 * kr),
+            "chol_solve": (r ** 3 / 3.0 + K * r * (r + 1.0), 2 * kr)}[family]
 
 
 def call_work(K, r):
@@ -207,8 +213,10 @@ def orth_error(Q):
 def kernels_at(X, reps):
     """per kernel family at X's shape: average launch duration and its algorithmic rates"""
     K, r = X.shape
+    kcholqr_f(X)
+    fams = FUSED_FAMILIES if get_plan(K, r, X.device).solve_rows > 0 else FAMILIES
     out = {}
-    for fam, which, per_call in FAMILIES:
+    for fam, which, per_call in fams:
         us = kernel_avg_us(X, which, reps)
         fl, by = algorithmic(fam, K, r)
         out[fam] = {"us": round(us, 3), "per_call": per_call, "tflops": round(fl / us / 1e6, 3),
@@ -221,11 +229,13 @@ def roofline_of(kern, shapes):
     """roofline of the kernel family with the largest share of the summed kernel time over the headline shapes:
     achieved = mean algorithmic work per launch / mean launch duration (both over one launch at each shape, as a
     trace of the timed region averages them)"""
-    tot = {fam: sum(kern[s][fam]["us"] * kern[s][fam]["per_call"] for s in shapes) for fam in kern[shapes[0]]}
+    tot = {fam: sum(kern[s][fam]["us"] * kern[s][fam]["per_call"] for s in shapes if fam in kern[s])
+           for fam in kern[shapes[0]]}
     dom = max(tot, key=tot.get)
     dims = {name: (K, r) for name, K, r, _ in HEADLINE}
     fl = statistics.mean(algorithmic(dom, *dims[s])[0] for s in shapes)
     by = statistics.mean(algorithmic(dom, *dims[s])[1] for s in shapes)
+    shapes = [s for s in shapes if dom in kern[s]]
     us = statistics.mean(kern[s][dom]["us"] for s in shapes)
     bound = "mfma" if fl / PEAK_FP32_TFLOPS >= by / PEAK_HBM_GBS * 1e-3 else "hbm"
     achieved = fl / us / 1e6 if bound == "mfma" else by / us / 1e3

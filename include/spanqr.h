@@ -53,6 +53,8 @@ enum {
     SPANQR_Q_BATCH = 7,          /* matrices per call the plan holds workspace for */
     SPANQR_Q_CHOL_BATCH = 8,     /* matrices per Cholesky launch (all their workgroups fit on the device at once) */
     SPANQR_Q_BLOCKS = 9,         /* 256-column blocks of a column-blocked plan (r > 512); 0 otherwise */
+    SPANQR_Q_SOLVE_ROWS = 10,    /* rows per solve workgroup when the solve runs in the Cholesky's launch; 0 when
+                                    they are separate launches */
 };
 
 /* Create a plan for X [K, r] on HIP device `device` (allocates the workspace and uploads the dust matrix).
@@ -126,10 +128,13 @@ enum {
     SPANQR_K_TRSM_PASS1 = 5,     /* solve with the fused s * x + eps * z operand */
     SPANQR_K_TRSM = 6,           /* solve */
     SPANQR_K_NS_APPLY = 7,       /* Newton-Schulz correction Y + Y D */
+    SPANQR_K_CHOL_SOLVE_PASS1 = 8,   /* the Cholesky with the pass-1 solve in one launch (plans with SOLVE_ROWS > 0) */
+    SPANQR_K_CHOL_SOLVE = 9,         /* the Cholesky with the solve in one launch */
 };
 
 /* Average duration of one kernel of the call: `reps` back-to-back launches on the plan's own workspace, between two
- * HIP events on `stream`, after one untimed launch; waits for the stream. For timing only: it leaves the workspace
+ * HIP events on `stream`, after one untimed launch (the Cholesky-with-solve launches: each between its own pair of
+ * events, after a small kernel that resets its column counters); waits for the stream. For timing only: it leaves the workspace
  * in an unspecified state (the next spanqr_orth_f32 rebuilds what it needs). No counterpart in the reference. */
 int spanqr_profile_kernel(spanqr_plan* plan, int which, int reps, float* avg_ms, void* stream);
 

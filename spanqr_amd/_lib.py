@@ -18,11 +18,13 @@ HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 # plan queries (include/spanqr.h)
-Q_K, Q_R, Q_SPLITS, Q_SPLIT_ROWS, Q_CHOL_GRID, Q_WORKSPACE_MB, Q_DEVICE, Q_BATCH, Q_CHOL_BATCH, Q_BLOCKS = range(10)
+(Q_K, Q_R, Q_SPLITS, Q_SPLIT_ROWS, Q_CHOL_GRID, Q_WORKSPACE_MB, Q_DEVICE, Q_BATCH, Q_CHOL_BATCH, Q_BLOCKS,
+ Q_SOLVE_ROWS) = range(11)
 MAX_BATCH = 32   # SPANQR_MAX_BATCH
 MAX_R = 4096     # SPANQR_MAX_R
 # kernels for spanqr_profile_kernel
-K_AMAX, K_GRAM_PASS1, K_GRAM, K_REDUCE, K_CHOL, K_TRSM_PASS1, K_TRSM, K_NS_APPLY = range(8)
+(K_AMAX, K_GRAM_PASS1, K_GRAM, K_REDUCE, K_CHOL, K_TRSM_PASS1, K_TRSM, K_NS_APPLY, K_CHOL_SOLVE_PASS1,
+ K_CHOL_SOLVE) = range(10)
 
 # every exported symbol of include/spanqr.h: (restype, argtypes)
 _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float

@@ -321,10 +321,14 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
 // ---------------------------------------------------------------------------------------------------------------
 // MODE 2 (the block projection): tile u = ti * nt + tj of a full (not symmetric) product, written once into G with
 // row stride r; no norm partials.
+// colcnt (MODE 0, may be null): the next Cholesky's column counters, cleared here (16 words, stride 16 per matrix).
 template <int MODE>
 __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int S, int nt, int r,
-                                                float* __restrict__ G, double* __restrict__ npart) {
+                                                float* __restrict__ G, double* __restrict__ npart,
+                                                uint32_t* colcnt = nullptr) {
     const int b = blockIdx.x, u = blockIdx.y, U = gridDim.y;
+    if (MODE == 0 && colcnt != nullptr && b == 0 && u == 0 && threadIdx.x < 16)
+        colcnt[((size_t)blockIdx.z * 16 + threadIdx.x) * 16] = 0u;
     P += (size_t)blockIdx.z * S * U * TB * TB;
     G += (size_t)blockIdx.z * r * r;
     if (MODE != 2) npart += (size_t)blockIdx.z * 16 * U;
@@ -928,15 +932,29 @@ size_t chol_lds_bytes(int r) {
 // Workgroups of eight wavefronts: waves 0-3 do all the work described here; waves 4-7 share the owners' row update
 // with them (two wavefronts per SIMD there, so one's LDS traffic overlaps the other's MFMA chain) and otherwise only
 // pass the same workgroup barriers.
+// colcnt (may be null): per column block k, a counter (stride CC_STRIDE) that every producer of the packed operands
+// of column k (Li_k and L(i, k), i > k) raises once those are released, for the solve that runs in the same launch:
+// owner i credits column j-1 when it publishes L(i, j) and column i-4 when it hands its row over; workgroup 0 credits
+// column k at the release that opens step k+2 (its stores of column k's operands completed during step k+1), column
+// nb-2 at a release of its own in the last step, and column nb-1 (Li_{nb-1} alone) right after the last tile factor.
+// Column k is complete at 1 + max(0, nb - 4 - k) credits; the counters start at zero.
+constexpr int CC_STRIDE = 16;   // uint32 words between column counters (one 64-byte line each)
+static_assert(CC_STRIDE == 16 && CH_MAXROW == 16, "k_reduce clears the column counters with stride 16, 16 per matrix");
+
+__device__ __forceinline__ void credit(uint32_t* colcnt, int k) {
+    if (colcnt != nullptr) __hip_atomic_fetch_add(colcnt + (size_t)k * CC_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The Cholesky of workgroup b of matrix z (the pointers address matrix 0 of the launch).
 template <bool STAMP>
-__global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
-                                              float tau_rel, float* L, float* Li, float* Lp, uint32_t* bar,
-                                              uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim) {
+__device__ __forceinline__ void chol_body(const int b, const size_t z, float* A, int r, const double* __restrict__ npart,
+                                          int nnp, float alpha, float tau_rel, float* L, float* Li, float* Lp,
+                                          uint32_t* bar, uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim,
+                                          uint32_t* colcnt) {
     extern __shared__ float4 chol_lds[];
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int b = blockIdx.x, nb = r / CB;
+    const int nb = r / CB;
     {
-        const size_t z = blockIdx.z;   // matrix of the batch
         A += z * r * r;
         L += z * r * r;
         Li += z * r * CB;
@@ -945,6 +963,7 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
         bar += z * BAR_STRIDE;
         flags += z * FLAG_STRIDE;
         if (scal != nullptr) scal += z * SCAL_STRIDE;
+        if (colcnt != nullptr) colcnt += z * CC_STRIDE * CH_MAXROW;
     }
     uint32_t* err = bar + 2;
     uint32_t* flagL = flags;
@@ -1033,7 +1052,12 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
         auto publish = [&](int j) {
             const int q = j & 1;
             const size_t o = (size_t)CB * j;
-            if (lane == 0) publish_flag(flagL + j * nb + j, ep);
+            if (lane == 0) {
+                publish_flag(flagL + j * nb + j, ep);
+                // the release covers column j-1's operands (stored in step j); column nb-2 is credited in the last
+                // step, column nb-1 by wave 0
+                if (j >= 1 && j < nb - 1) credit(colcnt, j - 1);
+            }
             store_tile_lower(L + o * r + o, r, z.dl[q], false, lane, 64);
             if (j + 1 < nb) store_tile(L + (o + CB) * r + o, r, z.P1[q], lane, 64);
             if (j + 2 < nb) store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
@@ -1046,6 +1070,12 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
             if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
             if (w == 0) {
                 factor_inv32(bl0, bl1, pq, z.id, z.D[p], tau, z.dl[p], z.li[p], Li + (size_t)CB * j * CB);
+                if (colcnt != nullptr && j == nb - 1) {
+                    // the last column of the factor is Li_{nb-1} alone: packed, released and credited at once
+                    store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[p], lane, 64);
+                    release();
+                    if (lane == 0) credit(colcnt, j);
+                }
             } else if (w < 4) {
                 // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p]. Wave 3
                 // publishes the previous step, then applies the part of the previous step's look-ahead that this
@@ -1057,6 +1087,10 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
                 const bool row2 = j + 2 < nb;
                 if (w == 3) {
                     if (j >= 1) publish(j - 1);
+                    if (colcnt != nullptr && j == nb - 1) {   // column nb-2's operands, stored just now
+                        release();
+                        if (lane == 0) credit(colcnt, nb - 2);
+                    }
                     if (j >= 1 && j + 1 < nb) {
                         const Tile* R1 = z.R2[pp];
                         update32_wave_to<false>(z.X1, R1[2], z.P2[pp], z.P1[pp]);      // T(j+1, j)
@@ -1139,8 +1173,11 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
             store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j]);   // threads 0-255
             __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
             __syncthreads();
-            if (tid == 0) publish_flag(flagL + i * nb + j, ep);
-            store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j]);   // for later kernels only
+            if (tid == 0) {
+                publish_flag(flagL + i * nb + j, ep);
+                if (j >= 1) credit(colcnt, j - 1);   // the release covers L(i, j-1)'s packed form, stored after it
+            }
+            store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j]);   // for the solve only
             // block j's panels of the rows between: L(k, j), k = j+1..i-1, all in LDS before the updates. At the
             // last block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed. Rows j+1 and j+2
             // are workgroup 0's: their panels are formed here, as workgroup 0 forms them. Row j+3 has just been
@@ -1230,12 +1267,23 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
                     store_tile(A + (size_t)CB * i * r + (size_t)CB * (i - 3 + t), r, rt[i - 3 + t]);
                 __builtin_amdgcn_s_waitcnt(0x0F70);
                 __syncthreads();
-                if (tid == 0) publish_flag(flagT + i, ep);
+                if (tid == 0) {
+                    publish_flag(flagT + i, ep);
+                    credit(colcnt, j);
+                }
             }
         }
     }
     __syncthreads();
     if (tid == 0) cnt[b] = ep;
+}
+
+template <bool STAMP>
+__global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
+                                              float tau_rel, float* L, float* Li, float* Lp, uint32_t* bar,
+                                              uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim) {
+    chol_body<STAMP>(blockIdx.x, blockIdx.z, A, r, npart, nnp, alpha, tau_rel, L, Li, Lp, bar, flags, scal, stamps,
+                     lim, nullptr);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1288,30 +1336,39 @@ __device__ __forceinline__ void trsm_fetch(TrsmOps<Q>& o, const float* __restric
     }
 }
 
-template <bool PASS1, int Q, int RB>
-__global__ __launch_bounds__(64 * TRSM_NW) void k_trsm(const MatsIn As, long lda, int K, int r,
-                                              const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
-                                              long ldz, float eps, const float* __restrict__ Lp, const MatsOut Ys,
-                                              long ldy,
-                                              float* scal) {
+// WAIT (the solve in the Cholesky's launch): the operands of column block k are read only once its counter in
+// colcnt has all its credits (see chol_body); wave 0 polls the counters in order, acquires, and raises an LDS word
+// the other waves poll. Li_k is then fetched with column k's operands rather than eight steps ahead. A poll that
+// gives up (after `lim` sleeps) records the error in err and proceeds, so the kernel always ends.
+template <bool PASS1, int Q, int RB, bool WAIT>
+__device__ __forceinline__ void trsm_body(const int rbi, const int z, const MatsIn& As, long lda, int K, int r,
+                                          const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
+                                          long ldz, float eps, const float* __restrict__ Lp, const MatsOut& Ys,
+                                          long ldy, float* scal, const uint32_t* colcnt, uint32_t* err, uint32_t lim) {
     extern __shared__ float smem[];
-    const float* __restrict__ A = As.p[blockIdx.z];
-    float* __restrict__ Y = Ys.p[blockIdx.z];
-    amax_part += (size_t)blockIdx.z * AMAX_BLOCKS;
-    Lp += (size_t)blockIdx.z * (r / CB) * (r / CB + 1) / 2 * CB * CB;
-    if (scal != nullptr) scal += (size_t)blockIdx.z * SCAL_STRIDE;
+    const float* __restrict__ A = As.p[z];
+    float* __restrict__ Y = Ys.p[z];
+    amax_part += (size_t)z * AMAX_BLOCKS;
+    Lp += (size_t)z * (r / CB) * (r / CB + 1) / 2 * CB * CB;
+    if (scal != nullptr) scal += (size_t)z * SCAL_STRIDE;
     const int ldsy = r + 4;
     float* sY = smem;                          // [16 RB][r + 4]: finished Y columns (MFMA A operands)
     float* sAcc = sY + 16 * RB * ldsy;         // [TRSM_NW][16][33]: per-wave transpose of the block being finished
     uint32_t* sFlag = reinterpret_cast<uint32_t*>(sAcc + TRSM_NW * 16 * 33);   // [nbc]
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
-    const int row0 = blockIdx.x * 16 * RB, nbc = r / CB;
+    const int row0 = rbi * 16 * RB, nbc = r / CB;
+    uint32_t* sReady = sFlag + nbc;            // WAIT: highest column block known complete, + 1
+    if (WAIT) {
+        colcnt += (size_t)z * CC_STRIDE * CH_MAXROW;
+        err += (size_t)z * BAR_STRIDE;
+    }
     float sc = 1.0f;
     if (PASS1) {
         sc = block_scale512(amax_part);
-        if (blockIdx.x == 0 && tid == 0 && scal != nullptr) scal[0] = sc;
+        if (rbi == 0 && tid == 0 && scal != nullptr) scal[0] = sc;
     }
     for (int k = tid; k < nbc; k += 64 * TRSM_NW) sFlag[k] = 0u;
+    if (WAIT && tid == 0) *sReady = 0u;
     f32x4 acc[RB][Q][2];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
@@ -1331,11 +1388,48 @@ __global__ __launch_bounds__(64 * TRSM_NW) void k_trsm(const MatsIn As, long lda
                     acc[rb][q][cb][v] = x;
                 }
         }
-    TrsmOps<Q> cur, nxt;
-    trsm_fetch<Q>(cur, Lp, nbc, 0, w, lane);
-    float li[2][8];   // Li of this wave's next block to finish (fetched TRSM_NW steps ahead)
-    trsm_fetch_li(li, Lp, nbc, w, lane);
     __syncthreads();   // flags cleared
+    // WAIT: column blocks < known are complete as far as this wave knows
+    int known = 0;
+    bool dead = false;
+    auto need_col = [&](int k) {
+        if (!WAIT || k >= nbc || k < known) return;
+        if (w == 0) {
+            if (lane == 0) {
+                for (int c = known; c <= k; ++c) {
+                    const uint32_t want = 1u + (uint32_t)(nbc - 4 - c > 0 ? nbc - 4 - c : 0);
+                    uint32_t n = 0;
+                    while (!dead && __hip_atomic_load(colcnt + (size_t)c * CC_STRIDE, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT) < want) {
+                        if (++n > lim) {
+                            __hip_atomic_store(err + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            dead = true;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(12);
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            if (lane == 0) __hip_atomic_store(sReady, (uint32_t)(k + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else {
+            uint32_t n = 0;
+            while (__hip_atomic_load(sReady, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)(k + 1)) {
+                if (++n > FLAG_SPIN_LIMIT) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        known = k + 1;
+    };
+    TrsmOps<Q> cur, nxt;
+    float li[2][8];   // Li of this wave's next block to finish
+    need_col(0);
+    trsm_fetch<Q>(cur, Lp, nbc, 0, w, lane);
+    if (WAIT) {
+        if (w == 0) trsm_fetch_li(li, Lp, nbc, 0, lane);
+    } else {
+        trsm_fetch_li(li, Lp, nbc, w, lane);   // fetched TRSM_NW steps ahead
+    }
     const bool full = row0 + 16 * RB <= K;   // every row of the workgroup exists: stores need no bounds check
     // finish block k (owner only): Y_k = acc_k Li_k^T into sY and Y, then raise its flag. The accumulator goes
     // through LDS into the MFMA A layout; both 16-column halves' chains run interleaved before any store.
@@ -1369,7 +1463,7 @@ __global__ __launch_bounds__(64 * TRSM_NW) void k_trsm(const MatsIn As, long lda
             __builtin_amdgcn_wave_barrier();
         }
         if (lane == 0) __hip_atomic_store(&sFlag[k], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        trsm_fetch_li(li, Lp, nbc, k + TRSM_NW, lane);
+        if (!WAIT) trsm_fetch_li(li, Lp, nbc, k + TRSM_NW, lane);
     };
     // acc_j -= Y_k L_jk^T for owned block q
     auto apply = [&](int k, int q) {
@@ -1392,7 +1486,9 @@ __global__ __launch_bounds__(64 * TRSM_NW) void k_trsm(const MatsIn As, long lda
         for (int ow = 0; ow < TRSM_NW; ++ow) {
             const int k = TRSM_NW * qk + ow;
             if (k < nbc) {
+                need_col(k + 1);
                 trsm_fetch<Q>(nxt, Lp, nbc, k + 1, w, lane);
+                if (WAIT && k + 1 < nbc && w == (k + 1) % TRSM_NW) trsm_fetch_li(li, Lp, nbc, k + 1, lane);
                 if (w != ow) {
                     uint32_t n = 0;
                     while (__hip_atomic_load(&sFlag[k], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u) {
@@ -1421,6 +1517,179 @@ __global__ __launch_bounds__(64 * TRSM_NW) void k_trsm(const MatsIn As, long lda
             }
         }
     }
+}
+
+template <bool PASS1, int Q, int RB>
+__global__ __launch_bounds__(64 * TRSM_NW) void k_trsm(const MatsIn As, long lda, int K, int r,
+                                              const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
+                                              long ldz, float eps, const float* __restrict__ Lp, const MatsOut Ys,
+                                              long ldy, float* scal) {
+    trsm_body<PASS1, Q, RB, false>(blockIdx.x, blockIdx.z, As, lda, K, r, amax_part, Z, ldz, eps, Lp, Ys, ldy, scal,
+                                   nullptr, nullptr, 0);
+}
+
+// The solve for tall X in the Cholesky's launch: each wavefront owns one block of 16 rows and all r/32 = NBC column
+// blocks (accumulators in registers) and runs right-looking through the column blocks as the factor's columns become
+// complete: Y_k = acc_k Li_k^T, then acc_j -= Y_k L_jk^T for every j > k. Same arithmetic, element by element, as
+// k_trsm (acc_j starts at a_j, or fmaf(eps, z, s x) on pass 1; its updates by k ascending, each one MFMA chain over
+// the 32 columns of block k; the product with Li_k a chain over m < 16 (c/16 + 1)). No wavefront waits on another but
+// for column readiness (wave 0 polls the counters, the others an LDS word), so after the factor's last column only
+// one block product remains. Workgroup g of a matrix takes row blocks 8g..8g+7; waves past K have no work.
+template <bool PASS1, int NBC>
+__device__ __forceinline__ void trsm_wave_body(const int g, const int z, const MatsIn& As, long lda, int K,
+                                               const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
+                                               long ldz, float eps, const float* __restrict__ Lp, const MatsOut& Ys,
+                                               long ldy, float* scal, const uint32_t* colcnt, uint32_t* err,
+                                               uint32_t lim) {
+    extern __shared__ float smem[];
+    constexpr int r = NBC * CB;
+    const float* __restrict__ A = As.p[z];
+    float* __restrict__ Y = Ys.p[z];
+    amax_part += (size_t)z * AMAX_BLOCKS;
+    Lp += (size_t)z * NBC * (NBC + 1) / 2 * CB * CB;
+    if (scal != nullptr) scal += (size_t)z * SCAL_STRIDE;
+    colcnt += (size_t)z * CC_STRIDE * CH_MAXROW;
+    err += (size_t)z * BAR_STRIDE;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, l16 = lane & 15,
+              lk = lane >> 4;
+    float* sT = smem + w * 16 * 33;                                       // this wave's transpose tile
+    uint32_t* sReady = reinterpret_cast<uint32_t*>(smem + TRSM_NW * 16 * 33);
+    float sc = 1.0f;
+    if (PASS1) {
+        sc = block_scale512(amax_part);
+        if (g == 0 && tid == 0 && scal != nullptr) scal[0] = sc;
+    }
+    if (tid == 0) *sReady = 0u;
+    __syncthreads();
+    const int row0 = (g * TRSM_NW + w) * 16;
+    if (w != 0 && row0 >= K) return;           // wave 0 (always in range) is the poller
+    const bool live = row0 < K;
+    // rows past K read row K-1 (in bounds) and are zeroed
+    int rowc[4];
+    bool rin[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int row = row0 + 4 * lk + v;
+        rin[v] = row < K;
+        rowc[v] = rin[v] ? row : K - 1;
+    }
+    f32x4 acc[NBC][2];
+#pragma unroll
+    for (int j = 0; j < NBC; ++j)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int col = CB * j + 16 * cb + l16;
+                float x = A[(size_t)rowc[v] * lda + col];
+                if (PASS1) x = __builtin_fmaf(eps, Z[(size_t)rowc[v] * ldz + col], sc * x);
+                acc[j][cb][v] = rin[v] ? x : 0.0f;
+            }
+    bool dead = false;
+#pragma unroll
+    for (int k = 0; k < NBC; ++k) {
+        // column block k of the factor complete (Li_k and L(j, k) for every j > k)
+        if (w == 0) {
+            if (lane == 0) {
+                const uint32_t want = 1u + (uint32_t)(NBC - 4 - k > 0 ? NBC - 4 - k : 0);
+                uint32_t n = 0;
+                while (!dead && __hip_atomic_load(colcnt + (size_t)k * CC_STRIDE, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT) < want) {
+                    if (++n > lim) {
+                        __hip_atomic_store(err + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        dead = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(12);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            if (lane == 0) __hip_atomic_store(sReady, (uint32_t)(k + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (!live) continue;
+        } else {
+            uint32_t n = 0;
+            while (__hip_atomic_load(sReady, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)(k + 1)) {
+                if (++n > FLAG_SPIN_LIMIT) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        // the column's operands: Li_k, then L(j, k) for j > k (each 16 floats per lane, packed)
+        float li[2][8];
+        fetch_op(li, Lp, k, k, lane);
+        float lo[NBC][2][8];
+#pragma unroll
+        for (int j = k + 1; j < NBC; ++j) fetch_op(lo[j], Lp, j, k, lane);
+        // Y_k = acc_k Li_k^T: the accumulator through LDS into the MFMA A layout
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sT[(4 * lk + v) * 33 + 16 * cb + l16] = acc[k][cb][v];
+        __builtin_amdgcn_wave_barrier();
+        float av[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) av[kk] = sT[l16 * 33 + 4 * kk + lk];
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 y[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            if (kk < 4) y[0] = mfma(av[kk], li[0][kk], y[0]);
+            y[1] = mfma(av[kk], li[1][kk], y[1]);
+        }
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (rin[v]) Y[(size_t)(row0 + 4 * lk + v) * ldy + CB * k + 16 * cb + l16] = y[cb][v];
+                sT[(4 * lk + v) * 33 + 16 * cb + l16] = y[cb][v];
+            }
+        if (k + 1 < NBC) {
+            // Y_k as the A operand of the later blocks' updates
+            __builtin_amdgcn_wave_barrier();
+            float ya[8];
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) ya[kk] = -sT[l16 * 33 + 4 * kk + lk];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = k + 1; j < NBC; ++j)
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) acc[j][cb] = mfma(ya[kk], lo[j][cb][kk], acc[j][cb]);
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
+// One pass's Cholesky and its solve in one launch: workgroups [0, nz grid) run the Cholesky of matrix
+// b / grid (workgroup b % grid), the rest the solve of matrix b' / nrb (row blocks of 16 RB rows, b' % nrb), the
+// solve following the factor column by column through the counters (the Cholesky's workgroups come first, so they
+// are dispatched first and never wait on a solve workgroup). Pointers address matrix 0 of the launch.
+struct CholArgs {
+    float* A; const double* npart; float* L; float* Li; float* Lp; uint32_t* bar; uint32_t* flags; float* scal;
+    uint32_t* colcnt; float alpha, tau_rel; int r, nnp, nz, grid; uint32_t lim;
+};
+struct SolveArgs {
+    MatsIn A; MatsOut Y; const uint32_t* amax_part; const float* Z; float* scal; long lda, ldz, ldy; float eps;
+    int K, nrb;
+};
+
+// Q > 0: the solve of k_trsm (Q column blocks per wave, RB row blocks of 16 per workgroup); Q = 0: trsm_wave_body
+// with NBC = RB column blocks (eight row blocks per workgroup).
+template <bool PASS1, int Q, int RB>
+__global__ __launch_bounds__(64 * TRSM_NW) void k_chol_solve(const CholArgs c, const SolveArgs t) {
+    const int nchol = c.nz * c.grid;
+    if ((int)blockIdx.x < nchol) {
+        chol_body<false>(blockIdx.x % c.grid, blockIdx.x / c.grid, c.A, c.r, c.npart, c.nnp, c.alpha, c.tau_rel, c.L,
+                         c.Li, c.Lp, c.bar, c.flags, c.scal, nullptr, c.lim, c.colcnt);
+        return;
+    }
+    const int b = blockIdx.x - nchol;
+    if constexpr (Q == 0)
+        trsm_wave_body<PASS1, RB>(b % t.nrb, b / t.nrb, t.A, t.lda, t.K, t.amax_part, t.Z, t.ldz, t.eps, c.Lp, t.Y,
+                                  t.ldy, t.scal, c.colcnt, c.bar, c.lim);
+    else
+        trsm_body<PASS1, Q, RB, true>(b % t.nrb, b / t.nrb, t.A, t.lda, t.K, c.r, t.amax_part, t.Z, t.ldz, t.eps,
+                                      c.Lp, t.Y, t.ldy, t.scal, c.colcnt, c.bar, c.lim);
 }
 
 // Triangular solve with a workgroup of two wavefronts per 16 rows (r = 32 NBC <= 256, tall X): wavefront h takes the
@@ -1712,6 +1981,10 @@ struct spanqr_plan {
     size_t lp_stride = 0;           // floats of packed factor per matrix
     int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0, trsm_rb = 1;
     bool trsm_rows = false;   // solve with a wavefront pair per 16 rows (k_trsm_rows) instead of k_trsm
+    int solve_rb = 0;         // row blocks per solve workgroup in the Cholesky's launch (0: separate launches)
+    int solve_nrb = 0;        // solve workgroups per matrix there
+    int solve_q = 0;          // their column blocks per wave (k_trsm's Q), or 0: one wavefront per row block
+    uint32_t* colcnt = nullptr;   // per matrix: the column counters of the solve in the Cholesky's launch
     size_t bytes = 0;
     char* base = nullptr;
     float *Z = nullptr, *P = nullptr, *G = nullptr, *L = nullptr, *Li = nullptr, *Y0 = nullptr, *Y1 = nullptr;
@@ -1759,7 +2032,7 @@ int check_mat(const spanqr_plan* p, const float* M, long ld, const char* name) {
     return SPANQR_OK;
 }
 
-size_t trsm_lds(int r, int rb) { return (size_t)(16 * rb * (r + 4) + TRSM_NW * 16 * 33 + r / CB) * sizeof(float); }
+size_t trsm_lds(int r, int rb) { return (size_t)(16 * rb * (r + 4) + TRSM_NW * 16 * 33 + r / CB + 1) * sizeof(float); }
 
 MatsIn mats_in(const float* const* X, int n) {
     MatsIn m{};
@@ -1805,7 +2078,7 @@ void launch_gram(const spanqr_plan* p, const MatsIn& A, long lda, int n, bool sc
 
 void launch_reduce(const spanqr_plan* p, int mode, float* out, int n, hipStream_t st) {
     const dim3 grid(16, p->U, n);
-    if (mode == 0) k_reduce<0><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart);
+    if (mode == 0) k_reduce<0><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart, p->colcnt);
     else k_reduce<1><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart);
 }
 
@@ -1851,6 +2124,35 @@ hipError_t trsm_set_lds_plan(int q, int rb, int r) {
     // two row blocks only with two column blocks per wave (r > 256, K >= 16384; taller r <= 256 takes k_trsm_rows)
     if (q == 1) return trsm_set_lds<1, 1>(r);
     return rb == 2 ? trsm_set_lds<2, 2>(r) : trsm_set_lds<2, 1>(r);
+}
+
+// LDS of the Cholesky's launch with its solve: the larger of the two roles' needs (q = 0: the wavefront-per-row-block
+// solve, eight transpose tiles and a word)
+size_t fused_lds(int r, int q, int rb) {
+    const size_t a = chol_lds_bytes(r), b = q ? trsm_lds(r, rb) : (TRSM_NW * 16 * 33 + 1) * sizeof(float);
+    return a > b ? a : b;
+}
+
+template <int Q, int RB>
+hipError_t fused_set_lds_t(int lds) {
+    hipError_t e = hipFuncSetAttribute((const void*)k_chol_solve<true, Q, RB>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       lds);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)k_chol_solve<false, Q, RB>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    return e;
+}
+
+// the instantiations: Q = 1 (r <= 256) with one row block, Q = 2 (r <= 512) with one or two, and the
+// wavefront-per-row-block solve (Q = 0) for r/32 = 2, 4, 6, 8 column blocks
+hipError_t fused_set_lds(int q, int rb, int lds) {
+    if (q == 2) return rb == 2 ? fused_set_lds_t<2, 2>(lds) : fused_set_lds_t<2, 1>(lds);
+    if (q == 1) return fused_set_lds_t<1, 1>(lds);
+    switch (rb) {
+        case 2: return fused_set_lds_t<0, 2>(lds);
+        case 4: return fused_set_lds_t<0, 4>(lds);
+        case 6: return fused_set_lds_t<0, 6>(lds);
+        default: return fused_set_lds_t<0, 8>(lds);
+    }
 }
 
 // the dust the pass-1 solve adds: the plan's own Z [K, r], or a column slice of a wider one (row stride ldz)
@@ -1910,6 +2212,78 @@ void launch_trsm(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, fl
     }
 }
 
+template <bool PASS1, int Q, int RB>
+void launch_fused_t(dim3 grid, size_t lds, hipStream_t st, const CholArgs& c, const SolveArgs& t) {
+    k_chol_solve<PASS1, Q, RB><<<grid, 64 * TRSM_NW, lds, st>>>(c, t);
+}
+
+template <bool PASS1>
+void launch_fused(int q, int rb, dim3 grid, size_t lds, hipStream_t st, const CholArgs& c, const SolveArgs& t) {
+    if (q == 2) {
+        if (rb == 2) launch_fused_t<PASS1, 2, 2>(grid, lds, st, c, t);
+        else launch_fused_t<PASS1, 2, 1>(grid, lds, st, c, t);
+        return;
+    }
+    if (q == 1) {
+        launch_fused_t<PASS1, 1, 1>(grid, lds, st, c, t);
+        return;
+    }
+    switch (rb) {
+        case 2: launch_fused_t<PASS1, 0, 2>(grid, lds, st, c, t); break;
+        case 4: launch_fused_t<PASS1, 0, 4>(grid, lds, st, c, t); break;
+        case 6: launch_fused_t<PASS1, 0, 6>(grid, lds, st, c, t); break;
+        default: launch_fused_t<PASS1, 0, 8>(grid, lds, st, c, t); break;
+    }
+}
+
+// One pass's Cholesky of the n matrices in p->G with the solve Y = A L^-T in the same launches (k_chol_solve), at most
+// chol_bmax matrices per launch. The column counters start at zero (k_reduce clears them before every Cholesky).
+int launch_chol_solve(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t st, int nnp, int n,
+                      const MatsIn& A, long lda, bool pass1, float eps, const Dust& dz, const MatsOut& Y, long ldy) {
+    const size_t r = p->r;
+    const int q = p->solve_q;
+    const size_t lds = fused_lds(p->r, q, p->solve_rb);
+    for (int z0 = 0; z0 < n; z0 += p->chol_bmax) {
+        const int nz = (n - z0 < p->chol_bmax) ? n - z0 : p->chol_bmax;
+        CholArgs c;
+        c.A = p->G + z0 * r * r;
+        c.npart = p->npart + (size_t)z0 * nnp;
+        c.L = p->L + z0 * r * r;
+        c.Li = p->Li + z0 * r * CB;
+        c.Lp = p->Lp + z0 * p->lp_stride;
+        c.bar = p->bar + (size_t)z0 * BAR_STRIDE;
+        c.flags = p->flags + (size_t)z0 * FLAG_STRIDE;
+        c.scal = scal ? scal + (size_t)z0 * SCAL_STRIDE : nullptr;
+        c.colcnt = p->colcnt + (size_t)z0 * CC_STRIDE * CH_MAXROW;
+        c.alpha = alpha;
+        c.tau_rel = tau;
+        c.r = p->r;
+        c.nnp = nnp;
+        c.nz = nz;
+        c.grid = p->chol_grid;
+        c.lim = g_spin_limit;
+        SolveArgs t{};
+        for (int i = 0; i < nz; ++i) {
+            t.A.p[i] = A.p[z0 + i];
+            t.Y.p[i] = Y.p[z0 + i];
+        }
+        t.amax_part = p->amax_part + (size_t)z0 * AMAX_BLOCKS;
+        t.Z = dz.z;
+        t.scal = p->scal + (size_t)z0 * SCAL_STRIDE;
+        t.lda = lda;
+        t.ldz = dz.ldz;
+        t.ldy = ldy;
+        t.eps = eps;
+        t.K = p->K;
+        t.nrb = p->solve_nrb;
+        const dim3 grid(nz * (p->chol_grid + p->solve_nrb));
+        if (pass1) launch_fused<true>(q, q ? p->solve_rb : p->r / CB, grid, lds, st, c, t);
+        else launch_fused<false>(q, q ? p->solve_rb : p->r / CB, grid, lds, st, c, t);
+        HIPCHK(hipGetLastError());
+    }
+    return SPANQR_OK;
+}
+
 void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsOut& Out, long ldo, int n,
                     hipStream_t st) {
     // 64-column steps: half the load-then-multiply steps of each workgroup's chain (1-1.5 us faster at 17408x256
@@ -1945,10 +2319,17 @@ int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut
         if ((rc = mark())) return rc;
         launch_reduce(p, 0, p->G, n, st);
         if ((rc = mark())) return rc;
-        if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U, n))) return rc;
-        if ((rc = mark())) return rc;
-        launch_trsm(p, *in, ldin, pass == 0, eps, dz, bout[cur], p->r, n, st);
-        if ((rc = mark())) return rc;
+        if (p->solve_rb > 0) {
+            if ((rc = launch_chol_solve(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U, n, *in, ldin, pass == 0,
+                                        eps, dz, bout[cur], p->r)))
+                return rc;
+            if ((rc = mark())) return rc;
+        } else {
+            if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U, n))) return rc;
+            if ((rc = mark())) return rc;
+            launch_trsm(p, *in, ldin, pass == 0, eps, dz, bout[cur], p->r, n, st);
+            if ((rc = mark())) return rc;
+        }
         in = &bin[cur];
         ldin = p->r;
         cur ^= 1;
@@ -2066,6 +2447,35 @@ int plan_device_setup(spanqr_plan* p, int device) {
     p->chol_bmax = (occ * cus * 3 / 4) / p->chol_grid;
     if (p->chol_bmax < 1) p->chol_bmax = 1;
     if (p->chol_bmax > p->batch) p->chol_bmax = p->batch;
+    // The solve in the Cholesky's launch: enough rows per workgroup that one matrix's solve workgroups are resident
+    // beside its Cholesky (one workgroup per CU: the launch's LDS is the Cholesky's); otherwise separate launches.
+    // Up to one row block per CU: k_trsm's structure (eight wavefronts share a row block's column blocks); taller X at
+    // r <= 256: one wavefront per row block (eight per workgroup); taller X at r > 256: k_trsm with two row blocks.
+    p->solve_rb = 0;
+    p->solve_nrb = 0;
+    p->solve_q = 0;
+    {
+        int maxsh = 0;
+        HIPCHK(hipDeviceGetAttribute(&maxsh, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+        const int avail = cus - p->chol_grid;
+        const int rowblocks = (p->K + 15) / 16;
+        int q = (r / CB + TRSM_NW - 1) / TRSM_NW, rb = 1, nwg = rowblocks;
+        if (rowblocks > avail) {
+            if (r <= 256) {
+                q = 0;
+                nwg = (rowblocks + TRSM_NW - 1) / TRSM_NW;
+            } else {
+                rb = 2;
+                nwg = (rowblocks + 1) / 2;
+            }
+        }
+        const size_t lds = fused_lds(r, q, rb);
+        if (nwg <= avail && lds <= (size_t)maxsh && fused_set_lds(q, q ? rb : r / CB, (int)lds) == hipSuccess) {
+            p->solve_q = q;
+            p->solve_rb = rb;
+            p->solve_nrb = nwg;
+        }
+    }
     return SPANQR_OK;
 }
 
@@ -2090,10 +2500,12 @@ size_t plan_layout(spanqr_plan* p, char* base) {
         al256(B * BAR_STRIDE * sizeof(uint32_t)),               // bar
         al256(2 * (4 * (512 / CB) + 2) * sizeof(uint64_t)),     // stamps
         al256(B * FLAG_STRIDE * sizeof(uint32_t)),              // flags
+        al256(B * CC_STRIDE * CH_MAXROW * sizeof(uint32_t)),    // colcnt
     };
     void** ptrs[] = {(void**)&p->Z, (void**)&p->P, (void**)&p->G, (void**)&p->L, (void**)&p->Li, (void**)&p->Lp,
                      (void**)&p->Y0, (void**)&p->Y1, (void**)&p->scal, (void**)&p->chscal, (void**)&p->npart,
-                     (void**)&p->amax_part, (void**)&p->bar, (void**)&p->stamps, (void**)&p->flags};
+                     (void**)&p->amax_part, (void**)&p->bar, (void**)&p->stamps, (void**)&p->flags,
+                     (void**)&p->colcnt};
     size_t off = 0;
     for (size_t i = 0; i < sizeof(sz) / sizeof(sz[0]); ++i) {
         if (base) *ptrs[i] = base + off;
@@ -2298,6 +2710,10 @@ long spanqr_plan_query(const spanqr_plan* p, int what) {
         case SPANQR_Q_BATCH: return p->batch;
         case SPANQR_Q_CHOL_BATCH: return p->blk ? p->blk->chol_bmax : p->chol_bmax;
         case SPANQR_Q_BLOCKS: return p->nblk;
+        case SPANQR_Q_SOLVE_ROWS: {
+            const spanqr_plan* q = p->blk ? p->blk : p;
+            return q->solve_rb == 0 ? 0 : (q->solve_q == 0 ? 16L * TRSM_NW : 16L * q->solve_rb);
+        }
         default: return -1;
     }
 }
@@ -2363,7 +2779,9 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
     if (!p || !avg_ms) return fail(SPANQR_EINVAL, "null argument");
     if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
     if (reps < 1 || reps > 100000) return fail(SPANQR_EINVAL, "reps = %d out of range", reps);
-    if (which < SPANQR_K_AMAX || which > SPANQR_K_NS_APPLY) return fail(SPANQR_EINVAL, "unknown kernel %d", which);
+    if (which < SPANQR_K_AMAX || which > SPANQR_K_CHOL_SOLVE) return fail(SPANQR_EINVAL, "unknown kernel %d", which);
+    if ((which == SPANQR_K_CHOL_SOLVE_PASS1 || which == SPANQR_K_CHOL_SOLVE) && p->solve_rb == 0)
+        return fail(SPANQR_EINVAL, "this plan runs the Cholesky and the solve in separate launches");
     DeviceGuard dg(p->device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
     hipStream_t st = (hipStream_t)stream;
@@ -2386,6 +2804,25 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
         return SPANQR_OK;
     };
     int rc;
+    if (which == SPANQR_K_CHOL_SOLVE_PASS1 || which == SPANQR_K_CHOL_SOLVE) {
+        // each launch needs its column counters at zero: cleared by a small kernel outside the timed pair of events
+        const bool p1 = which == SPANQR_K_CHOL_SOLVE_PASS1;
+        double total = 0.0;
+        for (int i = 0; i <= reps; ++i) {
+            k_clear_words<<<1, 64, 0, st>>>(p->colcnt, CH_MAXROW, CC_STRIDE);
+            HIPCHK(hipEventRecord(p->ev[0], st));
+            if ((rc = launch_chol_solve(p, 1e-7f, 1e-8f, p->scal + 1, st, 16 * p->U, 1, y0, r, p1, p1 ? 5e-7f : 0.0f,
+                                        Dust{p->Z, r}, y1, r)))
+                return rc;
+            HIPCHK(hipEventRecord(p->ev[1], st));
+            HIPCHK(hipEventSynchronize(p->ev[1]));
+            float ms = 0.0f;
+            HIPCHK(hipEventElapsedTime(&ms, p->ev[0], p->ev[1]));
+            if (i > 0) total += ms;   // the first launch is untimed
+        }
+        *avg_ms = (float)(total / reps);
+        return SPANQR_OK;
+    }
     if ((rc = launch())) return rc;
     HIPCHK(hipEventRecord(p->ev[0], st));
     for (int i = 0; i < reps; ++i)

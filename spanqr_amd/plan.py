@@ -46,6 +46,11 @@ class Plan:
         return self.query(_lib.Q_CHOL_GRID)
 
     @property
+    def solve_rows(self):
+        """rows per solve workgroup in the Cholesky's launch (0: the solve runs as its own launch)"""
+        return self.query(_lib.Q_SOLVE_ROWS)
+
+    @property
     def chol_batch(self):
         return self.query(_lib.Q_CHOL_BATCH)
 

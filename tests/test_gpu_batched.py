@@ -114,3 +114,14 @@ def test_batched_layer_set(cuda):
         assert_bits(Q, orth(X.to(cuda)), f"layer {i} ({K}x{r}) vs its single call")
         assert_bits(Q, oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows), f"layer {i} ({K}x{r}) vs oracle")
         gate(X, Q, f"layer {i} ({K}x{r})")
+
+
+def test_batched_tall_solve(cuda):
+    """a batch whose solves run one wavefront per 16 rows in the Cholesky's launches"""
+    K, r, n = 5000, 128, 3
+    g = torch.Generator().manual_seed(9)
+    Xs = [torch.randn(K, r, generator=g) for _ in range(n)]
+    print(f"batched {n} x {K}x{r}", flush=True)
+    Qs = kcholqr_f_many([X.to(cuda) for X in Xs])
+    for i in range(n):
+        assert_bits(Qs[i], oracle.orth(Xs[i].numpy(), get_plan(K, r, cuda, n).split_rows), f"element {i} vs oracle")

@@ -131,3 +131,27 @@ def test_keyword_arguments(cuda):
     for kw in (dict(eps=1e-6), dict(alpha=1e-6), dict(tau=1e-7), dict(ns=1), dict(ns=0), dict(ns=3)):
         Q = kcholqr_f(X.to(cuda), **kw)
         assert_bits(Q, oracle.orth(X.numpy(), KS, **kw), f"kcholqr_f({kw})")
+
+
+@pytest.mark.parametrize("K,r", [(768, 512), (2048, 512), (1024, 256), (3584, 256), (6144, 256), (17408, 256)])
+def test_solve_runs_in_the_cholesky_launch(cuda, K, r):
+    """at the benchmark shapes each pass's solve runs in its Cholesky's launch, and the call stays bit-exact"""
+    plan = get_plan(K, r, cuda)
+    assert plan.solve_rows > 0, f"{K}x{r}: the solve is a separate launch"
+    X = gen.bench_input(K, r, seed=3)
+    print(f"fused solve {K}x{r}: {plan.solve_rows} rows per solve workgroup", flush=True)
+    assert_bits(kcholqr_f(X.to(cuda)), oracle.orth(X.numpy(), plan.split_rows), f"{K}x{r} vs oracle")
+
+
+@pytest.mark.parametrize("K,r", [(5000, 64), (4500, 128), (4111, 192), (4100, 256), (9217, 256)])
+def test_tall_solve_in_cholesky_launch(cuda, K, r):
+    """X taller than one row block per CU: the solve in the Cholesky's launch runs one wavefront per 16 rows, at every
+    column-block count (r/32 = 2, 4, 6, 8) and with a ragged last row block"""
+    plan = get_plan(K, r, cuda)
+    assert plan.solve_rows == 128, f"{K}x{r}: expected the wavefront-per-row-block solve, got {plan.solve_rows}"
+    g = torch.Generator().manual_seed(K + r)
+    X = torch.randn(K, r, generator=g) * torch.logspace(0, -3, r)
+    print(f"tall solve {K}x{r}", flush=True)
+    Q = kcholqr_f(X.to(cuda))
+    assert_bits(Q, oracle.orth(X.numpy(), plan.split_rows), f"{K}x{r} vs oracle")
+    gate(X, Q, f"{K}x{r}")
