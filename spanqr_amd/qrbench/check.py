@@ -1,93 +1,99 @@
-"""Accuracy / robustness check of orth(X) on the MI355X against the reference's requirements (qrbench/check.py).
+"""Accuracy and robustness check of orth(X) on the GPU, case by case, against the requirements in metrics.py.
 
-    python -m spanqr_amd.qrbench.check                                   # all cases, acceptance shapes
-    python -m spanqr_amd.qrbench.check --shapes 768x512 --cases mixed ttf
-    python -m spanqr_amd.qrbench.check --real dumps/ --real-only          # matrices dumped from training
+    python -m spanqr_amd.qrbench.check                                    # acceptance + extra cases, bench shapes
+    python -m spanqr_amd.qrbench.check --shapes 768x512 --cases mixed ttf --target
+    python -m spanqr_amd.qrbench.check --real dumps/ --real-only          # matrices dumped from a training run
 
-Every case also runs through Householder QR (torch.linalg.qr, the span reference: orth must be within SPAN_RATIO of
-it). Per case: run_checked (warm-up, a call under torch's sync-debug "error" mode, a determinism call, input left
-intact) and the hard requirements of qrbench/metrics.py; --target also applies this build's tighter orthogonality
-gate (2e-7). The exit status is 0 when every acceptance case passes.
+For every matrix the fp64 reference is built once; every method named with -m (orth: this library; householder:
+torch.linalg.qr) is run through metrics.check_call, and Householder's span error on the same matrix sets the span
+bar. --target uses this project's 2e-7 orthogonality bar instead of the reference's 1e-6. Exit status 0 when every
+acceptance ("hard") case of every method passes. The cases and the requirements are the reference's (qrbench/gen.py,
+qrbench/metrics.py); this command line is this project's own.
 """
 import argparse
 import json
 import sys
 import time
+from dataclasses import asdict, dataclass, field
 
 import torch
 
 from . import gen, metrics
 
-METHODS = {"orth": None, "householder": metrics.householder}
+
+def _orth():
+    from spanqr_amd import orth     # the native path; raises if the library is missing
+    return orth
 
 
-def _method(name):
-    if name == "orth":
-        from spanqr_amd import orth     # the native path; raises if the library is missing
-        return orth
-    return METHODS[name]
+METHODS = {"orth": _orth, "householder": lambda: metrics.householder}
 
 
 def parse_shapes(spec):
-    """bench | all | 110m | 0.8b | 27b | KxR[,KxR...] (qrbench/check.py:19-26)"""
-    if spec == "bench":
-        return gen.BENCH_SHAPES
-    if spec == "all":
-        return gen.ALL_SHAPES
-    if spec in gen.SHAPES:
-        return gen.SHAPES[spec]
-    return [tuple(int(v) for v in s.split("x")) for s in spec.split(",")]
+    """shape list from: bench | all | a model name (110m, 0.8b, 27b) | KxR[,KxR...]"""
+    named = {"bench": gen.BENCH_SHAPES, "all": gen.ALL_SHAPES, **gen.SHAPES}
+    if spec in named:
+        return list(named[spec])
+    return [tuple(int(v) for v in item.split("x")) for item in spec.split(",")]
 
 
-def run(method_names, shapes, case_names=None, seeds=(0,), real=None, extra=True, check_sync=True, target=False,
-        device="cuda", verbose=True):
-    """rows of results, one per (method, shape, case) -- qrbench/check.py:29-48"""
-    fns = {n: _method(n) for n in method_names}
-    rows = []
-    for K, r in shapes:
-        cases = [] if case_names == ["__none__"] else list(gen.make_cases(K, r, case_names, seeds, include_extra=extra))
-        if real:
-            cases += list(gen.real_cases(real, (K, r)))
-        for case in cases:
-            X = case.X.to(device)
-            ref = metrics.reference(case.X)
-            hres, _ = metrics.run_checked(metrics.householder, X, ref, check_sync=False)
-            cond = float(ref[0][0] / ref[0][-1]) if ref[0][-1] > 0 else float("inf")
-            for n, fn in fns.items():
-                res, _ = metrics.run_checked(fn, X, ref, check_sync=check_sync)
-                tol = metrics.ORTH_TOL_TARGET if target else metrics.ORTH_TOL
-                fails = res.failures(span_ref=hres.span_n, orth_tol=tol)
-                row = dict(method=n, K=K, r=r, case=case.name, hard=case.hard, cond=cond, hh_span_n=hres.span_n,
-                           fails=fails, **res.as_dict())
-                rows.append(row)
-                if verbose:
-                    _print_row(row)
-    return rows
+@dataclass
+class Record:
+    """one (method, matrix) outcome"""
+    method: str
+    K: int
+    r: int
+    case: str
+    hard: bool
+    cond: float
+    hh_span_n: float
+    fails: list = field(default_factory=list)
+    report: dict = field(default_factory=dict)
+
+    def line(self):
+        tag = "ok  " if not self.fails else ("FAIL" if self.hard else "fail")
+        rep = self.report
+        return (f"{tag} {self.method:<12} {self.K:>5}x{self.r:<4} {self.case:<28} cond {self.cond:8.1e} "
+                f"orth {rep.get('orth', float('nan')):8.1e} span_n {rep.get('span_n', 0.0):7.3g} "
+                f"(hh {self.hh_span_n:6.3g})  {'; '.join(self.fails)}")
 
 
-def _fmt(v, f="{:.1e}"):
-    return "-" if v is None or v != v else f.format(v)
+def cases_for(K, r, names, seeds, real, extra):
+    """the synthetic cases (none when names == []) and, with real, the dumped matrices of this shape"""
+    if names != []:
+        yield from gen.make_cases(K, r, names, seeds, include_extra=extra)
+    if real:
+        yield from gen.real_cases(real, (K, r))
 
 
-def _print_row(w):
-    status = "ok  " if not w["fails"] else ("FAIL" if w["hard"] else "fail")
-    print(f"{status} {w['method']:<12} {w['K']:>5}x{w['r']:<4} {w['case']:<28} cond {_fmt(w['cond'], '{:.0e}'):>6}"
-          f"  orth {_fmt(w['orth']):>7}  span_n {_fmt(w['span_n'], '{:.3g}'):>7} (hh {_fmt(w['hh_span_n'], '{:.3g}'):>6})"
-          f"  {'; '.join(w['fails'])}", flush=True)
+def check_case(case, fns, device, orth_tol, check_sync):
+    """Records of every method on one case"""
+    K, r = case.X.shape
+    X = case.X.to(device)
+    ref = metrics.reference(case.X)
+    hh, _ = metrics.check_call(metrics.householder, X, ref, check_sync=False)
+    out = []
+    for name, fn in fns.items():
+        rep, _ = metrics.check_call(fn, X, ref, check_sync=check_sync)
+        out.append(Record(name, K, r, case.name, case.hard, ref.cond, hh.span_n,
+                          rep.failures(span_ref=hh.span_n, orth_tol=orth_tol), rep.as_dict()))
+    return out
 
 
-def summarize(rows):
-    print("\nsummary (hard = acceptance cases, extra = robustness cases):")
-    for n in dict.fromkeys(w["method"] for w in rows):
-        mine = [w for w in rows if w["method"] == n]
-        hard = [w for w in mine if w["hard"]]
-        extra = [w for w in mine if not w["hard"]]
-        worst = max((w["orth"] for w in mine if w["orth"] == w["orth"]), default=float("nan"))
-        print(f"  {n:<12} hard {sum(not w['fails'] for w in hard)}/{len(hard)}  "
-              f"extra {sum(not w['fails'] for w in extra)}/{len(extra)}  worst orth {_fmt(worst)}")
-        for w in hard:
-            if w["fails"]:
-                print(f"      FAIL {w['K']}x{w['r']} {w['case']}: {'; '.join(w['fails'])}")
+def tally(records):
+    """per method: passed/total acceptance cases, passed/total extra cases, worst orth, failing acceptance cases"""
+    out = {}
+    for rec in records:
+        t = out.setdefault(rec.method, {"hard": [0, 0], "extra": [0, 0], "worst_orth": 0.0, "hard_failures": []})
+        kind = t["hard"] if rec.hard else t["extra"]
+        kind[0] += not rec.fails
+        kind[1] += 1
+        orth = rec.report.get("orth", float("nan"))
+        if orth == orth:
+            t["worst_orth"] = max(t["worst_orth"], orth)
+        if rec.hard and rec.fails:
+            t["hard_failures"].append(f"{rec.K}x{rec.r} {rec.case}: {'; '.join(rec.fails)}")
+    return out
 
 
 def main(argv=None):
@@ -100,19 +106,31 @@ def main(argv=None):
     p.add_argument("--real-only", action="store_true", help="only the dumped matrices (with --real)")
     p.add_argument("--no-extra", action="store_true", help="acceptance cases only")
     p.add_argument("--no-sync-check", action="store_true")
-    p.add_argument("--target", action="store_true", help="orthogonality gate 2e-7 instead of the reference's 1e-6")
-    p.add_argument("--json", help="write all rows to this file")
+    p.add_argument("--target", action="store_true", help="orthogonality bar 2e-7 instead of the reference's 1e-6")
+    p.add_argument("--json", help="write every record to this file")
     a = p.parse_args(argv)
     t0 = time.time()
-    cases = ["__none__"] if a.real_only else a.cases
-    rows = run(a.methods, parse_shapes(a.shapes), cases, tuple(range(a.seeds)), a.real, extra=not a.no_extra,
-               check_sync=not a.no_sync_check, target=a.target)
-    summarize(rows)
+    fns = {name: METHODS[name]() for name in a.methods}
+    tol = metrics.ORTH_TOL_TARGET if a.target else metrics.ORTH_TOL
+    names = [] if a.real_only else a.cases
+    records = []
+    for K, r in parse_shapes(a.shapes):
+        for case in cases_for(K, r, names, tuple(range(a.seeds)), a.real, not a.no_extra):
+            for rec in check_case(case, fns, "cuda", tol, not a.no_sync_check):
+                records.append(rec)
+                print(rec.line(), flush=True)
+    summary = tally(records)
+    for name, t in summary.items():
+        print(f"{name}: acceptance {t['hard'][0]}/{t['hard'][1]}, extra {t['extra'][0]}/{t['extra'][1]}, "
+              f"worst orth {t['worst_orth']:.2e}")
+        for f in t["hard_failures"]:
+            print(f"    FAIL {f}")
     print(f"({time.time() - t0:.0f} s, {torch.cuda.get_device_name()})")
     if a.json:
-        with open(a.json, "w") as f:
-            json.dump(dict(device=torch.cuda.get_device_name(), rows=rows), f, indent=1)
-    return 0 if all(not w["fails"] for w in rows if w["hard"]) else 1
+        with open(a.json, "w") as fh:
+            json.dump({"device": torch.cuda.get_device_name(), "records": [asdict(r) for r in records],
+                       "summary": summary}, fh, indent=1)
+    return 0 if all(t["hard"][0] == t["hard"][1] for t in summary.values()) else 1
 
 
 if __name__ == "__main__":

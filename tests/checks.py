@@ -18,7 +18,7 @@ def assert_bits(a, b, what):
 def gate(X, Q, what):
     """the spec's robustness gates: no collapsed columns, max|Q^T Q - I| <= 2e-7, the reference's span rule"""
     ref = metrics.reference(X)
-    res = metrics.evaluate(Q, X.to(Q.device), ref)
-    hh = metrics.evaluate(metrics.householder(X.cpu()), X.cpu(), ref)
+    res = metrics.assess(Q, X.to(Q.device), ref)
+    hh = metrics.assess(metrics.householder(X.cpu()), X.cpu(), ref)
     fails = res.failures(span_ref=hh.span_n, orth_tol=metrics.ORTH_TOL_TARGET)
     assert not fails, f"{what}: {fails} (orth {res.orth:.3e}, span_n {res.span_n:.2f})"

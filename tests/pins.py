@@ -373,8 +373,8 @@ def check_orth_small():
         c = next(gen.make_cases(K, r, [name], (0,)))
         Q = oracle.orth(c.X.numpy(), 64)
         ref = metrics.reference(c.X)
-        res = metrics.evaluate(torch.from_numpy(Q), c.X, ref)
-        hh = metrics.evaluate(metrics.householder(c.X), c.X, ref)
+        res = metrics.assess(torch.from_numpy(Q), c.X, ref)
+        hh = metrics.assess(metrics.householder(c.X), c.X, ref)
         fails = res.failures(span_ref=hh.span_n, orth_tol=metrics.ORTH_TOL_TARGET)
         if fails:
             f.append(f"orth {name}: {fails}")

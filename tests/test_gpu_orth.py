@@ -32,7 +32,7 @@ def test_adversarial(cuda, adversarial_inputs, K, r, name):
     print(f"adversarial {K}x{r} {name}", flush=True)
     X = adversarial_inputs[(K, r)][name]
     Xd = X.to(cuda)
-    res, Q = metrics.run_checked(orth, Xd, metrics.reference(X))
+    res, Q = metrics.check_call(orth, Xd, metrics.reference(X))
     assert not res.error, res.error
     assert res.deterministic and res.input_intact and res.sync_free
     assert stages.scalars(K, r, cuda)[7].item() == 0, "grid barrier timed out"

@@ -42,7 +42,7 @@ def _check_shape(K, r, rows):
     for c in _cases(K, r):
         want = rows[f"{K}x{r}/{c.name}"]
         ref = metrics.reference(c.X)
-        cond = metrics.cond_of(ref)
+        cond = ref.cond
         saved = [want[d]["cond"] for d in DEVS]
         if all(math.isfinite(v) for v in saved) and abs(saved[0] - saved[1]) < 1e-6 * saved[0]:
             # below ~1e7 the smallest singular value sits far above the fp32 rounding level of X, so cond is fixed
@@ -53,7 +53,7 @@ def _check_shape(K, r, rows):
             assert err < tol, f"{c.name}: cond {cond!r} vs saved {saved}"
         Q = oracle.orth(c.X.numpy(), KS)
         assert np.array_equal(Q, oracle.orth(c.X.numpy(), KS)), f"{c.name}: not deterministic"
-        res = metrics.evaluate(torch.from_numpy(Q), c.X, ref)
+        res = metrics.assess(torch.from_numpy(Q), c.X, ref)
         ref_orth = max(want[d]["orth"] for d in DEVS)
         ref_span = max(want[d]["span_n"] for d in DEVS)
         ref_hh = max(want[d]["hh_span_n"] for d in DEVS)
