@@ -1984,6 +1984,7 @@ struct spanqr_plan {
     int solve_rb = 0;         // row blocks per solve workgroup in the Cholesky's launch (0: separate launches)
     int solve_nrb = 0;        // solve workgroups per matrix there
     int solve_q = 0;          // their column blocks per wave (k_trsm's Q), or 0: one wavefront per row block
+    int cus = 0;              // the device's compute units
     uint32_t* colcnt = nullptr;   // per matrix: the column counters of the solve in the Cholesky's launch
     size_t bytes = 0;
     char* base = nullptr;
@@ -2319,7 +2320,9 @@ int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut
         if ((rc = mark())) return rc;
         launch_reduce(p, 0, p->G, n, st);
         if ((rc = mark())) return rc;
-        if (p->solve_rb > 0) {
+        // the solve in the Cholesky's launch when every workgroup of the launch fits on the device at once (one per
+        // CU); a larger batch runs them as separate launches, where the solve keeps its own, smaller LDS
+        if (p->solve_rb > 0 && n * (p->chol_grid + p->solve_nrb) <= p->cus) {
             if ((rc = launch_chol_solve(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U, n, *in, ldin, pass == 0,
                                         eps, dz, bout[cur], p->r)))
                 return rc;
@@ -2440,6 +2443,7 @@ int plan_device_setup(spanqr_plan* p, int device) {
     }
     HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol<true>, 512, chol_lds_bytes(r)));
     HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+    p->cus = cus;
     if (occ * cus < p->chol_grid)
         return fail(SPANQR_EHIP, "the Cholesky needs %d co-resident workgroups, device holds %d", p->chol_grid, occ * cus);
     // a batch's launch takes at most three quarters of the device's resident capacity: the flag waits need every
