@@ -6,7 +6,7 @@ Workload (the quoted target shapes): one orth() call at 768x512 (the 110M attent
 N = 768, U's singular values log-uniform over [1, 1e4], u unit-RMS Gaussian, seed 0) and one at 17408x256 (the 27B
 down_proj layer, same generator with N = 5120), generated on the CPU and resident on the GPU before timing. Each
 input has its own captured hipGraph; one step replays both. `value` = timed wall time / (steps x 2) in microseconds
-per call (lower is better); the per-shape figures are in `targets` at the end of the line.
+per call (lower is better); the per-shape figures and their targets are in `targets`, right after `orth_max`.
 
 Per headline shape, as the reference's qrbench/bench.py:28-53 measures: "thr" (median of 5 bursts of 20
 back-to-back replays), "lat" (one replay between two events after a synchronisation, median of 20) and "lat_flush"
@@ -383,10 +383,11 @@ def main(argv=None):
     targets = {name: {"us_per_call": head[name]["thr_us"], "target_us": TARGET_US[name],
                       "met": head[name]["thr_us"] <= TARGET_US[name], "lat_us": head[name]["lat_us"],
                       "orth": head[name]["orth"], "chol_us": head[name]["chol_us"]} for name in head}
+    # the per-shape targets right after the headline fields, so that a reader of the line's first part sees them
     line.update({
-        "roofline": roofline, "cpu_baseline": cpu, "headline": head,
+        "targets": targets, "roofline": roofline, "cpu_baseline": cpu, "headline": head,
         "shapes_0.8b_thr_us": w08, "shapes": others, "blocked_shapes": blocked, "batched_layers": batched,
-        "device": torch.cuda.get_device_name(dev), "targets": targets,
+        "device": torch.cuda.get_device_name(dev),
     })
     if a.detail:
         with open(a.detail, "w") as f:

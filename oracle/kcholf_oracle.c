@@ -255,8 +255,9 @@ float spqo_shift(float* G, int r, float nrm, float alpha, float tau_rel) {
 
 static inline int mend(int b) { return 16 * (b / 16 + 1); }
 
-/* reciprocal square root used for the pivots (the reference uses CUDA rsqrtf, chol.cu:45): bit-trick start
- * 0x5f375a86 - (bits >> 1), then three Newton steps y <- y * (1.5 - (0.5x * y) * y), the bracket as one fmaf. */
+/* reciprocal square root used for the pivots (the reference uses CUDA rsqrtf, chol.cu:45): the published fast
+ * inverse square root start 0x5f375a86 - (bits >> 1) (C. Lomont, "Fast Inverse Square Root", 2003), then three
+ * Newton steps y <- y * (1.5 - (0.5x * y) * y), the bracket as one fmaf. */
 float spqo_rsqrt(float x) {
     float y = u2f(0x5f375a86u - (f2u(x) >> 1));
     const float h = 0.5f * x;
@@ -575,8 +576,9 @@ void spqo_borth(const float* X, long ldx, int K, int r, float eps, float alpha, 
 /* spqo_chol in double -- 32-wide diagonal tiles, pivots fmax(D_cc, tau) (NaN -> tau), tile inverses by forward */
 /* substitution, panels A Li^T over m < mend(b), trailing updates as fma chains over the block's 32 columns from */
 /* A -- plus fp32 copies of L and Li (chol.cu:175-176, 215, 255: (float) of each fp64 value). The reciprocal     */
-/* square root (CUDA's rsqrt in the reference) is this project's own: start 0x5FE6EB50C7B537A9 - (bits >> 1),    */
-/* then four Newton steps y <- y * (1.5 - (0.5x * y) * y), the bracket as one fma.                              */
+/* square root (CUDA's rsqrt in the reference) is this project's own: start 0x5FE6EB50C7B537A9 - (bits >> 1)     */
+/* (M. Robertson's published 64-bit constant, "A Brief History of InvSqrt", 2012), then four Newton steps        */
+/* y <- y * (1.5 - (0.5x * y) * y), the bracket as one fma.                                                      */
 /* ------------------------------------------------------------------------------------------------------------ */
 static inline uint64_t d2u(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
 static inline double u2d(uint64_t u) { double d; memcpy(&d, &u, 8); return d; }

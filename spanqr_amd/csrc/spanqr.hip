@@ -127,7 +127,8 @@ __device__ float block_scale128(const uint32_t* __restrict__ part) {
     return pow2_scale_bits(t);
 }
 
-// Pivot reciprocal square root (the reference uses CUDA rsqrtf, chol.cu:45): bit-trick start and three Newton steps
+// Pivot reciprocal square root (the reference uses CUDA rsqrtf, chol.cu:45): the published fast inverse square root
+// start 0x5f375a86 - (bits >> 1) (C. Lomont, "Fast Inverse Square Root", 2003) and three Newton steps
 // y <- y * (1.5 - (0.5x * y) * y), each bracket one fma, so the result is a fixed function of x.
 __device__ __forceinline__ float rsqrt_sw(float x) {
     float y = __uint_as_float(0x5f375a86u - (__float_as_uint(x) >> 1));
@@ -3113,8 +3114,9 @@ __device__ __forceinline__ double readlane_d(double v, int l) {
     return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-// reciprocal square root for the fp64 pivots (CUDA's rsqrt in the reference): start 0x5FE6EB50C7B537A9 - (bits >> 1),
-// then four Newton steps y <- y * (1.5 - (0.5x * y) * y), the bracket as one fma
+// reciprocal square root for the fp64 pivots (CUDA's rsqrt in the reference): start 0x5FE6EB50C7B537A9 - (bits >> 1)
+// (the 64-bit constant published by M. Robertson, "A Brief History of InvSqrt", 2012), then four Newton steps
+// y <- y * (1.5 - (0.5x * y) * y), the bracket as one fma
 __device__ __forceinline__ double rsqrt64_sw(double x) {
 #pragma clang fp contract(off)
     double y = __longlong_as_double((long long)(0x5FE6EB50C7B537A9ull - ((uint64_t)__double_as_longlong(x) >> 1)));
