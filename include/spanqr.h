@@ -8,7 +8,7 @@
  * Conventions
  *   - Matrices are row-major fp32 in device memory; X and Q need 16-byte alignment and a leading dimension that is a
  *     multiple of 4 (the contiguous [K, r] case always qualifies). X is never written.
- *   - r must be a multiple of 64 with 64 <= r <= 512, or a multiple of 256 with 512 < r <= 4096 (the column-blocked
+ *   - r must be a multiple of 32 with 32 <= r <= 512, or a multiple of 256 with 512 < r <= 4096 (the column-blocked
  *     path: block Gram-Schmidt over 256-column blocks, as the reference's orth does above 512 columns); K >= r.
  *   - Every entry point that takes a stream only enqueues work on it: no host synchronisation, no allocation, so a
  *     call can be captured into a hipGraph. Plan creation allocates and synchronises.
@@ -94,7 +94,7 @@ int spanqr_orth_batched_f32(spanqr_plan* plan, int n, const float* const* X, lon
  * memory (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc). Q = orth(X) for
  * X [K, r] on the current device, bit-identical to spanqr_orth_f32 on a plan for (K, r), but without a plan: the
  * workspace lives in a fixed 64 MiB device array of the library (each GPU the library runs on holds its own copy
- * until the process ends), and nothing is allocated or synchronised. Limits: r a multiple of 64 in [64, 512] (no
+ * until the process ends), and nothing is allocated or synchronised. Limits: r a multiple of 32 in [32, 512] (no
  * column-blocked path), K >= r, and the workspace of (K, r) within 64 MiB (17408 x 256 fits; 32768 x 512 does
  * not): larger shapes return SPANQR_EINVAL. The dust is generated on the device and kept with a shape tag, so a call
  * after one of another shape regenerates it (a few extra kernels). Every call on one GPU shares the array, which

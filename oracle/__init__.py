@@ -132,7 +132,7 @@ def gram(A, KS, kahan, s=None):
     """(G [r, r], norm partials [16 U] fp64); s: scale on load (None: no scale)"""
     A = _c32(A)
     K, r = A.shape
-    nt = r // TB
+    nt = (r + TB - 1) // TB
     G = np.empty((r, r), np.float32)
     npart = np.empty(16 * nt * (nt + 1) // 2, np.float64)
     lib().spqo_gram(A, r, K, r, 1.0 if s is None else float(s), s is not None, int(bool(kahan)), KS, G,

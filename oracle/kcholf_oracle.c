@@ -160,7 +160,9 @@ int spqo_gram_splits(int K, int KS) { return (K + KS - 1) / KS; }
 void spqo_gram(const float* A, long lda, int K, int r, float s, int use_s, int kahan, int KS, float* G,
                double* npart) {
     fp_env();
-    const int nt = r / TB, U = nt * (nt + 1) / 2, S = spqo_gram_splits(K, KS);
+    /* nt tile columns of 64; when r % 64 == 32 the last is half outside X: those columns read as 0, and entries
+     * past r are neither stored nor counted in the norm (tri.py's masked loads and stores) */
+    const int nt = (r + TB - 1) / TB, U = nt * (nt + 1) / 2, S = spqo_gram_splits(K, KS);
     float* P = (float*)malloc((size_t)S * U * TB * TB * sizeof(float));
     int* uti = (int*)malloc(U * sizeof(int));
     int* utj = (int*)malloc(U * sizeof(int));
@@ -181,8 +183,8 @@ void spqo_gram(const float* A, long lda, int K, int r, float s, int use_s, int k
             for (int kk = 0; kk < BK; ++kk) {
                 const int k = k0 + ch * BK + kk;
                 for (int t = 0; t < TB; ++t) {
-                    float a = (k < k1) ? A[(size_t)k * lda + ti * TB + t] : 0.0f;
-                    float b = (k < k1) ? A[(size_t)k * lda + tj * TB + t] : 0.0f;
+                    float a = (k < k1 && ti * TB + t < r) ? A[(size_t)k * lda + ti * TB + t] : 0.0f;
+                    float b = (k < k1 && tj * TB + t < r) ? A[(size_t)k * lda + tj * TB + t] : 0.0f;
                     if (use_s) { a = s * a; b = s * b; }
                     ai[t] = a; aj[t] = b;
                 }
@@ -213,9 +215,12 @@ void spqo_gram(const float* A, long lda, int K, int r, float s, int use_s, int k
                     double sum = 0.0;
                     for (int sp = 0; sp < S; ++sp) sum += (double)P[((size_t)sp * U + u) * TB * TB + i * TB + j];
                     float g = (float)sum;
-                    G[(size_t)(ti * TB + i) * r + tj * TB + j] = g;
-                    G[(size_t)(tj * TB + j) * r + ti * TB + i] = g;
-                    q[j] = (double)g * (double)g;
+                    const int in = ti * TB + i < r && tj * TB + j < r;
+                    if (in) {
+                        G[(size_t)(ti * TB + i) * r + tj * TB + j] = g;
+                        G[(size_t)(tj * TB + j) * r + ti * TB + i] = g;
+                    }
+                    q[j] = in ? (double)g * (double)g : 0.0;
                 }
                 row_tree64(q);
                 w[rr] = q[0];
@@ -419,7 +424,7 @@ static void orth_z(const float* X, long ldx, int K, int r, int KS, float eps, fl
                    float* Q, long ldq, float* Gs, float* Ls, float* Lis, float* Ys, float* scal, const float* Zx,
                    long ldz) {
     fp_env();
-    const int nt = r / TB, U = nt * (nt + 1) / 2;
+    const int nt = (r + TB - 1) / TB, U = nt * (nt + 1) / 2;
     const float s = spqo_pow2_scale(spqo_amax(X, ldx, K, r));
     float* Z = (float*)malloc((size_t)K * r * sizeof(float));
     float* G = (float*)malloc((size_t)r * r * sizeof(float));

@@ -210,10 +210,13 @@ __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
 
 // CROSS: partials of A^T B instead (the block projection of the column-blocked path, kbig.py:88-89): every tile
 // u = ti * ntb + tj of the (columns of A) x (ntb * 64 columns of B) product, A's panel ti against B's panel tj.
+// rc: the columns of A; when r % 64 == 32 the last tile column is half outside A and those columns read as 0 (they
+// only feed outputs past r, which are never read).
 template <bool KAHAN, bool SCALE, bool CROSS = false, int NCH = 1>
 __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, int nt, int KS,
                                               const uint32_t* __restrict__ amax_part, float* __restrict__ P,
-                                              const float* __restrict__ Bx = nullptr, long ldb = 0, int ntb = 0) {
+                                              const float* __restrict__ Bx = nullptr, long ldb = 0, int ntb = 0,
+                                              int rc = 1 << 30) {
     const int u = blockIdx.x, sp = blockIdx.y, U = gridDim.x;
     const float* __restrict__ A = As.p[blockIdx.z];
     amax_part += (size_t)blockIdx.z * AMAX_BLOCKS;
@@ -247,13 +250,16 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
     // multiplied; rows past the split read row k1 - 1 (in bounds) and are zeroed, so the loads are unconditional
     float4 ra[NCH], rb[NCH];
     const int grow = tid >> 4, gc4 = tid & 15;   // this thread's float4 of each 32 x 64 chunk
+    const bool ina = ti * TB + 4 * gc4 < rc, inb = CROSS || tj * TB + 4 * gc4 < rc;
     auto gload = [&](int kc) {
 #pragma unroll
         for (int h = 0; h < NCH; ++h) {
             const int k = kc + h * BK + grow;
             const int kr = k < k1 ? k : k1 - 1;
-            ra[h] = *reinterpret_cast<const float4*>(A + (size_t)kr * lda + ti * TB + 4 * gc4);
-            rb[h] = *reinterpret_cast<const float4*>(B + (size_t)kr * ldbb + tj * TB + 4 * gc4);
+            ra[h] = ina ? *reinterpret_cast<const float4*>(A + (size_t)kr * lda + ti * TB + 4 * gc4)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+            rb[h] = inb ? *reinterpret_cast<const float4*>(B + (size_t)kr * ldbb + tj * TB + 4 * gc4)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     gload(k0);
@@ -364,10 +370,14 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
     for (; s < S; ++s) sum = sum + (double)p[(size_t)s * stride];
     const float g = (float)sum;
     const int gi = ti * TB + row, gj = tj * TB + col;
+    // a tile past r (r % 64 == 32) holds entries outside G: neither written nor counted in the norm
+    const bool in = MODE == 2 || (gi < r && gj < r);
     if (MODE == 0) {
-        G[(size_t)gi * r + gj] = g;
-        if (ti != tj) G[(size_t)gj * r + gi] = g;
-        double q = (double)g * (double)g;
+        if (in) {
+            G[(size_t)gi * r + gj] = g;
+            if (ti != tj) G[(size_t)gj * r + gi] = g;
+        }
+        double q = in ? (double)g * (double)g : 0.0;
         for (int off = 32; off >= 1; off >>= 1) q = q + __shfl_down(q, off);
         __shared__ double sw[4];
         if ((t & 63) == 0) sw[t >> 6] = q;
@@ -378,8 +388,10 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
         }
     } else if (MODE == 1) {
         const float d = ((gi == gj ? 1.0f : 0.0f) - g) * 0.5f;
-        G[(size_t)gi * r + gj] = d;
-        if (ti != tj) G[(size_t)gj * r + gi] = d;
+        if (in) {
+            G[(size_t)gi * r + gj] = d;
+            if (ti != tj) G[(size_t)gj * r + gi] = d;
+        }
     } else {
         G[(size_t)gi * r + gj] = g;
     }
@@ -1869,8 +1881,10 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
 #pragma unroll
         for (int q = 0; q < MS / 16; ++q) {
             const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15;
-            *reinterpret_cast<float4*>(&sD[row][4 * c4]) =
-                *reinterpret_cast<const float4*>(D + (size_t)(m0 + row) * ldD + col0 + 4 * c4);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (SUB || col0 + 4 * c4 < r)   // columns past r (r % 64 == 32) feed only outputs that are not written
+                v = *reinterpret_cast<const float4*>(D + (size_t)(m0 + row) * ldD + col0 + 4 * c4);
+            *reinterpret_cast<float4*>(&sD[row][4 * c4]) = v;
         }
         __syncthreads();
 #pragma unroll
@@ -1886,7 +1900,7 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int row = row0 + 16 * rb + 4 * lk + v, col = col0 + 16 * (cbase + c) + l16;
-            if (row < K) {
+            if (row < K && (SUB || col < r)) {
                 const float cv = Cin[(size_t)row * ldC + col];
                 Out[(size_t)row * ldo + col] = failed ? __builtin_nanf("") : SUB ? cv - acc[c][v] : cv + acc[c][v];
             }
@@ -1980,7 +1994,7 @@ struct spanqr_plan {
     int K = 0, r = 0, device = 0;
     int batch = 1, chol_bmax = 1;   // matrices per call; matrices per Cholesky launch
     size_t lp_stride = 0;           // floats of packed factor per matrix
-    int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0, trsm_rb = 1;
+    int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0, trsm_rb = 1;   // NB: 32-column blocks
     bool trsm_rows = false;   // solve with a wavefront pair per 16 rows (k_trsm_rows) instead of k_trsm
     int solve_rb = 0;         // row blocks per solve workgroup in the Cholesky's launch (0: separate launches)
     int solve_nrb = 0;        // solve workgroups per matrix there
@@ -2064,10 +2078,15 @@ constexpr int GRAM_DEEP_KS = 8 * BK;
 
 template <int NCH>
 void launch_gram_n(const spanqr_plan* p, const MatsIn& A, long lda, dim3 grid, bool scale, bool kahan, hipStream_t st) {
-    if (kahan && scale) k_gram<true, true, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
-    else if (kahan) k_gram<true, false, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
-    else if (scale) k_gram<false, true, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
-    else k_gram<false, false, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P);
+    const int rc = p->r;
+    if (kahan && scale)
+        k_gram<true, true, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P, nullptr, 0, 0, rc);
+    else if (kahan)
+        k_gram<true, false, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P, nullptr, 0, 0, rc);
+    else if (scale)
+        k_gram<false, true, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P, nullptr, 0, 0, rc);
+    else
+        k_gram<false, false, false, NCH><<<grid, 512, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->amax_part, p->P, nullptr, 0, 0, rc);
 }
 
 void launch_gram(const spanqr_plan* p, const MatsIn& A, long lda, int n, bool scale, bool kahan, hipStream_t st) {
@@ -2290,8 +2309,12 @@ void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsO
                     hipStream_t st) {
     // 64-column steps: half the load-then-multiply steps of each workgroup's chain (1-1.5 us faster at 17408x256
     // and 768x512 than 32-column steps, level elsewhere)
-    const dim3 grid((p->K + 31) / 32, p->r / 64, n);
-    k_nsapply<false, 64><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, nullptr, 0, 0, p->bar);
+    // r % 64 == 32: 32-column steps (the chain over r stays exact: no step past r) and a half-used last column tile
+    const dim3 grid((p->K + 31) / 32, (p->r + 63) / 64, n);
+    if (p->r % 64 == 0)
+        k_nsapply<false, 64><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, nullptr, 0, 0, p->bar);
+    else
+        k_nsapply<false, 32><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, nullptr, 0, 0, p->bar);
 }
 
 
@@ -2392,9 +2415,9 @@ int spanqr_dust_host(int K, int r, float* Z) {
 
 static int check_shape(int K, int r, bool blocked_ok = false) {
     const bool blocked = blocked_ok && r > 512 && r <= SPANQR_MAX_R && (r % BW) == 0;
-    if (!blocked && (r < 64 || r > 512 || (r % 64) != 0))
-        return fail(SPANQR_EINVAL, blocked_ok ? "r = %d: must be a multiple of 64 in [64, 512] or of 256 up to 4096"
-                                              : "r = %d: must be a multiple of 64 in [64, 512]", r);
+    if (!blocked && (r < 32 || r > 512 || (r % 32) != 0))
+        return fail(SPANQR_EINVAL, blocked_ok ? "r = %d: must be a multiple of 32 in [32, 512] or of 256 up to 4096"
+                                              : "r = %d: must be a multiple of 32 in [32, 512]", r);
     if (K < r) return fail(SPANQR_EINVAL, "K = %d < r = %d", K, r);
     if ((long)K * r >= (1L << 30)) return fail(SPANQR_EINVAL, "K * r too large");
     return SPANQR_OK;
@@ -2407,7 +2430,7 @@ size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 // Shape-derived fields of a kcholf plan (r <= 512): the Gram's split rule, the Cholesky's grid, the solve variant.
 void plan_shape(spanqr_plan* p, int K, int r, int batch) {
     p->K = K; p->r = r; p->batch = batch;
-    p->nt = r / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / 64;
+    p->nt = (r + TB - 1) / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / CB;
     split_policy(K, p->U, &p->S, &p->KS);
     p->chol_grid = (r / CB > 4) ? r / CB - 3 : 1;     // workgroup 0 + one per tile row 4..r/32-1
     p->trsm_q = (r / CB + TRSM_NW - 1) / TRSM_NW;
@@ -2416,7 +2439,7 @@ void plan_shape(spanqr_plan* p, int K, int r, int batch) {
     // a wavefront pair per 16 rows once there are enough rows to occupy the SIMDs (the chain over r/32 blocks is
     // long; the measured crossover at r = 256 lies near K = 8192-10240); below that, k_trsm splits each row block's
     // columns over eight waves
-    p->trsm_rows = r <= 256 && K >= 9216;
+    p->trsm_rows = r <= 256 && K >= 9216 && (r / CB) % 2 == 0;   // instantiated for 2, 4, 6, 8 column blocks
     p->lp_stride = (size_t)(r / CB) * (r / CB + 1) / 2 * CB * CB;
 }
 
@@ -2466,7 +2489,9 @@ int plan_device_setup(spanqr_plan* p, int device) {
         const int rowblocks = (p->K + 15) / 16;
         int q = (r / CB + TRSM_NW - 1) / TRSM_NW, rb = 1, nwg = rowblocks;
         if (rowblocks > avail) {
-            if (r <= 256) {
+            if (r <= 256 && (r / CB) % 2 != 0) {
+                nwg = avail + 1;   // the one-wavefront solve is built for an even number of column blocks: separate
+            } else if (r <= 256) {
                 q = 0;
                 nwg = (rowblocks + TRSM_NW - 1) / TRSM_NW;
             } else {
@@ -2629,7 +2654,7 @@ int enqueue_borth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, 
 int spanqr_split_rows(int K, int r) {
     const int rc = check_shape(K, r);
     if (rc != SPANQR_OK) return rc;
-    const int nt = r / TB;
+    const int nt = (r + TB - 1) / TB;
     int S = 0, KS = 0;
     split_policy(K, nt * (nt + 1) / 2, &S, &KS);
     return KS;
@@ -2928,10 +2953,10 @@ int spanqr_profile_chol(spanqr_plan* p, const float* G, const double* npart, flo
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
-    HIPCHK(hipMemsetAsync(p->stamps, 0, (size_t)12 * p->NB * sizeof(uint64_t), st));
+    HIPCHK(hipMemsetAsync(p->stamps, 0, (size_t)6 * p->NB * sizeof(uint64_t), st));
     int rc = launch_chol(p, alpha, tau, p->chscal, st, 16 * p->U, 1, true);
     if (rc) return rc;
-    HIPCHK(hipMemcpyAsync(stamps_out, p->stamps, (size_t)12 * p->NB * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipMemcpyAsync(stamps_out, p->stamps, (size_t)6 * p->NB * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));
     int khz = 0;
     HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, p->device));

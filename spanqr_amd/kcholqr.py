@@ -10,7 +10,7 @@ from . import _lib
 from .plan import get_plan, stream_handle
 
 CB = 32          # Cholesky tile (chol.cu:15 TB = 32)
-TILE = 64        # the native kernels need r to be a multiple of this
+TILE = 32        # the native kernels need r to be a multiple of this (kcholqr.py:98-99, TB = 32)
 R_MAX = 512      # orth.py:18: wider X goes through block Gram-Schmidt in the reference
 BLOCK = 256      # its block width (orth.py:19, borth(X, 256))
 
@@ -33,7 +33,7 @@ def _prepare(X):
 
 
 def kcholqr_f(X, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
-    """Q = orth(X) for fp32 X [K, r] on a ROCm device, r a multiple of 64 in [64, 512], K >= r
+    """Q = orth(X) for fp32 X [K, r] on a ROCm device, r a multiple of 32 in [32, 512], K >= r
     (candidates/kcholqr.py:92-112). eps: dust scale (first solve only); alpha: diagonal shift relative to ||G||_F;
     tau: pivot clamp relative to ||G||_F (plus 1e-30); ns: Newton-Schulz polish steps (the last with a Kahan Gram).
     """
@@ -139,8 +139,8 @@ def orth(X):
 
     Dispatch as orth.py:18-20: r > 512 and a multiple of 256 goes through block Gram-Schmidt over 256-column blocks
     (borth); r <= 512 through kcholqr_f. Shapes outside the native kernels -- r not a multiple of 32
-    (kcholqr.py:98-99) and, here, r a multiple of 32 but not of 64, K < r, r > 4096, or r > 512 and not a multiple of
-    256 (where the reference runs kcholqr_f at full width) -- go to torch.linalg.qr.
+    (kcholqr.py:98-99, as the reference) and, here, K < r, r > 4096, or r > 512 and not a multiple of 256 (where the
+    reference runs kcholqr_f at full width) -- go to torch.linalg.qr.
     """
     _check_input(X)
     K, r = X.shape

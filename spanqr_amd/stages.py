@@ -64,7 +64,7 @@ def gram(A, kahan, use_scale=False):
     K, r = A.shape
     plan = get_plan(K, r, _dev(A))
     G = torch.empty(r, r, device=A.device, dtype=torch.float32)
-    npart = torch.empty(16 * _u(r // 64), device=A.device, dtype=torch.float64)
+    npart = torch.empty(16 * _u((r + 63) // 64), device=A.device, dtype=torch.float64)
     _lib.check(_lib.lib().spanqr_stage_gram(plan.handle, A.data_ptr(), A.stride(0), int(bool(use_scale)),
                                             int(bool(kahan)), G.data_ptr(), npart.data_ptr(),
                                             stream_handle(A.device)))

@@ -197,23 +197,28 @@ def check_dust():
 def check_gram():
     f = []
     rng = np.random.default_rng(3)
-    K, r, KS = 200, 128, 64                 # ragged last split (200 = 3 x 64 + 8)
+    # ragged last split (200 = 3 x 64 + 8); r = 96 and 32: the last 64-column tile is half outside X (its columns
+    # read as 0, entries past r neither stored nor counted in the norm partials)
+    for K, r, KS in ((200, 128, 64), (200, 96, 64), (150, 32, 64)):
+        X = rng.standard_normal((K, r)).astype(np.float32)
+        X[:, 5] *= 1e3
+        G64 = X.astype(np.float64).T @ X.astype(np.float64)
+        A64 = np.abs(X.astype(np.float64)).T @ np.abs(X.astype(np.float64))
+        for kahan, c in ((True, 4.0), (False, KS + 8.0)):
+            G, npart = oracle.gram(X, KS, kahan)
+            ratio = (np.abs(G - G64) / (A64 * U32)).max()
+            if not ratio <= c:
+                f.append(f"gram(r={r}, kahan={kahan}) error {ratio:.1f} u|X|^T|X| > {c}")
+            if not np.array_equal(G, G.T):
+                f.append(f"gram (r={r}) not exactly symmetric")
+            fro2 = float((G.astype(np.float64) ** 2).sum())
+            if not abs(npart.sum() - fro2) <= 1e-12 * fro2:
+                f.append(f"norm partials (r={r}) do not sum to ||G||_F^2")
+            if not abs(float(oracle.norm(npart)) - math.sqrt(fro2)) <= 2 * U32 * math.sqrt(fro2):
+                f.append(f"norm() (r={r}) is not ||G||_F")
+    K, r, KS = 200, 128, 64
     X = rng.standard_normal((K, r)).astype(np.float32)
     X[:, 5] *= 1e3
-    G64 = X.astype(np.float64).T @ X.astype(np.float64)
-    A64 = np.abs(X.astype(np.float64)).T @ np.abs(X.astype(np.float64))
-    for kahan, c in ((True, 4.0), (False, KS + 8.0)):
-        G, npart = oracle.gram(X, KS, kahan)
-        ratio = (np.abs(G - G64) / (A64 * U32)).max()
-        if not ratio <= c:
-            f.append(f"gram(kahan={kahan}) error {ratio:.1f} u|X|^T|X| > {c}")
-        if not np.array_equal(G, G.T):
-            f.append("gram not exactly symmetric")
-        fro2 = float((G.astype(np.float64) ** 2).sum())
-        if not abs(npart.sum() - fro2) <= 1e-12 * fro2:
-            f.append("norm partials do not sum to ||G||_F^2")
-        if not abs(float(oracle.norm(npart)) - math.sqrt(fro2)) <= 2 * U32 * math.sqrt(fro2):
-            f.append("norm() is not ||G||_F")
     # one long split (128 chunks of 32 rows): Kahan compensation across chunks keeps the error near 1 u|X|^T|X|
     # where a plain chain reaches tens of u
     X2 = (rng.standard_normal((4096, 64)) + 3.0).astype(np.float32)

@@ -36,6 +36,9 @@ def case_x(K, r, name="mixed_c4", seed=0):
 
 
 SHAPES = [(256, 64), (256, 128), (384, 256), (768, 512)]
+# r a multiple of 32 but not of 64 (kcholqr.py:98-99 runs kcholf there too): the last 64-column Gram / NS tile is
+# half outside X, and an odd number of 32-column blocks in the Cholesky and the solve
+SHAPES32 = [(100, 32), (300, 96), (512, 160), (640, 224), (1000, 480)]
 
 
 @pytest.mark.parametrize("K,r", SHAPES)
@@ -45,7 +48,7 @@ def test_dust_on_device(cuda, K, r):
     assert_bits(Z, oracle.dust(K, r), "dust")
 
 
-@pytest.mark.parametrize("K,r", SHAPES)
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32)
 @pytest.mark.parametrize("kahan", [True, False])
 def test_gram(cuda, K, r, kahan):
     print(f"gram {K}x{r} kahan={kahan}", flush=True)
@@ -57,7 +60,7 @@ def test_gram(cuda, K, r, kahan):
     assert_bits(npart, npo, "norm partials")
 
 
-@pytest.mark.parametrize("K,r", SHAPES)
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32)
 def test_gram_scaled(cuda, K, r):
     print(f"gram scaled {K}x{r}", flush=True)
     X = case_x(K, r, "huge_1e25")
@@ -71,7 +74,7 @@ def test_gram_scaled(cuda, K, r):
     assert_bits(npart, npo, "norm partials (scaled)")
 
 
-@pytest.mark.parametrize("K,r", SHAPES)
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32)
 @pytest.mark.parametrize("name", ["mixed_c4", "rank_half", "zero"])
 def test_chol(cuda, K, r, name):
     print(f"chol {K}x{r} {name}", flush=True)
@@ -105,7 +108,8 @@ def test_chol32_absolute(cuda, K, r):
 # K >= 9216 (r <= 256) takes the row-blocked solve (a wavefront pair per 16 rows), below it the column-blocked one
 # (16400 x 384: two column blocks per wave and two row blocks per workgroup, the last one past K); ragged K on all
 @pytest.mark.parametrize("K,r", SHAPES + [(16384, 256), (32768, 64), (4100, 128), (4111, 192), (9230, 192),
-                                          (16400, 256), (16425, 128), (16400, 384)])
+                                          (16400, 256), (16425, 128), (16400, 384)] + SHAPES32 +
+                         [(9300, 96), (10000, 224), (16400, 288)])
 @pytest.mark.parametrize("pass1", [True, False])
 def test_trsm(cuda, K, r, pass1):
     print(f"trsm {K}x{r} pass1={pass1}", flush=True)
@@ -127,7 +131,7 @@ def test_trsm(cuda, K, r, pass1):
     assert_bits(Y, Yo, "Y")
 
 
-@pytest.mark.parametrize("K,r", SHAPES)
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32)
 @pytest.mark.parametrize("kahan", [True, False])
 def test_ns_step(cuda, K, r, kahan):
     print(f"ns {K}x{r} kahan={kahan}", flush=True)
@@ -142,7 +146,9 @@ def test_ns_step(cuda, K, r, kahan):
 
 ORTH_CASES = [(256, 64, "mixed_c4"), (256, 128, "zero"), (384, 256, "rank_half"), (768, 512, "ttf_cu4_t1e-2"),
               (768, 512, "dup_cols"), (1024, 256, "huge_1e25"), (1024, 256, "tiny_1e-25"), (2048, 512, "mixed_c8"),
-              (17408, 256, "ttf_cu4_t1e-2"), (4100, 192, "mixed_c6")]
+              (17408, 256, "ttf_cu4_t1e-2"), (4100, 192, "mixed_c6"),
+              (64, 32, "zero"), (300, 96, "mixed_c4"), (1000, 160, "rank_half"), (4100, 224, "ttf_cu4_t1e-2"),
+              (768, 480, "mixed_c8"), (12000, 160, "mixed_c4"), (2048, 352, "huge_1e25")]
 
 
 @pytest.mark.parametrize("K,r,name", ORTH_CASES)
