@@ -52,9 +52,11 @@ enum {
     SPANQR_Q_DEVICE = 6,
     SPANQR_Q_BATCH = 7,          /* matrices per call the plan holds workspace for */
     SPANQR_Q_CHOL_BATCH = 8,     /* matrices per Cholesky launch (all their workgroups fit on the device at once) */
-    SPANQR_Q_BLOCKS = 9,         /* 256-column blocks of a column-blocked plan (r > 512); 0 otherwise */
+    SPANQR_Q_BLOCKS = 9,         /* column blocks of a column-blocked plan (r > 512, or spanqr_plan_create_borth); 0
+                                    otherwise */
     SPANQR_Q_SOLVE_ROWS = 10,    /* rows per solve workgroup when the solve runs in the Cholesky's launch; 0 when
                                     they are separate launches */
+    SPANQR_Q_BLOCK_WIDTH = 11,   /* columns per block of a column-blocked plan; 0 otherwise */
 };
 
 /* Create a plan for X [K, r] on HIP device `device` (allocates the workspace and uploads the dust matrix).
@@ -69,6 +71,15 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out);
 /* Plan for up to `batch` (1..SPANQR_MAX_BATCH) matrices [K, r] per call (spanqr_orth_batched_f32): one workspace
  * per matrix, one shared dust matrix. spanqr_plan_create is the batch = 1 case. */
 int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan** out);
+
+/* Column-blocked plan for borth(X, b, reorth) (candidates/kbig.py:69-95, whose parameters these are): block
+ * Gram-Schmidt over b-column blocks, each block projected twice against the finished ones and orthonormalised by
+ * kcholf at width b with its column slice of the K x r dust; with reorth != 0 projected and orthonormalised once more
+ * (kbig.py:91-92). b a multiple of 64 in [64, 512], r > b a multiple of b up to 4096, K >= r (the reference runs
+ * kcholf at full width when r <= b or r % b != 0: the caller's choice, kbig.py:77-78). spanqr_orth_f32 on the plan
+ * runs it (eps, alpha, tau, ns apply to every block's kcholf); spanqr_plan_create for r > 512 is b = 256 with reorth,
+ * the call orth.py:19 makes. */
+int spanqr_plan_create_borth(int K, int r, int b, int reorth, int device, spanqr_plan** out);
 void spanqr_plan_destroy(spanqr_plan* plan);
 long spanqr_plan_query(const spanqr_plan* plan, int what);
 

@@ -60,9 +60,10 @@ def _bind(L):
                                  _f32p, c_long]
     L.spqo_split_rows.argtypes = [c_int, c_int]
     L.spqo_split_rows.restype = c_int
-    L.spqo_xgram.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, _f32p]
-    L.spqo_project.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, _f32p, c_long]
-    L.spqo_borth.argtypes = [_f32p, c_long, c_int, c_int, c_float, c_float, c_float, c_int, _f32p, c_long]
+    L.spqo_xgram.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, c_int, _f32p]
+    L.spqo_project.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, c_int, _f32p, c_long]
+    L.spqo_borth.argtypes = [_f32p, c_long, c_int, c_int, c_int, c_int, c_float, c_float, c_float, c_int, _f32p,
+                             c_long]
     L.spqo_rsqrt64.argtypes = [ctypes.c_double]
     L.spqo_rsqrt64.restype = ctypes.c_double
     L.spqo_diag_factor64.argtypes = [_f64p, c_long, ctypes.c_double, _f64p, c_long, _f64p]
@@ -245,7 +246,7 @@ def orth_dust(X, Z, KS, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
 
 # ---- column-blocked path (kbig.py:69-95) ----
 
-BW = 256   # borth block width (orth.py:19)
+BW = 256   # the borth block width orth.py:19 uses
 
 
 def split_rows(K, U):
@@ -254,12 +255,13 @@ def split_rows(K, U):
 
 
 def xgram(P, C, KS):
-    """T = P^T C for P [K, j], C [K, 256]: fp32 chains per split of KS rows, fp64 across splits"""
+    """T = P^T C for P [K, j], C [K, b]: fp32 chains per split of KS rows, fp64 across splits"""
     P, C = _c32(P), _c32(C)
     K, j = P.shape
-    assert C.shape == (K, BW)
-    T = np.empty((j, BW), np.float32)
-    lib().spqo_xgram(_ptr(P), j, K, j, _ptr(C), BW, KS, T)
+    b = C.shape[1]
+    assert C.shape[0] == K
+    T = np.empty((j, b), np.float32)
+    lib().spqo_xgram(_ptr(P), j, K, j, _ptr(C), b, b, KS, T)
     return T
 
 
@@ -267,18 +269,21 @@ def project(P, C, KS):
     """C - P (P^T C) (kbig.py:88-89)"""
     P, C = _c32(P), _c32(C)
     K, j = P.shape
-    Out = np.empty((K, BW), np.float32)
-    lib().spqo_project(_ptr(P), j, K, j, _ptr(C), BW, KS, Out, BW)
+    b = C.shape[1]
+    Out = np.empty((K, b), np.float32)
+    lib().spqo_project(_ptr(P), j, K, j, _ptr(C), b, b, KS, Out, b)
     return Out
 
 
-def borth(X, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
-    """Q = borth(X, 256) with reorthogonalisation (kbig.py:69-95), r a multiple of 256"""
+def borth(X, b=BW, reorth=True, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
+    """Q = borth(X, b, reorth) (kbig.py:69-95), b a multiple of 64, r > b a multiple of b; the default b is the 256
+    orth.py:19 passes"""
     X = _c32(X)
     K, r = X.shape
-    assert r % BW == 0
+    assert b % 64 == 0 and r % b == 0 and r > b
     Q = np.empty((K, r), np.float32)
-    lib().spqo_borth(X, r, K, r, float(np.float32(eps)), float(np.float32(alpha)), float(np.float32(tau)), ns, Q, r)
+    lib().spqo_borth(X, r, K, r, b, int(bool(reorth)), float(np.float32(eps)), float(np.float32(alpha)),
+                     float(np.float32(tau)), ns, Q, r)
     return Q
 
 

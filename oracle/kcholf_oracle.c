@@ -492,84 +492,85 @@ int spqo_split_rows(int K, int U) {
 }
 
 /* ------------------------------------------------------------------------------------------------------------ */
-/* borth's projection (kbig.py:88-89, :91): Out = C - P (P^T C) for P [K, j] and C [K, 256].                    */
+/* borth's projection (kbig.py:88-89, :91): Out = C - P (P^T C) for P [K, j] and C [K, bw].                    */
 /* T = P^T C over 64x64 tiles: per split of KS rows, per element, an fmaf chain over the split's rows in order    */
 /* from +0 (rows past K read as 0); T[i][c] = fp32(((0.0 + T_0) + T_1) + ... ) in fp64, split order. Then        */
 /* Out[k][c] = C[k][c] - (fmaf chain over m = 0..j-1 from +0 of P[k][m] * T[m][c]). Out may be C.               */
 /* ------------------------------------------------------------------------------------------------------------ */
-#define BWID 256   /* borth block width (orth.py:19 calls borth(X, 256)) */
-
-void spqo_xgram(const float* P, long ldp, int K, int j, const float* C, long ldc, int KS, float* T) {
+void spqo_xgram(const float* P, long ldp, int K, int j, const float* C, long ldc, int bw, int KS, float* T) {
     fp_env();
     const int S = spqo_gram_splits(K, KS);
-    double* sum = (double*)calloc((size_t)j * BWID, sizeof(double));
-    float* part = (float*)malloc((size_t)j * BWID * sizeof(float));
+    double* sum = (double*)calloc((size_t)j * bw, sizeof(double));
+    float* part = (float*)malloc((size_t)j * bw * sizeof(float));
     for (int sp = 0; sp < S; ++sp) {
         const int k0 = sp * KS, k1 = (k0 + KS < K) ? k0 + KS : K;
         #pragma omp parallel for schedule(static)
         for (int i = 0; i < j; ++i) {
             fp_env();
-            float* a = part + (size_t)i * BWID;
-            for (int c = 0; c < BWID; ++c) a[c] = 0.0f;
+            float* a = part + (size_t)i * bw;
+            for (int c = 0; c < bw; ++c) a[c] = 0.0f;
             for (int k = k0; k < k1; ++k) {
                 const float pk = P[(size_t)k * ldp + i];
-                for (int c = 0; c < BWID; ++c)
-                    a[c] = fmaf(pk, PLANTED(11) ? C[(size_t)k * ldc + i % BWID] : C[(size_t)k * ldc + c], a[c]);   /* 11 */
+                for (int c = 0; c < bw; ++c)
+                    a[c] = fmaf(pk, PLANTED(11) ? C[(size_t)k * ldc + i % bw] : C[(size_t)k * ldc + c], a[c]);   /* 11 */
             }
-            for (int c = 0; c < BWID; ++c) sum[(size_t)i * BWID + c] = sum[(size_t)i * BWID + c] + (double)a[c];
+            for (int c = 0; c < bw; ++c) sum[(size_t)i * bw + c] = sum[(size_t)i * bw + c] + (double)a[c];
         }
     }
-    for (size_t e = 0; e < (size_t)j * BWID; ++e) T[e] = (float)sum[e];
+    for (size_t e = 0; e < (size_t)j * bw; ++e) T[e] = (float)sum[e];
     free(sum); free(part);
 }
 
-void spqo_project(const float* P, long ldp, int K, int j, const float* C, long ldc, int KS, float* Out, long ldo) {
-    float* T = (float*)malloc((size_t)j * BWID * sizeof(float));
-    spqo_xgram(P, ldp, K, j, C, ldc, KS, T);
+void spqo_project(const float* P, long ldp, int K, int j, const float* C, long ldc, int bw, int KS, float* Out,
+                  long ldo) {
+    float* T = (float*)malloc((size_t)j * bw * sizeof(float));
+    spqo_xgram(P, ldp, K, j, C, ldc, bw, KS, T);
     #pragma omp parallel for schedule(static)
     for (int k = 0; k < K; ++k) {
         fp_env();
-        float acc[BWID];
-        for (int c = 0; c < BWID; ++c) acc[c] = 0.0f;
+        float* acc = (float*)malloc((size_t)bw * sizeof(float));
+        for (int c = 0; c < bw; ++c) acc[c] = 0.0f;
         for (int m = 0; m < j; ++m) {
             const float pm = P[(size_t)k * ldp + m];
-            for (int c = 0; c < BWID; ++c) acc[c] = fmaf(pm, T[(size_t)m * BWID + c], acc[c]);
+            for (int c = 0; c < bw; ++c) acc[c] = fmaf(pm, T[(size_t)m * bw + c], acc[c]);
         }
-        for (int c = 0; c < BWID; ++c)
+        for (int c = 0; c < bw; ++c)
             Out[(size_t)k * ldo + c] = PLANTED(12) ? C[(size_t)k * ldc + c] + acc[c] : C[(size_t)k * ldc + c] - acc[c];   /* 12 */
+        free(acc);
     }
     free(T);
 }
 
 /* ------------------------------------------------------------------------------------------------------------ */
-/* borth (kbig.py:69-95 with b = 256, reorth): s = _pow2_scale(max |X|) of the whole X (kbig.py:85); dust Zf =     */
-/* spqo_dust(K, r), block jb using columns 256 jb.. of it. Per block j: W = fp32(s * X[:, j:j+256]); for j > 0    */
-/* W = project(W) twice; Q_j = orth_z(W, dust slice) (_kf = kcholqr_f with the dust given, kbig.py:48-63); for    */
-/* j > 0 W = project(Q_j), Q_j = orth_z(W, dust slice). P = Q[:, :j], the finished blocks. Every orth_z uses the  */
-/* 256-column split rule; every projection the rule for its (j / 64) * 4 tiles.                                  */
+/* borth (kbig.py:69-95, borth(X, b, reorth); orth.py:19 calls it with b = 256 and the default reorth): s =        */
+/* _pow2_scale(max |X|) of the whole X (kbig.py:85); dust Zf = spqo_dust(K, r), block jb using columns b jb.. of  */
+/* it. Per block j: W = fp32(s * X[:, j:j+b]); for j > 0 W = project(W) twice; Q_j = orth_z(W, dust slice) (_kf = */
+/* kcholqr_f with the dust given, kbig.py:48-63); with reorth, for j > 0 W = project(Q_j), Q_j = orth_z(W, dust   */
+/* slice). P = Q[:, :j], the finished blocks. Every orth_z uses the b-column split rule; every projection the rule */
+/* for its (j / 64) (b / 64) tiles. b a multiple of 64, r a multiple of b.                                       */
 /* ------------------------------------------------------------------------------------------------------------ */
-void spqo_borth(const float* X, long ldx, int K, int r, float eps, float alpha, float tau_rel, int ns, float* Q,
-                long ldq) {
+void spqo_borth(const float* X, long ldx, int K, int r, int b, int reorth, float eps, float alpha, float tau_rel,
+                int ns, float* Q, long ldq) {
     fp_env();
     const float s = spqo_pow2_scale(spqo_amax(X, ldx, K, r));
     float* Zf = (float*)malloc((size_t)K * r * sizeof(float));
-    float* W = (float*)malloc((size_t)K * BWID * sizeof(float));
+    float* W = (float*)malloc((size_t)K * b * sizeof(float));
     spqo_dust(K, r, Zf);
-    const int KSb = spqo_split_rows(K, (BWID / TB) * (BWID / TB + 1) / 2);
-    for (int j = 0; j < r; j += BWID) {
-        const int KSp = j > 0 ? spqo_split_rows(K, (j / TB) * (BWID / TB)) : 0;
+    const int KSb = spqo_split_rows(K, (b / TB) * (b / TB + 1) / 2);
+    for (int j = 0; j < r; j += b) {
+        const int KSp = j > 0 ? spqo_split_rows(K, (j / TB) * (b / TB)) : 0;
         float* Qj = Q + j;
         const float* Zj = Zf + (PLANTED(13) ? 0 : j);   /* 13: every block gets the first dust slice */
         for (int k = 0; k < K; ++k)
-            for (int c = 0; c < BWID; ++c) W[(size_t)k * BWID + c] = s * X[(size_t)k * ldx + j + c];
+            for (int c = 0; c < b; ++c) W[(size_t)k * b + c] = s * X[(size_t)k * ldx + j + c];
         if (j > 0) {
-            spqo_project(Q, ldq, K, j, W, BWID, KSp, W, BWID);
-            if (!PLANTED(14)) spqo_project(Q, ldq, K, j, W, BWID, KSp, W, BWID);   /* 14: projected once */
+            spqo_project(Q, ldq, K, j, W, b, b, KSp, W, b);
+            if (!PLANTED(14)) spqo_project(Q, ldq, K, j, W, b, b, KSp, W, b);   /* 14: projected once */
         }
-        orth_z(W, BWID, K, BWID, KSb, eps, alpha, tau_rel, ns, Qj, ldq, NULL, NULL, NULL, NULL, NULL, Zj, r);
-        if (j > 0) {
-            spqo_project(Q, ldq, K, j, Qj, ldq, KSp, W, BWID);
-            orth_z(W, BWID, K, BWID, KSb, eps, alpha, tau_rel, ns, Qj, ldq, NULL, NULL, NULL, NULL, NULL, Zj, r);
+        orth_z(W, b, K, b, KSb, eps, alpha, tau_rel, ns, Qj, ldq, NULL, NULL, NULL, NULL, NULL, Zj, r);
+        if (j > 0 && reorth) {
+            spqo_project(Q, ldq, K, j, Qj, ldq, b, KSp, W, b);
+            orth_z(W, b, K, b, KSb, eps, alpha, tau_rel, ns, Qj, ldq, NULL, NULL, NULL, NULL, NULL, Zj, r);
         }
     }
     free(Zf); free(W);

@@ -19,7 +19,7 @@ HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
 
 # plan queries (include/spanqr.h)
 (Q_K, Q_R, Q_SPLITS, Q_SPLIT_ROWS, Q_CHOL_GRID, Q_WORKSPACE_MB, Q_DEVICE, Q_BATCH, Q_CHOL_BATCH, Q_BLOCKS,
- Q_SOLVE_ROWS) = range(11)
+ Q_SOLVE_ROWS, Q_BLOCK_WIDTH) = range(12)
 MAX_BATCH = 32   # SPANQR_MAX_BATCH
 MAX_R = 4096     # SPANQR_MAX_R
 # kernels for spanqr_profile_kernel
@@ -31,6 +31,7 @@ _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float
 SIGNATURES = {
     "spanqr_plan_create": (_I, [_I, _I, _I, ctypes.POINTER(ctypes.c_void_p)]),
     "spanqr_plan_create_batched": (_I, [_I, _I, _I, _I, ctypes.POINTER(ctypes.c_void_p)]),
+    "spanqr_plan_create_borth": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_void_p)]),
     "spanqr_plan_destroy": (None, [_P]),
     "spanqr_plan_query": (_L, [_P, _I]),
     "spanqr_orth_f32": (_I, [_P, _P, _L, _P, _L, _F, _F, _F, _I, _P]),

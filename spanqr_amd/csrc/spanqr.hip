@@ -1931,16 +1931,16 @@ __global__ __launch_bounds__(256) void k_copy_out(const MatsIn Ys, long ldy, int
 // Column-blocked path (r > 512, kbig.py:69-95): W = s X[:, j:j+256] for one block, s the power-of-2 scale of all of
 // X (from the amax partials of the whole matrix). Exact: s is a power of 2.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int BW = 256;   // block width of the column-blocked path (orth.py:19, borth(X, 256))
-__global__ __launch_bounds__(256) void k_scale_block(const float* __restrict__ X, long ldx, int K,
+constexpr int BW = 256;   // block width orth.py:19 uses (borth(X, 256)); spanqr_plan_create_borth takes others
+__global__ __launch_bounds__(256) void k_scale_block(const float* __restrict__ X, long ldx, int K, int bw,
                                                      const uint32_t* __restrict__ amax_part, float* __restrict__ W) {
     const float sc = block_scale(amax_part);
-    const int n4 = K * (BW / 4);
+    const int b4 = bw / 4, n4 = K * b4;
     for (int e = blockIdx.x * 256 + threadIdx.x; e < n4; e += gridDim.x * 256) {
-        const int row = e / (BW / 4), c4 = e - row * (BW / 4);
+        const int row = e / b4, c4 = e - row * b4;
         float4 v = *reinterpret_cast<const float4*>(X + (size_t)row * ldx + 4 * c4);
         v.x = sc * v.x; v.y = sc * v.y; v.z = sc * v.z; v.w = sc * v.w;
-        *reinterpret_cast<float4*>(W + (size_t)row * BW + 4 * c4) = v;
+        *reinterpret_cast<float4*>(W + (size_t)row * bw + 4 * c4) = v;
     }
 }
 
@@ -2017,7 +2017,8 @@ struct spanqr_plan {
     // use, the block buffer W [K, 256], the projection's split partials and its product T [r - 256, 256], the amax
     // partials of the whole X
     spanqr_plan* blk = nullptr;
-    int nblk = 0;
+    int nblk = 0, bw = 0;   // column-blocked plan: blocks of bw columns
+    bool reorth = true;     // project and orthonormalise each block a second time (kbig.py:91-92)
     char* bbase = nullptr;
     float *Zb = nullptr, *W = nullptr, *Tp = nullptr, *T = nullptr;
     uint32_t* bamax = nullptr;
@@ -2548,25 +2549,25 @@ size_t plan_layout(spanqr_plan* p, char* base) {
 
 namespace {
 
-// Column-blocked plan: a 256-column block plan plus the blocked path's own buffers (no Gram or Cholesky of its own).
-int create_blocked(int K, int r, int device, spanqr_plan** out) {
+// Column-blocked plan: a bw-column block plan plus the blocked path's own buffers (no Gram or Cholesky of its own).
+int create_blocked(int K, int r, int bw, bool reorth, int device, spanqr_plan** out) {
     spanqr_plan* p = new spanqr_plan;
-    p->K = K; p->r = r; p->device = device; p->batch = 1; p->nblk = r / BW;
-    int rc = spanqr_plan_create_batched(K, BW, 1, device, &p->blk);
+    p->K = K; p->r = r; p->device = device; p->batch = 1; p->nblk = r / bw; p->bw = bw; p->reorth = reorth;
+    int rc = spanqr_plan_create_batched(K, bw, 1, device, &p->blk);
     if (rc != SPANQR_OK) {
         delete p;
         return rc;
     }
-    size_t maxp = 0;   // split partials of the largest projection (U = (j / 64) * 4 tiles for j = r - 256 columns)
+    size_t maxp = 0;   // split partials of the largest projection (U = (j / 64) (bw / 64) tiles for j = r - bw)
     for (int jb = 1; jb < p->nblk; ++jb) {
         int S = 0, KS = 0;
-        const int U = (BW * jb / TB) * (BW / TB);
+        const int U = (bw * jb / TB) * (bw / TB);
         split_policy(K, U, &S, &KS);
         if ((size_t)S * U > maxp) maxp = (size_t)S * U;
     }
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
-    const size_t sz_Z = al((size_t)K * r * sizeof(float)), sz_W = al((size_t)K * BW * sizeof(float));
-    const size_t sz_Tp = al(maxp * TB * TB * sizeof(float)), sz_T = al((size_t)r * BW * sizeof(float));
+    const size_t sz_Z = al((size_t)K * r * sizeof(float)), sz_W = al((size_t)K * bw * sizeof(float));
+    const size_t sz_Tp = al(maxp * TB * TB * sizeof(float)), sz_T = al((size_t)r * bw * sizeof(float));
     const size_t sz_am = al(AMAX_BLOCKS * sizeof(uint32_t));
     const size_t bytes = sz_Z + sz_W + sz_Tp + sz_T + sz_am;
     DeviceGuard dg(device);
@@ -2598,11 +2599,12 @@ int create_blocked(int K, int r, int device, spanqr_plan** out) {
     return SPANQR_OK;
 }
 
-// Out = Cin - P (P^T Cin) for P = the j leading columns of Q (row stride ldq) and Cin [K, 256] (row stride ldc): the
+// Out = Cin - P (P^T Cin) for P = the j leading columns of Q (row stride ldq) and Cin [K, bw] (row stride ldc): the
 // projection of kbig.py:88-89. P^T Cin is a split-K product (fp32 MFMA chains per split, fp64 across splits in split
 // order, tri.py's Gram rule for the split count), then one MFMA chain per element of P T, subtracted once.
 void project(const spanqr_plan* p, const float* Q, long ldq, int j, const float* Cin, long ldc, float* Out,
              hipStream_t st) {
+    const int BW = p->bw;
     const int U = (j / TB) * (BW / TB);
     int S = 0, KS = 0;
     split_policy(p->K, U, &S, &KS);
@@ -2616,12 +2618,13 @@ void project(const spanqr_plan* p, const float* Q, long ldq, int j, const float*
                                                                     ldc, BW);
 }
 
-// borth (kbig.py:69-95, BCGS2 over 256-column blocks as orth.py:18-19 calls it): per block, W = s X_blk, projected
-// twice against the finished blocks, orthonormalised by the full kcholf call with the block's slice of the K x r dust;
-// then projected once more and orthonormalised again (reorth). Each block's result goes straight into its columns of Q.
+// borth (kbig.py:69-95, BCGS2 over bw-column blocks; orth.py:18-19 calls it with 256): per block, W = s X_blk,
+// projected twice against the finished blocks, orthonormalised by the full kcholf call with the block's slice of the
+// K x r dust; with reorth, projected once more and orthonormalised again. Each block's result goes straight into its
+// columns of Q.
 int enqueue_borth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, float eps, float alpha, float tau,
                   int ns, hipStream_t st) {
-    const int K = p->K;
+    const int K = p->K, BW = p->bw;
     k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(mats_in(&X, 1), ldx, K, p->r, p->bamax);
     const int sgrid = (K * (BW / 4) + 255) / 256 < 1024 ? (K * (BW / 4) + 255) / 256 : 1024;
     int rc;
@@ -2630,7 +2633,7 @@ int enqueue_borth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, 
         float* Qj = Q + j;
         const float* Wc = p->W;
         const Dust dz{p->Zb + j, p->r};
-        k_scale_block<<<sgrid, 256, 0, st>>>(X + j, ldx, K, p->bamax, p->W);
+        k_scale_block<<<sgrid, 256, 0, st>>>(X + j, ldx, K, BW, p->bamax, p->W);
         if (j > 0) {
             project(p, Q, ldq, j, p->W, BW, p->W, st);
             project(p, Q, ldq, j, p->W, BW, p->W, st);
@@ -2638,7 +2641,7 @@ int enqueue_borth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, 
         if ((rc = enqueue_orth(p->blk, 1, mats_in(&Wc, 1), BW, mats_out(&Qj, 1), ldq, eps, alpha, tau, ns, st, false,
                                dz)))
             return rc;
-        if (j > 0) {
+        if (j > 0 && p->reorth) {
             project(p, Q, ldq, j, Qj, ldq, p->W, st);
             if ((rc = enqueue_orth(p->blk, 1, mats_in(&Wc, 1), BW, mats_out(&Qj, 1), ldq, eps, alpha, tau, ns, st,
                                    false, dz)))
@@ -2664,6 +2667,17 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
     return spanqr_plan_create_batched(K, r, 1, device, out);
 }
 
+int spanqr_plan_create_borth(int K, int r, int b, int reorth, int device, spanqr_plan** out) {
+    if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
+    *out = nullptr;
+    if (b < 64 || b > 512 || b % 64 != 0) return fail(SPANQR_EINVAL, "b = %d: must be a multiple of 64 in [64, 512]", b);
+    if (r <= b || r % b != 0 || r > SPANQR_MAX_R)
+        return fail(SPANQR_EINVAL, "r = %d: must be a multiple of b = %d above it, at most %d", r, b, SPANQR_MAX_R);
+    if (K < r) return fail(SPANQR_EINVAL, "K = %d < r = %d", K, r);
+    if ((long)K * r >= (1L << 30)) return fail(SPANQR_EINVAL, "K * r too large");
+    return create_blocked(K, r, b, reorth != 0, device, out);
+}
+
 int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan** out) {
     if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
     *out = nullptr;
@@ -2673,7 +2687,7 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
         return fail(SPANQR_EINVAL, "batch = %d: must be in [1, %d]", batch, SPANQR_MAX_BATCH);
     if (r > 512) {
         if (batch != 1) return fail(SPANQR_EINVAL, "r = %d > 512 (column-blocked path): batch must be 1", r);
-        return create_blocked(K, r, device, out);
+        return create_blocked(K, r, BW, true, device, out);
     }
     DeviceGuard dg(device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", device);
@@ -2740,6 +2754,7 @@ long spanqr_plan_query(const spanqr_plan* p, int what) {
         case SPANQR_Q_BATCH: return p->batch;
         case SPANQR_Q_CHOL_BATCH: return p->blk ? p->blk->chol_bmax : p->chol_bmax;
         case SPANQR_Q_BLOCKS: return p->nblk;
+        case SPANQR_Q_BLOCK_WIDTH: return p->bw;
         case SPANQR_Q_SOLVE_ROWS: {
             const spanqr_plan* q = p->blk ? p->blk : p;
             return q->solve_rb == 0 ? 0 : (q->solve_q == 0 ? 16L * TRSM_NW : 16L * q->solve_rb);

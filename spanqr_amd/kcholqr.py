@@ -7,7 +7,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .plan import get_plan, stream_handle
+from .plan import get_borth_plan, get_plan, stream_handle
 
 CB = 32          # Cholesky tile (chol.cu:15 TB = 32)
 TILE = 32        # the native kernels need r to be a multiple of this (kcholqr.py:98-99, TB = 32)
@@ -105,26 +105,29 @@ def orth_many(Xs):
     return out
 
 
-def borth(X, b=BLOCK):
-    """Q for fp32 X [K, r], K >= r, by block Gram-Schmidt over b-column blocks (candidates/kbig.py:69-95, BCGS2 with
-    the reorthogonalisation): each block, scaled by the power of 2 of the whole X, has the finished blocks' span
-    removed twice, goes through the kcholf recipe with its own column slice of a K x r dust, then is projected and
-    orthonormalised once more. One native call for the whole X, no host synchronisation.
+def borth(X, b=512, reorth=True):
+    """Q for fp32 X [K, r], K >= r, by block Gram-Schmidt over b-column blocks (candidates/kbig.py:69-95, BCGS2, with
+    the reference's signature and defaults): each block, scaled by the power of 2 of the whole X, has the finished
+    blocks' span removed twice and goes through the kcholf recipe with its own column slice of a K x r dust; with
+    reorth it is projected and orthonormalised once more. One native call for the whole X, no host synchronisation.
 
-    b = 256 is the width orth.py:19 uses and the only one implemented (the reference's default is 512). As in
-    kbig.py:77-78, r <= b or r not a multiple of b is one orth call at full width instead; r above 4096 raises.
+    As kbig.py:77-78, r <= b or r not a multiple of b is one kcholf call at full width instead (here for r <= 512;
+    wider full-width kcholf is not built, so those shapes use torch.linalg.qr). Natively b is a multiple of 64 in
+    [64, 512] (orth passes 256, the reference's default is 512); other b raise ValueError, as does r above 4096.
     """
     _check_input(X)
-    if b != BLOCK:
-        raise ValueError(f"borth: only b = {BLOCK} is implemented (the width orth.py:19 uses)")
     K, r = X.shape
     if r <= b or r % b:
-        return orth(X)
+        if r <= R_MAX and r % TILE == 0 and K >= r:
+            return kcholqr_f(X)
+        return torch.linalg.qr(X)[0]
+    if b % 64 or not 64 <= b <= R_MAX:
+        raise ValueError(f"borth: b = {b}: the native block width must be a multiple of 64 in [64, {R_MAX}]")
     if r > _lib.MAX_R or K < r:
         raise ValueError(f"borth: shape [{K}, {r}] needs r <= {_lib.MAX_R} and K >= r")
     X = _prepare(X)
     dev = X.device
-    plan = get_plan(K, r, dev)
+    plan = get_borth_plan(K, r, b, reorth, dev)
     Q = torch.empty_like(X)
     with torch.cuda.device(dev):
         _lib.check(_lib.lib().spanqr_orth_f32(plan.handle, X.data_ptr(), r, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2,
@@ -146,7 +149,7 @@ def orth(X):
     K, r = X.shape
     if r > R_MAX:
         if r % BLOCK == 0 and r <= _lib.MAX_R and K >= r:
-            return borth(X)
+            return borth(X, BLOCK)
         return torch.linalg.qr(X)[0]
     if r % TILE or K < r:
         return torch.linalg.qr(X)[0]

@@ -24,10 +24,16 @@ def _mark_shutdown():
 
 
 class Plan:
-    def __init__(self, K, r, device_index, batch=1):
+    def __init__(self, K, r, device_index, batch=1, borth=None):
+        """borth = (b, reorth): a column-blocked plan for borth(X, b, reorth) (spanqr_plan_create_borth)"""
         self.K, self.r, self.device, self.batch = int(K), int(r), int(device_index), int(batch)
         h = ctypes.c_void_p()
-        _lib.check(_lib.lib().spanqr_plan_create_batched(self.K, self.r, self.batch, self.device, ctypes.byref(h)))
+        if borth is None:
+            _lib.check(_lib.lib().spanqr_plan_create_batched(self.K, self.r, self.batch, self.device, ctypes.byref(h)))
+        else:
+            b, reorth = borth
+            _lib.check(_lib.lib().spanqr_plan_create_borth(self.K, self.r, int(b), int(bool(reorth)), self.device,
+                                                           ctypes.byref(h)))
         self.handle = h
 
     def query(self, what):
@@ -83,6 +89,19 @@ def get_plan(K, r, device, batch=1):
         p = _PLANS.get(key)
         if p is None:
             p = Plan(K, r, idx, batch)
+            _PLANS[key] = p
+        return p
+
+
+def get_borth_plan(K, r, b, reorth, device):
+    """the cached column-blocked plan for borth(X [K, r], b, reorth) on `device` and the current stream"""
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = ("borth", int(K), int(r), int(b), bool(reorth), idx, stream_handle(idx))
+    with _LOCK:
+        p = _PLANS.get(key)
+        if p is None:
+            p = Plan(K, r, idx, borth=(b, reorth))
             _PLANS[key] = p
         return p
 

@@ -15,10 +15,11 @@ def assert_bits(a, b, what):
                              f"max abs diff {np.nanmax(d):.3e}")
 
 
-def gate(X, Q, what):
-    """the spec's robustness gates: no collapsed columns, max|Q^T Q - I| <= 2e-7, the reference's span rule"""
+def gate(X, Q, what, orth_tol=metrics.ORTH_TOL_TARGET):
+    """the spec's robustness gates: no collapsed columns, max|Q^T Q - I| <= orth_tol (2e-7 unless given), the
+    reference's span rule"""
     ref = metrics.reference(X)
     res = metrics.assess(Q, X.to(Q.device), ref)
     hh = metrics.assess(metrics.householder(X.cpu()), X.cpu(), ref)
-    fails = res.failures(span_ref=hh.span_n, orth_tol=metrics.ORTH_TOL_TARGET)
+    fails = res.failures(span_ref=hh.span_n, orth_tol=orth_tol)
     assert not fails, f"{what}: {fails} (orth {res.orth:.3e}, span_n {res.span_n:.2f})"

@@ -492,28 +492,35 @@ def check_borth():
 
 
 def check_borth_composition():
-    """kbig.py:85-93 step by step from the pieces pinned above: s from all of X, each block twice projected, _kf with
-    its dust slice, once more projected and _kf again"""
+    """kbig.py:85-93 step by step from the pieces pinned above, for orth's b = 256 and for b = 128 with and without
+    the reorthogonalisation: s from all of X, each block twice projected, _kf with its dust slice, and with reorth
+    once more projected and _kf again"""
     f = []
     rng = np.random.default_rng(14)
     K, r = 800, 768
     X = (rng.standard_normal((K, r)) * np.exp(rng.uniform(-3, 3, r))).astype(np.float32)
-    Q = oracle.borth(X)
     s = oracle.pow2_scale(oracle.amax(X))
     Z = oracle.dust(K, r)
-    KSb = oracle.split_rows(K, 10)
-    R = np.empty_like(X)
-    for j in range(0, r, 256):
-        W = X[:, j:j + 256] * s
-        if j:
-            KSp = oracle.split_rows(K, (j // 64) * 4)
-            W = oracle.project(R[:, :j], oracle.project(R[:, :j], W, KSp), KSp)
-        W = oracle.orth_dust(W, Z[:, j:j + 256], KSb)
-        if j:
-            W = oracle.orth_dust(oracle.project(R[:, :j], W, KSp), Z[:, j:j + 256], KSb)
-        R[:, j:j + 256] = W
-    if not np.array_equal(Q.view(np.uint32), R.view(np.uint32)):
-        f.append("borth is not kbig.py's composition of scale, projections and _kf")
+    for b, reorth in ((256, True), (128, True), (128, False)):
+        Q = oracle.borth(X, b, reorth)
+        KSb = oracle.split_rows(K, (b // 64) * (b // 64 + 1) // 2)
+        R = np.empty_like(X)
+        for j in range(0, r, b):
+            W = X[:, j:j + b] * s
+            if j:
+                KSp = oracle.split_rows(K, (j // 64) * (b // 64))
+                W = oracle.project(R[:, :j], oracle.project(R[:, :j], W, KSp), KSp)
+            W = oracle.orth_dust(W, Z[:, j:j + b], KSb)
+            if j and reorth:
+                W = oracle.orth_dust(oracle.project(R[:, :j], W, KSp), Z[:, j:j + b], KSb)
+            R[:, j:j + b] = W
+        if not np.array_equal(Q.view(np.uint32), R.view(np.uint32)):
+            f.append(f"borth(b={b}, reorth={reorth}) is not kbig.py's composition of scale, projections and _kf")
+    # b = 128 without the reorthogonalisation still gives the thin-QR Q on a well-conditioned X
+    Xw = rng.standard_normal((1000, 512)).astype(np.float32)
+    Qw = oracle.borth(Xw, 128, False).astype(np.float64)
+    if not np.abs(Qw - _thin_q(Xw)).max() <= 1e-4:
+        f.append("borth(b=128, reorth=False): not the thin-QR Q on a well-conditioned X")
     return f
 
 

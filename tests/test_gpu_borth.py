@@ -8,8 +8,8 @@ import torch
 
 import oracle
 from spanqr_amd import _lib, borth, orth
-from spanqr_amd.plan import get_plan, stream_handle
-from spanqr_amd.qrbench import gen
+from spanqr_amd.plan import get_borth_plan, get_plan, stream_handle
+from spanqr_amd.qrbench import gen, metrics
 
 from checks import assert_bits, gate
 
@@ -50,8 +50,37 @@ def test_borth_block_width_and_dispatch(cuda):
     Q = orth(X)
     E = Q.double().T @ Q.double() - torch.eye(576, device=cuda, dtype=torch.float64)
     assert E.abs().max().item() < 1e-5
-    with pytest.raises(ValueError):
-        borth(torch.randn(1024, 1024, device=cuda), b=512)
+    with pytest.raises(ValueError):                              # b not a multiple of 64: not built natively
+        borth(torch.randn(1024, 960, device=cuda), b=96)
+    X = torch.randn(1024, 768, generator=g).to(cuda)             # r % b != 0 above 512: full width -> torch.linalg.qr
+    Q = borth(X, b=512)
+    E = Q.double().T @ Q.double() - torch.eye(768, device=cuda, dtype=torch.float64)
+    assert E.abs().max().item() < 1e-5
+
+
+# borth(X, b, reorth) with the reference's parameters (kbig.py:69): its default b = 512, narrower blocks, and the
+# single projection without the reorthogonalisation
+OPTION_CASES = [(1024, 1024, 512, True, "mixed_c4"), (1000, 768, 128, True, "rank_half"),
+                (1000, 768, 128, False, "mixed_c4"), (1400, 640, 64, True, "zero"), (2048, 1536, 512, False, "dup_cols"),
+                (1200, 1024, 256, False, "ttf_cu4_t1e-2")]
+
+
+@pytest.mark.parametrize("K,r,b,reorth,name", OPTION_CASES)
+def test_borth_block_width_and_reorth_options(cuda, K, r, b, reorth, name):
+    c = next(gen.make_cases(K, r, [name], (0,)))
+    print(f"borth {K}x{r} b={b} reorth={reorth} {c.name}", flush=True)
+    Q = borth(c.X.to(cuda), b=b, reorth=reorth)
+    assert_bits(Q, oracle.borth(c.X.numpy(), b, reorth), f"borth b={b} reorth={reorth} {c.name} {K}x{r}")
+    if reorth:
+        gate(c.X, Q, f"borth b={b} reorth={reorth} {c.name}")
+    elif name == "mixed_c4":
+        # one projection per block leaves orthogonality at the level of a single Gram-Schmidt pass (2.2e-7 here;
+        # 1.1e-5 on the ill-conditioned TTF input, bit-identical to the oracle), and dust completions of dependent
+        # columns are not made orthogonal to the earlier blocks (kbig.py:91-92 is what does both), so without
+        # reorth: the reference's 1e-6 bar, on a well-conditioned input only
+        gate(c.X, Q, f"borth b={b} reorth={reorth} {c.name}", orth_tol=metrics.ORTH_TOL)
+    h = get_borth_plan(K, r, b, reorth, cuda)
+    assert h.query(_lib.Q_BLOCK_WIDTH) == b and h.query(_lib.Q_BLOCKS) == r // b
 
 
 def test_borth_large_shape_properties(cuda):
