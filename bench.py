@@ -101,7 +101,7 @@ def chol_steps_us(X):
     plan = get_plan(K, r, X.device)
     G, npart = stages.gram(X, kahan=True, use_scale=True)
     nb = r // 32
-    stamps = (ctypes.c_ulonglong * (6 * nb))()
+    stamps = (ctypes.c_ulonglong * (6 * nb + 2))()
     tick = ctypes.c_double()
     _lib.check(_lib.lib().spanqr_profile_chol(plan.handle, G.data_ptr(), npart.data_ptr(), 1e-7, 1e-8, stamps,
                                               ctypes.byref(tick), stream_handle(X.device)))

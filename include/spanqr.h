@@ -122,10 +122,12 @@ int spanqr_profile_orth(spanqr_plan* plan, const float* X, long ldx, float* Q, l
                         float tau, int ns, void* stream, float* ms, int max_n, int* n_out);
 
 /* Profiling form of the Cholesky stage (spanqr_stage_chol with npart): runs an instrumented copy of the kernel whose
- * workgroup 0 stamps the device wall clock, copies 6 r/32 stamps to host memory and waits for the stream: [0] kernel
- * start; for each 32-column diagonal step j, [1 + 4j] step start, [2 + 4j] tile factored and the next tile row
- * fetched, [3 + 4j] look-ahead done; [1 + 4 r/32] end; the rest zero. *tick_ns: nanoseconds per wall-clock tick. The
- * reference keeps similar stamps behind a debug define (candidates/cuk/chol.cu:17-23). */
+ * workgroup 0 stamps the device wall clock, copies 6 r/32 + 2 stamps to host memory and waits for the stream: [0]
+ * kernel start; for each 32-column diagonal step j (nb = r/32 steps), [1 + 4j] step start, [2 + 4j] tile factored and
+ * the next tile row fetched (the whole workgroup), [3 + 4j] look-ahead done, [4 + 4j] the tile factor's wavefront
+ * done; [1 + 4 nb] end; [2 + 4 nb + j] the next tile row's wavefronts done; [2 + 5 nb + j] the publishing wavefront
+ * done; zero where a step has no such work. *tick_ns: nanoseconds per wall-clock tick. The reference keeps similar
+ * stamps behind a debug define (candidates/cuk/chol.cu:17-23). */
 int spanqr_profile_chol(spanqr_plan* plan, const float* G, const double* npart, float alpha, float tau,
                         unsigned long long* stamps_out, double* tick_ns, void* stream);
 

@@ -637,8 +637,14 @@ __device__ __forceinline__ void panel32x2_inplace(Tile& A, Tile& B, const Tile& 
     __syncthreads();
 }
 
-// One wave, a whole 32x32 tile: out = in Li^T (out must not alias in). Each operand element is read from LDS once and
-// the four quadrants' MFMA chains (over m < 16 (bj + 1)) are interleaved.
+// quadrant masks: the row half h of the A operand (bi = h) and the row half of the B operand (bj = h) that a set of
+// 16x16 quadrants qd = 2 bi + bj uses
+constexpr bool qm_uses_a(int qm, int h) { return (qm >> (2 * h)) & 3; }
+constexpr bool qm_uses_b(int qm, int h) { return (qm >> h) & 5; }
+
+// One wave: out = in Li^T on the quadrants whose bit is set in QM (all four: a whole 32x32 tile; out must not alias
+// in). Each operand element is read from LDS once and the quadrants' MFMA chains (over m < 16 (bj + 1)) interleaved.
+template <int QM = 0xF>
 __device__ __forceinline__ void panel32_wave(Tile& out, const Tile& in, const Tile& li) {
     const int lane = threadIdx.x & 63, l16 = lane & 15, lk = lane >> 4;
     float a[2][8], b[2][8];
@@ -646,8 +652,8 @@ __device__ __forceinline__ void panel32_wave(Tile& out, const Tile& in, const Ti
     for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
-            a[h][kk] = in[16 * h + l16][4 * kk + lk];
-            b[h][kk] = (kk < 4 * (h + 1)) ? li[16 * h + l16][4 * kk + lk] : 0.0f;
+            a[h][kk] = qm_uses_a(QM, h) ? in[16 * h + l16][4 * kk + lk] : 0.0f;
+            b[h][kk] = (qm_uses_b(QM, h) && kk < 4 * (h + 1)) ? li[16 * h + l16][4 * kk + lk] : 0.0f;
         }
     __builtin_amdgcn_sched_barrier(0);
     f32x4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -656,18 +662,19 @@ __device__ __forceinline__ void panel32_wave(Tile& out, const Tile& in, const Ti
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
             const int bi = qd >> 1, bj = qd & 1;
-            if (kk < 4 * (bj + 1)) acc[qd] = mfma(a[bi][kk], b[bj][kk], acc[qd]);
+            if (((QM >> qd) & 1) && kk < 4 * (bj + 1)) acc[qd] = mfma(a[bi][kk], b[bj][kk], acc[qd]);
         }
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd)
+        if ((QM >> qd) & 1)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) out[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16] = acc[qd][v];
+            for (int v = 0; v < 4; ++v) out[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16] = acc[qd][v];
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the tile is written before this wave reads it back
     __builtin_amdgcn_wave_barrier();
 }
 
 // One wave: dst = C - Pi Pk^T on the 16x16 quadrants qd = 2 bi + bj whose bit is set in QM (dst may alias C);
-// operands read once, the quadrants' chains (over m = 0..31 from C) interleaved.
+// the operands those quadrants use read once, their chains (over m = 0..31 from C) interleaved.
 template <int QM>
 __device__ __forceinline__ void update32_wave_q(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk) {
     const int lane = threadIdx.x & 63, l16 = lane & 15, lk = lane >> 4;
@@ -676,14 +683,15 @@ __device__ __forceinline__ void update32_wave_q(Tile& dst, const Tile& C, const 
     for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
-            a[h][kk] = -Pi[16 * h + l16][4 * kk + lk];
-            b[h][kk] = Pk[16 * h + l16][4 * kk + lk];
+            a[h][kk] = qm_uses_a(QM, h) ? -Pi[16 * h + l16][4 * kk + lk] : 0.0f;
+            b[h][kk] = qm_uses_b(QM, h) ? Pk[16 * h + l16][4 * kk + lk] : 0.0f;
         }
     f32x4 acc[4];
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[qd][v] = C[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16];
+        for (int v = 0; v < 4; ++v)
+            acc[qd][v] = ((QM >> qd) & 1) ? C[16 * (qd >> 1) + 4 * lk + v][16 * (qd & 1) + l16] : 0.0f;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
@@ -941,7 +949,8 @@ size_t chol_lds_bytes(int r) {
 // shift = alpha * nrm added to the diagonal after the first load, tau = tau_rel * nrm + 1e-30 (kcholqr.py:107-109).
 // flags: [nb * nb] panel flags (L(i, j) published; (j, j): L(j, j) and Li_j), [nb] hand-over flags (tile row i),
 // [64] per-workgroup call counters. STAMP: workgroup 0 records wall_clock64() at 1 + 4j + s for step j: s = 0 step
-// start, 1 tile factored and row j+2 fetched, 2 look-ahead done; slot 0 is the kernel start, 1 + 4 nb the end.
+// start, 1 tile factored and row j+2 fetched, 2 look-ahead done, 3 wave 0's tile factor done; slot 0 is the kernel
+// start, 1 + 4 nb the end; 2 + 4 nb + j: wave 1's row work of step j done; 2 + 5 nb + j: wave 3's done.
 // Workgroups of eight wavefronts: waves 0-3 do all the work described here; waves 4-7 share the owners' row update
 // with them (two wavefronts per SIMD there, so one's LDS traffic overlaps the other's MFMA chain) and otherwise only
 // pass the same workgroup barriers.
@@ -1083,6 +1092,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
             if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
             if (w == 0) {
                 factor_inv32(bl0, bl1, pq, z.id, z.D[p], tau, z.dl[p], z.li[p], Li + (size_t)CB * j * CB);
+                if (STAMP && lane == 0) stamps[4 + 4 * j] = wall_clock64();
                 if (colcnt != nullptr && j == nb - 1) {
                     // the last column of the factor is Li_{nb-1} alone: packed, released and credited at once
                     store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[p], lane, 64);
@@ -1110,6 +1120,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                         store_tile(A + (size_t)CB * (j + 1) * r + CB * j, r, z.X1, lane, 64);
                         update32_wave_to<true>(z.D[pp], R1[3], z.P2[pp], z.P2[pp]);    // T(j+1, j+1)
                     }
+                    if (STAMP && lane == 0) stamps[2 + 5 * nb + j] = wall_clock64();
                 } else if (row2) {
                     const int i2 = j + 2, wl = (w - 1) * 64 + lane;
                     const float* rowp = A + (size_t)CB * i2 * r;
@@ -1144,6 +1155,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                             store_tile_op(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], lane, 64);
                         }
                     }
+                    if (STAMP && w == 1 && lane == 0) stamps[2 + 4 * nb + j] = wall_clock64();
                 }
             }
             __syncthreads();
@@ -1311,6 +1323,12 @@ __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __r
 // ---------------------------------------------------------------------------------------------------------------
 constexpr uint32_t FLAG_SPIN_LIMIT = 1u << 22;
 
+// A solve running in the Cholesky's launch writes Y with agent-scope (write-through) stores, so that the lines are not
+// left dirty in the L2 of an XCD whose Cholesky workgroups release there (a release writes every dirty line back)
+__device__ __forceinline__ void store_wt(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int Q>
 struct TrsmOps {
     float l[Q][2][8];    // L_jk B operands: [owned block][column half][kk]
@@ -1471,7 +1489,10 @@ __device__ __forceinline__ void trsm_body(const int rbi, const int z, const Mats
                 for (int v = 0; v < 4; ++v) {
                     const int rl = 16 * rb + 4 * lk + v, col = CB * k + 16 * cb + l16;
                     sY[rl * ldsy + col] = y[cb][v];
-                    if (full || row0 + rl < K) Y[(size_t)(row0 + rl) * ldy + col] = y[cb][v];
+                    if (full || row0 + rl < K) {
+                        if (WAIT) store_wt(&Y[(size_t)(row0 + rl) * ldy + col], y[cb][v]);
+                        else Y[(size_t)(row0 + rl) * ldy + col] = y[cb][v];
+                    }
                 }
             __builtin_amdgcn_wave_barrier();
         }
@@ -1547,9 +1568,11 @@ __global__ __launch_bounds__(64 * TRSM_NW) void k_trsm(const MatsIn As, long lda
 // k_trsm (acc_j starts at a_j, or fmaf(eps, z, s x) on pass 1; its updates by k ascending, each one MFMA chain over
 // the 32 columns of block k; the product with Li_k a chain over m < 16 (c/16 + 1)). No wavefront waits on another but
 // for column readiness (wave 0 polls the counters, the others an LDS word), so after the factor's last column only
-// one block product remains. Workgroup g of a matrix takes row blocks 8g..8g+7; waves past K have no work.
+// one block product remains. Workgroup g of a matrix takes row blocks wpg g .. wpg g + wpg - 1 (wpg <= 8: the plan
+// spreads the row blocks over every CU the Cholesky leaves free, one workgroup per CU, so that fewer wavefronts
+// share a SIMD); waves past wpg or past K have no work.
 template <bool PASS1, int NBC>
-__device__ __forceinline__ void trsm_wave_body(const int g, const int z, const MatsIn& As, long lda, int K,
+__device__ __forceinline__ void trsm_wave_body(const int g, const int z, const MatsIn& As, long lda, int K, int wpg,
                                                const uint32_t* __restrict__ amax_part, const float* __restrict__ Z,
                                                long ldz, float eps, const float* __restrict__ Lp, const MatsOut& Ys,
                                                long ldy, float* scal, const uint32_t* colcnt, uint32_t* err,
@@ -1574,9 +1597,9 @@ __device__ __forceinline__ void trsm_wave_body(const int g, const int z, const M
     }
     if (tid == 0) *sReady = 0u;
     __syncthreads();
-    const int row0 = (g * TRSM_NW + w) * 16;
-    if (w != 0 && row0 >= K) return;           // wave 0 (always in range) is the poller
-    const bool live = row0 < K;
+    const int row0 = (g * wpg + w) * 16;
+    if (w != 0 && (w >= wpg || row0 >= K)) return;   // wave 0 (always in range) is the poller
+    const bool live = w < wpg && row0 < K;
     // rows past K read row K-1 (in bounds) and are zeroed
     int rowc[4];
     bool rin[4];
@@ -1652,7 +1675,7 @@ __device__ __forceinline__ void trsm_wave_body(const int g, const int z, const M
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                if (rin[v]) Y[(size_t)(row0 + 4 * lk + v) * ldy + CB * k + 16 * cb + l16] = y[cb][v];
+                if (rin[v]) store_wt(&Y[(size_t)(row0 + 4 * lk + v) * ldy + CB * k + 16 * cb + l16], y[cb][v]);
                 sT[(4 * lk + v) * 33 + 16 * cb + l16] = y[cb][v];
             }
         if (k + 1 < NBC) {
@@ -1683,7 +1706,7 @@ struct CholArgs {
 };
 struct SolveArgs {
     MatsIn A; MatsOut Y; const uint32_t* amax_part; const float* Z; float* scal; long lda, ldz, ldy; float eps;
-    int K, nrb;
+    int K, nrb, wpg;   // wpg: row blocks (wavefronts) per workgroup of the one-wavefront-per-row-block solve
 };
 
 // Q > 0: the solve of k_trsm (Q column blocks per wave, RB row blocks of 16 per workgroup); Q = 0: trsm_wave_body
@@ -1698,7 +1721,7 @@ __global__ __launch_bounds__(64 * TRSM_NW) void k_chol_solve(const CholArgs c, c
     }
     const int b = blockIdx.x - nchol;
     if constexpr (Q == 0)
-        trsm_wave_body<PASS1, RB>(b % t.nrb, b / t.nrb, t.A, t.lda, t.K, t.amax_part, t.Z, t.ldz, t.eps, c.Lp, t.Y,
+        trsm_wave_body<PASS1, RB>(b % t.nrb, b / t.nrb, t.A, t.lda, t.K, t.wpg, t.amax_part, t.Z, t.ldz, t.eps, c.Lp, t.Y,
                                   t.ldy, t.scal, c.colcnt, c.bar, c.lim);
     else
         trsm_body<PASS1, Q, RB, true>(b % t.nrb, b / t.nrb, t.A, t.lda, t.K, c.r, t.amax_part, t.Z, t.ldz, t.eps,
@@ -1998,6 +2021,7 @@ struct spanqr_plan {
     bool trsm_rows = false;   // solve with a wavefront pair per 16 rows (k_trsm_rows) instead of k_trsm
     int solve_rb = 0;         // row blocks per solve workgroup in the Cholesky's launch (0: separate launches)
     int solve_nrb = 0;        // solve workgroups per matrix there
+    int solve_wpg = TRSM_NW;  // row blocks per workgroup of the one-wavefront-per-row-block solve
     int solve_q = 0;          // their column blocks per wave (k_trsm's Q), or 0: one wavefront per row block
     int cus = 0;              // the device's compute units
     uint32_t* colcnt = nullptr;   // per matrix: the column counters of the solve in the Cholesky's launch
@@ -2298,6 +2322,7 @@ int launch_chol_solve(spanqr_plan* p, float alpha, float tau, float* scal, hipSt
         t.eps = eps;
         t.K = p->K;
         t.nrb = p->solve_nrb;
+        t.wpg = p->solve_wpg;
         const dim3 grid(nz * (p->chol_grid + p->solve_nrb));
         if (pass1) launch_fused<true>(q, q ? p->solve_rb : p->r / CB, grid, lds, st, c, t);
         else launch_fused<false>(q, q ? p->solve_rb : p->r / CB, grid, lds, st, c, t);
@@ -2488,13 +2513,16 @@ int plan_device_setup(spanqr_plan* p, int device) {
         HIPCHK(hipDeviceGetAttribute(&maxsh, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
         const int avail = cus - p->chol_grid;
         const int rowblocks = (p->K + 15) / 16;
-        int q = (r / CB + TRSM_NW - 1) / TRSM_NW, rb = 1, nwg = rowblocks;
+        int q = (r / CB + TRSM_NW - 1) / TRSM_NW, rb = 1, nwg = rowblocks, wpg = TRSM_NW;
         if (rowblocks > avail) {
             if (r <= 256 && (r / CB) % 2 != 0) {
                 nwg = avail + 1;   // the one-wavefront solve is built for an even number of column blocks: separate
             } else if (r <= 256) {
+                // one wavefront per row block, as few per workgroup (and so per CU) as the free CUs allow
                 q = 0;
-                nwg = (rowblocks + TRSM_NW - 1) / TRSM_NW;
+                wpg = (rowblocks + avail - 1) / avail;
+                if (wpg > TRSM_NW) wpg = TRSM_NW;
+                nwg = (rowblocks + wpg - 1) / wpg;
             } else {
                 rb = 2;
                 nwg = (rowblocks + 1) / 2;
@@ -2505,6 +2533,7 @@ int plan_device_setup(spanqr_plan* p, int device) {
             p->solve_q = q;
             p->solve_rb = rb;
             p->solve_nrb = nwg;
+            p->solve_wpg = wpg;
         }
     }
     return SPANQR_OK;
@@ -2757,7 +2786,7 @@ long spanqr_plan_query(const spanqr_plan* p, int what) {
         case SPANQR_Q_BLOCK_WIDTH: return p->bw;
         case SPANQR_Q_SOLVE_ROWS: {
             const spanqr_plan* q = p->blk ? p->blk : p;
-            return q->solve_rb == 0 ? 0 : (q->solve_q == 0 ? 16L * TRSM_NW : 16L * q->solve_rb);
+            return q->solve_rb == 0 ? 0 : (q->solve_q == 0 ? 16L * q->solve_wpg : 16L * q->solve_rb);
         }
         default: return -1;
     }
@@ -2968,10 +2997,10 @@ int spanqr_profile_chol(spanqr_plan* p, const float* G, const double* npart, flo
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
-    HIPCHK(hipMemsetAsync(p->stamps, 0, (size_t)6 * p->NB * sizeof(uint64_t), st));
+    HIPCHK(hipMemsetAsync(p->stamps, 0, (size_t)(6 * p->NB + 2) * sizeof(uint64_t), st));
     int rc = launch_chol(p, alpha, tau, p->chscal, st, 16 * p->U, 1, true);
     if (rc) return rc;
-    HIPCHK(hipMemcpyAsync(stamps_out, p->stamps, (size_t)6 * p->NB * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipMemcpyAsync(stamps_out, p->stamps, (size_t)(6 * p->NB + 2) * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));
     int khz = 0;
     HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, p->device));

@@ -145,10 +145,11 @@ def test_solve_runs_in_the_cholesky_launch(cuda, K, r):
 
 @pytest.mark.parametrize("K,r", [(5000, 64), (4500, 128), (4111, 192), (4100, 256), (9217, 256)])
 def test_tall_solve_in_cholesky_launch(cuda, K, r):
-    """X taller than one row block per CU: the solve in the Cholesky's launch runs one wavefront per 16 rows, at every
-    column-block count (r/32 = 2, 4, 6, 8) and with a ragged last row block"""
+    """X taller than one row block per CU: the solve in the Cholesky's launch runs one wavefront per 16 rows, 2 to 8
+    of them per workgroup (as many workgroups as CUs are free), at every column-block count (r/32 = 2, 4, 6, 8), with a
+    ragged last row block and a last workgroup with fewer row blocks than the others"""
     plan = get_plan(K, r, cuda)
-    assert plan.solve_rows == 128, f"{K}x{r}: expected the wavefront-per-row-block solve, got {plan.solve_rows}"
+    assert 32 <= plan.solve_rows <= 128, f"{K}x{r}: expected the wavefront-per-row-block solve, got {plan.solve_rows}"
     g = torch.Generator().manual_seed(K + r)
     X = torch.randn(K, r, generator=g) * torch.logspace(0, -3, r)
     print(f"tall solve {K}x{r}", flush=True)
