@@ -288,14 +288,28 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
             f32x4 part[2];
 #pragma unroll
             for (int a = 0; a < 2; ++a) part[a] = KAHAN ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[a];
+            float xa[BK / 4], xb[BK / 4], yb[BK / 4];
 #pragma unroll
             for (int kk = 0; kk < BK / 4; ++kk) {
                 const int kr = h * BK + 4 * kk + lk;
-                const float a0 = sA[kr][qi * 32 + l16], a1 = sA[kr][qi * 32 + 16 + l16];
-                const float b0 = sB[kr][qj * 32 + 16 * hb + l16];
-                part[0] = mfma(a0, b0, part[0]);
-                part[1] = mfma(a1, b0, part[1]);
+                xa[kk] = sA[kr][qi * 32 + l16];
+                xb[kk] = sA[kr][qi * 32 + 16 + l16];
+                yb[kk] = sB[kr][qj * 32 + 16 * hb + l16];
             }
+#pragma unroll
+            for (int kk = 0; kk < BK / 4; ++kk) {
+                part[0] = mfma(xa[kk], yb[kk], part[0]);
+                part[1] = mfma(xb[kk], yb[kk], part[1]);
+            }
+            // issue order: the first two steps' operands, then each step's two MFMAs followed by the reads of the
+            // step two ahead, so the LDS latency overlaps the chains
+            __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+            for (int g = 0; g < BK / 4 - 2; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 #pragma unroll
             for (int a = 0; a < 2; ++a) {
                 if (KAHAN) {
