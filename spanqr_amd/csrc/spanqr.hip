@@ -1217,44 +1217,27 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 if (j >= 1) credit(colcnt, j - 1);   // the release covers L(i, j-1)'s packed form, stored after it
             }
             store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j]);   // for the solve only
-            // block j's panels of the rows between: L(k, j), k = j+1..i-1, all in LDS before the updates. At the
-            // last block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed. Rows j+1 and j+2
+            // block j's panels of the rows between: L(k, j), k = j+1..i-1, each in LDS before the tile it updates. At
+            // the last block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed. Rows j+1 and j+2
             // are workgroup 0's: their panels are formed here, as workgroup 0 forms them. Row j+3 has just been
             // handed to workgroup 0 (before block j; row 3 never had an owner): its panel too is formed here, from
             // the handed-over T(j+3, j). Rows j+4.. publish their own.
             panel32x2_inplace(op[j + 1], op[j + 2], lij, q4);             // L(j+1, j), L(j+2, j)
             const int kend = (j + 4 == i) ? i - 1 : i;
             const bool own3 = j + 3 < kend;
-            if (w == 0) {
-                const int k = j + 3 + lane;
-                const uint32_t* f = nullptr;
-                if (k < kend) f = (k != j + 3) ? flagL + k * nb + j : (k >= 4 ? flagT + k : nullptr);
-                wait_flags_wave(f, ep, err, dead, lim);
-            }
-            __syncthreads();
-            if (q4)
-                load_tiles<CH_MAXROW, 256>(&op[j + 3], kend - j - 3, r, 0u, 0.f, tid, [&](int q) {
-                    const int k = j + 3 + q;
-                    return (k == j + 3 ? A : L) + (size_t)CB * k * r + (size_t)CB * j;
-                });
-            __syncthreads();
-            if (own3) panel32(op[j + 3], op[j + 3], lij, q4);     // L(j+3, j)
-            {
-                // every tile's quadrant in one phase (the tiles are independent): waves w and w + 4 take quadrant
-                // (bi, bj) = (w & 3) of alternate tiles of the row (the tiles k = j+1..i in order, without T(i, i-1)
-                // at the last block and without the upper quadrant of T(i, i)); the panel's A operands stay in
-                // registers, and the next tile's B operands and accumulator are read while this tile's chain runs
-                const int l16 = lane & 15, lk = lane >> 4, qd = w & 3, bi = qd >> 1, bj = qd & 1;
+            // Row i's update by block j, every tile's quadrant chain in one phase (the tiles are independent): waves
+            // w and w + 4 take quadrant (bi, bj) = (w & 3) of alternate tiles of a sequence (without the upper
+            // quadrant of T(i, i)); the panel's A operands stay in registers, and the next tile's B operands and
+            // accumulator are read while this tile's chain runs. For long rows, first the tiles whose panels this
+            // workgroup has formed -- T(i, j+1), T(i, j+2) and T(i, i) -- while the other rows' panel flags are in
+            // flight; then, once those are loaded, T(i, j+3..kend-1) (T(i, i-1) at the last block, j = i-4, is left
+            // to workgroup 0).
+            const int l16 = lane & 15, lk = lane >> 4, qd = w & 3, bi = qd >> 1, bj = qd & 1;
+            const bool upq = (bi == 0 && bj == 1);
+            auto update_tiles = [&](int n, auto kof) {
                 float an[8];
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk) an[kk] = -rt[j][16 * bi + l16][4 * kk + lk];
-                const bool upq = (bi == 0 && bj == 1);
-                const int n = i - j - (j + 4 == i ? 1 : 0) - (upq ? 1 : 0);   // tiles in this quadrant's sequence
-                auto kof = [&](int t) {                                       // tile t of the sequence, t < n
-                    int k = j + 1 + t;
-                    if (j + 4 == i && k >= i - 1) ++k;
-                    return k;
-                };
                 auto fetch = [&](int k, float (&bv)[8], f32x4& acc) {
                     const Tile& Pk = (k == i) ? rt[j] : op[k];
 #pragma unroll
@@ -1271,8 +1254,8 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
 #pragma unroll
                     for (int v = 0; v < 4; ++v) rt[k][16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
                 };
-                // In-order issue: the next tile's reads go between the chain's first MFMAs (two after each), where they
-                // issue while the previous MFMA runs and complete before the chain ends.
+                // In-order issue: the next tile's reads go between the chain's first MFMAs (two after each), where
+                // they issue while the previous MFMA runs and complete before the chain ends.
                 auto interleave = [&]() {
 #pragma unroll
                     for (int g = 0; g < 3; ++g) {
@@ -1298,8 +1281,34 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     interleave();
                     t = tn;
                 }
-                __syncthreads();
+            };
+            // T(i, j+1), T(i, j+2), T(i, i) (the upper quadrant's sequence stops before T(i, i)) -- where rows are
+            // long (r > 256); with at most 8 tiles per row the flags arrive before these would finish, and the row
+            // runs as one sequence after them
+            const bool early = nb > 8;
+            if (early) update_tiles(upq ? 2 : 3, [&](int t) { return t < 2 ? j + 1 + t : i; });
+            if (w == 0) {
+                const int k = j + 3 + lane;
+                const uint32_t* f = nullptr;
+                if (k < kend) f = (k != j + 3) ? flagL + k * nb + j : (k >= 4 ? flagT + k : nullptr);
+                wait_flags_wave(f, ep, err, dead, lim);
             }
+            __syncthreads();
+            if (q4)
+                load_tiles<CH_MAXROW, 256>(&op[j + 3], kend - j - 3, r, 0u, 0.f, tid, [&](int q) {
+                    const int k = j + 3 + q;
+                    return (k == j + 3 ? A : L) + (size_t)CB * k * r + (size_t)CB * j;
+                });
+            __syncthreads();
+            if (own3) panel32(op[j + 3], op[j + 3], lij, q4);     // L(j+3, j)
+            if (early) {
+                update_tiles(kend - j - 3, [&](int t) { return j + 3 + t; });
+            } else {
+                // T(i, j+1..kend-1), then T(i, i)
+                const int n = kend - j - (upq ? 1 : 0);
+                update_tiles(n, [&](int t) { return j + 1 + t < kend ? j + 1 + t : i; });
+            }
+            __syncthreads();
             if (j + 4 == i) {
                 // hand T(i, i-3..i) to workgroup 0
                 for (int t = 0; t < 4; ++t)
