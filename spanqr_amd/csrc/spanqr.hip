@@ -419,10 +419,11 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 //     plus the owner's panel L(j+2, j-2)) while wave 3 publishes the previous step's L tiles and Li; then wave 1
 //     forms the panel L(j+2, j-1) (the previous step's Li_{j-1}, L(j, j-1), L(j+1, j-1) are still in LDS), wave 2
 //     applies the block j-2 update of T(j+2, j+1) that the owner leaves out, and the two waves apply block j-1 to
-//     T(j+2, j) and the lower half of T(j+2, j+2) (wave 1), T(j+2, j+1) and the rest (wave 2); wave 3, after
-//     publishing, applies block j-1 to T(j+1, j) and T(j+1, j+1). Then all waves form the panels L(j+1, j),
-//     L(j+2, j) and apply column block j to T(j+1, j+1), the tile the next step factors (look-ahead over the next two
-//     tile rows; block j on the rest of row j+2 is wave 3's work in the next step).
+//     T(j+2, j) and the lower half of T(j+2, j+2) (wave 1), T(j+2, j+1) and the rest (wave 2); wave 7 forms the
+//     previous step's L(j+1, j-1), which wave 3 publishes and waves 2-3 use; wave 3, after publishing, applies block
+//     j-1 to T(j+1, j) and T(j+1, j+1). Then waves 0-3 form the panel L(j+1, j) and apply column block j to
+//     T(j+1, j+1), the tile the next step factors (look-ahead over the next two tile rows; block j on the rest of
+//     row j+2 is wave 3's work in the next step).
 //   * Workgroup i-3 owns tile row i >= 4 for the whole factorisation, in LDS. For column block j = 0..i-4 in order:
 //     panel L(i, j) = T(i, j) Li_j^T (published), then T(i, k) -= L(i, j) L(k, j)^T for k = j+1..i with the other
 //     rows' panels of block j fetched together (at its last block, j = i-4, T(i, i-1) is left to workgroup 0); after
@@ -934,6 +935,23 @@ __device__ __forceinline__ void wave_group_barrier(uint32_t* ctr, uint32_t targe
     __builtin_amdgcn_wave_barrier();
 }
 
+// Wait (lane 0 polls, bounded) until an LDS word that another wavefront of the workgroup raises reaches `target`.
+__device__ __forceinline__ void wait_lds(const uint32_t* word, uint32_t target, uint32_t* err, bool& dead,
+                                         uint32_t lim) {
+    if ((threadIdx.x & 63) == 0) {
+        uint32_t n = 0;
+        while (!dead && __hip_atomic_load(word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+            if (++n > lim) {
+                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                dead = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
 constexpr int CH_MAXROW = 16;      // tiles in a tile row at most (r <= 512)
 constexpr int CH_WG0_TILES = 24;   // workgroup 0: D[2], X1, R2[2][5], dl[2], li[2], P1[2], P2[2], C2[2], id
 
@@ -965,9 +983,9 @@ size_t chol_lds_bytes(int r) {
 // [64] per-workgroup call counters. STAMP: workgroup 0 records wall_clock64() at 1 + 4j + s for step j: s = 0 step
 // start, 1 tile factored and row j+2 fetched, 2 look-ahead done, 3 wave 0's tile factor done; slot 0 is the kernel
 // start, 1 + 4 nb the end; 2 + 4 nb + j: wave 1's row work of step j done; 2 + 5 nb + j: wave 3's done.
-// Workgroups of eight wavefronts: waves 0-3 do all the work described here; waves 4-7 share the owners' row update
-// with them (two wavefronts per SIMD there, so one's LDS traffic overlaps the other's MFMA chain) and otherwise only
-// pass the same workgroup barriers.
+// Workgroups of eight wavefronts: waves 0-3 do the work described here (and wave 7 of workgroup 0 the L(j+1, j-1)
+// above); waves 4-7 share the owners' row update with them (two wavefronts per SIMD there, so one's LDS traffic
+// overlaps the other's MFMA chain) and otherwise only pass the same workgroup barriers.
 // colcnt (may be null): per column block k, a counter (stride CC_STRIDE) that every producer of the packed operands
 // of column k (Li_k and L(i, k), i > k) raises once those are released, for the solve that runs in the same launch:
 // owner i credits column j-1 when it publishes L(i, j) and column i-4 when it hands its row over; workgroup 0 credits
@@ -1008,7 +1026,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
     bool dead = false;
     if (STAMP && b == 0 && tid == 0) stamps[0] = wall_clock64();
     const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
-    // misc: [0..2] nrm, shift, tau; [4] the waves 1-2 barrier counter; [32..63] the tile factor's diagonal;
+    // misc: [0..2] nrm, shift, tau; [4] the waves 1-2 barrier counter; [5] the last step whose L(j+2, j) is formed; [32..63] the tile factor's diagonal;
     // [64..159] and [160..255] tile-factor broadcast buffers
     float* misc = reinterpret_cast<float*>(chol_lds);
     Tile* tiles = reinterpret_cast<Tile*>(misc + 256);
@@ -1043,6 +1061,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_down(s, off);
         if (lane == 0) {
             reinterpret_cast<uint32_t*>(misc)[4] = 0u;
+            reinterpret_cast<uint32_t*>(misc)[5] = 0u;
             if (nnp > 0) {
                 const float nrm = sqrtf((float)s);
                 misc[0] = nrm;
@@ -1077,6 +1096,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         }
         CholWG0& z = *reinterpret_cast<CholWG0*>(tiles);
         uint32_t* bar12 = reinterpret_cast<uint32_t*>(misc + 4);    // waves 1-2 barrier counter (zeroed above)
+        uint32_t* p2done = reinterpret_cast<uint32_t*>(misc + 5);   // L(j+2, j) of step j formed: j + 1 (zeroed above)
         uint32_t n12 = 0;
         // wave 3: publish L(j, j), Li_j, L(j+1, j), L(j+2, j) of step j (parity q = j & 1)
         // What the owners need for column block j -- Li_j (into its place in Li), T(j+1, j) and T(j+2, j) through
@@ -1096,10 +1116,13 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
             }
             store_tile_lower(L + o * r + o, r, z.dl[q], false, lane, 64);
             if (j + 1 < nb) store_tile(L + (o + CB) * r + o, r, z.P1[q], lane, 64);
-            if (j + 2 < nb) store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
             store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[q], lane, 64);
             if (j + 1 < nb) store_tile_op(Lp + (size_t)op_pair(j + 1, j) * CB * CB, z.P1[q], lane, 64);
-            if (j + 2 < nb) store_tile_op(Lp + (size_t)op_pair(j + 2, j) * CB * CB, z.P2[q], lane, 64);
+            if (j + 2 < nb) {
+                wait_lds(p2done, (uint32_t)j + 1, err, dead, lim);   // L(j+2, j), formed by wave 7
+                store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
+                store_tile_op(Lp + (size_t)op_pair(j + 2, j) * CB * CB, z.P2[q], lane, 64);
+            }
         };
         for (int j = 0; j < nb; ++j) {
             const int p = j & 1, pp = p ^ 1;
@@ -1161,6 +1184,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                             store_tile(A + (size_t)CB * (j + 2) * r + CB * j, r, R2[1], lane, 64);
                             update32_wave_q<0xC>(R2[3], R2[3], z.C2[p], z.C2[p]);      // T(j+2, j+2), lower half
                         } else {
+                            wait_lds(p2done, (uint32_t)j, err, dead, lim);             // L(j+1, j-1) formed
                             update32_wave<false>(R2[2], z.C2[p], z.P2[pp]);            // T(j+2, j+1)
                             update32_wave_q<0x1>(R2[3], R2[3], z.C2[p], z.C2[p]);      // T(j+2, j+2), quadrant (0, 0)
                             // L(j+2, j-1) for the output and the later kernels (the owners form their own copy)
@@ -1171,17 +1195,19 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     }
                     if (STAMP && w == 1 && lane == 0) stamps[2 + 4 * nb + j] = wall_clock64();
                 }
+            } else if (w == 7 && j >= 1 && j + 1 < nb) {
+                // the previous step's L(j+1, j-1) = T(j+1, j-1) Li_{j-1}^T (row j+1 as fetched at step j-1), which
+                // only this step's waves 2 and 3 use: formed here, beside the factor, not in the look-ahead
+                panel32_wave(z.P2[pp], z.R2[pp][1], z.li[pp]);
+                if (lane == 0) __hip_atomic_store(p2done, (uint32_t)j, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
             __syncthreads();
             if (STAMP && tid == 0) stamps[2 + 4 * j] = wall_clock64();
-            // look-ahead, the part the next factor needs: L(j+1, j) (and L(j+2, j), in the same phase), then block j
-            // on T(j+1, j+1); block j on tile row j+2 is left to wave 3 of the next step
+            // look-ahead, the part the next factor needs: L(j+1, j), then block j on T(j+1, j+1); L(j+2, j) is formed
+            // by wave 7 and block j on tile row j+2 applied by wave 3, both in the next step
             const bool q4 = w < 4;
-            if (j + 2 < nb) {
-                panel32x2(z.P1[p], z.X1, z.P2[p], z.R2[p][1], z.li[p], q4);    // L(j+1, j), L(j+2, j)
-                update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true, q4);
-            } else if (j + 1 < nb) {
-                panel32(z.P1[p], z.X1, z.li[p], q4);
+            if (j + 1 < nb) {
+                panel32(z.P1[p], z.X1, z.li[p], q4);                           // L(j+1, j)
                 update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true, q4);
             }
             if (STAMP && tid == 0) stamps[3 + 4 * j] = wall_clock64();
