@@ -77,6 +77,18 @@ def test_plan_create_without_gpu_fails_cleanly():
     assert _lib.lib().spanqr_last_error()
 
 
+def test_borth_plan_arguments_checked_before_any_device_work():
+    """spanqr_plan_create_borth (kbig.py:69's b and reorth): b a multiple of 64 in [64, 512], r > b a multiple of b up
+    to 4096, K >= r -- refused with SPANQR_EINVAL and no plan before any device call"""
+    h = ctypes.c_void_p()
+    f = _lib.lib().spanqr_plan_create_borth
+    for K, r, b in [(1024, 1024, 96), (1024, 1024, 32), (1024, 1024, 576), (1024, 512, 512), (1024, 768, 512),
+                    (1000, 1024, 256), (8192, 8192, 512), (2048, 1024, 0)]:
+        assert f(K, r, b, 1, 0, ctypes.byref(h)) == -1 and not h.value, (K, r, b)
+        assert _lib.lib().spanqr_last_error()
+    assert f(1024, 1024, 256, 1, 0, None) == -1
+
+
 def test_bad_shapes_rejected_before_any_device_work():
     h = ctypes.c_void_p()
     assert _lib.lib().spanqr_plan_create(100, 128, 0, ctypes.byref(h)) == -1
