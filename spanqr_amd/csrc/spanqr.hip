@@ -501,9 +501,9 @@ __device__ __forceinline__ void load_tiles(Tile* dst, int n, int ld, uint32_t di
             }
 }
 
-// As load_tiles, without diagonal shifts, tile q from srcf(q) with row stride ldf(q)
-template <int NMAX, int NTHR, class SrcF, class LdF>
-__device__ __forceinline__ void load_tiles_ld(Tile* dst, int n, int t, SrcF srcf, LdF ldf) {
+// As load_tiles without shifts, tile q from srcf(q) with row stride ldf(q) into dstf(q)
+template <int NMAX, int NTHR, class DstF, class SrcF, class LdF>
+__device__ __forceinline__ void load_tiles_to(int n, int t, DstF dstf, SrcF srcf, LdF ldf) {
     constexpr int PER = 256 / NTHR;
     float4 v[NMAX][PER];
 #pragma unroll
@@ -516,15 +516,17 @@ __device__ __forceinline__ void load_tiles_ld(Tile* dst, int n, int t, SrcF srcf
             }
 #pragma unroll
     for (int q = 0; q < NMAX; ++q)
-        if (q < n)
+        if (q < n) {
+            Tile& d = dstf(q);
 #pragma unroll
             for (int u = 0; u < PER; ++u) {
                 const int e = t + u * NTHR, row = e >> 3, c4 = e & 7;
-                dst[q][row][4 * c4 + 0] = v[q][u].x;
-                dst[q][row][4 * c4 + 1] = v[q][u].y;
-                dst[q][row][4 * c4 + 2] = v[q][u].z;
-                dst[q][row][4 * c4 + 3] = v[q][u].w;
+                d[row][4 * c4 + 0] = v[q][u].x;
+                d[row][4 * c4 + 1] = v[q][u].y;
+                d[row][4 * c4 + 2] = v[q][u].z;
+                d[row][4 * c4 + 3] = v[q][u].w;
             }
+        }
 }
 
 // the lower triangle of a diagonal tile (zeros above the diagonal), straight and transposed
@@ -954,6 +956,36 @@ __device__ __forceinline__ void wait_lds(const uint32_t* word, uint32_t target, 
 
 constexpr int CH_MAXROW = 16;      // tiles in a tile row at most (r <= 512)
 constexpr int CH_WG0_TILES = 24;   // workgroup 0: D[2], X1, R2[2][5], dl[2], li[2], P1[2], P2[2], C2[2], id
+// Owner parts: tile row i (i + 1 tiles) is split over P = ceil((i + 1) / OWNER_W) workgroups, each holding a run of
+// consecutive tiles T(i, s..e-1): widths floor((i + 1) / P), the last (i + 1) % P parts one wider, so that for
+// OWNER_W >= 6 the last part (which holds T(i, i-3..i) and hands them to workgroup 0) has at least 4 tiles for every
+// row i >= 4. A part's work per column block shrinks with its width, so long rows keep up with workgroup 0's steps.
+constexpr int OWNER_W = 6;   // (6: the best of 6, 7, 8 and 16 measured at r = 512)
+static_assert(OWNER_W >= 6 && OWNER_W <= CH_MAXROW, "owner parts: the last part of a row needs 4 tiles");
+__host__ __device__ constexpr int row_parts(int i) { return (i + OWNER_W) / OWNER_W; }
+__host__ __device__ inline void part_range(int i, int q, int& s, int& e) {
+    const int n = i + 1, P = row_parts(i), base = n / P, lo = P - n % P;   // parts q < lo have base tiles
+    s = q * base + (q > lo ? q - lo : 0);
+    e = s + base + (q >= lo ? 1 : 0);
+}
+// workgroup b >= 1 of the Cholesky: row i, tiles [s, e); the rows' parts in order of i, then of s
+__device__ inline void owner_part(int b, int nb, int& i, int& s, int& e) {
+    int q = b - 1;
+    i = 4;
+    while (i < nb - 1 && q >= row_parts(i)) {
+        q -= row_parts(i);
+        ++i;
+    }
+    part_range(i, q, s, e);
+}
+// LDS tiles of an owner part: its row tiles and their panels (at most min(nb, OWNER_W) each), Li_j and L(i, j)
+__host__ __device__ constexpr int owner_lds_tiles(int nb) { return 2 * (nb < OWNER_W ? nb : OWNER_W) + 2; }
+// workgroups of one Cholesky: workgroup 0 and the parts of rows 4..nb-1
+constexpr int chol_workgroups(int nb) {
+    int n = 1;
+    for (int i = 4; i < nb; ++i) n += row_parts(i);
+    return n;
+}
 
 struct CholWG0 {
     Tile D[2];      // D[j & 1]: T(j, j) through block j-1 (factored at step j); D[(j+1) & 1]: T(j+1, j+1)
@@ -969,8 +1001,7 @@ struct CholWG0 {
 };
 
 size_t chol_lds_bytes(int r) {
-    const int nb = r / CB;
-    const int owner_tiles = 2 * nb;       // a tile row (up to nb tiles), the panels of one column block and Li_j
+    const int owner_tiles = owner_lds_tiles(r / CB);
     const int tiles = owner_tiles > CH_WG0_TILES ? owner_tiles : CH_WG0_TILES;
     return (size_t)tiles * sizeof(Tile) + 256 * sizeof(float);
 }
@@ -992,6 +1023,8 @@ size_t chol_lds_bytes(int r) {
 // column k at the release that opens step k+2 (its stores of column k's operands completed during step k+1), column
 // nb-2 at a release of its own in the last step, and column nb-1 (Li_{nb-1} alone) right after the last tile factor.
 // Column k is complete at 1 + max(0, nb - 4 - k) credits; the counters start at zero.
+static_assert(chol_workgroups(CH_MAXROW) <= FLAG_STRIDE - CH_MAXROW * (CH_MAXROW + 1),
+              "a call counter per Cholesky workgroup after the panel and hand-over flags");
 constexpr int CC_STRIDE = 16;   // uint32 words between column counters (one 64-byte line each)
 static_assert(CC_STRIDE == 16 && CH_MAXROW == 16, "k_reduce clears the column counters with stride 16, 16 per matrix");
 
@@ -1030,17 +1063,20 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
     // [64..159] and [160..255] tile-factor broadcast buffers
     float* misc = reinterpret_cast<float*>(chol_lds);
     Tile* tiles = reinterpret_cast<Tile*>(misc + 256);
+    // an owner part: tile row oi, tiles T(oi, os..oe-1)
+    int oi = 0, os = 0, oe = 0;
+    if (b > 0) owner_part(b, nb, oi, os, oe);
     // Waves 1-2 load the workgroup's first tiles (workgroup 0: T(0, 0), T(1, 1), T(1, 0) into D[0], D[1], X1; an
-    // owner: its tile row) while wave 0 sums the norm partials; the diagonal shift is added once it is known (the same
-    // single addition as on a shifted load).
+    // owner part: its tiles of the row) while wave 0 sums the norm partials; the diagonal shift is added once it is
+    // known (the same single addition as on a shifted load).
     if (w == 1 || w == 2) {
         if (b == 0) {
             load_tiles<3, 128>(tiles, nb > 1 ? 3 : 1, r, 0u, 0.f, tid - 64, [&](int q) {
                 return A + (q == 0 ? (size_t)0 : (size_t)CB * r + (q == 1 ? CB : 0));
             });
         } else {
-            load_tiles<CH_MAXROW, 128>(tiles, b + 4, r, 0u, 0.f, tid - 64,
-                                       [&](int q) { return A + (size_t)CB * (b + 3) * r + (size_t)CB * q; });
+            load_tiles<OWNER_W, 128>(tiles, oe - os, r, 0u, 0.f, tid - 64,
+                                     [&](int q) { return A + (size_t)CB * oi * r + (size_t)CB * (os + q); });
         }
     }
     if (w == 3 && b == 0) {
@@ -1080,8 +1116,8 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         if (b == 0) {
             tiles[0][tid][tid] = tiles[0][tid][tid] + shift;
             if (nb > 1) tiles[1][tid][tid] = tiles[1][tid][tid] + shift;
-        } else {
-            tiles[b + 3][tid][tid] = tiles[b + 3][tid][tid] + shift;
+        } else if (oe == oi + 1) {
+            tiles[oi - os][tid][tid] = tiles[oi - os][tid][tid] + shift;
         }
     }
     __syncthreads();
@@ -1215,61 +1251,79 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         if (w == 3) publish(nb - 1);
         if (STAMP && tid == 0) stamps[1 + 4 * nb] = wall_clock64();
     } else {
-        // tile row i = b + 3 (i >= 4): rt[k] = T(i, k); op[k] = L(k, j) of the current column block
-        const int i = b + 3;
+        // Owner part: tile row i, tiles T(i, s..e-1) in LDS. rt[k - s] = T(i, k); pn[k - s] = L(k, j) of the current
+        // column block for the part's columns k < i; li = Li_j; pin = L(i, j) when another part of the row forms it
+        // (the part that holds T(i, j)). Each part runs blocks j until its tiles are done: the last part (which holds
+        // T(i, i)) to block i-4, after which it hands T(i, i-3..i) to workgroup 0; an earlier part to block e-1, its
+        // last panel.
+        const int i = oi, s = os, e = oe;
+        const bool last = e == i + 1;
+        const int jl = last ? i - 4 : e - 1;
+        const int pw = owner_lds_tiles(nb) / 2 - 1;
         Tile* rt = tiles;
-        Tile* op = tiles + nb;
-        for (int j = 0; j + 4 <= i; ++j) {
-            // workgroup 0's block j: Li_j into op[j], T(j+1, j) and T(j+2, j) (through block j-1) into op[j+1..j+2]
+        Tile* pn = tiles + pw;
+        Tile& li = tiles[2 * pw];
+        Tile& pin = tiles[2 * pw + 1];
+        const int l16 = lane & 15, lk = lane >> 4, qd = w & 3, bi = qd >> 1, bj = qd & 1;
+        const bool upq = (bi == 0 && bj == 1);
+        for (int j = 0; j <= jl; ++j) {
             const bool q4 = w < 4;
+            const bool mine = j >= s;                               // this part forms L(i, j)
+            const bool h1 = j + 1 >= s && j + 1 < e, h2 = j + 2 >= s && j + 2 < e;
+            // workgroup 0's block j: Li_j into li; T(j+1, j) and T(j+2, j) (through block j-1), where they are in
+            // the part's columns, into their panel slots
             if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead, lim);
             __syncthreads();
             if (q4)
-                load_tiles_ld<3, 256>(&op[j], 3, tid,
-                                  [&](int q) {
-                                      return q == 0 ? Li + (size_t)CB * j * CB
-                                                    : A + (size_t)CB * (j + q) * r + (size_t)CB * j;
-                                  },
-                                  [&](int q) { return q == 0 ? CB : r; });
+                load_tiles_to<3, 256>(1 + (h1 ? 1 : 0) + (h2 ? 1 : 0), tid,
+                                      [&](int q) -> Tile& { return q == 0 ? li : pn[j + q + (h1 ? 0 : 1) - s]; },
+                                      [&](int q) {
+                                          return q == 0 ? Li + (size_t)CB * j * CB
+                                                        : A + (size_t)CB * (j + q + (h1 ? 0 : 1)) * r + (size_t)CB * j;
+                                      },
+                                      [&](int q) { return q == 0 ? CB : r; });   // Li_j's rows are 32 apart
             __syncthreads();
-            const Tile& lij = op[j];
-            // panel L(i, j) = T(i, j) Li_j^T, published before anything else (so no row waits on a chain of rows)
-            panel32(rt[j], rt[j], lij, q4);
-            store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j]);   // threads 0-255
-            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-            __syncthreads();
-            if (tid == 0) {
-                publish_flag(flagL + i * nb + j, ep);
-                if (j >= 1) credit(colcnt, j - 1);   // the release covers L(i, j-1)'s packed form, stored after it
+            const Tile& lij = mine ? rt[j - s] : pin;
+            if (mine) {
+                // panel L(i, j) = T(i, j) Li_j^T, published before anything else (so no row waits on a chain of rows)
+                panel32(rt[j - s], rt[j - s], li, q4);
+                store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j - s]);   // threads 0-255
+                __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+                __syncthreads();
+                if (tid == 0) {
+                    publish_flag(flagL + i * nb + j, ep);
+                    if (j > s) credit(colcnt, j - 1);   // the release covers L(i, j-1)'s packed form, stored after it
+                }
+                store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j - s]);   // for the solve only
             }
-            store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j]);   // for the solve only
-            // block j's panels of the rows between: L(k, j), k = j+1..i-1, each in LDS before the tile it updates. At
-            // the last block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed. Rows j+1 and j+2
-            // are workgroup 0's: their panels are formed here, as workgroup 0 forms them. Row j+3 has just been
-            // handed to workgroup 0 (before block j; row 3 never had an owner): its panel too is formed here, from
-            // the handed-over T(j+3, j). Rows j+4.. publish their own.
-            panel32x2_inplace(op[j + 1], op[j + 2], lij, q4);             // L(j+1, j), L(j+2, j)
-            const int kend = (j + 4 == i) ? i - 1 : i;
-            const bool own3 = j + 3 < kend;
+            // block j's panels of the part's rows between: L(k, j), k = j+1..i-1, each in LDS before the tile it
+            // updates. Rows j+1 and j+2 are workgroup 0's: their panels are formed here, as workgroup 0 forms them.
+            // Row j+3 has just been handed to workgroup 0 (before block j; row 3 never had an owner): its panel too
+            // is formed here, from the handed-over T(j+3, j). Rows j+4.. publish their own. At the last part's last
+            // block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed.
+            if (h1 && h2)
+                panel32x2_inplace(pn[j + 1 - s], pn[j + 2 - s], li, q4);      // L(j+1, j), L(j+2, j)
+            else if (h1 || h2)
+                panel32(pn[j + (h1 ? 1 : 2) - s], pn[j + (h1 ? 1 : 2) - s], li, q4);
+            const int ke = last ? (j + 4 == i ? i - 1 : i) : e;     // the part's columns k < i updated: [.., ke)
+            const int k3 = j + 3 > s ? j + 3 : s;                   // [k3, ke): panels from global memory
+            const int nr = ke > k3 ? ke - k3 : 0;
             // Row i's update by block j, every tile's quadrant chain in one phase (the tiles are independent): waves
             // w and w + 4 take quadrant (bi, bj) = (w & 3) of alternate tiles of a sequence (without the upper
             // quadrant of T(i, i)); the panel's A operands stay in registers, and the next tile's B operands and
-            // accumulator are read while this tile's chain runs. For long rows, first the tiles whose panels this
-            // workgroup has formed -- T(i, j+1), T(i, j+2) and T(i, i) -- while the other rows' panel flags are in
-            // flight; then, once those are loaded, T(i, j+3..kend-1) (T(i, i-1) at the last block, j = i-4, is left
-            // to workgroup 0).
-            const int l16 = lane & 15, lk = lane >> 4, qd = w & 3, bi = qd >> 1, bj = qd & 1;
-            const bool upq = (bi == 0 && bj == 1);
+            // accumulator are read while this tile's chain runs. For long rows, when the part forms L(i, j), first
+            // the tiles whose panels it has formed -- T(i, j+1), T(i, j+2) and T(i, i) -- while the other rows'
+            // panel flags are in flight; then, once those are loaded, the rest.
             auto update_tiles = [&](int n, auto kof) {
                 float an[8];
 #pragma unroll
-                for (int kk = 0; kk < 8; ++kk) an[kk] = -rt[j][16 * bi + l16][4 * kk + lk];
+                for (int kk = 0; kk < 8; ++kk) an[kk] = -lij[16 * bi + l16][4 * kk + lk];
                 auto fetch = [&](int k, float (&bv)[8], f32x4& acc) {
-                    const Tile& Pk = (k == i) ? rt[j] : op[k];
+                    const Tile& Pk = (k == i) ? lij : pn[k - s];
 #pragma unroll
                     for (int kk = 0; kk < 8; ++kk) bv[kk] = Pk[16 * bj + l16][4 * kk + lk];
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[v] = rt[k][16 * bi + 4 * lk + v][16 * bj + l16];
+                    for (int v = 0; v < 4; ++v) acc[v] = rt[k - s][16 * bi + 4 * lk + v][16 * bj + l16];
                 };
                 // two operand sets in turn: tile t's chain runs while the operands of this wave's next tile are in
                 // flight; the prefetch is unconditional (past the last tile it reads tile t again, unused), so the
@@ -1278,7 +1332,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
 #pragma unroll
                     for (int kk = 0; kk < 8; ++kk) acc = mfma(an[kk], bv[kk], acc);
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) rt[k][16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
+                    for (int v = 0; v < 4; ++v) rt[k - s][16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
                 };
                 // In-order issue: the next tile's reads go between the chain's first MFMAs (two after each), where
                 // they issue while the previous MFMA runs and complete before the chain ends.
@@ -1308,43 +1362,64 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     t = tn;
                 }
             };
-            // T(i, j+1), T(i, j+2), T(i, i) (the upper quadrant's sequence stops before T(i, i)) -- where rows are
-            // long (r > 256); with at most 8 tiles per row the flags arrive before these would finish, and the row
-            // runs as one sequence after them
-            const bool early = nb > 8;
-            if (early) update_tiles(upq ? 2 : 3, [&](int t) { return t < 2 ? j + 1 + t : i; });
+            // with at most 8 tiles per row the flags arrive before the early tiles would finish, and the part runs
+            // as one sequence after them
+            const bool early = mine && nb > 8;
+            if (early) {
+                const int a0 = h1 ? j + 1 : j + 2, nh = (h1 ? 1 : 0) + (h2 ? 1 : 0);
+                update_tiles(nh + (last && !upq ? 1 : 0), [&](int t) { return t < nh ? a0 + t : i; });
+            }
+            // the other rows' panels (and L(i, j) when another part forms it): flags polled together, one batch of
+            // loads
             if (w == 0) {
-                const int k = j + 3 + lane;
                 const uint32_t* f = nullptr;
-                if (k < kend) f = (k != j + 3) ? flagL + k * nb + j : (k >= 4 ? flagT + k : nullptr);
+                if (lane < nr) {
+                    const int k = k3 + lane;
+                    f = (k != j + 3) ? flagL + k * nb + j : (k >= 4 ? flagT + k : nullptr);
+                } else if (lane == nr && !mine) {
+                    f = flagL + i * nb + j;
+                }
                 wait_flags_wave(f, ep, err, dead, lim);
             }
             __syncthreads();
             if (q4)
-                load_tiles<CH_MAXROW, 256>(&op[j + 3], kend - j - 3, r, 0u, 0.f, tid, [&](int q) {
-                    const int k = j + 3 + q;
-                    return (k == j + 3 ? A : L) + (size_t)CB * k * r + (size_t)CB * j;
-                });
+                load_tiles_to<OWNER_W + 1, 256>(nr + (mine ? 0 : 1), tid,
+                                                [&](int q) -> Tile& { return q < nr ? pn[k3 + q - s] : pin; },
+                                                [&](int q) {
+                                                    const int k = q < nr ? k3 + q : i;
+                                                    return (k == j + 3 ? A : L) + (size_t)CB * k * r + (size_t)CB * j;
+                                                },
+                                                [&](int) { return r; });
             __syncthreads();
-            if (own3) panel32(op[j + 3], op[j + 3], lij, q4);     // L(j+3, j)
+            if (j + 3 >= s && j + 3 < ke) panel32(pn[j + 3 - s], pn[j + 3 - s], li, q4);     // L(j+3, j)
             if (early) {
-                update_tiles(kend - j - 3, [&](int t) { return j + 3 + t; });
+                update_tiles(nr, [&](int t) { return k3 + t; });
             } else {
-                // T(i, j+1..kend-1), then T(i, i)
-                const int n = kend - j - (upq ? 1 : 0);
-                update_tiles(n, [&](int t) { return j + 1 + t < kend ? j + 1 + t : i; });
+                // T(i, k0..ke-1), then T(i, i)
+                const int k0 = j + 1 > s ? j + 1 : s;
+                const int n = (ke > k0 ? ke - k0 : 0) + (last && !upq ? 1 : 0);
+                update_tiles(n, [&](int t) { return k0 + t < ke ? k0 + t : i; });
             }
             __syncthreads();
-            if (j + 4 == i) {
+            if (last && j + 4 == i) {
                 // hand T(i, i-3..i) to workgroup 0
                 for (int t = 0; t < 4; ++t)
-                    store_tile(A + (size_t)CB * i * r + (size_t)CB * (i - 3 + t), r, rt[i - 3 + t]);
+                    store_tile(A + (size_t)CB * i * r + (size_t)CB * (i - 3 + t), r, rt[i - 3 + t - s]);
                 __builtin_amdgcn_s_waitcnt(0x0F70);
                 __syncthreads();
                 if (tid == 0) {
                     publish_flag(flagT + i, ep);
-                    credit(colcnt, j);
+                    if (mine) credit(colcnt, j);   // L(i, i-4)'s packed form
                 }
+            }
+        }
+        if (!last) {
+            // the packed form of the part's last panel, L(i, e-1), stored after its publication: released and credited
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+            if (tid == 0) {
+                release();
+                credit(colcnt, e - 1);
             }
         }
     }
@@ -2507,7 +2582,7 @@ void plan_shape(spanqr_plan* p, int K, int r, int batch) {
     p->K = K; p->r = r; p->batch = batch;
     p->nt = (r + TB - 1) / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / CB;
     split_policy(K, p->U, &p->S, &p->KS);
-    p->chol_grid = (r / CB > 4) ? r / CB - 3 : 1;     // workgroup 0 + one per tile row 4..r/32-1
+    p->chol_grid = chol_workgroups(r / CB);     // workgroup 0 + the parts of tile rows 4..r/32-1
     p->trsm_q = (r / CB + TRSM_NW - 1) / TRSM_NW;
     // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU
     p->trsm_rb = ((K + 15) / 16 >= 1024) ? 2 : 1;
