@@ -905,8 +905,14 @@ __device__ __forceinline__ void wait_flags_wave(const uint32_t* mine, uint32_t e
 
 // Publish: the calling lane's wave (or, after a workgroup sync, the workgroup) has its stores issued. release()
 // waits for them and makes them visible at agent scope (one L2 write-back); the flags that follow are plain
-// agent-scope stores.
-__device__ __forceinline__ void release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+// agent-scope stores. The fence's write-back (buffer_wbl2) is counted in vmcnt, and the wait for it must come
+// before the flag store: the compiler drops its own wait where no other vector memory operation is outstanding,
+// and a flag that overtakes the write-back lets a reader on another XCD fetch the previous launch's data from
+// memory. The explicit wait keeps the order.
+__device__ __forceinline__ void release() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the L2 write-back has completed
+}
 __device__ __forceinline__ void set_flag(uint32_t* f, uint32_t ep) {
     __hip_atomic_store(f, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
