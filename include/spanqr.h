@@ -8,8 +8,9 @@
  * Conventions
  *   - Matrices are row-major fp32 in device memory; X and Q need 16-byte alignment and a leading dimension that is a
  *     multiple of 4 (the contiguous [K, r] case always qualifies). X is never written.
- *   - r must be a multiple of 32 with 32 <= r <= 512, or a multiple of 256 with 512 < r <= 4096 (the column-blocked
- *     path: block Gram-Schmidt over 256-column blocks, as the reference's orth does above 512 columns); K >= r.
+ *   - r must be a multiple of 32 with 32 <= r <= 1024 (kcholf at full width), or a multiple of 256 with
+ *     512 < r <= 4096 (the column-blocked path: block Gram-Schmidt over 256-column blocks, as the reference's orth
+ *     does above 512 columns; spanqr_plan_create picks it for those r); K >= r.
  *   - Every entry point that takes a stream only enqueues work on it: no host synchronisation, no allocation, so a
  *     call can be captured into a hipGraph. Plan creation allocates and synchronises.
  *   - Return value 0 means success; a negative value is an error whose message spanqr_last_error() returns (per
@@ -33,6 +34,8 @@ typedef struct spanqr_plan spanqr_plan;
 
 /* Widest X a plan takes: above 512 columns (a multiple of 256) the plan is column-blocked (see spanqr_plan_create). */
 #define SPANQR_MAX_R 4096
+/* Widest X kcholf runs on at full width (candidates/kcholqr.py:92-112 with chol.cu's Cholesky, n <= ~1024). */
+#define SPANQR_KCHOLF_MAX_R 1024
 
 enum {
     SPANQR_OK = 0,
@@ -59,17 +62,21 @@ enum {
     SPANQR_Q_BLOCK_WIDTH = 11,   /* columns per block of a column-blocked plan; 0 otherwise */
 };
 
-/* Create a plan for X [K, r] on HIP device `device` (allocates the workspace and uploads the dust matrix).
- * Replaces the per-call allocations and module-level caches of the reference: the dust cache _Z
- * (candidates/kcholqr.py:26, :83-89), chol32's G clone / L / Li / barrier (candidates/kchol.py:12-18, :40-42) and the
- * Gram partials (candidates/tri.py:371). For r > 512 the plan is column-blocked (borth, candidates/kbig.py:69-95,
- * called from orth.py:18-19 with 256-column blocks): it holds the plan of one 256-column block, the K x r dust whose
- * column slices the blocks use (_ZB, kbig.py:76-83) and the projection's buffers; such a plan runs spanqr_orth_f32
- * only (the stage, profiling and batched entry points return SPANQR_EINVAL for it). */
+/* Create a plan for X [K, r] on HIP device `device` (allocates the workspace and uploads the dust matrix), with
+ * orth's dispatch (orth.py:13-20). Replaces the per-call allocations and module-level caches of the reference: the
+ * dust cache _Z (candidates/kcholqr.py:26, :83-89), chol32's G clone / L / Li / barrier (candidates/kchol.py:12-18,
+ * :40-42) and the Gram partials (candidates/tri.py:371). For r > 512 a multiple of 256 (up to SPANQR_MAX_R) the plan
+ * is column-blocked (borth, candidates/kbig.py:69-95, called from orth.py:18-19 with 256-column blocks): it holds the
+ * plan of one 256-column block, the K x r dust whose column slices the blocks use (_ZB, kbig.py:76-83) and the
+ * projection's buffers; such a plan runs spanqr_orth_f32 only (the stage, profiling and batched entry points return
+ * SPANQR_EINVAL for it). Any other r a multiple of 32 up to SPANQR_KCHOLF_MAX_R runs kcholf at full width
+ * (orth.py:20), as spanqr_plan_create_batched with batch = 1. */
 int spanqr_plan_create(int K, int r, int device, spanqr_plan** out);
 
-/* Plan for up to `batch` (1..SPANQR_MAX_BATCH) matrices [K, r] per call (spanqr_orth_batched_f32): one workspace
- * per matrix, one shared dust matrix. spanqr_plan_create is the batch = 1 case. */
+/* Plan for kcholf at full width (candidates/kcholqr.py:92-112) on up to `batch` (1..SPANQR_MAX_BATCH) matrices
+ * [K, r] per call (spanqr_orth_batched_f32): r a multiple of 32 in [32, SPANQR_KCHOLF_MAX_R], one workspace per
+ * matrix, one shared dust matrix. Differs from spanqr_plan_create only at r = 768 and 1024, where this is the
+ * full-width kcholf of kcholqr_f and spanqr_plan_create the column-blocked orth. */
 int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan** out);
 
 /* Column-blocked plan for borth(X, b, reorth) (candidates/kbig.py:69-95, whose parameters these are): block
@@ -84,7 +91,7 @@ void spanqr_plan_destroy(spanqr_plan* plan);
 long spanqr_plan_query(const spanqr_plan* plan, int what);
 
 /* Q = orth(X) with the reference's keyword arguments (defaults eps 5e-7, alpha 1e-7, tau 1e-8, ns 2).
- * Replaces orth (orth.py:13-20): for r <= 512 kcholqr_f (candidates/kcholqr.py:92-112); on a column-blocked plan
+ * Replaces orth (orth.py:13-20): on a kcholf plan kcholqr_f (candidates/kcholqr.py:92-112); on a column-blocked plan
  * borth(X, 256) (candidates/kbig.py:69-95): per 256-column block, W = s X_blk (s of the whole X), twice
  * W -= P (P^T W) against the finished columns P, the kcholf recipe on W with the block's dust slice (kbig.py:50-63),
  * then once more W -= P (P^T W) and the recipe again. stream: a hipStream_t (torch.cuda.current_stream().cuda_stream

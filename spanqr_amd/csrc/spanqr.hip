@@ -49,7 +49,12 @@ constexpr uint32_t SPIN_LIMIT = 1u << 20;
 // the matrix): scalars (floats), error word and padding (uint32), Cholesky flags (uint32).
 constexpr int SCAL_STRIDE = 16;
 constexpr int BAR_STRIDE = 64;
-constexpr int FLAG_STRIDE = 384;   // >= 16 * 16 panel flags + 16 hand-over flags + 64 call counters
+constexpr int KCH_MAX_R = 1024;    // kcholf at full width: r a multiple of 32 up to this
+constexpr int CH_MAXROW = KCH_MAX_R / CB;   // tiles in a tile row at most
+// Cholesky flags: [nb * nb] panel flags, [nb] hand-over flags, then a call counter per Cholesky workgroup (99 at
+// r = 1024, checked below)
+constexpr int FLAG_STRIDE = 1280;
+constexpr int CC_STRIDE = 16;      // uint32 words between the solve's column counters (one 64-byte line each)
 
 // The caller's matrices of one launch, passed by value (a captured graph keeps the pointers): matrix z of the
 // batch is p[z]. Plan-owned [K, r] buffers are passed the same way.
@@ -348,8 +353,8 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
                                                 float* __restrict__ G, double* __restrict__ npart,
                                                 uint32_t* colcnt = nullptr) {
     const int b = blockIdx.x, u = blockIdx.y, U = gridDim.y;
-    if (MODE == 0 && colcnt != nullptr && b == 0 && u == 0 && threadIdx.x < 16)
-        colcnt[((size_t)blockIdx.z * 16 + threadIdx.x) * 16] = 0u;
+    if (MODE == 0 && colcnt != nullptr && b == 0 && u == 0 && threadIdx.x < CH_MAXROW)
+        colcnt[((size_t)blockIdx.z * CH_MAXROW + threadIdx.x) * CC_STRIDE] = 0u;
     P += (size_t)blockIdx.z * S * U * TB * TB;
     G += (size_t)blockIdx.z * r * r;
     if (MODE != 2) npart += (size_t)blockIdx.z * 16 * U;
@@ -424,11 +429,12 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 //     j-1 to T(j+1, j) and T(j+1, j+1). Then waves 0-3 form the panel L(j+1, j) and apply column block j to
 //     T(j+1, j+1), the tile the next step factors (look-ahead over the next two tile rows; block j on the rest of
 //     row j+2 is wave 3's work in the next step).
-//   * Workgroup i-3 owns tile row i >= 4 for the whole factorisation, in LDS. For column block j = 0..i-4 in order:
-//     panel L(i, j) = T(i, j) Li_j^T (published), then T(i, k) -= L(i, j) L(k, j)^T for k = j+1..i with the other
-//     rows' panels of block j fetched together (at its last block, j = i-4, T(i, i-1) is left to workgroup 0); after
-//     block i-4 it hands T(i, i-3..i) to workgroup 0, two steps before workgroup 0 factors T(i, i). The panel
-//     L(j+3, j) of the row just handed over it forms itself from the handed-over T(j+3, j).
+//   * Tile row i >= 4 is owned for the whole factorisation, in LDS, by ceil((i + 1) / OWNER_W) workgroups (parts),
+//     each holding a run of its tiles. For column block j = 0..i-4 in order: panel L(i, j) = T(i, j) Li_j^T
+//     (published by the part holding T(i, j)), then T(i, k) -= L(i, j) L(k, j)^T for each part's k = j+1..i with the
+//     other rows' panels of block j fetched together (at the last block, j = i-4, T(i, i-1) is left to workgroup 0);
+//     after block i-4 the last part hands T(i, i-3..i) to workgroup 0, two steps before workgroup 0 factors T(i, i).
+//     The panel L(j+3, j) of the row just handed over a part forms itself from the handed-over T(j+3, j).
 // Every element keeps the reference order: updates by column block in increasing order, each one MFMA chain over the
 // block's 32 columns. A producer publishes with an agent-scope release after its stores; a consumer polls with
 // bounded waits (after `lim` polls it records an error and stops waiting, so the kernel always ends). Each
@@ -960,14 +966,13 @@ __device__ __forceinline__ void wait_lds(const uint32_t* word, uint32_t target, 
     __builtin_amdgcn_wave_barrier();
 }
 
-constexpr int CH_MAXROW = 16;      // tiles in a tile row at most (r <= 512)
 constexpr int CH_WG0_TILES = 24;   // workgroup 0: D[2], X1, R2[2][5], dl[2], li[2], P1[2], P2[2], C2[2], id
 // Owner parts: tile row i (i + 1 tiles) is split over P = ceil((i + 1) / OWNER_W) workgroups, each holding a run of
 // consecutive tiles T(i, s..e-1): widths floor((i + 1) / P), the last (i + 1) % P parts one wider, so that for
 // OWNER_W >= 6 the last part (which holds T(i, i-3..i) and hands them to workgroup 0) has at least 4 tiles for every
 // row i >= 4. A part's work per column block shrinks with its width, so long rows keep up with workgroup 0's steps.
 constexpr int OWNER_W = 6;   // (6: the best of 6, 7, 8 and 16 measured at r = 512)
-static_assert(OWNER_W >= 6 && OWNER_W <= CH_MAXROW, "owner parts: the last part of a row needs 4 tiles");
+static_assert(OWNER_W >= 6 && OWNER_W <= 16, "owner parts: the last part of a row needs 4 tiles");
 __host__ __device__ constexpr int row_parts(int i) { return (i + OWNER_W) / OWNER_W; }
 __host__ __device__ inline void part_range(int i, int q, int& s, int& e) {
     const int n = i + 1, P = row_parts(i), base = n / P, lo = P - n % P;   // parts q < lo have base tiles
@@ -1012,7 +1017,7 @@ size_t chol_lds_bytes(int r) {
     return (size_t)tiles * sizeof(Tile) + 256 * sizeof(float);
 }
 
-// nb = r/32 tile rows; grid = max(1, nb - 3) workgroups. With nnp == 0 the shift is 0 and tau_rel is the absolute
+// nb = r/32 tile rows; grid = chol_workgroups(nb) workgroups. With nnp == 0 the shift is 0 and tau_rel is the absolute
 // pivot floor (chol32's contract); otherwise ||G||_F comes from the nnp fp64 partials: lane l of wave 0 sums
 // npart[l], npart[l + 64], ... in order, then a shift-down tree over the 64 lane sums; nrm = sqrtf(fp32(sum)),
 // shift = alpha * nrm added to the diagonal after the first load, tau = tau_rel * nrm + 1e-30 (kcholqr.py:107-109).
@@ -1031,8 +1036,6 @@ size_t chol_lds_bytes(int r) {
 // Column k is complete at 1 + max(0, nb - 4 - k) credits; the counters start at zero.
 static_assert(chol_workgroups(CH_MAXROW) <= FLAG_STRIDE - CH_MAXROW * (CH_MAXROW + 1),
               "a call counter per Cholesky workgroup after the panel and hand-over flags");
-constexpr int CC_STRIDE = 16;   // uint32 words between column counters (one 64-byte line each)
-static_assert(CC_STRIDE == 16 && CH_MAXROW == 16, "k_reduce clears the column counters with stride 16, 16 per matrix");
 
 __device__ __forceinline__ void credit(uint32_t* colcnt, int k) {
     if (colcnt != nullptr) __hip_atomic_fetch_add(colcnt + (size_t)k * CC_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1485,6 +1488,8 @@ __device__ __forceinline__ void trsm_fetch_li(float (&li)[2][8], const float* __
 }
 
 constexpr int TRSM_NW = 8;   // wavefronts per k_trsm workgroup; wave w owns the column blocks w + TRSM_NW q
+// column blocks per wavefront for nb 32-column blocks: 1 (r <= 256), 2 (r <= 512) or 4 (r <= 1024)
+constexpr int trsm_q_for(int nb) { return nb <= TRSM_NW ? 1 : nb <= 2 * TRSM_NW ? 2 : 4; }
 
 template <int Q>
 __device__ __forceinline__ void trsm_fetch(TrsmOps<Q>& o, const float* __restrict__ Lp, int nbc, int k, int w,
@@ -2299,6 +2304,7 @@ hipError_t trsm_set_lds(int r) {
 hipError_t trsm_set_lds_plan(int q, int rb, int r) {
     // two row blocks only with two column blocks per wave (r > 256, K >= 16384; taller r <= 256 takes k_trsm_rows)
     if (q == 1) return trsm_set_lds<1, 1>(r);
+    if (q == 4) return trsm_set_lds<4, 1>(r);
     return rb == 2 ? trsm_set_lds<2, 2>(r) : trsm_set_lds<2, 1>(r);
 }
 
@@ -2318,9 +2324,10 @@ hipError_t fused_set_lds_t(int lds) {
     return e;
 }
 
-// the instantiations: Q = 1 (r <= 256) with one row block, Q = 2 (r <= 512) with one or two, and the
-// wavefront-per-row-block solve (Q = 0) for r/32 = 2, 4, 6, 8 column blocks
+// the instantiations: Q = 1 (r <= 256) with one row block, Q = 2 (r <= 512) with one or two, Q = 4 (r <= 1024)
+// with one, and the wavefront-per-row-block solve (Q = 0) for r/32 = 2, 4, 6, 8 column blocks
 hipError_t fused_set_lds(int q, int rb, int lds) {
+    if (q == 4) return fused_set_lds_t<4, 1>(lds);
     if (q == 2) return rb == 2 ? fused_set_lds_t<2, 2>(lds) : fused_set_lds_t<2, 1>(lds);
     if (q == 1) return fused_set_lds_t<1, 1>(lds);
     switch (rb) {
@@ -2382,9 +2389,10 @@ void launch_trsm(const spanqr_plan* p, const MatsIn& A, long lda, bool pass1, fl
         }
         return;
     }
-    switch (p->trsm_q) {   // r <= 512: at most two column blocks per wavefront
+    switch (p->trsm_q) {
         case 1: launch_trsm_q<1>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
-        default: launch_trsm_q<2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+        case 2: launch_trsm_q<2>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
+        default: launch_trsm_q<4>(p, A, lda, pass1, eps, dz, Y, ldy, n, st); break;
     }
 }
 
@@ -2395,6 +2403,10 @@ void launch_fused_t(dim3 grid, size_t lds, hipStream_t st, const CholArgs& c, co
 
 template <bool PASS1>
 void launch_fused(int q, int rb, dim3 grid, size_t lds, hipStream_t st, const CholArgs& c, const SolveArgs& t) {
+    if (q == 4) {
+        launch_fused_t<PASS1, 4, 1>(grid, lds, st, c, t);
+        return;
+    }
     if (q == 2) {
         if (rb == 2) launch_fused_t<PASS1, 2, 2>(grid, lds, st, c, t);
         else launch_fused_t<PASS1, 2, 1>(grid, lds, st, c, t);
@@ -2571,9 +2583,9 @@ int spanqr_dust_host(int K, int r, float* Z) {
 
 static int check_shape(int K, int r, bool blocked_ok = false) {
     const bool blocked = blocked_ok && r > 512 && r <= SPANQR_MAX_R && (r % BW) == 0;
-    if (!blocked && (r < 32 || r > 512 || (r % 32) != 0))
-        return fail(SPANQR_EINVAL, blocked_ok ? "r = %d: must be a multiple of 32 in [32, 512] or of 256 up to 4096"
-                                              : "r = %d: must be a multiple of 32 in [32, 512]", r);
+    if (!blocked && (r < 32 || r > KCH_MAX_R || (r % 32) != 0))
+        return fail(SPANQR_EINVAL, blocked_ok ? "r = %d: must be a multiple of 32 in [32, 1024] or of 256 up to 4096"
+                                              : "r = %d: must be a multiple of 32 in [32, 1024]", r);
     if (K < r) return fail(SPANQR_EINVAL, "K = %d < r = %d", K, r);
     if ((long)K * r >= (1L << 30)) return fail(SPANQR_EINVAL, "K * r too large");
     return SPANQR_OK;
@@ -2589,9 +2601,10 @@ void plan_shape(spanqr_plan* p, int K, int r, int batch) {
     p->nt = (r + TB - 1) / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / CB;
     split_policy(K, p->U, &p->S, &p->KS);
     p->chol_grid = chol_workgroups(r / CB);     // workgroup 0 + the parts of tile rows 4..r/32-1
-    p->trsm_q = (r / CB + TRSM_NW - 1) / TRSM_NW;
-    // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU
-    p->trsm_rb = ((K + 15) / 16 >= 1024) ? 2 : 1;
+    p->trsm_q = trsm_q_for(r / CB);
+    // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU (and
+    // always one with four column blocks per wavefront, r > 512)
+    p->trsm_rb = ((K + 15) / 16 >= 1024 && p->trsm_q <= 2) ? 2 : 1;
     // a wavefront pair per 16 rows once there are enough rows to occupy the SIMDs (the chain over r/32 blocks is
     // long; the measured crossover at r = 256 lies near K = 8192-10240); below that, k_trsm splits each row block's
     // columns over eight waves
@@ -2643,10 +2656,12 @@ int plan_device_setup(spanqr_plan* p, int device) {
         HIPCHK(hipDeviceGetAttribute(&maxsh, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
         const int avail = cus - p->chol_grid;
         const int rowblocks = (p->K + 15) / 16;
-        int q = (r / CB + TRSM_NW - 1) / TRSM_NW, rb = 1, nwg = rowblocks, wpg = TRSM_NW;
+        int q = trsm_q_for(r / CB), rb = 1, nwg = rowblocks, wpg = TRSM_NW;
         if (rowblocks > avail) {
-            if (r <= 256 && (r / CB) % 2 != 0) {
-                nwg = avail + 1;   // the one-wavefront solve is built for an even number of column blocks: separate
+            if (q == 4 || (r <= 256 && (r / CB) % 2 != 0)) {
+                // separate launches: the one-wavefront solve is built for an even number of column blocks, and
+                // four column blocks per wavefront for one row block per workgroup only
+                nwg = avail + 1;
             } else if (r <= 256) {
                 // one wavefront per row block, as few per workgroup (and so per CU) as the free CUs allow
                 q = 0;
@@ -2688,7 +2703,7 @@ size_t plan_layout(spanqr_plan* p, char* base) {
         al256(B * 16 * p->U * sizeof(double)),                  // npart
         al256(B * AMAX_BLOCKS * sizeof(uint32_t)),              // amax_part
         al256(B * BAR_STRIDE * sizeof(uint32_t)),               // bar
-        al256(2 * (4 * (512 / CB) + 2) * sizeof(uint64_t)),     // stamps
+        al256((6 * CH_MAXROW + 2) * sizeof(uint64_t)),          // stamps
         al256(B * FLAG_STRIDE * sizeof(uint32_t)),              // flags
         al256(B * CC_STRIDE * CH_MAXROW * sizeof(uint32_t)),    // colcnt
     };
@@ -2823,6 +2838,12 @@ int spanqr_split_rows(int K, int r) {
 }
 
 int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
+    if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
+    *out = nullptr;
+    const int shape_rc = check_shape(K, r, true);
+    if (shape_rc != SPANQR_OK) return shape_rc;
+    // orth.py:18-19: above 512 columns, a multiple of 256 goes through borth over 256-column blocks
+    if (r > 512 && r % BW == 0) return create_blocked(K, r, BW, true, device, out);
     return spanqr_plan_create_batched(K, r, 1, device, out);
 }
 
@@ -2840,14 +2861,10 @@ int spanqr_plan_create_borth(int K, int r, int b, int reorth, int device, spanqr
 int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan** out) {
     if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
     *out = nullptr;
-    const int shape_rc = check_shape(K, r, true);
+    const int shape_rc = check_shape(K, r);   // kcholf at full width
     if (shape_rc != SPANQR_OK) return shape_rc;
     if (batch < 1 || batch > SPANQR_MAX_BATCH)
         return fail(SPANQR_EINVAL, "batch = %d: must be in [1, %d]", batch, SPANQR_MAX_BATCH);
-    if (r > 512) {
-        if (batch != 1) return fail(SPANQR_EINVAL, "r = %d > 512 (column-blocked path): batch must be 1", r);
-        return create_blocked(K, r, BW, true, device, out);
-    }
     DeviceGuard dg(device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", device);
     spanqr_plan* p = new spanqr_plan;
@@ -3232,7 +3249,7 @@ char* g_na_base[MAX_DEVICES] = {};   // the array's device address on each devic
 
 // The array: the dust's shape tag and column norms at fixed offsets (every call finds the tag of the dust the array
 // holds at the same place, whatever the shape of the call that wrote it), then a plan's workspace.
-constexpr size_t NA_TAG = 0, NA_NRM = 256, NA_WS = NA_NRM + 512 * sizeof(double);
+constexpr size_t NA_TAG = 0, NA_NRM = 256, NA_WS = NA_NRM + KCH_MAX_R * sizeof(double);   // tag, dust column norms
 
 size_t noalloc_bytes(int K, int r) {
     spanqr_plan p;
@@ -3248,6 +3265,7 @@ int spanqr_orth_f32_noalloc(int K, int r, const float* X, long ldx, float* Q, lo
                             float tau, int ns, void* stream) {
     int rc = check_shape(K, r);
     if (rc != SPANQR_OK) return rc;
+    if (r > 512) return fail(SPANQR_EINVAL, "noalloc: r = %d: at most 512 (use a plan)", r);
     const size_t need = noalloc_bytes(K, r);
     if (need > SCRATCH_BYTES)
         return fail(SPANQR_EINVAL, "noalloc: X [%d, %d] needs %zu bytes of workspace, more than the fixed %zu "

@@ -13,6 +13,17 @@ CB = 32          # Cholesky tile (chol.cu:15 TB = 32)
 TILE = 32        # the native kernels need r to be a multiple of this (kcholqr.py:98-99, TB = 32)
 R_MAX = 512      # orth.py:18: wider X goes through block Gram-Schmidt in the reference
 BLOCK = 256      # its block width (orth.py:19, borth(X, 256))
+KCHOLF_MAX_R = 1024   # full-width kcholf (orth.py:20 for r > 512 not a multiple of 256; chol.cu:1 takes n <= ~1024)
+
+
+def _full_width(K, r):
+    """kcholf at full width natively: r a multiple of 32 up to 1024, K >= r"""
+    return r % TILE == 0 and r <= KCHOLF_MAX_R and K >= r
+
+
+def _blocked(r):
+    """orth.py:18: above 512 columns a multiple of 256 goes through borth over 256-column blocks"""
+    return r > R_MAX and r % BLOCK == 0
 
 
 def _check_input(X):
@@ -33,14 +44,15 @@ def _prepare(X):
 
 
 def kcholqr_f(X, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
-    """Q = orth(X) for fp32 X [K, r] on a ROCm device, r a multiple of 32 in [32, 512], K >= r
-    (candidates/kcholqr.py:92-112). eps: dust scale (first solve only); alpha: diagonal shift relative to ||G||_F;
-    tau: pivot clamp relative to ||G||_F (plus 1e-30); ns: Newton-Schulz polish steps (the last with a Kahan Gram).
+    """Q = orth(X) for fp32 X [K, r] on a ROCm device, r a multiple of 32 in [32, 1024] (at full width, also where
+    orth takes borth), K >= r (candidates/kcholqr.py:92-112). eps: dust scale (first solve only); alpha:
+    diagonal shift relative to ||G||_F; tau: pivot clamp relative to ||G||_F (plus 1e-30); ns: Newton-Schulz polish
+    steps (the last with a Kahan Gram).
     """
     _check_input(X)
     K, r = X.shape
-    if r % TILE or r > R_MAX or K < r:
-        raise ValueError(f"kcholqr_f: shape [{K}, {r}] needs r % {TILE} == 0, r <= {R_MAX} and K >= r")
+    if not _full_width(K, r):
+        raise ValueError(f"kcholqr_f: shape [{K}, {r}] needs r % {TILE} == 0, r <= {KCHOLF_MAX_R} and K >= r")
     X = _prepare(X)
     dev = X.device
     plan = get_plan(K, r, dev)
@@ -67,8 +79,8 @@ def kcholqr_f_many(Xs, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
     for X in Xs:
         if tuple(X.shape) != (K, r) or X.device != dev:
             raise ValueError("kcholqr_f_many: every X must have the same shape and device")
-    if r % TILE or r > R_MAX or K < r:
-        raise ValueError(f"kcholqr_f_many: shape [{K}, {r}] needs r % {TILE} == 0, r <= {R_MAX} and K >= r")
+    if not _full_width(K, r):
+        raise ValueError(f"kcholqr_f_many: shape [{K}, {r}] needs r % {TILE} == 0, r <= {KCHOLF_MAX_R} and K >= r")
     Xs = [_prepare(X) for X in Xs]
     Qs = [torch.empty_like(X) for X in Xs]
     n_all = len(Xs)
@@ -95,7 +107,7 @@ def orth_many(Xs):
     for i, X in enumerate(Xs):
         _check_input(X)
         K, r = X.shape
-        if r % TILE == 0 and r <= R_MAX and K >= r:
+        if _full_width(K, r) and not _blocked(r):
             groups.setdefault((K, r, X.device), []).append(i)
         else:
             out[i] = orth(X)
@@ -111,14 +123,14 @@ def borth(X, b=512, reorth=True):
     blocks' span removed twice and goes through the kcholf recipe with its own column slice of a K x r dust; with
     reorth it is projected and orthonormalised once more. One native call for the whole X, no host synchronisation.
 
-    As kbig.py:77-78, r <= b or r not a multiple of b is one kcholf call at full width instead (here for r <= 512;
-    wider full-width kcholf is not built, so those shapes use torch.linalg.qr). Natively b is a multiple of 64 in
+    As kbig.py:77-78, r <= b or r not a multiple of b is one kcholf call at full width instead (here for r a multiple
+    of 32 up to 1024; other such shapes use torch.linalg.qr). Natively b is a multiple of 64 in
     [64, 512] (orth passes 256, the reference's default is 512); other b raise ValueError, as does r above 4096.
     """
     _check_input(X)
     K, r = X.shape
     if r <= b or r % b:
-        if r <= R_MAX and r % TILE == 0 and K >= r:
+        if _full_width(K, r):
             return kcholqr_f(X)
         return torch.linalg.qr(X)[0]
     if b % 64 or not 64 <= b <= R_MAX:
@@ -141,16 +153,17 @@ def orth(X):
     Deterministic and free of host synchronisation.
 
     Dispatch as orth.py:18-20: r > 512 and a multiple of 256 goes through block Gram-Schmidt over 256-column blocks
-    (borth); r <= 512 through kcholqr_f. Shapes outside the native kernels -- r not a multiple of 32
-    (kcholqr.py:98-99, as the reference) and, here, K < r, r > 4096, or r > 512 and not a multiple of 256 (where the
-    reference runs kcholqr_f at full width) -- go to torch.linalg.qr.
+    (borth); any other r that is a multiple of 32 through kcholqr_f at full width. Shapes outside the native kernels
+    -- r not a multiple of 32 (kcholqr.py:98-99, as the reference) and, here, K < r, r > 4096, or r > 1024 and not a
+    multiple of 256 (where the reference's kcholqr_f would run a Cholesky wider than its chol.cu:1 bound) -- go to
+    torch.linalg.qr.
     """
     _check_input(X)
     K, r = X.shape
-    if r > R_MAX:
-        if r % BLOCK == 0 and r <= _lib.MAX_R and K >= r:
+    if _blocked(r):
+        if r <= _lib.MAX_R and K >= r:
             return borth(X, BLOCK)
         return torch.linalg.qr(X)[0]
-    if r % TILE or K < r:
+    if not _full_width(K, r):
         return torch.linalg.qr(X)[0]
     return kcholqr_f(X)

@@ -33,14 +33,15 @@ def test_split_policy():
     f = _lib.lib().spanqr_split_rows
     # tri.py:364-367 with 512 target workgroups: S = min(ceil(512 / U), ceil(K / 128)), KS = 32 ceil(ceil(K/S) / 32)
     for K, r in [(1024, 256), (2048, 256), (3584, 256), (768, 512), (2048, 512), (5120, 256), (17408, 256),
-                 (64, 64), (100, 64), (12345, 192), (1024, 96), (4100, 160), (32, 32), (9217, 224), (768, 480)]:
+                 (64, 64), (100, 64), (12345, 192), (1024, 96), (4100, 160), (32, 32), (9217, 224), (768, 480),
+                 (1024, 576), (2048, 768), (1100, 1024), (5000, 992)]:
         nt = -(-r // 64)
         U = nt * (nt + 1) // 2
         S = max(1, min(-(-512 // U), -(-K // 128)))
         KS = 32 * -(-(-(-K // S)) // 32)
         assert f(K, r) == KS, (K, r)
         assert KS % 32 == 0 and -(-K // KS) <= S
-    for K, r in [(100, 128), (1024, 80), (1024, 576), (1024, 0), (2048, 768), (1024, 16), (10, 32)]:
+    for K, r in [(100, 128), (1024, 80), (2048, 1056), (1024, 0), (4096, 1280), (1024, 16), (10, 32), (544, 576)]:
         assert f(K, r) == -1
         assert _lib.lib().spanqr_last_error()
 
@@ -49,18 +50,22 @@ def test_split_policy_is_the_oracle_rule():
     """the library's split rule (every Gram and block projection) is the one the oracle restates"""
     f = _lib.lib().spanqr_split_rows
     for K in (64, 100, 513, 1024, 3000, 17408, 65536):
-        for r in range(32, 513, 32):
+        for r in range(32, 1025, 32):
             if K >= r:
                 nt = -(-r // 64)
                 assert f(K, r) == oracle.split_rows(K, nt * (nt + 1) // 2), (K, r)
 
 
 def test_column_blocked_shapes_checked_before_any_device_work():
+    """spanqr_plan_create: column-blocked above 512 columns for multiples of 256 up to 4096, full-width kcholf for
+    other multiples of 32 up to 1024; spanqr_plan_create_batched: full-width kcholf only (up to 1024 columns)"""
     h = ctypes.c_void_p()
-    f = _lib.lib().spanqr_plan_create_batched
-    for K, r in [(1024, 640), (1024, 800), (512, 768), (8192, 4352), (1 << 19, 4096)]:
-        assert f(K, r, 1, 0, ctypes.byref(h)) == -1 and not h.value, (K, r)
-    assert f(2048, 768, 2, 0, ctypes.byref(h)) == -1 and b"batch" in _lib.lib().spanqr_last_error()
+    f = _lib.lib().spanqr_plan_create
+    for K, r in [(1024, 1056), (2048, 1312), (512, 768), (8192, 4352), (1 << 19, 4096)]:
+        assert f(K, r, 0, ctypes.byref(h)) == -1 and not h.value, (K, r)
+    fb = _lib.lib().spanqr_plan_create_batched
+    for K, r in [(2048, 1280), (4096, 2048), (1024, 1056), (512, 544)]:
+        assert fb(K, r, 1, 0, ctypes.byref(h)) == -1 and not h.value, (K, r)
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")
@@ -93,7 +98,7 @@ def test_bad_shapes_rejected_before_any_device_work():
     h = ctypes.c_void_p()
     assert _lib.lib().spanqr_plan_create(100, 128, 0, ctypes.byref(h)) == -1
     assert _lib.lib().spanqr_plan_create(1024, 80, 0, ctypes.byref(h)) == -1     # r not a multiple of 32
-    assert _lib.lib().spanqr_plan_create(1024, 544, 0, ctypes.byref(h)) == -1    # above 512, not a multiple of 256
+    assert _lib.lib().spanqr_plan_create(2048, 1056, 0, ctypes.byref(h)) == -1   # above 1024, not a multiple of 256
     assert _lib.lib().spanqr_plan_create(1024, 256, 0, None) == -1
 
 

@@ -27,6 +27,20 @@ def test_batch_matches_single_calls(cuda):
     assert_bits(Qs[2], oracle.orth(Xs[2].numpy(), get_plan(K, r, cuda).split_rows), "batch element 2 vs oracle")
 
 
+def test_full_width_batch_matches_single_calls(cuda):
+    """kcholf at full width above 512 columns (tile rows split over several owner workgroups), batched: each Q equals
+    the single call and the oracle"""
+    K, r, n = 700, 544, 3
+    g = torch.Generator().manual_seed(11)
+    Xs = [torch.randn(K, r, generator=g) * torch.logspace(0, -4, r) for _ in range(n)]
+    print(f"batched {n} x {K}x{r}", flush=True)
+    Qs = kcholqr_f_many([X.to(cuda) for X in Xs])
+    for i, (X, Q) in enumerate(zip(Xs, Qs)):
+        assert_bits(Q, kcholqr_f(X.to(cuda)), f"batch element {i} vs single call")
+    assert_bits(Qs[1], oracle.orth(Xs[1].numpy(), get_plan(K, r, cuda).split_rows), "batch element 1 vs oracle")
+    gate(Xs[1], Qs[1], "batch element 1")
+
+
 def test_cholesky_in_several_launches(cuda):
     """more matrices than one Cholesky launch holds (every workgroup of a launch must be resident at once)"""
     K, r, n = 512, 512, 24
@@ -112,8 +126,9 @@ def test_batched_layer_set(cuda):
     Qs = orth_many([X.to(cuda) for X in Xs])
     for i, (X, Q) in enumerate(zip(Xs, Qs)):
         K, r = X.shape
-        assert_bits(Q, orth(X.to(cuda)), f"layer {i} ({K}x{r}) vs its single call")
-        assert_bits(Q, oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows), f"layer {i} ({K}x{r}) vs oracle")
+        Qo = oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows)
+        assert_bits(Q, Qo, f"layer {i} ({K}x{r}), batched, vs oracle")
+        assert_bits(orth(X.to(cuda)), Qo, f"layer {i} ({K}x{r}), single call, vs oracle")
         gate(X, Q, f"layer {i} ({K}x{r})")
 
 

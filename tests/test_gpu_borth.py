@@ -8,7 +8,7 @@ import torch
 
 import oracle
 from spanqr_amd import _lib, borth, orth
-from spanqr_amd.plan import get_borth_plan, get_plan, stream_handle
+from spanqr_amd.plan import get_borth_plan, stream_handle
 from spanqr_amd.qrbench import gen, metrics
 
 from checks import assert_bits, gate
@@ -108,7 +108,7 @@ def test_borth_strided_operands(cuda):
     Xw = torch.zeros(K, r + 64, device=cuda)
     Xw[:, :r] = X
     Qw = torch.full((K, r + 128), 7.0, device=cuda)
-    plan = get_plan(K, r, cuda)
+    plan = get_borth_plan(K, r, 256, True, cuda)   # spanqr_plan_create's plan at r = 768
     print(f"borth strided {K}x{r}", flush=True)
     _lib.check(_lib.lib().spanqr_orth_f32(plan.handle, Xw.data_ptr(), r + 64, Qw.data_ptr(), r + 128, 5e-7, 1e-7, 1e-8,
                                            2, stream_handle(cuda)))
@@ -139,7 +139,7 @@ def test_borth_graph_capture(cuda):
 
 def test_blocked_plan_refused_where_it_does_not_apply(cuda):
     K, r = 1024, 768
-    plan = get_plan(K, r, cuda)
+    plan = get_borth_plan(K, r, 256, True, cuda)   # spanqr_plan_create's plan at r = 768
     L = _lib.lib()
     assert L.spanqr_plan_query(plan.handle, _lib.Q_BLOCKS) == 3
     assert L.spanqr_plan_query(plan.handle, _lib.Q_SPLIT_ROWS) == oracle.split_rows(K, 10)

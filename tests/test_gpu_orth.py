@@ -156,3 +156,50 @@ def test_tall_solve_in_cholesky_launch(cuda, K, r):
     Q = kcholqr_f(X.to(cuda))
     assert_bits(Q, oracle.orth(X.numpy(), plan.split_rows), f"{K}x{r} vs oracle")
     gate(X, Q, f"{K}x{r}")
+
+
+@pytest.mark.parametrize("K,r", [(1100, 544), (3000, 736), (2048, 992)])
+def test_full_width_above_512_columns(cuda, K, r):
+    """orth.py:20: above 512 columns, r not a multiple of 256 runs kcholf at full width -- bit-exact vs the oracle,
+    within the gates, and the same through the C ABI's orth-dispatch plan (spanqr_plan_create)"""
+    X = next(gen.make_cases(K, r, ["mixed_c6"], (0,))).X
+    plan = get_plan(K, r, cuda)
+    assert plan.query(_lib.Q_BLOCKS) == 0
+    print(f"full width {K}x{r}: {plan.chol_grid} Cholesky workgroups", flush=True)
+    Q = orth(X.to(cuda))
+    assert_bits(Q, oracle.orth(X.numpy(), plan.split_rows), f"{K}x{r} vs oracle")
+    gate(X, Q, f"{K}x{r}")
+    h = ctypes.c_void_p()
+    _lib.check(_lib.lib().spanqr_plan_create(K, r, cuda.index or 0, ctypes.byref(h)))
+    try:
+        assert _lib.lib().spanqr_plan_query(h, _lib.Q_BLOCKS) == 0
+        Xd, Qd = X.to(cuda), torch.empty(K, r, device=cuda)
+        _lib.check(_lib.lib().spanqr_orth_f32(h, Xd.data_ptr(), r, Qd.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2,
+                                              stream_handle(cuda)))
+        torch.cuda.synchronize()
+        assert_bits(Qd, Q, "spanqr_plan_create's plan vs orth")
+    finally:
+        _lib.lib().spanqr_plan_destroy(h)
+
+
+def test_kcholf_full_width_where_orth_is_blocked(cuda):
+    """at r = 768 orth takes borth over 256-column blocks (orth.py:18-19) while kcholqr_f runs at full width, as the
+    reference's kcholqr_f does (kcholqr.py:92-112)"""
+    K, r = 1100, 768
+    X = next(gen.make_cases(K, r, ["mixed_c4"], (1,))).X
+    print(f"kcholf full width {K}x{r}", flush=True)
+    Qk = kcholqr_f(X.to(cuda))
+    assert_bits(Qk, oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows), "kcholqr_f vs oracle")
+    assert_bits(orth(X.to(cuda)), oracle.borth(X.numpy()), "orth (borth) vs oracle")
+
+
+@pytest.mark.parametrize("K,r", [(3000, 736), (1100, 1024), (2048, 512)])
+def test_repeated_calls_bit_identical(cuda, K, r):
+    """forty calls on one plan give the same bits: every flag and column credit is published only after the L2
+    write-back of what it covers has completed (a flag that overtook the write-back let readers on another XCD see
+    the previous launch's values, most often at these shapes)"""
+    X = next(gen.make_cases(K, r, ["mixed_c6"], (0,))).X.to(cuda)
+    print(f"repeated calls {K}x{r}", flush=True)
+    Q0 = kcholqr_f(X)
+    for i in range(40):
+        assert_bits(kcholqr_f(X), Q0, f"call {i + 1}")

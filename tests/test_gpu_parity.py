@@ -39,6 +39,9 @@ SHAPES = [(256, 64), (256, 128), (384, 256), (768, 512)]
 # r a multiple of 32 but not of 64 (kcholqr.py:98-99 runs kcholf there too): the last 64-column Gram / NS tile is
 # half outside X, and an odd number of 32-column blocks in the Cholesky and the solve
 SHAPES32 = [(100, 32), (300, 96), (512, 160), (640, 224), (1000, 480)]
+# kcholf at full width above 512 columns (orth.py:20 for r not a multiple of 256; kcholqr_f at any multiple of 32):
+# tile rows of up to 32 tiles over up to six owner workgroups each, four column blocks per solve wavefront
+SHAPESW = [(600, 544), (1100, 640), (2000, 800), (1024, 992), (1100, 1024)]
 
 
 @pytest.mark.parametrize("K,r", SHAPES)
@@ -48,7 +51,7 @@ def test_dust_on_device(cuda, K, r):
     assert_bits(Z, oracle.dust(K, r), "dust")
 
 
-@pytest.mark.parametrize("K,r", SHAPES + SHAPES32)
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32 + SHAPESW)
 @pytest.mark.parametrize("kahan", [True, False])
 def test_gram(cuda, K, r, kahan):
     print(f"gram {K}x{r} kahan={kahan}", flush=True)
@@ -60,7 +63,7 @@ def test_gram(cuda, K, r, kahan):
     assert_bits(npart, npo, "norm partials")
 
 
-@pytest.mark.parametrize("K,r", SHAPES + SHAPES32)
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32 + SHAPESW)
 def test_gram_scaled(cuda, K, r):
     print(f"gram scaled {K}x{r}", flush=True)
     X = case_x(K, r, "huge_1e25")
@@ -74,7 +77,7 @@ def test_gram_scaled(cuda, K, r):
     assert_bits(npart, npo, "norm partials (scaled)")
 
 
-@pytest.mark.parametrize("K,r", SHAPES + SHAPES32)
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32 + SHAPESW)
 @pytest.mark.parametrize("name", ["mixed_c4", "rank_half", "zero"])
 def test_chol(cuda, K, r, name):
     print(f"chol {K}x{r} {name}", flush=True)
@@ -109,7 +112,7 @@ def test_chol32_absolute(cuda, K, r):
 # (16400 x 384: two column blocks per wave and two row blocks per workgroup, the last one past K); ragged K on all
 @pytest.mark.parametrize("K,r", SHAPES + [(16384, 256), (32768, 64), (4100, 128), (4111, 192), (9230, 192),
                                           (16400, 256), (16425, 128), (16400, 384)] + SHAPES32 +
-                         [(9300, 96), (10000, 224), (16400, 288)])
+                         [(9300, 96), (10000, 224), (16400, 288)] + SHAPESW + [(9000, 800)])
 @pytest.mark.parametrize("pass1", [True, False])
 def test_trsm(cuda, K, r, pass1):
     print(f"trsm {K}x{r} pass1={pass1}", flush=True)
@@ -131,7 +134,7 @@ def test_trsm(cuda, K, r, pass1):
     assert_bits(Y, Yo, "Y")
 
 
-@pytest.mark.parametrize("K,r", SHAPES + SHAPES32)
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32 + SHAPESW)
 @pytest.mark.parametrize("kahan", [True, False])
 def test_ns_step(cuda, K, r, kahan):
     print(f"ns {K}x{r} kahan={kahan}", flush=True)
@@ -148,7 +151,9 @@ ORTH_CASES = [(256, 64, "mixed_c4"), (256, 128, "zero"), (384, 256, "rank_half")
               (768, 512, "dup_cols"), (1024, 256, "huge_1e25"), (1024, 256, "tiny_1e-25"), (2048, 512, "mixed_c8"),
               (17408, 256, "ttf_cu4_t1e-2"), (4100, 192, "mixed_c6"),
               (64, 32, "zero"), (300, 96, "mixed_c4"), (1000, 160, "rank_half"), (4100, 224, "ttf_cu4_t1e-2"),
-              (768, 480, "mixed_c8"), (12000, 160, "mixed_c4"), (2048, 352, "huge_1e25")]
+              (768, 480, "mixed_c8"), (12000, 160, "mixed_c4"), (2048, 352, "huge_1e25"),
+              (600, 544, "mixed_c4"), (2000, 800, "ttf_cu4_t1e-2"), (1024, 992, "rank_half"), (4096, 640, "huge_1e25"),
+              (672, 672, "zero")]
 
 
 @pytest.mark.parametrize("K,r,name", ORTH_CASES)
