@@ -967,34 +967,35 @@ __device__ __forceinline__ void wait_lds(const uint32_t* word, uint32_t target, 
 }
 
 constexpr int CH_WG0_TILES = 24;   // workgroup 0: D[2], X1, R2[2][5], dl[2], li[2], P1[2], P2[2], C2[2], id
-// Owner parts: tile row i (i + 1 tiles) is split over P = ceil((i + 1) / OWNER_W) workgroups, each holding a run of
+// Owner parts: tile row i (i + 1 tiles) is split over P = ceil((i + 1) / w) workgroups, each holding a run of
 // consecutive tiles T(i, s..e-1): widths floor((i + 1) / P), the last (i + 1) % P parts one wider, so that for
-// OWNER_W >= 6 the last part (which holds T(i, i-3..i) and hands them to workgroup 0) has at least 4 tiles for every
-// row i >= 4. A part's work per column block shrinks with its width, so long rows keep up with workgroup 0's steps.
-constexpr int OWNER_W = 6;   // (6: the best of 6, 7, 8 and 16 measured at r = 512)
-static_assert(OWNER_W >= 6 && OWNER_W <= 16, "owner parts: the last part of a row needs 4 tiles");
-__host__ __device__ constexpr int row_parts(int i) { return (i + OWNER_W) / OWNER_W; }
-__host__ __device__ inline void part_range(int i, int q, int& s, int& e) {
-    const int n = i + 1, P = row_parts(i), base = n / P, lo = P - n % P;   // parts q < lo have base tiles
+// w >= 6 the last part (which holds T(i, i-3..i) and hands them to workgroup 0) has at least 4 tiles for every row
+// i >= 4. A part's work per column block shrinks with its width, so long rows keep up with workgroup 0's steps; the
+// plan picks w (a single matrix: OWNER_W; a batch: wider parts where that puts it in fewer co-resident launches).
+constexpr int OWNER_W = 6;       // (6: the best of 6, 7, 8 and 16 measured at r = 512 for one matrix)
+constexpr int OWNER_WMAX = 16;   // widest parts (one part per row up to r = 512)
+__host__ __device__ constexpr int row_parts(int i, int w) { return (i + w) / w; }
+__host__ __device__ inline void part_range(int i, int q, int w, int& s, int& e) {
+    const int n = i + 1, P = row_parts(i, w), base = n / P, lo = P - n % P;   // parts q < lo have base tiles
     s = q * base + (q > lo ? q - lo : 0);
     e = s + base + (q >= lo ? 1 : 0);
 }
 // workgroup b >= 1 of the Cholesky: row i, tiles [s, e); the rows' parts in order of i, then of s
-__device__ inline void owner_part(int b, int nb, int& i, int& s, int& e) {
+__device__ inline void owner_part(int b, int nb, int w, int& i, int& s, int& e) {
     int q = b - 1;
     i = 4;
-    while (i < nb - 1 && q >= row_parts(i)) {
-        q -= row_parts(i);
+    while (i < nb - 1 && q >= row_parts(i, w)) {
+        q -= row_parts(i, w);
         ++i;
     }
-    part_range(i, q, s, e);
+    part_range(i, q, w, s, e);
 }
-// LDS tiles of an owner part: its row tiles and their panels (at most min(nb, OWNER_W) each), Li_j and L(i, j)
-__host__ __device__ constexpr int owner_lds_tiles(int nb) { return 2 * (nb < OWNER_W ? nb : OWNER_W) + 2; }
+// LDS tiles of an owner part: its row tiles and their panels (at most min(nb, w) each), Li_j and L(i, j)
+__host__ __device__ constexpr int owner_lds_tiles(int nb, int w) { return 2 * (nb < w ? nb : w) + 2; }
 // workgroups of one Cholesky: workgroup 0 and the parts of rows 4..nb-1
-constexpr int chol_workgroups(int nb) {
+constexpr int chol_workgroups(int nb, int w) {
     int n = 1;
-    for (int i = 4; i < nb; ++i) n += row_parts(i);
+    for (int i = 4; i < nb; ++i) n += row_parts(i, w);
     return n;
 }
 
@@ -1011,8 +1012,8 @@ struct CholWG0 {
     Tile id;        // identity (the tile factor's inverse lanes start from it)
 };
 
-size_t chol_lds_bytes(int r) {
-    const int owner_tiles = owner_lds_tiles(r / CB);
+size_t chol_lds_bytes(int r, int w) {
+    const int owner_tiles = owner_lds_tiles(r / CB, w);
     const int tiles = owner_tiles > CH_WG0_TILES ? owner_tiles : CH_WG0_TILES;
     return (size_t)tiles * sizeof(Tile) + 256 * sizeof(float);
 }
@@ -1034,7 +1035,7 @@ size_t chol_lds_bytes(int r) {
 // column k at the release that opens step k+2 (its stores of column k's operands completed during step k+1), column
 // nb-2 at a release of its own in the last step, and column nb-1 (Li_{nb-1} alone) right after the last tile factor.
 // Column k is complete at 1 + max(0, nb - 4 - k) credits; the counters start at zero.
-static_assert(chol_workgroups(CH_MAXROW) <= FLAG_STRIDE - CH_MAXROW * (CH_MAXROW + 1),
+static_assert(chol_workgroups(CH_MAXROW, OWNER_W) <= FLAG_STRIDE - CH_MAXROW * (CH_MAXROW + 1),
               "a call counter per Cholesky workgroup after the panel and hand-over flags");
 
 __device__ __forceinline__ void credit(uint32_t* colcnt, int k) {
@@ -1046,7 +1047,7 @@ template <bool STAMP>
 __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A, int r, const double* __restrict__ npart,
                                           int nnp, float alpha, float tau_rel, float* L, float* Li, float* Lp,
                                           uint32_t* bar, uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim,
-                                          uint32_t* colcnt) {
+                                          uint32_t* colcnt, int ow) {
     extern __shared__ float4 chol_lds[];
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int nb = r / CB;
@@ -1074,7 +1075,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
     Tile* tiles = reinterpret_cast<Tile*>(misc + 256);
     // an owner part: tile row oi, tiles T(oi, os..oe-1)
     int oi = 0, os = 0, oe = 0;
-    if (b > 0) owner_part(b, nb, oi, os, oe);
+    if (b > 0) owner_part(b, nb, ow, oi, os, oe);
     // Waves 1-2 load the workgroup's first tiles (workgroup 0: T(0, 0), T(1, 1), T(1, 0) into D[0], D[1], X1; an
     // owner part: its tiles of the row) while wave 0 sums the norm partials; the diagonal shift is added once it is
     // known (the same single addition as on a shifted load).
@@ -1084,7 +1085,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 return A + (q == 0 ? (size_t)0 : (size_t)CB * r + (q == 1 ? CB : 0));
             });
         } else {
-            load_tiles<OWNER_W, 128>(tiles, oe - os, r, 0u, 0.f, tid - 64,
+            load_tiles<OWNER_WMAX, 128>(tiles, oe - os, r, 0u, 0.f, tid - 64,
                                      [&](int q) { return A + (size_t)CB * oi * r + (size_t)CB * (os + q); });
         }
     }
@@ -1268,7 +1269,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         const int i = oi, s = os, e = oe;
         const bool last = e == i + 1;
         const int jl = last ? i - 4 : e - 1;
-        const int pw = owner_lds_tiles(nb) / 2 - 1;
+        const int pw = owner_lds_tiles(nb, ow) / 2 - 1;
         Tile* rt = tiles;
         Tile* pn = tiles + pw;
         Tile& li = tiles[2 * pw];
@@ -1392,7 +1393,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
             }
             __syncthreads();
             if (q4)
-                load_tiles_to<OWNER_W + 1, 256>(nr + (mine ? 0 : 1), tid,
+                load_tiles_to<OWNER_WMAX + 1, 256>(nr + (mine ? 0 : 1), tid,
                                                 [&](int q) -> Tile& { return q < nr ? pn[k3 + q - s] : pin; },
                                                 [&](int q) {
                                                     const int k = q < nr ? k3 + q : i;
@@ -1439,9 +1440,9 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
 template <bool STAMP>
 __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
                                               float tau_rel, float* L, float* Li, float* Lp, uint32_t* bar,
-                                              uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim) {
+                                              uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim, int ow) {
     chol_body<STAMP>(blockIdx.x, blockIdx.z, A, r, npart, nnp, alpha, tau_rel, L, Li, Lp, bar, flags, scal, stamps,
-                     lim, nullptr);
+                     lim, nullptr, ow);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1837,7 +1838,7 @@ __device__ __forceinline__ void trsm_wave_body(const int g, const int z, const M
 // are dispatched first and never wait on a solve workgroup). Pointers address matrix 0 of the launch.
 struct CholArgs {
     float* A; const double* npart; float* L; float* Li; float* Lp; uint32_t* bar; uint32_t* flags; float* scal;
-    uint32_t* colcnt; float alpha, tau_rel; int r, nnp, nz, grid; uint32_t lim;
+    uint32_t* colcnt; float alpha, tau_rel; int r, nnp, nz, grid, ow; uint32_t lim;   // ow: owner part width
 };
 struct SolveArgs {
     MatsIn A; MatsOut Y; const uint32_t* amax_part; const float* Z; float* scal; long lda, ldz, ldy; float eps;
@@ -1851,7 +1852,7 @@ __global__ __launch_bounds__(64 * TRSM_NW) void k_chol_solve(const CholArgs c, c
     const int nchol = c.nz * c.grid;
     if ((int)blockIdx.x < nchol) {
         chol_body<false>(blockIdx.x % c.grid, blockIdx.x / c.grid, c.A, c.r, c.npart, c.nnp, c.alpha, c.tau_rel, c.L,
-                         c.Li, c.Lp, c.bar, c.flags, c.scal, nullptr, c.lim, c.colcnt);
+                         c.Li, c.Lp, c.bar, c.flags, c.scal, nullptr, c.lim, c.colcnt, c.ow);
         return;
     }
     const int b = blockIdx.x - nchol;
@@ -2153,6 +2154,7 @@ struct spanqr_plan {
     int batch = 1, chol_bmax = 1;   // matrices per call; matrices per Cholesky launch
     size_t lp_stride = 0;           // floats of packed factor per matrix
     int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0, trsm_rb = 1;   // NB: 32-column blocks
+    int owner_w = OWNER_W;    // tiles per Cholesky owner part at most
     bool trsm_rows = false;   // solve with a wavefront pair per 16 rows (k_trsm_rows) instead of k_trsm
     int solve_rb = 0;         // row blocks per solve workgroup in the Cholesky's launch (0: separate launches)
     int solve_nrb = 0;        // solve workgroups per matrix there
@@ -2269,7 +2271,7 @@ void launch_reduce(const spanqr_plan* p, int mode, float* out, int n, hipStream_
 int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t st, int nnp, int n,
                 bool stamp = false) {
     const size_t r = p->r;
-    const size_t lds = chol_lds_bytes(p->r);
+    const size_t lds = chol_lds_bytes(p->r, p->owner_w);
     for (int z0 = 0; z0 < n; z0 += p->chol_bmax) {
         const int nz = (n - z0 < p->chol_bmax) ? n - z0 : p->chol_bmax;
         float* A = p->G + z0 * r * r;
@@ -2283,10 +2285,10 @@ int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t
         const dim3 grid(p->chol_grid, 1, nz);
         if (stamp)
             k_chol<true><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps,
-                                                 g_spin_limit);
+                                                 g_spin_limit, p->owner_w);
         else
             k_chol<false><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps,
-                                                  g_spin_limit);
+                                                  g_spin_limit, p->owner_w);
         HIPCHK(hipGetLastError());
     }
     return SPANQR_OK;
@@ -2310,8 +2312,8 @@ hipError_t trsm_set_lds_plan(int q, int rb, int r) {
 
 // LDS of the Cholesky's launch with its solve: the larger of the two roles' needs (q = 0: the wavefront-per-row-block
 // solve, eight transpose tiles and a word)
-size_t fused_lds(int r, int q, int rb) {
-    const size_t a = chol_lds_bytes(r), b = q ? trsm_lds(r, rb) : (TRSM_NW * 16 * 33 + 1) * sizeof(float);
+size_t fused_lds(int r, int ow, int q, int rb) {
+    const size_t a = chol_lds_bytes(r, ow), b = q ? trsm_lds(r, rb) : (TRSM_NW * 16 * 33 + 1) * sizeof(float);
     return a > b ? a : b;
 }
 
@@ -2430,7 +2432,7 @@ int launch_chol_solve(spanqr_plan* p, float alpha, float tau, float* scal, hipSt
                       const MatsIn& A, long lda, bool pass1, float eps, const Dust& dz, const MatsOut& Y, long ldy) {
     const size_t r = p->r;
     const int q = p->solve_q;
-    const size_t lds = fused_lds(p->r, q, p->solve_rb);
+    const size_t lds = fused_lds(p->r, p->owner_w, q, p->solve_rb);
     for (int z0 = 0; z0 < n; z0 += p->chol_bmax) {
         const int nz = (n - z0 < p->chol_bmax) ? n - z0 : p->chol_bmax;
         CholArgs c;
@@ -2449,6 +2451,7 @@ int launch_chol_solve(spanqr_plan* p, float alpha, float tau, float* scal, hipSt
         c.nnp = nnp;
         c.nz = nz;
         c.grid = p->chol_grid;
+        c.ow = p->owner_w;
         c.lim = g_spin_limit;
         SolveArgs t{};
         for (int i = 0; i < nz; ++i) {
@@ -2600,7 +2603,8 @@ void plan_shape(spanqr_plan* p, int K, int r, int batch) {
     p->K = K; p->r = r; p->batch = batch;
     p->nt = (r + TB - 1) / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / CB;
     split_policy(K, p->U, &p->S, &p->KS);
-    p->chol_grid = chol_workgroups(r / CB);     // workgroup 0 + the parts of tile rows 4..r/32-1
+    p->owner_w = OWNER_W;
+    p->chol_grid = chol_workgroups(r / CB, p->owner_w);     // workgroup 0 + the parts of tile rows 4..r/32-1
     p->trsm_q = trsm_q_for(r / CB);
     // solve: RB row blocks of 16 per workgroup; one block while that leaves fewer than ~2 workgroups per CU (and
     // always one with four column blocks per wavefront, r > 512)
@@ -2627,18 +2631,44 @@ int plan_device_setup(spanqr_plan* p, int device) {
     }
     int occ = 0, cus = 0;
     {
-        const int need = (int)chol_lds_bytes(r);
+        // the largest Cholesky LDS of any part width (the attribute is per kernel, shared by every plan)
+        const int need = (int)chol_lds_bytes(r, OWNER_WMAX);
         hipError_t e = hipFuncSetAttribute((const void*)k_chol<true>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)k_chol<false>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
         if (e != hipSuccess)
             return fail(SPANQR_EHIP, "setting the Cholesky's LDS size (%d bytes) failed: %s", need, hipGetErrorString(e));
     }
-    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k_chol<true>, 512, chol_lds_bytes(r)));
     HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
     p->cus = cus;
-    if (occ * cus < p->chol_grid)
-        return fail(SPANQR_EHIP, "the Cholesky needs %d co-resident workgroups, device holds %d", p->chol_grid, occ * cus);
+    // The owner part width: OWNER_W for one matrix; for a batch, the narrowest of 6, 8, 12 and 16 tiles that runs
+    // the batch's Cholesky in the fewest launches (each launch needs all its workgroups resident at once, within
+    // three quarters of the device: the margin leaves room for work of other streams)
+    {
+        const int widths[] = {OWNER_W, 8, 12, OWNER_WMAX};
+        int best_w = 0, best_n = 1 << 30, best_occ = 0;
+        for (int w : widths) {
+            if (p->batch == 1 && w != OWNER_W) break;
+            int o = 0;
+            HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, (const void*)k_chol<true>, 512, chol_lds_bytes(r, w)));
+            const int grid = chol_workgroups(r / CB, w);
+            if (o * cus < grid) continue;
+            int bmax = (o * cus * 3 / 4) / grid;
+            if (bmax < 1) bmax = 1;
+            const int launches = (p->batch + bmax - 1) / bmax;
+            if (launches < best_n) {
+                best_n = launches;
+                best_w = w;
+                best_occ = o;
+            }
+        }
+        if (best_w == 0)
+            return fail(SPANQR_EHIP, "the Cholesky needs %d co-resident workgroups, device holds too few",
+                        chol_workgroups(r / CB, OWNER_WMAX));
+        p->owner_w = best_w;
+        p->chol_grid = chol_workgroups(r / CB, best_w);
+        occ = best_occ;
+    }
     // a batch's launch takes at most three quarters of the device's resident capacity: the flag waits need every
     // workgroup of a launch resident at once, and the margin leaves room for work of other streams
     p->chol_bmax = (occ * cus * 3 / 4) / p->chol_grid;
@@ -2673,7 +2703,7 @@ int plan_device_setup(spanqr_plan* p, int device) {
                 nwg = (rowblocks + 1) / 2;
             }
         }
-        const size_t lds = fused_lds(r, q, rb);
+        const size_t lds = fused_lds(r, p->owner_w, q, rb);
         if (nwg <= avail && lds <= (size_t)maxsh && fused_set_lds(q, q ? rb : r / CB, (int)lds) == hipSuccess) {
             p->solve_q = q;
             p->solve_rb = rb;
