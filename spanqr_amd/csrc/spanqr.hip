@@ -2066,6 +2066,125 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
         }
 }
 
+// The Newton-Schulz step of k_nsapply (same tiles, chains and rounding, so the same bits) for grids of about one
+// workgroup per CU, where no other workgroup hides a step's load latency: the MS-column steps go through two LDS
+// buffers, and the global loads of step s + 3 are issued as step s ends, into one of two register sets, so each load
+// has two steps of MFMA work to arrive in (one barrier per step).
+template <int MS>
+__global__ __launch_bounds__(256) void k_nsapply_pipe(const MatsIn Ys, long ldy, int K, int r,
+                                                      const float* __restrict__ D, const MatsOut Outs, long ldo,
+                                                      const uint32_t* err) {
+    const float* __restrict__ Yin = Ys.p[blockIdx.z];
+    float* __restrict__ Out = Outs.p[blockIdx.z];
+    D += (size_t)blockIdx.z * r * r;
+    const bool failed = err != nullptr && err[(size_t)blockIdx.z * BAR_STRIDE + 2] != 0u;
+    __shared__ float sY[2][32][MS + 2];
+    __shared__ float sD[2][MS][80];
+    const int row0 = blockIdx.x * 32, col0 = blockIdx.y * 64;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
+    const int rb = w >> 1, cbase = (w & 1) * 2;
+    constexpr int NY = MS / 32, ND = MS / 16;
+    struct Regs { float4 y[NY], d[ND]; } R0, R1;
+    const int ns = r / MS;
+    auto gload = [&](int s, Regs& R) {
+        const int m0 = s * MS;
+#pragma unroll
+        for (int q = 0; q < NY; ++q) {
+            const int idx = tid + 256 * q, row = idx / (MS / 4), c4 = idx % (MS / 4);
+            // unconditional loads from clamped (in-bounds) addresses: no branch between a step's loads, so the wait
+            // before a register set's LDS store counts only the loads issued before it. Row i of Y feeds only output
+            // row i, and column j of D only output column j, so rows past K and columns past r (r % 64 == 32) read
+            // any in-bounds values: they reach only outputs that are not written.
+            const int gr = row0 + row < K ? row0 + row : K - 1;
+            R.y[q] = *reinterpret_cast<const float4*>(Yin + (size_t)gr * ldy + m0 + 4 * c4);
+        }
+#pragma unroll
+        for (int q = 0; q < ND; ++q) {
+            const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15;
+            const int gc = col0 + 4 * c4 < r ? col0 + 4 * c4 : 0;
+            R.d[q] = *reinterpret_cast<const float4*>(D + (size_t)(m0 + row) * r + gc);
+        }
+    };
+    auto lstore = [&](int buf, const Regs& R) {
+#pragma unroll
+        for (int q = 0; q < NY; ++q) {
+            const int idx = tid + 256 * q, row = idx / (MS / 4), c4 = idx % (MS / 4);
+            sY[buf][row][4 * c4 + 0] = R.y[q].x; sY[buf][row][4 * c4 + 1] = R.y[q].y;
+            sY[buf][row][4 * c4 + 2] = R.y[q].z; sY[buf][row][4 * c4 + 3] = R.y[q].w;
+        }
+#pragma unroll
+        for (int q = 0; q < ND; ++q) {
+            const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15;
+            *reinterpret_cast<float4*>(&sD[buf][row][4 * c4]) = R.d[q];
+        }
+    };
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    // a step's LDS operands are read ahead of its MFMAs (two steps' worth in flight), so the LDS latency overlaps the
+    // chains
+    auto compute = [&](int buf) {
+        float xa[MS / 4], xb[2][MS / 4];
+#pragma unroll
+        for (int kk = 0; kk < MS / 4; ++kk) {
+            xa[kk] = sY[buf][16 * rb + l16][4 * kk + lk];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) xb[c][kk] = sD[buf][4 * kk + lk][16 * (cbase + c) + l16];
+        }
+#pragma unroll
+        for (int kk = 0; kk < MS / 4; ++kk)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) acc[c] = mfma(xa[kk], xb[c][kk], acc[c]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+        for (int g = 0; g < MS / 4 - 2; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
+    // ns is even (checked at launch). Every load and LDS store is unconditional (steps past the last reload the last
+    // step, whose copy in a buffer is never multiplied), so the loop body has no branch and each LDS store waits only
+    // for its own register set
+    const int last = ns - 1;
+    gload(0, R0);
+    gload(1, R1);
+    lstore(0, R0);
+    __syncthreads();
+    // the residual's Y elements (this lane's outputs), fetched now so the epilogue does not wait for them
+    float cv[2][4];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = row0 + 16 * rb + 4 * lk + v, col = col0 + 16 * (cbase + c) + l16;
+            cv[c][v] = Yin[(size_t)(row < K ? row : K - 1) * ldy + (col < r ? col : 0)];
+        }
+    gload(min(2, last), R0);
+    __builtin_amdgcn_sched_barrier(0);   // the loads go out here, not next to their LDS stores
+    // steps s, s + 1: multiply from buffer 0 (1), move register set 1 (0) -- step s + 1 (s + 2) -- into the other
+    // buffer, then refill that set with step s + 3 (s + 4)
+    int s = 0;
+    do {   // (a do-while: no guard before the loop, below which the set-1 loads above could be moved)
+        compute(0);
+        lstore(1, R1);
+        __syncthreads();
+        gload(min(s + 3, last), R1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(1);
+        lstore(0, R0);
+        __syncthreads();
+        gload(min(s + 4, last), R0);
+        __builtin_amdgcn_sched_barrier(0);
+        s += 2;
+    } while (s < ns);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = row0 + 16 * rb + 4 * lk + v, col = col0 + 16 * (cbase + c) + l16;
+            if (row < K && col < r) Out[(size_t)row * ldo + col] = failed ? __builtin_nanf("") : cv[c][v] + acc[c][v];
+        }
+}
+
 // word[i * stride] = 0 for i < n (clears wait-error words where no k_amax runs first)
 __global__ void k_clear_words(uint32_t* word, int n, int stride) {
     if ((int)threadIdx.x < n) word[(size_t)threadIdx.x * stride] = 0u;
@@ -2482,7 +2601,13 @@ void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsO
     // and 768x512 than 32-column steps, level elsewhere)
     // r % 64 == 32: 32-column steps (the chain over r stays exact: no step past r) and a half-used last column tile
     const dim3 grid((p->K + 31) / 32, (p->r + 63) / 64, n);
-    if (p->r % 64 == 0)
+    if ((long)grid.x * grid.y * n <= 2L * p->cus && p->r % 64 == 0) {
+        // an even number of steps: 64 columns when r % 128 == 0, else 32
+        if (p->r % 128 == 0)
+            k_nsapply_pipe<64><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, p->bar);
+        else
+            k_nsapply_pipe<32><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, p->bar);
+    } else if (p->r % 64 == 0)
         k_nsapply<false, 64><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, nullptr, 0, 0, p->bar);
     else
         k_nsapply<false, 32><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, nullptr, 0, 0, p->bar);

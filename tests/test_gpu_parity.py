@@ -134,7 +134,12 @@ def test_trsm(cuda, K, r, pass1):
     assert_bits(Y, Yo, "Y")
 
 
-@pytest.mark.parametrize("K,r", SHAPES + SHAPES32 + SHAPESW)
+# grids of at most two workgroups per CU take the two-buffer Newton-Schulz apply: ragged K, 64-column steps
+# (r % 128 == 0) and 32-column steps (r % 128 == 64), an even number of them
+SHAPES_NSP = [(1000, 384), (777, 320), (2100, 448)]
+
+
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32 + SHAPESW + SHAPES_NSP)
 @pytest.mark.parametrize("kahan", [True, False])
 def test_ns_step(cuda, K, r, kahan):
     print(f"ns {K}x{r} kahan={kahan}", flush=True)
