@@ -2185,6 +2185,102 @@ __global__ __launch_bounds__(256) void k_nsapply_pipe(const MatsIn Ys, long ldy,
         }
 }
 
+// The Newton-Schulz step for tall Y (same chains and rounding as k_nsapply, so the same bits), r % 64 == 0, r <= MAXR.
+// Workgroup (slab, g) of nslab * G: its four wavefronts own the four 16-column tiles of 64-column slab `slab` and keep
+// their MFMA B operands (the tile's r rows of D) in registers for the whole launch, so D is read once per workgroup
+// instead of once per 32 rows; the workgroup walks 16-row blocks g, g + G, ... of Y through two LDS buffers, the
+// next block's loads in flight during a block's chain. The four slabs of one row group sit on one XCD (workgroup id
+// mod 8), so each Y row is fetched into one L2. LDS holds a block as [row][k mod 4][k / 4] (rows padded): the A
+// operands of four consecutive MFMAs are one 16-byte read; the residual Y is read back from the same buffer.
+constexpr int NSR_PADK = 4;
+template <int MAXR>
+constexpr int nsr_row_stride() { return 4 * (MAXR / 4 + NSR_PADK) + 4; }
+template <int MAXR>
+__global__ __launch_bounds__(256, 2) void k_nsapply_res(const MatsIn Ys, long ldy, int K, int r,
+                                                        const float* __restrict__ D, const MatsOut Outs, long ldo,
+                                                        const uint32_t* err, int G) {
+    constexpr int KS = MAXR / 4 + NSR_PADK, RS = nsr_row_stride<MAXR>();
+    __shared__ __align__(16) float sY[2][16 * RS];
+    const float* __restrict__ Yin = Ys.p[blockIdx.z];
+    float* __restrict__ Out = Outs.p[blockIdx.z];
+    D += (size_t)blockIdx.z * r * r;
+    const bool failed = err != nullptr && err[(size_t)blockIdx.z * BAR_STRIDE + 2] != 0u;
+    const int nslab = r / 64, id = blockIdx.x, rest = id >> 3;
+    const int slab = rest % nslab, g = (id & 7) + 8 * (rest / nslab);
+    const int nblk = (K + 15) / 16;
+    if (g >= nblk) return;   // (the launch keeps G <= nblk; whole workgroup, before any barrier)
+    const int nb = (nblk - g + G - 1) / G;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lk = lane >> 4;
+    const int c0 = slab * 64 + 16 * w, r4 = r / 4;
+    // B operands: bD[kk] = D[4 kk + lk][c0 + l16] (kk >= r / 4 loads a valid row and is never multiplied)
+    float bD[MAXR / 4];
+#pragma unroll
+    for (int kk = 0; kk < MAXR / 4; ++kk) bD[kk] = D[(size_t)(4 * (kk < r4 ? kk : r4 - 1) + lk) * r + c0 + l16];
+    // Y block loads: float4 q of this thread is row qrow[q] = (tid + 256 q) / r4, columns 4 c4 .. 4 c4 + 3 with c4
+    // the remainder (divided once, here)
+    constexpr int NQ = MAXR / 64;
+    float4 R[NQ];
+    int qrow[NQ], qc4[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int idx = tid + 256 * q;
+        qrow[q] = idx / r4;
+        qc4[q] = idx - qrow[q] * r4;
+    }
+    auto gload = [&](int i) {
+        const int row0 = (g + i * G) * 16;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            // rows past K (and past the block, q >= r / 64, never stored) read row K - 1: row i of Y feeds only
+            // output row i, which is not written
+            const int gr = row0 + qrow[q] < K ? row0 + qrow[q] : K - 1;
+            R[q] = *reinterpret_cast<const float4*>(Yin + (size_t)gr * ldy + 4 * qc4[q]);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            if (q < r / 64) {
+                float* d = &sY[buf][qrow[q] * RS + qc4[q]];
+                d[0] = R[q].x; d[KS] = R[q].y; d[2 * KS] = R[q].z; d[3 * KS] = R[q].w;
+            }
+        }
+    };
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    if (nb > 1) gload(1);
+    for (int i = 0; i < nb; ++i) {
+        const int buf = i & 1;
+        const float* sb = &sY[buf][l16 * RS + lk * KS];
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < MAXR / 4; k0 += 16) {
+            if (k0 >= r4) break;
+            float4 a[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const float4*>(sb + k0 + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc = mfma(a[j].x, bD[k0 + 4 * j + 0], acc);
+                acc = mfma(a[j].y, bD[k0 + 4 * j + 1], acc);
+                acc = mfma(a[j].z, bD[k0 + 4 * j + 2], acc);
+                acc = mfma(a[j].w, bD[k0 + 4 * j + 3], acc);
+            }
+        }
+        if (i + 1 < nb) lstore(buf ^ 1);   // its last readers finished before the previous barrier
+        const int row0 = (g + i * G) * 16, col = c0 + l16;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = row0 + 4 * lk + v;
+            const float cv = sY[buf][(4 * lk + v) * RS + (col & 3) * KS + (col >> 2)];
+            if (row < K) Out[(size_t)row * ldo + col] = failed ? __builtin_nanf("") : cv + acc[v];
+        }
+        __syncthreads();
+        if (i + 2 < nb) gload(i + 2);
+    }
+}
+
 // word[i * stride] = 0 for i < n (clears wait-error words where no k_amax runs first)
 __global__ void k_clear_words(uint32_t* word, int n, int stride) {
     if ((int)threadIdx.x < n) word[(size_t)threadIdx.x * stride] = 0u;
@@ -2601,7 +2697,13 @@ void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsO
     // and 768x512 than 32-column steps, level elsewhere)
     // r % 64 == 32: 32-column steps (the chain over r stays exact: no step past r) and a half-used last column tile
     const dim3 grid((p->K + 31) / 32, (p->r + 63) / 64, n);
-    if ((long)grid.x * grid.y * n <= 2L * p->cus && p->r % 64 == 0) {
+    if ((long)grid.x * grid.y * n > 2L * p->cus && p->r % 64 == 0 && p->r <= 256) {
+        // two workgroups per CU: G row groups (a multiple of 8, at most the number of 16-row blocks rounded up)
+        const int nslab = p->r / 64, nblk = (p->K + 15) / 16;
+        int G = (2 * p->cus / nslab) / 8 * 8;
+        G = std::max(8, std::min(G, (nblk + 7) / 8 * 8));
+        k_nsapply_res<256><<<dim3(nslab * G, 1, n), 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, p->bar, G);
+    } else if ((long)grid.x * grid.y * n <= 2L * p->cus && p->r % 64 == 0) {
         // an even number of steps: 64 columns when r % 128 == 0, else 32
         if (p->r % 128 == 0)
             k_nsapply_pipe<64><<<grid, 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, p->bar);
