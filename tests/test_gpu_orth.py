@@ -102,9 +102,10 @@ def test_abi_rejects_bad_operands(cuda):
     assert _lib.lib().spanqr_last_error()
 
 
-def test_graph_capture_replays(cuda):
-    """the whole call captured into one hipGraph; replays with eager work in between equal the eager result"""
-    K, r = 2048, 256
+@pytest.mark.parametrize("K,r", [(2048, 256), (768, 512), (17408, 256)])
+def test_graph_capture_replays(cuda, K, r):
+    """the whole call captured into one hipGraph; replays with eager work in between equal the eager result (both
+    Newton-Schulz apply forms: two-buffer at 2048x256 and 768x512, D in registers at 17408x256)"""
     X = gen.bench_input(K, r, seed=1).to(cuda)
     Qe = kcholqr_f(X)
     st = torch.cuda.Stream(cuda)
