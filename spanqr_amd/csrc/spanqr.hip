@@ -2698,9 +2698,10 @@ void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsO
     // r % 64 == 32: 32-column steps (the chain over r stays exact: no step past r) and a half-used last column tile
     const dim3 grid((p->K + 31) / 32, (p->r + 63) / 64, n);
     if ((long)grid.x * grid.y * n > 2L * p->cus && p->r % 64 == 0 && p->r <= 256) {
-        // two workgroups per CU: G row groups (a multiple of 8, at most the number of 16-row blocks rounded up)
+        // two workgroups per CU over the n matrices: G row groups per matrix (a multiple of 8, at most the number of
+        // 16-row blocks rounded up)
         const int nslab = p->r / 64, nblk = (p->K + 15) / 16;
-        int G = (2 * p->cus / nslab) / 8 * 8;
+        int G = (2 * p->cus / (nslab * n)) / 8 * 8;
         G = std::max(8, std::min(G, (nblk + 7) / 8 * 8));
         k_nsapply_res<256><<<dim3(nslab * G, 1, n), 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, p->bar, G);
     } else if ((long)grid.x * grid.y * n <= 2L * p->cus && p->r % 64 == 0) {

@@ -141,3 +141,16 @@ def test_batched_tall_solve(cuda):
     Qs = kcholqr_f_many([X.to(cuda) for X in Xs])
     for i in range(n):
         assert_bits(Qs[i], oracle.orth(Xs[i].numpy(), get_plan(K, r, cuda, n).split_rows), f"element {i} vs oracle")
+
+
+def test_batched_ns_apply_forms_agree(cuda):
+    """12 x 1100x192: the batch's Newton-Schulz apply keeps D's columns in registers (eight row groups per matrix),
+    each single call uses the two-buffer form; every Q is bit-identical across the two"""
+    K, r, n = 1100, 192, 12
+    g = torch.Generator().manual_seed(13)
+    Xs = [torch.randn(K, r, generator=g) * torch.logspace(0, -3, r) for _ in range(n)]
+    print(f"batched {n} x {K}x{r}", flush=True)
+    Qs = kcholqr_f_many([X.to(cuda) for X in Xs])
+    for i in (0, 5, n - 1):
+        assert_bits(Qs[i], kcholqr_f(Xs[i].to(cuda)), f"batch element {i} vs single call")
+    assert_bits(Qs[n - 1], oracle.orth(Xs[n - 1].numpy(), get_plan(K, r, cuda).split_rows), "last element vs oracle")
