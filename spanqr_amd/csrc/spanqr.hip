@@ -2192,15 +2192,19 @@ __global__ __launch_bounds__(256) void k_nsapply_pipe(const MatsIn Ys, long ldy,
 // next block's loads in flight during a block's chain. The four slabs of one row group sit on one XCD (workgroup id
 // mod 8), so each Y row is fetched into one L2. LDS holds a block as [row][k mod 4][k / 4] (rows padded): the A
 // operands of four consecutive MFMAs are one 16-byte read; the residual Y is read back from the same buffer.
+// The two buffers are dynamic LDS: nsr_lds_bytes (35 KB for MAXR = 256, 67 KB for 512).
 constexpr int NSR_PADK = 4;
 template <int MAXR>
 constexpr int nsr_row_stride() { return 4 * (MAXR / 4 + NSR_PADK) + 4; }
+template <int MAXR>
+constexpr size_t nsr_lds_bytes() { return (size_t)2 * 16 * nsr_row_stride<MAXR>() * sizeof(float); }
 template <int MAXR>
 __global__ __launch_bounds__(256, 2) void k_nsapply_res(const MatsIn Ys, long ldy, int K, int r,
                                                         const float* __restrict__ D, const MatsOut Outs, long ldo,
                                                         const uint32_t* err, int G) {
     constexpr int KS = MAXR / 4 + NSR_PADK, RS = nsr_row_stride<MAXR>();
-    __shared__ __align__(16) float sY[2][16 * RS];
+    extern __shared__ __align__(16) float nsr_lds[];
+    auto sY = [&](int buf) { return nsr_lds + buf * 16 * RS; };   // buffer buf
     const float* __restrict__ Yin = Ys.p[blockIdx.z];
     float* __restrict__ Out = Outs.p[blockIdx.z];
     D += (size_t)blockIdx.z * r * r;
@@ -2241,7 +2245,7 @@ __global__ __launch_bounds__(256, 2) void k_nsapply_res(const MatsIn Ys, long ld
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
             if (q < r / 64) {
-                float* d = &sY[buf][qrow[q] * RS + qc4[q]];
+                float* d = &sY(buf)[qrow[q] * RS + qc4[q]];
                 d[0] = R[q].x; d[KS] = R[q].y; d[2 * KS] = R[q].z; d[3 * KS] = R[q].w;
             }
         }
@@ -2252,7 +2256,7 @@ __global__ __launch_bounds__(256, 2) void k_nsapply_res(const MatsIn Ys, long ld
     if (nb > 1) gload(1);
     for (int i = 0; i < nb; ++i) {
         const int buf = i & 1;
-        const float* sb = &sY[buf][l16 * RS + lk * KS];
+        const float* sb = &sY(buf)[l16 * RS + lk * KS];
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k0 = 0; k0 < MAXR / 4; k0 += 16) {
@@ -2273,7 +2277,7 @@ __global__ __launch_bounds__(256, 2) void k_nsapply_res(const MatsIn Ys, long ld
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int row = row0 + 4 * lk + v;
-            const float cv = sY[buf][(4 * lk + v) * RS + (col & 3) * KS + (col >> 2)];
+            const float cv = sY(buf)[(4 * lk + v) * RS + (col & 3) * KS + (col >> 2)];
             if (row < K) Out[(size_t)row * ldo + col] = failed ? __builtin_nanf("") : cv + acc[v];
         }
         __syncthreads();
@@ -2697,13 +2701,18 @@ void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsO
     // and 768x512 than 32-column steps, level elsewhere)
     // r % 64 == 32: 32-column steps (the chain over r stays exact: no step past r) and a half-used last column tile
     const dim3 grid((p->K + 31) / 32, (p->r + 63) / 64, n);
-    if ((long)grid.x * grid.y * n > 2L * p->cus && p->r % 64 == 0 && p->r <= 256) {
+    if ((long)grid.x * grid.y * n > 2L * p->cus && p->r % 64 == 0 && p->r <= 512) {
         // two workgroups per CU over the n matrices: G row groups per matrix (a multiple of 8, at most the number of
         // 16-row blocks rounded up)
         const int nslab = p->r / 64, nblk = (p->K + 15) / 16;
         int G = (2 * p->cus / (nslab * n)) / 8 * 8;
         G = std::max(8, std::min(G, (nblk + 7) / 8 * 8));
-        k_nsapply_res<256><<<dim3(nslab * G, 1, n), 256, 0, st>>>(Y, ldy, p->K, p->r, p->G, Out, ldo, p->bar, G);
+        if (p->r <= 256)
+            k_nsapply_res<256><<<dim3(nslab * G, 1, n), 256, nsr_lds_bytes<256>(), st>>>(Y, ldy, p->K, p->r, p->G,
+                                                                                       Out, ldo, p->bar, G);
+        else
+            k_nsapply_res<512><<<dim3(nslab * G, 1, n), 256, nsr_lds_bytes<512>(), st>>>(Y, ldy, p->K, p->r, p->G,
+                                                                                       Out, ldo, p->bar, G);
     } else if ((long)grid.x * grid.y * n <= 2L * p->cus && p->r % 64 == 0) {
         // an even number of steps: 64 columns when r % 128 == 0, else 32
         if (p->r % 128 == 0)
@@ -2866,6 +2875,14 @@ int plan_device_setup(spanqr_plan* p, int device) {
             e = hipFuncSetAttribute((const void*)k_chol<false>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
         if (e != hipSuccess)
             return fail(SPANQR_EHIP, "setting the Cholesky's LDS size (%d bytes) failed: %s", need, hipGetErrorString(e));
+    }
+    {
+        const int need = (int)nsr_lds_bytes<512>();
+        const hipError_t e = hipFuncSetAttribute((const void*)k_nsapply_res<512>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, need);
+        if (e != hipSuccess)
+            return fail(SPANQR_EHIP, "setting the Newton-Schulz apply's LDS size (%d bytes) failed: %s", need,
+                        hipGetErrorString(e));
     }
     HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
     p->cus = cus;

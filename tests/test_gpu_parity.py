@@ -137,9 +137,9 @@ def test_trsm(cuda, K, r, pass1):
 # grids of at most two workgroups per CU take the two-buffer Newton-Schulz apply: ragged K, 64-column steps
 # (r % 128 == 0) and 32-column steps (r % 128 == 64), an even number of them
 SHAPES_NSP = [(1000, 384), (777, 320), (2100, 448)]
-# more than two workgroups per CU and r <= 256 take the apply with D's columns held in registers: 16-row blocks,
-# ragged K, one to four 64-column slabs
-SHAPES_NSR = [(17408, 256), (9000, 128), (6001, 192), (20000, 64)]
+# more than two workgroups per CU and r <= 512 take the apply with D's columns held in registers: 16-row blocks,
+# ragged K, one to eight 64-column slabs (r <= 256 and r <= 512 forms)
+SHAPES_NSR = [(17408, 256), (9000, 128), (6001, 192), (20000, 64), (4100, 512), (5000, 320)]
 
 
 @pytest.mark.parametrize("K,r", SHAPES + SHAPES32 + SHAPESW + SHAPES_NSP + SHAPES_NSR)
