@@ -368,9 +368,19 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
     const int t = threadIdx.x, row = 4 * b + (t >> 6), col = t & 63;
     const float* p = P + (size_t)u * TB * TB + row * TB + col;
     const size_t stride = (size_t)U * TB * TB;
-    // the partials in order of s, loaded eight (then four) at a time: one memory latency per batch
+    // the partials in order of s, loaded eight (then four) at a time: one memory latency per batch; up to eight
+    // splits in one batch (loads past S repeat partial S - 1 and are not added)
     double sum = 0.0;
     int s = 0;
+    if (S <= 8) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = p[(size_t)(e < S ? e : S - 1) * stride];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (e < S) sum = sum + (double)v[e];
+        s = S;
+    }
     for (; s + 8 <= S; s += 8) {
         float v[8];
 #pragma unroll
