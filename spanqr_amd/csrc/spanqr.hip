@@ -1258,6 +1258,9 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 if (lane == 0) __hip_atomic_store(p2done, (uint32_t)j, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
             __syncthreads();
+            // start the L2 write-back of this step's stores now (wave 7 has no part in the look-ahead); the
+            // publication at the next step's start then finds the lines clean
+            if (w == 7) asm volatile("buffer_wbl2 sc1" ::: "memory");
             if (STAMP && tid == 0) stamps[2 + 4 * j] = wall_clock64();
             // look-ahead, the part the next factor needs: L(j+1, j), then block j on T(j+1, j+1); L(j+2, j) is formed
             // by wave 7 and block j on tile row j+2 applied by wave 3, both in the next step
