@@ -95,18 +95,24 @@ def kernel_avg_us(X, which, reps):
 
 def chol_steps_us(X):
     """per 32-column diagonal step of the Cholesky: the device wall clock stamped by workgroup 0 of an instrumented
-    copy of the kernel (spanqr_profile_chol): (list of step us, factorisation us)"""
+    copy of the kernel (spanqr_profile_chol), warm (the median of five launches after two untimed ones, per step):
+    (list of step us, factorisation us)"""
     K, r = X.shape
     kcholqr_f(X)
     plan = get_plan(K, r, X.device)
     G, npart = stages.gram(X, kahan=True, use_scale=True)
     nb = r // 32
-    stamps = (ctypes.c_ulonglong * (6 * nb + 2))()
-    tick = ctypes.c_double()
-    _lib.check(_lib.lib().spanqr_profile_chol(plan.handle, G.data_ptr(), npart.data_ptr(), 1e-7, 1e-8, stamps,
-                                              ctypes.byref(tick), stream_handle(X.device)))
-    us = lambda a, b: (stamps[b] - stamps[a]) * tick.value / 1000.0
-    return [round(us(1 + 4 * j, 1 + 4 * (j + 1)), 2) for j in range(nb)], round(us(0, 1 + 4 * nb), 2)
+    runs = []
+    for rep in range(7):
+        stamps = (ctypes.c_ulonglong * (6 * nb + 2))()
+        tick = ctypes.c_double()
+        _lib.check(_lib.lib().spanqr_profile_chol(plan.handle, G.data_ptr(), npart.data_ptr(), 1e-7, 1e-8, stamps,
+                                                  ctypes.byref(tick), stream_handle(X.device)))
+        us = lambda a, b: (stamps[b] - stamps[a]) * tick.value / 1000.0
+        if rep >= 2:
+            runs.append(([us(1 + 4 * j, 1 + 4 * (j + 1)) for j in range(nb)], us(0, 1 + 4 * nb)))
+    steps = [round(statistics.median(rn[0][j] for rn in runs), 2) for j in range(nb)]
+    return steps, round(statistics.median(rn[1] for rn in runs), 2)
 
 
 def traffic_bytes(family, shape):
