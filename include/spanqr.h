@@ -208,6 +208,25 @@ int spanqr_stage_ns(spanqr_plan* plan, const float* Y, long ldy, int kahan, floa
 int spanqr_plan_copy_dust(spanqr_plan* plan, float* Z, void* stream);
 int spanqr_plan_copy_scalars(spanqr_plan* plan, float* scal8, void* stream);
 
+/* Host-visible outcome of the last call enqueued on the plan (spanqr_orth_f32, spanqr_orth_batched_f32 with its n
+ * matrices, spanqr_chol32): synchronises the stream, then returns SPANQR_OK, or SPANQR_EHIP naming the first matrix
+ * whose Cholesky gave up a bounded wait (its Q is NaN). The reference launches its Cholesky cooperatively
+ * (candidates/kchol.py:43, cudak.py:95-106), so a launch that cannot be co-scheduled fails there with a CUresult;
+ * here the launch is an ordinary one whose flag waits need every workgroup resident, and a wait that gives up after
+ * ~1 s of polling (another kernel holding the CUs) turns that matrix's Q into NaN without a host synchronisation.
+ * This call is the opt-in check for it (not for the hot path: it synchronises). */
+int spanqr_plan_status(spanqr_plan* plan, void* stream);
+
+/* chol32(G, tau) (candidates/kchol.py:35-44 -> chol_f32, candidates/cuk/chol.cu:273-276): the clamped Cholesky of
+ * G [n, n] fp32 (lower triangle read, row stride ldg >= n; not modified) with the absolute pivot floor *tau (a device
+ * pointer to one float, as the reference passes it: no host synchronisation) and no shift. Writes L [n, n] (row
+ * stride ldl >= n; zeros above the diagonal) and Li [n, 32] (the inverses of L's 32 x 32 diagonal tiles). plan: a
+ * kcholf plan with r = n (spanqr_plan_create_batched(K, n, 1, ...) for any K >= n; its workspace holds the
+ * factorisation's scratch and flags, so calls on one plan must not overlap). spanqr_plan_status reports a wait that
+ * gave up (L and Li are then unspecified). */
+int spanqr_chol32(spanqr_plan* plan, const float* G, long ldg, const float* tau, float* L, long ldl, float* Li,
+                  void* stream);
+
 /* Testing only (no counterpart in the reference): polls one bounded wait of the Cholesky makes before it gives up
  * (default 2^20, about a second). Lowered to 0, a wait gives up unless its flag is already set, so the tests can
  * exercise the failure path with every kernel still ending normally: the wait-error word is set and the call's Q

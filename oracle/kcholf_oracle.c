@@ -23,7 +23,20 @@
  * one fixed sequence of IEEE operations, and the MI355X kernels produce the same sequence (an fp32 MFMA chain on
  * gfx950 rounds exactly like a sequential fmaf chain in k order), so results are compared bit for bit.
  * Where the reference leaves an order open (its Triton dots, cuBLAS GEMMs, tree reductions, CUDA rsqrtf) this file
- * fixes one, documented at each function:
+ * fixes one, documented at each function. In three places it also departs, deliberately, from an order the
+ * reference's own source does fix; each is the same mathematics, and the accumulation chosen is the one an MFMA
+ * chain on gfx950 produces in a single pass (bitwise parity with the reference's Q is out of reach anyway: its
+ * dust comes from CUDA Philox, its pivots from CUDA rsqrtf, its solve dots from Triton tf32x3):
+ *   - the trailing update of a Cholesky tile, A_ik -= L_ij L_kj^T, is one fmaf chain over the block's 32 columns
+ *     starting from A_ik; the reference accumulates the product from 0 and subtracts it once
+ *     (candidates/cuk/chol.cu:63-70 mm22, :252 cur - acc);
+ *   - the diagonal-tile inverse (forward substitution for column kk) is one chain per element over m < i starting
+ *     from delta_i,kk; the reference runs four interleaved chains summed as ((acc0 + acc1) + (acc2 + acc3))
+ *     (candidates/cuk/chol.cu:157-164);
+ *   - in the blocked solve the off-diagonal blocks are one chain per element starting from the operand a, over the
+ *     earlier column blocks in order; the reference takes each block's dot product and subtracts it
+ *     (candidates/tri.py:396-399 acc - tl.dot(Yk, Ljk^T));
+ * and where it fixes an order the reference leaves open:
  *   - dot products are fmaf chains in ascending summation index, starting from +0 (or from the value being updated);
  *   - Gram output tiles are 64 wide, Cholesky tiles and TRSM column blocks 32 wide (as in the reference); products
  *     with a triangular tile inverse skip the 16-column groups above the diagonal block (exact zeros);

@@ -5,7 +5,8 @@
 
 The hot path is hand-written HIP in csrc/spanqr.hip behind the C ABI of include/spanqr.h, loaded with ctypes.
 """
-from .kcholqr import borth, kcholqr_f, kcholqr_f_many, orth, orth_many  # noqa: F401
+from .kcholqr import borth, kcholqr_f, kcholqr_f_many, orth, orth_many, set_checked, status  # noqa: F401
 from .plan import clear_plans, get_plan  # noqa: F401
 
-__all__ = ["orth", "orth_many", "kcholqr_f", "kcholqr_f_many", "borth", "get_plan", "clear_plans"]
+__all__ = ["orth", "orth_many", "kcholqr_f", "kcholqr_f_many", "borth", "get_plan", "clear_plans", "set_checked",
+           "status"]

@@ -50,6 +50,8 @@ SIGNATURES = {
     "spanqr_stage_ns": (_I, [_P, _P, _L, _I, _P, _L, _P]),
     "spanqr_plan_copy_dust": (_I, [_P, _P, _P]),
     "spanqr_plan_copy_scalars": (_I, [_P, _P, _P]),
+    "spanqr_plan_status": (_I, [_P, _P]),
+    "spanqr_chol32": (_I, [_P, _P, _L, _P, _P, _L, _P, _P]),
     "spanqr_debug_spin_limit": (_I, [ctypes.c_uint]),
     "spanqr_chol64_plan_create": (_I, [_I, _I, ctypes.POINTER(ctypes.c_void_p)]),
     "spanqr_chol64_plan_destroy": (None, [_P]),

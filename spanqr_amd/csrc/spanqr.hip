@@ -28,8 +28,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
 
 #include "../../include/spanqr.h"
 
@@ -1057,7 +1059,7 @@ template <bool STAMP>
 __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A, int r, const double* __restrict__ npart,
                                           int nnp, float alpha, float tau_rel, float* L, float* Li, float* Lp,
                                           uint32_t* bar, uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim,
-                                          uint32_t* colcnt, int ow) {
+                                          uint32_t* colcnt, int ow, const float* tau_ptr = nullptr) {
     extern __shared__ float4 chol_lds[];
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int nb = r / CB;
@@ -1126,7 +1128,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
             } else {
                 misc[0] = 0.0f;
                 misc[1] = 0.0f;
-                misc[2] = tau_rel;
+                misc[2] = tau_ptr != nullptr ? *tau_ptr : tau_rel;
             }
         }
     }
@@ -1450,12 +1452,15 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
     if (tid == 0) cnt[b] = ep;
 }
 
+// tau_ptr (nnp == 0 only; may be null): the absolute pivot floor read from device memory instead of tau_rel (chol32
+// with tau as a device tensor, kchol.py:24-28: no host synchronisation)
 template <bool STAMP>
 __global__ __launch_bounds__(512) void k_chol(float* A, int r, const double* __restrict__ npart, int nnp, float alpha,
                                               float tau_rel, float* L, float* Li, float* Lp, uint32_t* bar,
-                                              uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim, int ow) {
+                                              uint32_t* flags, float* scal, uint64_t* stamps, uint32_t lim, int ow,
+                                              const float* tau_ptr) {
     chol_body<STAMP>(blockIdx.x, blockIdx.z, A, r, npart, nnp, alpha, tau_rel, L, Li, Lp, bar, flags, scal, stamps,
-                     lim, nullptr, ow);
+                     lim, nullptr, ow, tau_ptr);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -2303,6 +2308,12 @@ __global__ void k_clear_words(uint32_t* word, int n, int stride) {
     if ((int)threadIdx.x < n) word[(size_t)threadIdx.x * stride] = 0u;
 }
 
+// bar[3] |= bar[2]: the column-blocked path runs kcholf once per block, each run clearing bar[2] first, so the
+// error of the whole call is kept in bar[3] (cleared at the call's start)
+__global__ void k_keep_error(uint32_t* bar) {
+    if (threadIdx.x == 0 && bar[2] != 0u) bar[3] = 1u;
+}
+
 // Q = Y for a call without polish steps (ns = 0), NaN when the call's Cholesky gave up a wait (as k_nsapply)
 __global__ __launch_bounds__(256) void k_copy_out(const MatsIn Ys, long ldy, int K, int r, const MatsOut Outs, long ldo,
                                                   const uint32_t* err) {
@@ -2416,6 +2427,7 @@ struct spanqr_plan {
     float *Zb = nullptr, *W = nullptr, *Tp = nullptr, *T = nullptr;
     uint32_t* bamax = nullptr;
     int nev = 0;
+    int last_n = 1;             // matrices of the last call enqueued on the plan (spanqr_plan_status reads theirs)
 };
 
 namespace {
@@ -2501,7 +2513,7 @@ void launch_reduce(const spanqr_plan* p, int mode, float* out, int n, hipStream_
 // chol_bmax * chol_grid workgroups fit on the device at once, which the flag waits of one launch rely on.
 // scal: the first matrix's scalar pair (stride SCAL_STRIDE per matrix) or null.
 int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t st, int nnp, int n,
-                bool stamp = false) {
+                bool stamp = false, const float* tau_ptr = nullptr) {
     const size_t r = p->r;
     const size_t lds = chol_lds_bytes(p->r, p->owner_w);
     for (int z0 = 0; z0 < n; z0 += p->chol_bmax) {
@@ -2517,29 +2529,13 @@ int launch_chol(spanqr_plan* p, float alpha, float tau, float* scal, hipStream_t
         const dim3 grid(p->chol_grid, 1, nz);
         if (stamp)
             k_chol<true><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps,
-                                                 g_spin_limit, p->owner_w);
+                                                 g_spin_limit, p->owner_w, tau_ptr);
         else
             k_chol<false><<<grid, 512, lds, st>>>(A, p->r, np, nnp, alpha, tau, L, Li, Lp, bar, flags, sc, p->stamps,
-                                                  g_spin_limit, p->owner_w);
+                                                  g_spin_limit, p->owner_w, tau_ptr);
         HIPCHK(hipGetLastError());
     }
     return SPANQR_OK;
-}
-
-template <int Q, int RB>
-hipError_t trsm_set_lds(int r) {
-    const int need = (int)trsm_lds(r, RB);
-    hipError_t e = hipFuncSetAttribute((const void*)k_trsm<true, Q, RB>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)k_trsm<false, Q, RB>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
-    return e;
-}
-
-hipError_t trsm_set_lds_plan(int q, int rb, int r) {
-    // two row blocks only with two column blocks per wave (r > 256, K >= 16384; taller r <= 256 takes k_trsm_rows)
-    if (q == 1) return trsm_set_lds<1, 1>(r);
-    if (q == 4) return trsm_set_lds<4, 1>(r);
-    return rb == 2 ? trsm_set_lds<2, 2>(r) : trsm_set_lds<2, 1>(r);
 }
 
 // LDS of the Cholesky's launch with its solve: the larger of the two roles' needs (q = 0: the wavefront-per-row-block
@@ -2549,27 +2545,66 @@ size_t fused_lds(int r, int ow, int q, int rb) {
     return a > b ? a : b;
 }
 
+// The widest r each solve instantiation runs: Q column blocks per wave cover up to 8 Q blocks of 32 columns
+constexpr int trsm_q_max_r(int q) { return 8 * q * CB; }
+
+// The maximum dynamic LDS of a kernel is an attribute of the kernel, shared by every plan that launches it, so each
+// instantiation's limit is set once per device to the most any plan can ask of it (the widest r it runs, the widest
+// owner parts): a later plan that needs less can then never lower the limit under an earlier plan's launches.
+// Limits above the device's per-workgroup maximum are clamped to it (plan creation checks each plan's own need).
+template <class F>
+hipError_t set_lds_limit(F* kernel, size_t need, int maxsh) {
+    const int v = need < (size_t)maxsh ? (int)need : maxsh;
+    return hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, v);
+}
+
 template <int Q, int RB>
-hipError_t fused_set_lds_t(int lds) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_chol_solve<true, Q, RB>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       lds);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)k_chol_solve<false, Q, RB>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+hipError_t trsm_limits(int maxsh) {
+    const size_t need = trsm_lds(trsm_q_max_r(Q), RB);
+    hipError_t e = set_lds_limit(k_trsm<true, Q, RB>, need, maxsh);
+    if (e == hipSuccess) e = set_lds_limit(k_trsm<false, Q, RB>, need, maxsh);
     return e;
 }
 
-// the instantiations: Q = 1 (r <= 256) with one row block, Q = 2 (r <= 512) with one or two, Q = 4 (r <= 1024)
-// with one, and the wavefront-per-row-block solve (Q = 0) for r/32 = 2, 4, 6, 8 column blocks
-hipError_t fused_set_lds(int q, int rb, int lds) {
-    if (q == 4) return fused_set_lds_t<4, 1>(lds);
-    if (q == 2) return rb == 2 ? fused_set_lds_t<2, 2>(lds) : fused_set_lds_t<2, 1>(lds);
-    if (q == 1) return fused_set_lds_t<1, 1>(lds);
-    switch (rb) {
-        case 2: return fused_set_lds_t<0, 2>(lds);
-        case 4: return fused_set_lds_t<0, 4>(lds);
-        case 6: return fused_set_lds_t<0, 6>(lds);
-        default: return fused_set_lds_t<0, 8>(lds);
-    }
+// the fused instantiations: Q = 1 (r <= 256) with one row block, Q = 2 (r <= 512) with one or two, Q = 4
+// (r <= 1024) with one, and the wavefront-per-row-block solve (Q = 0) for r/32 = RB = 2, 4, 6, 8 column blocks
+template <int Q, int RB>
+hipError_t fused_limits(int maxsh) {
+    const int rmax = Q > 0 ? trsm_q_max_r(Q) : RB * CB;
+    const size_t need = fused_lds(rmax, OWNER_WMAX, Q, RB);
+    hipError_t e = set_lds_limit(k_chol_solve<true, Q, RB>, need, maxsh);
+    if (e == hipSuccess) e = set_lds_limit(k_chol_solve<false, Q, RB>, need, maxsh);
+    return e;
+}
+
+std::mutex g_lds_mu;
+bool g_lds_done[64] = {};
+
+// every dynamic-LDS kernel's limit on `device` (current), once per process
+int kernel_lds_limits(int device) {
+    std::lock_guard<std::mutex> lk(g_lds_mu);
+    const bool track = device >= 0 && device < 64;
+    if (track && g_lds_done[device]) return SPANQR_OK;
+    int maxsh = 0;
+    HIPCHK(hipDeviceGetAttribute(&maxsh, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+    hipError_t e = trsm_limits<1, 1>(maxsh);
+    if (e == hipSuccess) e = trsm_limits<2, 1>(maxsh);
+    if (e == hipSuccess) e = trsm_limits<2, 2>(maxsh);
+    if (e == hipSuccess) e = trsm_limits<4, 1>(maxsh);
+    if (e == hipSuccess) e = fused_limits<1, 1>(maxsh);
+    if (e == hipSuccess) e = fused_limits<2, 1>(maxsh);
+    if (e == hipSuccess) e = fused_limits<2, 2>(maxsh);
+    if (e == hipSuccess) e = fused_limits<4, 1>(maxsh);
+    if (e == hipSuccess) e = fused_limits<0, 2>(maxsh);
+    if (e == hipSuccess) e = fused_limits<0, 4>(maxsh);
+    if (e == hipSuccess) e = fused_limits<0, 6>(maxsh);
+    if (e == hipSuccess) e = fused_limits<0, 8>(maxsh);
+    if (e == hipSuccess) e = set_lds_limit(k_chol<true>, chol_lds_bytes(KCH_MAX_R, OWNER_WMAX), maxsh);
+    if (e == hipSuccess) e = set_lds_limit(k_chol<false>, chol_lds_bytes(KCH_MAX_R, OWNER_WMAX), maxsh);
+    if (e == hipSuccess) e = set_lds_limit(k_nsapply_res<512>, nsr_lds_bytes<512>(), maxsh);
+    if (e != hipSuccess) return fail(SPANQR_EHIP, "setting the kernels' LDS limits failed: %s", hipGetErrorString(e));
+    if (track) g_lds_done[device] = true;
+    return SPANQR_OK;
 }
 
 // the dust the pass-1 solve adds: the plan's own Z [K, r], or a column slice of a wider one (row stride ldz)
@@ -2745,6 +2780,7 @@ void launch_nsapply(const spanqr_plan* p, const MatsIn& Y, long ldy, const MatsO
 int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut& Q, long ldq, float eps, float alpha,
                  float tau, int ns, hipStream_t st, bool rec, Dust dz = Dust{nullptr, 0}) {
     if (dz.z == nullptr) dz = Dust{p->Z, p->r};
+    p->last_n = n;
     int rc;
     auto mark = [&]() -> int {
         if (rec) {
@@ -2870,33 +2906,16 @@ void plan_shape(spanqr_plan* p, int K, int r, int batch) {
 // co-residency check that the Cholesky's flag waits rely on; sets chol_bmax (at most batch).
 int plan_device_setup(spanqr_plan* p, int device) {
     const int r = p->r;
+    int rc = kernel_lds_limits(device);
+    if (rc != SPANQR_OK) return rc;
     {
         const size_t need = trsm_lds(r, p->trsm_rb);
         int maxsh = 0;
         HIPCHK(hipDeviceGetAttribute(&maxsh, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
         if ((size_t)maxsh < need)
             return fail(SPANQR_EHIP, "the solve needs %zu bytes of LDS per workgroup, device allows %d", need, maxsh);
-        const hipError_t e = trsm_set_lds_plan(p->trsm_q, p->trsm_rb, r);
-        if (e != hipSuccess) return fail(SPANQR_EHIP, "setting the solve's LDS size failed: %s", hipGetErrorString(e));
     }
     int occ = 0, cus = 0;
-    {
-        // the largest Cholesky LDS of any part width (the attribute is per kernel, shared by every plan)
-        const int need = (int)chol_lds_bytes(r, OWNER_WMAX);
-        hipError_t e = hipFuncSetAttribute((const void*)k_chol<true>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)k_chol<false>, hipFuncAttributeMaxDynamicSharedMemorySize, need);
-        if (e != hipSuccess)
-            return fail(SPANQR_EHIP, "setting the Cholesky's LDS size (%d bytes) failed: %s", need, hipGetErrorString(e));
-    }
-    {
-        const int need = (int)nsr_lds_bytes<512>();
-        const hipError_t e = hipFuncSetAttribute((const void*)k_nsapply_res<512>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, need);
-        if (e != hipSuccess)
-            return fail(SPANQR_EHIP, "setting the Newton-Schulz apply's LDS size (%d bytes) failed: %s", need,
-                        hipGetErrorString(e));
-    }
     HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
     p->cus = cus;
     // The owner part width: OWNER_W for one matrix; for a batch, the narrowest of 6, 8, 12 and 16 tiles that runs
@@ -2962,7 +2981,7 @@ int plan_device_setup(spanqr_plan* p, int device) {
             }
         }
         const size_t lds = fused_lds(r, p->owner_w, q, rb);
-        if (nwg <= avail && lds <= (size_t)maxsh && fused_set_lds(q, q ? rb : r / CB, (int)lds) == hipSuccess) {
+        if (nwg <= avail && lds <= (size_t)maxsh) {
             p->solve_q = q;
             p->solve_rb = rb;
             p->solve_nrb = nwg;
@@ -3087,6 +3106,8 @@ void project(const spanqr_plan* p, const float* Q, long ldq, int j, const float*
 int enqueue_borth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, float eps, float alpha, float tau,
                   int ns, hipStream_t st) {
     const int K = p->K, BW = p->bw;
+    p->last_n = 1;
+    k_clear_words<<<1, 64, 0, st>>>(p->blk->bar + 3, 1, BAR_STRIDE);
     k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(mats_in(&X, 1), ldx, K, p->r, p->bamax);
     const int sgrid = (K * (BW / 4) + 255) / 256 < 1024 ? (K * (BW / 4) + 255) / 256 : 1024;
     int rc;
@@ -3103,11 +3124,13 @@ int enqueue_borth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, 
         if ((rc = enqueue_orth(p->blk, 1, mats_in(&Wc, 1), BW, mats_out(&Qj, 1), ldq, eps, alpha, tau, ns, st, false,
                                dz)))
             return rc;
+        k_keep_error<<<1, 64, 0, st>>>(p->blk->bar);
         if (j > 0 && p->reorth) {
             project(p, Q, ldq, j, Qj, ldq, p->W, st);
             if ((rc = enqueue_orth(p->blk, 1, mats_in(&Wc, 1), BW, mats_out(&Qj, 1), ldq, eps, alpha, tau, ns, st,
                                    false, dz)))
                 return rc;
+            k_keep_error<<<1, 64, 0, st>>>(p->blk->bar);
         }
     }
     HIPCHK(hipGetLastError());
@@ -3466,6 +3489,46 @@ int spanqr_plan_copy_scalars(spanqr_plan* p, float* scal8, void* stream) {
     return SPANQR_OK;
 }
 
+int spanqr_plan_status(spanqr_plan* p, void* stream) {
+    if (!p) return fail(SPANQR_EINVAL, "plan is null");
+    DeviceGuard dg(p->device);
+    if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
+    const spanqr_plan* q = p->blk ? p->blk : p;
+    const int n = p->blk ? 1 : (p->last_n < 1 ? 1 : p->last_n);
+    const int word = p->blk ? 3 : 2;   // the column-blocked path keeps the whole call's error in word 3
+    uint32_t w[SPANQR_MAX_BATCH * BAR_STRIDE];
+    HIPCHK(hipMemcpyAsync(w, q->bar, (size_t)n * BAR_STRIDE * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                          (hipStream_t)stream));
+    HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+    for (int i = 0; i < n; ++i)
+        if (w[(size_t)i * BAR_STRIDE + word] != 0u)
+            return fail(SPANQR_EHIP, "matrix %d of the last call: a bounded wait of its Cholesky gave up (not every "
+                                     "workgroup of the launch was resident); its Q is NaN", i);
+    return SPANQR_OK;
+}
+
+int spanqr_chol32(spanqr_plan* p, const float* G, long ldg, const float* tau, float* L, long ldl, float* Li,
+                  void* stream) {
+    if (!p || !G || !tau || !L || !Li) return fail(SPANQR_EINVAL, "null argument");
+    if (p->blk) return fail(SPANQR_EINVAL, "not available on a column-blocked plan (r > 512)");
+    const long n = p->r;
+    if (ldg < n || ldl < n) return fail(SPANQR_EINVAL, "ldg = %ld, ldl = %ld: must be >= n = %ld", ldg, ldl, n);
+    DeviceGuard dg(p->device);
+    if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
+    hipStream_t st = (hipStream_t)stream;
+    const size_t row = (size_t)n * sizeof(float);
+    HIPCHK(hipMemcpy2DAsync(p->G, row, G, (size_t)ldg * sizeof(float), row, n, hipMemcpyDeviceToDevice, st));
+    k_clear_words<<<1, 64, 0, st>>>(p->bar + 2, 1, BAR_STRIDE);
+    p->last_n = 1;
+    int rc = launch_chol(p, 0.0f, 0.0f, nullptr, st, 0, 1, false, tau);
+    if (rc) return rc;
+    // L: the plan's factor, whose tiles above the diagonal no kernel writes (zero since the plan was made)
+    HIPCHK(hipMemcpy2DAsync(L, (size_t)ldl * sizeof(float), p->L, row, row, n, hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemcpyAsync(Li, p->Li, (size_t)n * CB * sizeof(float), hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipGetLastError());
+    return SPANQR_OK;
+}
+
 }  // extern "C"
 
 // ===============================================================================================================
@@ -3503,16 +3566,37 @@ __global__ __launch_bounds__(256) void k_dust_raw(float* Z, int K, int r, const 
     }
 }
 
-// column norms of the raw draws: sqrt of the squares summed in double in ascending k (one thread per column)
-__global__ __launch_bounds__(256) void k_dust_norm(const float* Z, int K, int r, double* nrm, const uint64_t* tag,
-                                                   uint64_t want) {
+// column norms of the raw draws: sqrt of the squares summed in double in ascending k (one thread per column, 64
+// columns per workgroup). The sum is one dependent chain per column; the loads are not: each thread keeps the rows
+// of the next 32-row group in flight while it adds the current group, so the chain, not the memory latency per
+// row, sets the time.
+constexpr int DUST_NORM_ROWS = 32;
+__global__ __launch_bounds__(64) void k_dust_norm(const float* Z, int K, int r, double* nrm, const uint64_t* tag,
+                                                  uint64_t want) {
     if (*tag == want) return;
-    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int c = blockIdx.x * 64 + threadIdx.x;
     if (c >= r) return;
+    constexpr int U = DUST_NORM_ROWS;
+    float a[U], b[U];
+    auto load = [&](float (&v)[U], int k0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = (k0 + u < K) ? Z[(size_t)(k0 + u) * r + c] : 0.0f;
+    };
+    auto add = [&](const float (&v)[U], int k0, double& acc) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (k0 + u < K) {
+                const double z = (double)v[u];
+                acc += z * z;
+            }
+    };
     double acc = 0.0;
-    for (int k = 0; k < K; ++k) {
-        const double z = (double)Z[(size_t)k * r + c];
-        acc += z * z;
+    load(a, 0);
+    for (int k0 = 0; k0 < K; k0 += 2 * U) {
+        load(b, k0 + U);
+        add(a, k0, acc);
+        load(a, k0 + 2 * U);
+        add(b, k0 + U, acc);
     }
     nrm[c] = sqrt(acc);
 }
@@ -3534,6 +3618,7 @@ __global__ __launch_bounds__(256) void k_noalloc_prep(uint32_t* flags, int nflag
 
 std::mutex g_na_mu;
 char* g_na_base[MAX_DEVICES] = {};   // the array's device address on each device (hipGetSymbolAddress)
+std::map<std::tuple<int, int, int>, spanqr_plan> g_na_setup;   // (device, K, r) -> the set-up plan fields
 
 // The array: the dust's shape tag and column norms at fixed offsets (every call finds the tag of the dust the array
 // holds at the same place, whatever the shape of the call that wrote it), then a plan's workspace.
@@ -3578,7 +3663,18 @@ int spanqr_orth_f32_noalloc(int K, int r, const float* X, long ldx, float* Q, lo
         base = g_na_base[dev];
     }
     p.device = dev;
-    if ((rc = plan_device_setup(&p, dev))) return rc;
+    {
+        // the device-derived fields of the plan (part width, co-residency, solve form), once per (device, K, r)
+        std::lock_guard<std::mutex> lk(g_na_mu);
+        const auto key = std::make_tuple(dev, K, r);
+        const auto it = g_na_setup.find(key);
+        if (it == g_na_setup.end()) {
+            if ((rc = plan_device_setup(&p, dev))) return rc;
+            g_na_setup.emplace(key, p);
+        } else {
+            p = it->second;
+        }
+    }
     plan_layout(&p, base + NA_WS);
     uint64_t* tag = (uint64_t*)(base + NA_TAG);
     double* nrm = (double*)(base + NA_NRM);
@@ -3586,7 +3682,7 @@ int spanqr_orth_f32_noalloc(int K, int r, const float* X, long ldx, float* Q, lo
     hipStream_t st = (hipStream_t)stream;
     const int eblocks = (int)(((size_t)K * r + 255) / 256 < 2048 ? ((size_t)K * r + 255) / 256 : 2048);
     k_dust_raw<<<eblocks, 256, 0, st>>>(p.Z, K, r, tag, want);
-    k_dust_norm<<<(r + 255) / 256, 256, 0, st>>>(p.Z, K, r, nrm, tag, want);
+    k_dust_norm<<<(r + 63) / 64, 64, 0, st>>>(p.Z, K, r, nrm, tag, want);
     k_dust_scale<<<eblocks, 256, 0, st>>>(p.Z, K, r, nrm, tag, want);
     k_noalloc_prep<<<1, 256, 0, st>>>(p.flags, FLAG_STRIDE, tag, want);
     HIPCHK(hipGetLastError());

@@ -3,6 +3,7 @@ library. The signature and keyword arguments are the reference's; the whole call
 with no host synchronisation.
 """
 import ctypes
+import os
 
 import torch
 
@@ -24,6 +25,37 @@ def _full_width(K, r):
 def _blocked(r):
     """orth.py:18: above 512 columns a multiple of 256 goes through borth over 256-column blocks"""
     return r > R_MAX and r % BLOCK == 0
+
+
+# Opt-in check of the Cholesky's bounded waits. The reference launches its Cholesky cooperatively (kchol.py:43), so a
+# launch that cannot be co-scheduled fails loudly there; here a wait that gives up (another kernel holding the CUs
+# for ~1 s) makes that matrix's Q NaN without a host synchronisation. With checking on (set_checked(True), or the
+# environment variable SPANQR_CHECK=1 at import), every call synchronises afterwards and raises SpanqrError instead.
+_CHECKED = [os.environ.get("SPANQR_CHECK", "") == "1"]
+
+
+def set_checked(on=True):
+    """turn the per-call status check on or off (off by default: it costs a host synchronisation per call); returns
+    the previous setting"""
+    prev = _CHECKED[0]
+    _CHECKED[0] = bool(on)
+    return prev
+
+
+def _after(plan):
+    if _CHECKED[0]:
+        plan.status()
+
+
+def status(X):
+    """raise SpanqrError if the last native call on X's shape (on X's device and the current stream) had a Cholesky
+    wait that gave up; X: the tensor, or a list of same-shape tensors as passed to kcholqr_f_many. Synchronises."""
+    Xs = list(X) if isinstance(X, (list, tuple)) else [X]
+    K, r = Xs[0].shape
+    dev = Xs[0].device
+    if _blocked(r) and len(Xs) == 1:
+        return get_borth_plan(K, r, BLOCK, True, dev).status()
+    return get_plan(K, r, dev, min(len(Xs), _lib.MAX_BATCH)).status()
 
 
 def _check_input(X):
@@ -60,6 +92,7 @@ def kcholqr_f(X, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
     with torch.cuda.device(dev):
         _lib.check(_lib.lib().spanqr_orth_f32(plan.handle, X.data_ptr(), r, Q.data_ptr(), r, float(eps), float(alpha),
                                                float(tau), int(ns), stream_handle(dev)))
+    _after(plan)
     return Q
 
 
@@ -93,6 +126,7 @@ def kcholqr_f_many(Xs, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
             qp = (ctypes.c_void_p * n)(*[q.data_ptr() for q in qs])
             _lib.check(_lib.lib().spanqr_orth_batched_f32(plan.handle, n, xp, r, qp, r, float(eps), float(alpha),
                                                           float(tau), int(ns), stream_handle(dev)))
+            _after(plan)
     return Qs
 
 
@@ -144,6 +178,7 @@ def borth(X, b=512, reorth=True):
     with torch.cuda.device(dev):
         _lib.check(_lib.lib().spanqr_orth_f32(plan.handle, X.data_ptr(), r, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2,
                                                stream_handle(dev)))
+    _after(plan)
     return Q
 
 

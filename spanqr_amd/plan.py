@@ -60,6 +60,11 @@ class Plan:
     def chol_batch(self):
         return self.query(_lib.Q_CHOL_BATCH)
 
+    def status(self):
+        """synchronise the current stream and raise SpanqrError if a bounded Cholesky wait of the plan's last call
+        gave up (that matrix's Q is NaN; spanqr_plan_status)"""
+        _lib.check(_lib.lib().spanqr_plan_status(self.handle, stream_handle(self.device)))
+
     def close(self):
         if self.handle and not _SHUTTING_DOWN[0]:
             _lib.lib().spanqr_plan_destroy(self.handle)

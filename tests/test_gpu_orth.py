@@ -40,14 +40,32 @@ def test_adversarial(cuda, adversarial_inputs, K, r, name):
     assert_bits(Q, oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows), "Q vs oracle")
 
 
-@pytest.mark.parametrize("K,r", [(1024, 256), (2048, 256), (3584, 256), (5120, 256), (6144, 256), (768, 512),
-                                 (2048, 512)])
-def test_benchmark_inputs(cuda, K, r):
-    print(f"bench input {K}x{r}", flush=True)
-    X = gen.bench_input(K, r, seed=0)
+# the benchmark inputs: the headline shapes (768x512; 17408x256 with N = 5120), both seeds of the 0.8B layer shapes
+# (1024, 2048, 3584 x 256, N = K), the other 27B shapes (N = 5120) and 2048x512
+@pytest.mark.parametrize("K,r,seed", [(1024, 256, 0), (1024, 256, 1), (2048, 256, 0), (2048, 256, 1),
+                                      (3584, 256, 0), (3584, 256, 1), (5120, 256, 0), (6144, 256, 0),
+                                      (17408, 256, 0), (768, 512, 0), (2048, 512, 0)])
+def test_benchmark_inputs(cuda, K, r, seed):
+    print(f"bench input {K}x{r} seed {seed}", flush=True)
+    X = gen.bench_input(K, r, seed=seed)
     Q = orth(X.to(cuda))
-    gate(X, Q, f"{K}x{r}")
+    gate(X, Q, f"{K}x{r} seed {seed}")
     assert_bits(Q, oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows), "Q vs oracle")
+
+
+def test_lds_limit_shared_by_plans(cuda):
+    """a kernel's dynamic-LDS limit is shared by every plan that launches it: a plan made later with a smaller need
+    (16400 x 320 runs the same two-row-block solve as 16400 x 512 with less LDS) must not lower it under the first"""
+    K, r = 16400, 512
+    X = gen.bench_input(K, r, seed=2)
+    Xd = X.to(cuda)
+    Q0 = kcholqr_f(Xd)
+    get_plan(K, 320, cuda)
+    kcholqr_f(torch.randn(K, 320, device=cuda))
+    print("lds limit: 16400x512 after a 16400x320 plan", flush=True)
+    Q1 = kcholqr_f(Xd)
+    assert_bits(Q1, Q0, "16400x512 after a 16400x320 plan vs before")
+    assert_bits(Q1, oracle.orth(X.numpy(), get_plan(K, r, cuda).split_rows), "Q vs oracle")
 
 
 def _tie_band_values():

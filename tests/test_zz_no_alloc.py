@@ -2,6 +2,10 @@
 a plan for the same X, on calls in a row whose second is smaller (the fixed workspace keeps the previous call's
 contents: flags, dust and tag are rebuilt as needed), under hipGraph capture with calls of another shape between the
 replays, and a shape whose workspace exceeds the fixed array is refused with an error."""
+import os
+import subprocess
+import sys
+
 import pytest
 import torch
 
@@ -64,3 +68,44 @@ def test_noalloc_refuses_oversize(cuda):
                                             stream_handle(cuda))
     assert rc == -1
     assert b"workspace" in _lib.lib().spanqr_last_error()
+
+
+_FIRST_CALL_CAPTURED = r"""
+import sys
+import torch
+from spanqr_amd import _lib, kcholqr_f
+from spanqr_amd.plan import stream_handle
+from spanqr_amd.qrbench import gen
+
+K, r = 1024, 256
+X = gen.ttf_uu(K, r, N=K, seed=9).to("cuda:0")
+Qg = torch.empty_like(X)
+st = torch.cuda.Stream()
+st.wait_stream(torch.cuda.current_stream())
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=st):   # the process's first allocation-free call: its set-up runs under capture
+    _lib.check(_lib.lib().spanqr_orth_f32_noalloc(K, r, X.data_ptr(), r, Qg.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2,
+                                                  stream_handle(X.device)))
+Qe = kcholqr_f(X)
+for rep in range(3):
+    Qg.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    same = torch.equal(Qg.view(torch.int32), Qe.view(torch.int32))
+    print(f"replay {rep}: bit-identical {same}", flush=True)
+    if not same:
+        sys.exit(1)
+"""
+
+
+def test_noalloc_first_call_captured(cuda):
+    """the first allocation-free call of a fresh process made under hipGraph capture (the array's device address,
+    the kernels' LDS limits and the plan fields are set up while capturing): every replay bit-identical to a plan
+    call"""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=root + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    print("noalloc: first call of a child process under capture", flush=True)
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED], env=env, cwd=root, capture_output=True,
+                         text=True, timeout=300)
+    print(res.stdout[-2000:], res.stderr[-2000:], flush=True)
+    assert res.returncode == 0, f"child exited with {res.returncode}"
