@@ -220,7 +220,10 @@ def kernels_at(X, reps):
     """per kernel family at X's shape: average launch duration and its algorithmic rates"""
     K, r = X.shape
     kcholqr_f(X)
-    fams = FUSED_FAMILIES if get_plan(K, r, X.device).solve_rows > 0 else FAMILIES
+    plan = get_plan(K, r, X.device)
+    fams = FUSED_FAMILIES if plan.solve_rows > 0 else FAMILIES
+    if plan.gram_short:   # the Gram reduces its splits in its own launch
+        fams = [f for f in fams if f[0] != "reduce"]
     out = {}
     for fam, which, per_call in fams:
         us = kernel_avg_us(X, which, reps)

@@ -60,6 +60,7 @@ enum {
     SPANQR_Q_SOLVE_ROWS = 10,    /* rows per solve workgroup when the solve runs in the Cholesky's launch; 0 when
                                     they are separate launches */
     SPANQR_Q_BLOCK_WIDTH = 11,   /* columns per block of a column-blocked plan; 0 otherwise */
+    SPANQR_Q_NORM_PARTIALS = 12, /* fp64 partials of ||G||_F^2 per matrix that the Gram writes (spanqr_norm_partials) */
 };
 
 /* Create a plan for X [K, r] on HIP device `device` (allocates the workspace and uploads the dust matrix), with
@@ -171,6 +172,15 @@ int spanqr_dust_host(int K, int r, float* Z);
  * of 3 x the device's SM count, so the summation order, and with it every bit of Q, is the same on every device.
  * Returns SPANQR_EINVAL for a shape the plan would reject. */
 int spanqr_split_rows(int K, int r);
+
+/* Host-side (no GPU needed): the number of fp64 ||G||_F^2 partials the Gram of X [K, r] writes, which also tells its
+ * form: short X with many tiles (K <= 1024, r >= 448) runs the Gram in one launch over upper 32 x 32 tiles, two row splits of
+ * spanqr_split_rows(K, r) rows summed in fp64 inside each tile's workgroup, one partial per tile (r/32 (r/32 + 1) / 2);
+ * other X runs the split Gram over upper 64 x 64 tiles and a reduction launch, 16 partials per tile. Both give every
+ * element of G the same arithmetic for the same split; the partials' grouping differs, and with it the bits of ||G||_F
+ * (the reference computes it with torch.linalg.matrix_norm, candidates/kcholqr.py:107; the oracle restates both forms).
+ * No counterpart in the reference. Returns SPANQR_EINVAL for a shape the plan would reject. */
+int spanqr_norm_partials(int K, int r);
 
 /* ---- stage entry points: one stage of the call on device buffers, for checking each kernel ---- */
 

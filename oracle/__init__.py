@@ -60,6 +60,14 @@ def _bind(L):
                                  _f32p, c_long]
     L.spqo_split_rows.argtypes = [c_int, c_int]
     L.spqo_split_rows.restype = c_int
+    L.spqo_gram_short.argtypes = [c_int, c_int]
+    L.spqo_gram_short.restype = c_int
+    L.spqo_gram_short_rows.argtypes = [c_int]
+    L.spqo_gram_short_rows.restype = c_int
+    L.spqo_npart_count.argtypes = [c_int, c_int]
+    L.spqo_npart_count.restype = c_int
+    L.spqo_gram_rows.argtypes = [c_int, c_int]
+    L.spqo_gram_rows.restype = c_int
     L.spqo_xgram.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, c_int, _f32p]
     L.spqo_project.argtypes = [_vp, c_long, c_int, c_int, _vp, c_long, c_int, c_int, _f32p, c_long]
     L.spqo_borth.argtypes = [_f32p, c_long, c_int, c_int, c_int, c_int, c_float, c_float, c_float, c_int, _f32p,
@@ -130,12 +138,12 @@ def dust(K, r):
 # ---- Gram (tri.py:255-297, 324-375) ----
 
 def gram(A, KS, kahan, s=None):
-    """(G [r, r], norm partials [16 U] fp64); s: scale on load (None: no scale)"""
+    """(G [r, r], norm partials fp64: 16 per upper 64x64 tile, or one per upper 32x32 tile for short X, the form
+    gram_short(K, r) picks); s: scale on load (None: no scale)"""
     A = _c32(A)
     K, r = A.shape
-    nt = (r + TB - 1) // TB
     G = np.empty((r, r), np.float32)
-    npart = np.empty(16 * nt * (nt + 1) // 2, np.float64)
+    npart = np.empty(npart_count(K, r), np.float64)
     lib().spqo_gram(A, r, K, r, 1.0 if s is None else float(s), s is not None, int(bool(kahan)), KS, G,
                     _ptr(npart))
     return G, npart
@@ -143,6 +151,20 @@ def gram(A, KS, kahan, s=None):
 
 def gram_splits(K, KS):
     return lib().spqo_gram_splits(K, KS)
+
+
+def gram_short(K, r):
+    """the Gram's form for X [K, r]: True for the one-launch form over 32x32 tiles (two row splits)"""
+    return bool(lib().spqo_gram_short(K, r))
+
+
+def gram_rows(K, r):
+    """rows per Gram split for X [K, r], either form (the library's spanqr_split_rows)"""
+    return lib().spqo_gram_rows(K, r)
+
+
+def npart_count(K, r):
+    return lib().spqo_npart_count(K, r)
 
 
 def norm(npart):

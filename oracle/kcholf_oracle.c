@@ -170,12 +170,54 @@ static void row_tree64(double* q) {
 
 int spqo_gram_splits(int K, int KS) { return (K + KS - 1) / KS; }
 
+/* The Gram's form, a function of (K, r) only (the library makes the same choice): short X with many tiles (K <= 1024,
+ * r >= 448) is computed in one launch over upper 32x32 tiles, two row splits of KS = ceil(K / 2) rounded up to 32
+ * rows per tile; the rest over upper 64x64 tiles with the split rule below. Every element of G has the same
+ * arithmetic either way (per split an fmaf chain, fp64 across splits in split order); the norm partials are grouped
+ * differently. */
+int spqo_gram_short(int K, int r) { return K <= 1024 && r >= 448; }
+int spqo_gram_short_rows(int K) { return ((K + 1) / 2 + BK - 1) / BK * BK; }
+int spqo_npart_count(int K, int r) {
+    const int nt = (r + TB - 1) / TB, nb = r / CB;
+    return spqo_gram_short(K, r) ? nb * (nb + 1) / 2 : 16 * nt * (nt + 1) / 2;
+}
+
+/* ||G||_F^2 partials of the short form, one per upper 32x32 tile (ti <= tj, row-major order of tiles): per 16x16
+ * quadrant q = 2 qi + qj in order 0..3 and lane l = 16 lk + c, the lane's value ((g_0^2 + g_1^2) + g_2^2) + g_3^2 with
+ * g_v = G[32 ti + 16 qi + 4 lk + v][32 tj + 16 qj + c], then a shift-down tree over the 64 lanes (Q_q); the tile's
+ * partial ((Q_0 + Q_1) + Q_2) + Q_3, doubled off the diagonal (the squares in fp64, exact). */
+static void npart32(const float* G, int r, double* npart) {
+    const int nb = r / CB;
+    int u = 0;
+    for (int ti = 0; ti < nb; ++ti)
+        for (int tj = ti; tj < nb; ++tj, ++u) {
+            double Qq[4];
+            for (int q = 0; q < 4; ++q) {
+                const int qi = q >> 1, qj = q & 1;
+                double lv[64];
+                for (int l = 0; l < 64; ++l) {
+                    const int lk = l >> 4, c = l & 15;
+                    const int i0 = CB * ti + 16 * qi + 4 * lk, j = CB * tj + 16 * qj + c;
+                    double s2 = (double)G[(size_t)i0 * r + j] * (double)G[(size_t)i0 * r + j];
+                    for (int v = 1; v < 4; ++v)
+                        s2 = s2 + (double)G[(size_t)(i0 + v) * r + j] * (double)G[(size_t)(i0 + v) * r + j];
+                    lv[l] = s2;
+                }
+                row_tree64(lv);
+                Qq[q] = lv[0];
+            }
+            const double tot = ((Qq[0] + Qq[1]) + Qq[2]) + Qq[3];
+            npart[u] = (ti == tj) ? tot : 2.0 * tot;
+        }
+}
+
 void spqo_gram(const float* A, long lda, int K, int r, float s, int use_s, int kahan, int KS, float* G,
                double* npart) {
     fp_env();
     /* nt tile columns of 64; when r % 64 == 32 the last is half outside X: those columns read as 0, and entries
      * past r are neither stored nor counted in the norm (tri.py's masked loads and stores) */
     const int nt = (r + TB - 1) / TB, U = nt * (nt + 1) / 2, S = spqo_gram_splits(K, KS);
+    const int short_form = spqo_gram_short(K, r);   /* the norm partials' grouping (G itself is the same) */
     float* P = (float*)malloc((size_t)S * U * TB * TB * sizeof(float));
     int* uti = (int*)malloc(U * sizeof(int));
     int* utj = (int*)malloc(U * sizeof(int));
@@ -239,9 +281,10 @@ void spqo_gram(const float* A, long lda, int K, int r, float s, int use_s, int k
                 w[rr] = q[0];
             }
             double tot = ((w[0] + w[1]) + w[2]) + w[3];
-            if (npart) npart[u * 16 + b] = (ti == tj) ? tot : 2.0 * tot;
+            if (npart && !short_form) npart[u * 16 + b] = (ti == tj) ? tot : 2.0 * tot;
         }
     }
+    if (npart && short_form) npart32(G, r, npart);
     free(P); free(uti); free(utj);
 }
 
@@ -437,7 +480,6 @@ static void orth_z(const float* X, long ldx, int K, int r, int KS, float eps, fl
                    float* Q, long ldq, float* Gs, float* Ls, float* Lis, float* Ys, float* scal, const float* Zx,
                    long ldz) {
     fp_env();
-    const int nt = (r + TB - 1) / TB, U = nt * (nt + 1) / 2;
     const float s = spqo_pow2_scale(spqo_amax(X, ldx, K, r));
     float* Z = (float*)malloc((size_t)K * r * sizeof(float));
     float* G = (float*)malloc((size_t)r * r * sizeof(float));
@@ -445,7 +487,7 @@ static void orth_z(const float* X, long ldx, int K, int r, int KS, float eps, fl
     float* Li = (float*)malloc((size_t)r * CB * sizeof(float));
     float* Ya = (float*)malloc((size_t)K * r * sizeof(float));
     float* Yb = (float*)malloc((size_t)K * r * sizeof(float));
-    double* np = (double*)malloc((size_t)U * 16 * sizeof(double));
+    double* np = (double*)malloc((size_t)spqo_npart_count(K, r) * sizeof(double));
     if (Zx == NULL) {
         spqo_dust(K, r, Z);
         Zx = Z;
@@ -457,7 +499,7 @@ static void orth_z(const float* X, long ldx, int K, int r, int KS, float eps, fl
     float* out = Ya;
     for (int p = 0; p < 3; ++p) {
         spqo_gram(in, ldin, K, r, s, p == 0, p == 0, KS, G, np);
-        const float nrm = spqo_norm(np, U * 16);
+        const float nrm = spqo_norm(np, spqo_npart_count(K, r));
         const float tau = spqo_shift(G, r, nrm, alpha, tau_rel);
         if (scal) { scal[1 + 2 * p] = nrm; scal[2 + 2 * p] = tau; }
         if (Gs) memcpy(Gs + (size_t)p * r * r, G, (size_t)r * r * sizeof(float));
@@ -502,6 +544,12 @@ int spqo_split_rows(int K, int U) {
     if (S > cap) S = cap;
     if (S < 1) S = 1;
     return ((K + S - 1) / S + BK - 1) / BK * BK;
+}
+
+/* rows per split of the Gram of X [K, r] in either form (spqo_gram_short) */
+int spqo_gram_rows(int K, int r) {
+    const int nt = (r + TB - 1) / TB;
+    return spqo_gram_short(K, r) ? spqo_gram_short_rows(K) : spqo_split_rows(K, nt * (nt + 1) / 2);
 }
 
 /* ------------------------------------------------------------------------------------------------------------ */
@@ -569,7 +617,7 @@ void spqo_borth(const float* X, long ldx, int K, int r, int b, int reorth, float
     float* Zf = (float*)malloc((size_t)K * r * sizeof(float));
     float* W = (float*)malloc((size_t)K * b * sizeof(float));
     spqo_dust(K, r, Zf);
-    const int KSb = spqo_split_rows(K, (b / TB) * (b / TB + 1) / 2);
+    const int KSb = spqo_gram_rows(K, b);   /* the block's kcholf: the Gram of a K x b block, either form */
     for (int j = 0; j < r; j += b) {
         const int KSp = j > 0 ? spqo_split_rows(K, (j / TB) * (b / TB)) : 0;
         float* Qj = Q + j;

@@ -19,7 +19,7 @@ HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
 
 # plan queries (include/spanqr.h)
 (Q_K, Q_R, Q_SPLITS, Q_SPLIT_ROWS, Q_CHOL_GRID, Q_WORKSPACE_MB, Q_DEVICE, Q_BATCH, Q_CHOL_BATCH, Q_BLOCKS,
- Q_SOLVE_ROWS, Q_BLOCK_WIDTH) = range(12)
+ Q_SOLVE_ROWS, Q_BLOCK_WIDTH, Q_NORM_PARTIALS) = range(13)
 MAX_BATCH = 32   # SPANQR_MAX_BATCH
 MAX_R = 4096     # SPANQR_MAX_R
 # kernels for spanqr_profile_kernel
@@ -43,6 +43,7 @@ SIGNATURES = {
     "spanqr_last_error": (ctypes.c_char_p, []),
     "spanqr_dust_host": (_I, [_I, _I, _P]),
     "spanqr_split_rows": (_I, [_I, _I]),
+    "spanqr_norm_partials": (_I, [_I, _I]),
     "spanqr_stage_amax": (_I, [_P, _P, _L, _P]),
     "spanqr_stage_gram": (_I, [_P, _P, _L, _I, _I, _P, _P, _P]),
     "spanqr_stage_chol": (_I, [_P, _P, _P, _F, _F, _P, _P, _P, _P]),

@@ -429,6 +429,162 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Gram of a short X in one launch, the split reduction inside the workgroup (tri.py:255-297, 324-375 with the sum
+// over splits of tri.py:297/375): workgroup u computes the upper 32x32 tile u = (ti, tj) of G = A^T A over all K rows
+// as two row splits of KS rows, one per group of four wavefronts (waves 0-3 rows [0, KS), waves 4-7 [KS, K)), each
+// wavefront a 16x16 quadrant of the tile. The 32-row chunks of both splits are staged through LDS together (two
+// buffers, one barrier per chunk), G32_DEPTH chunks fetched into registers ahead of the one being multiplied.
+// KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one chain runs over the
+// split. SCALE: operands are s * a (the pass-1 power-of-2 scale). The splits are summed in fp64 in split order,
+// rounded once, and the tile and its mirror stored in G. MODE 0 also writes the tile's ||G||_F^2 partial npart[u]
+// (per quadrant, each lane's four squares added in row order and a shift-down tree over the 64 lanes; the quadrants
+// (0,0), (0,1), (1,0), (1,1) added in that order; doubled off the diagonal) and clears the next Cholesky's column
+// counters; MODE 1 stores D = fp32(I - G) * 0.5 for the Newton-Schulz step (kcholqr.py:21) instead of G. Per element
+// the arithmetic is k_gram's + k_reduce's for the same split; only the norm partials' grouping differs. Taken where
+// it measured faster than the split Gram, its reduction launch and the gap between them: short X with many tiles
+// (the plan's rule).
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int G32_LD = 48;   // LDS row stride of a chunk panel: a quadrant read's four row groups hit distinct banks
+constexpr int G32_DEPTH = 6; // chunks of each split in flight (in registers) ahead of the one being multiplied
+template <bool KAHAN, bool SCALE, int MODE>
+__global__ __launch_bounds__(512) void k_gram32(const MatsIn As, long lda, int K, int nb, int KS,
+                                                const uint32_t* __restrict__ amax_part, float* __restrict__ G,
+                                                double* __restrict__ npart, int r, uint32_t* colcnt) {
+    const int u = blockIdx.x, U = gridDim.x;
+    const float* __restrict__ A = As.p[blockIdx.z];
+    amax_part += (size_t)blockIdx.z * AMAX_BLOCKS;
+    G += (size_t)blockIdx.z * r * r;
+    if (MODE == 0) npart += (size_t)blockIdx.z * U;
+    if (MODE == 0 && colcnt != nullptr && u == 0 && threadIdx.x < CH_MAXROW)
+        colcnt[((size_t)blockIdx.z * CH_MAXROW + threadIdx.x) * CC_STRIDE] = 0u;
+    int ti, tj;
+    upper_tile(u, nb, ti, tj);
+    const bool diag = ti == tj;
+    __shared__ float sA[2][2][BK][G32_LD];   // [buffer][split][row of the chunk][column of tile ti]
+    __shared__ float sB[2][2][BK][G32_LD];   // the same for tile column tj
+    __shared__ float xch[4][4][64];          // split 1's accumulators, per quadrant
+    __shared__ double qn[4];
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int g = w >> 2, q = w & 3, qi = q >> 1, qj = q & 1, l16 = lane & 15, lk = lane >> 4;
+    // the split of this thread's group and its float4 of each 32 x 32 chunk panel
+    const int gt = tid & 255, grow = gt >> 3, gc4 = gt & 7;
+    const int k0 = g * KS, k1 = (k0 + KS < K) ? k0 + KS : K;
+    const int nch = k1 > k0 ? (k1 - k0 + BK - 1) / BK : 0;       // this split's chunks
+    const int nch0 = ((KS < K ? KS : K) + BK - 1) / BK;          // split 0's chunks (the longer split)
+    // stages: a multiple of G32_DEPTH, every one unconditional (a stage past the chunks stores zeros and skips the
+    // MFMAs), so no load sits under a branch and each stage waits only for its own slot
+    const int nst = (nch0 + G32_DEPTH - 1) / G32_DEPTH * G32_DEPTH;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, comp = {0.f, 0.f, 0.f, 0.f};
+    // Slot d holds chunk c with c % G32_DEPTH == d. Loads are unconditional: a chunk past split 0's last reads that
+    // one again (unused); rows past the split read row k1 - 1 (in bounds -- the second split's k1 - 1 >= 0 even when
+    // it is empty -- and zeroed), so the compiler keeps them where they are issued.
+    float4 ra[G32_DEPTH], rb[G32_DEPTH];
+    const float* __restrict__ pa = A + ti * CB + 4 * gc4;
+    const float* __restrict__ pb = A + tj * CB + 4 * gc4;   // (a diagonal tile reads its panel twice: cache hits)
+    auto gload = [&](int c, float4& xa, float4& xb) {
+        const int cc = c < nch0 ? c : nch0 - 1;
+        const int k = k0 + cc * BK + grow;
+        const size_t off = (size_t)(k < k1 ? k : k1 - 1) * lda;
+        xa = *reinterpret_cast<const float4*>(pa + off);
+        xb = *reinterpret_cast<const float4*>(pb + off);
+    };
+#pragma unroll
+    for (int d = 0; d < G32_DEPTH; ++d) {
+        gload(d, ra[d], rb[d]);
+        __builtin_amdgcn_sched_barrier(0);   // issued in slot order, so each stage waits only for its own slot
+    }
+    float sc = 1.0f;
+    if (SCALE) sc = block_scale512(amax_part);   // (its reduction's barriers wait behind the first loads)
+    for (int c0 = 0; c0 < nst; c0 += G32_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < G32_DEPTH; ++d) {
+            const int c = c0 + d;
+            const int bf = c & 1;            // LDS buffers alternate: one barrier per stage
+            // rows past the split are zeroed with a bit mask (no branch: a branch that overwrites a loaded register
+            // waits for every load in flight)
+            const uint32_t keep = k0 + c * BK + grow < k1 ? 0xffffffffu : 0u;
+            float4 va = ra[d], vb = rb[d];
+            if (SCALE) {
+                va.x = sc * va.x; va.y = sc * va.y; va.z = sc * va.z; va.w = sc * va.w;
+                vb.x = sc * vb.x; vb.y = sc * vb.y; vb.z = sc * vb.z; vb.w = sc * vb.w;
+            }
+            va.x = __uint_as_float(__float_as_uint(va.x) & keep);
+            va.y = __uint_as_float(__float_as_uint(va.y) & keep);
+            va.z = __uint_as_float(__float_as_uint(va.z) & keep);
+            va.w = __uint_as_float(__float_as_uint(va.w) & keep);
+            vb.x = __uint_as_float(__float_as_uint(vb.x) & keep);
+            vb.y = __uint_as_float(__float_as_uint(vb.y) & keep);
+            vb.z = __uint_as_float(__float_as_uint(vb.z) & keep);
+            vb.w = __uint_as_float(__float_as_uint(vb.w) & keep);
+            *reinterpret_cast<float4*>(&sA[bf][g][grow][4 * gc4]) = va;
+            *reinterpret_cast<float4*>(&sB[bf][g][grow][4 * gc4]) = vb;
+            __syncthreads();
+            gload(c + G32_DEPTH, ra[d], rb[d]);   // refill the slot just stored
+            __builtin_amdgcn_sched_barrier(0);     // the loads go out before the MFMAs
+            if (c < nch) {                         // a chunk wholly past the split is not part of the sum
+                f32x4 part = KAHAN ? f32x4{0.f, 0.f, 0.f, 0.f} : acc;
+                float xa[BK / 4], yb[BK / 4];
+#pragma unroll
+                for (int kk = 0; kk < BK / 4; ++kk) {
+                    xa[kk] = sA[bf][g][4 * kk + lk][16 * qi + l16];
+                    yb[kk] = sB[bf][g][4 * kk + lk][16 * qj + l16];
+                }
+#pragma unroll
+                for (int kk = 0; kk < BK / 4; ++kk) part = mfma(xa[kk], yb[kk], part);
+                if (KAHAN) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float y = part[v] - comp[v];
+                        const float t = acc[v] + y;
+                        comp[v] = (t - acc[v]) - y;
+                        acc[v] = t;
+                    }
+                } else {
+                    acc = part;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (g == 1)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xch[q][v][lane] = acc[v];
+    __syncthreads();
+    if (g == 0) {
+        const bool two = KS < K;   // a second split exists
+        float gv[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            double sum = 0.0;
+            sum = sum + (double)acc[v];
+            if (two) sum = sum + (double)xch[q][v][lane];
+            gv[v] = (float)sum;
+        }
+        const int gi0 = ti * CB + 16 * qi + 4 * lk, gj = tj * CB + 16 * qj + l16;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float o = MODE == 1 ? (((gi0 + v == gj) ? 1.0f : 0.0f) - gv[v]) * 0.5f : gv[v];
+            G[(size_t)(gi0 + v) * r + gj] = o;
+            if (!diag) G[(size_t)gj * r + gi0 + v] = o;
+        }
+        if (MODE == 0) {
+            double s2 = (double)gv[0] * (double)gv[0];
+#pragma unroll
+            for (int v = 1; v < 4; ++v) s2 = s2 + (double)gv[v] * (double)gv[v];
+            for (int off = 32; off >= 1; off >>= 1) s2 = s2 + __shfl_down(s2, off);
+            if (lane == 0) qn[q] = s2;
+        }
+    }
+    if (MODE == 0) {
+        __syncthreads();
+        if (tid == 0) {
+            const double tot = ((qn[0] + qn[1]) + qn[2]) + qn[3];
+            npart[u] = diag ? tot : 2.0 * tot;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // Clamped Cholesky (chol.cu:115-271): one persistent kernel over 32x32 tiles T(i, k), i >= k, nb = r / 32 tile rows,
 // synchronised by per-tile flags instead of grid barriers.
 //   * Workgroup 0 runs the critical chain. Step j: wave 0 factors T(j, j) and inverts the factor in one pass; at the
@@ -2397,6 +2553,8 @@ struct spanqr_plan {
     int batch = 1, chol_bmax = 1;   // matrices per call; matrices per Cholesky launch
     size_t lp_stride = 0;           // floats of packed factor per matrix
     int nt = 0, U = 0, NB = 0, S = 0, KS = 0, chol_grid = 0, trsm_q = 0, trsm_rb = 1;   // NB: 32-column blocks
+    bool gram_short = false;  // one-launch Gram over upper 32x32 tiles (k_gram32) instead of split Gram + reduction
+    int nnp = 0;              // norm partials per matrix the Gram writes (16 per 64x64 tile, or 1 per 32x32 tile)
     int owner_w = OWNER_W;    // tiles per Cholesky owner part at most
     bool trsm_rows = false;   // solve with a wavefront pair per 16 rows (k_trsm_rows) instead of k_trsm
     int solve_rb = 0;         // row blocks per solve workgroup in the Cholesky's launch (0: separate launches)
@@ -2443,6 +2601,14 @@ void split_policy(int K, int U, int* S_out, int* KS_out) {
     *KS_out = KS;
     *S_out = (K + KS - 1) / KS;
 }
+
+// Short X with many tiles takes the one-launch Gram (k_gram32): two row splits of KS = ceil(K / 2) rounded up to 32
+// rows inside each 32x32-tile workgroup, where that measured faster than the split Gram with its reduction launch
+// (768 x 512: 9.3 against 5.5 + 3.5 us and a launch gap; at r <= 384 or K > 1024 the split Gram's parallelism wins).
+// Fixed by (K, r) alone, as the split rule is, so results do not depend on the device.
+constexpr int GRAM_SHORT_KMAX = 1024, GRAM_SHORT_RMIN = 448;
+bool gram_short_rule(int K, int r) { return K <= GRAM_SHORT_KMAX && r >= GRAM_SHORT_RMIN; }
+int gram_short_rows(int K) { return ((K + 1) / 2 + BK - 1) / BK * BK; }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -2507,6 +2673,38 @@ void launch_reduce(const spanqr_plan* p, int mode, float* out, int n, hipStream_
     const dim3 grid(16, p->U, n);
     if (mode == 0) k_reduce<0><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart, p->colcnt);
     else k_reduce<1><<<grid, 256, 0, st>>>(p->P, p->S, p->nt, p->r, out, p->npart);
+}
+
+template <bool KAHAN, bool SCALE, int MODE>
+void launch_gram32_t(const spanqr_plan* p, const MatsIn& A, long lda, int n, hipStream_t st) {
+    const int nb = p->r / CB;
+    k_gram32<KAHAN, SCALE, MODE><<<dim3(nb * (nb + 1) / 2, 1, n), 512, 0, st>>>(A, lda, p->K, nb, p->KS, p->amax_part,
+                                                                              p->G, p->npart, p->r, p->colcnt);
+}
+
+// G of a pass (mode 0: G, the norm partials, the next Cholesky's column counters cleared) or D = (I - G) / 2 of a
+// polish step (mode 1) into p->G: one launch on a short-X plan, else the split Gram and its reduction. mark() after
+// each launch (profiling).
+template <class Mark>
+int launch_gram_g(const spanqr_plan* p, const MatsIn& A, long lda, int n, bool scale, bool kahan, int mode,
+                  hipStream_t st, Mark mark) {
+    if (p->gram_short) {
+        if (mode == 0) {
+            if (kahan && scale) launch_gram32_t<true, true, 0>(p, A, lda, n, st);
+            else if (kahan) launch_gram32_t<true, false, 0>(p, A, lda, n, st);
+            else if (scale) launch_gram32_t<false, true, 0>(p, A, lda, n, st);
+            else launch_gram32_t<false, false, 0>(p, A, lda, n, st);
+        } else {
+            if (kahan) launch_gram32_t<true, false, 1>(p, A, lda, n, st);
+            else launch_gram32_t<false, false, 1>(p, A, lda, n, st);
+        }
+        return mark();
+    }
+    launch_gram(p, A, lda, n, scale, kahan, st);
+    int rc = mark();
+    if (rc) return rc;
+    launch_reduce(p, mode, p->G, n, st);
+    return mark();
 }
 
 // Cholesky of the n matrices in p->G, in launches of at most chol_bmax matrices: plan creation has checked that
@@ -2797,19 +2995,16 @@ int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut
     long ldin = ldx;
     int cur = 0;
     for (int pass = 0; pass < 3; ++pass) {
-        launch_gram(p, *in, ldin, n, pass == 0, pass == 0, st);
-        if ((rc = mark())) return rc;
-        launch_reduce(p, 0, p->G, n, st);
-        if ((rc = mark())) return rc;
+        if ((rc = launch_gram_g(p, *in, ldin, n, pass == 0, pass == 0, 0, st, mark))) return rc;
         // the solve in the Cholesky's launch when every workgroup of the launch fits on the device at once (one per
         // CU); a larger batch runs them as separate launches, where the solve keeps its own, smaller LDS
         if (p->solve_rb > 0 && n * (p->chol_grid + p->solve_nrb) <= p->cus) {
-            if ((rc = launch_chol_solve(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U, n, *in, ldin, pass == 0,
+            if ((rc = launch_chol_solve(p, alpha, tau, p->scal + 1 + 2 * pass, st, p->nnp, n, *in, ldin, pass == 0,
                                         eps, dz, bout[cur], p->r)))
                 return rc;
             if ((rc = mark())) return rc;
         } else {
-            if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, 16 * p->U, n))) return rc;
+            if ((rc = launch_chol(p, alpha, tau, p->scal + 1 + 2 * pass, st, p->nnp, n))) return rc;
             if ((rc = mark())) return rc;
             launch_trsm(p, *in, ldin, pass == 0, eps, dz, bout[cur], p->r, n, st);
             if ((rc = mark())) return rc;
@@ -2819,10 +3014,7 @@ int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut
         cur ^= 1;
     }
     for (int i = 0; i < ns; ++i) {
-        launch_gram(p, *in, ldin, n, false, i == ns - 1, st);
-        if ((rc = mark())) return rc;
-        launch_reduce(p, 1, p->G, n, st);
-        if ((rc = mark())) return rc;
+        if ((rc = launch_gram_g(p, *in, ldin, n, false, i == ns - 1, 1, st, mark))) return rc;
         if (i == ns - 1) {
             launch_nsapply(p, *in, ldin, Q, ldq, n, st);
         } else {
@@ -2888,7 +3080,15 @@ size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 void plan_shape(spanqr_plan* p, int K, int r, int batch) {
     p->K = K; p->r = r; p->batch = batch;
     p->nt = (r + TB - 1) / TB; p->U = p->nt * (p->nt + 1) / 2; p->NB = r / CB;
-    split_policy(K, p->U, &p->S, &p->KS);
+    p->gram_short = gram_short_rule(K, r);
+    if (p->gram_short) {
+        p->KS = gram_short_rows(K);
+        p->S = (K + p->KS - 1) / p->KS;
+        p->nnp = p->NB * (p->NB + 1) / 2;
+    } else {
+        split_policy(K, p->U, &p->S, &p->KS);
+        p->nnp = 16 * p->U;
+    }
     p->owner_w = OWNER_W;
     p->chol_grid = chol_workgroups(r / CB, p->owner_w);     // workgroup 0 + the parts of tile rows 4..r/32-1
     p->trsm_q = trsm_q_for(r / CB);
@@ -3007,7 +3207,7 @@ size_t plan_layout(spanqr_plan* p, char* base) {
         al256(B * nKr), al256(B * nKr),                         // Y0, Y1
         al256(B * SCAL_STRIDE * sizeof(float)),                 // scal
         al256(B * SCAL_STRIDE * sizeof(float)),                 // chscal
-        al256(B * 16 * p->U * sizeof(double)),                  // npart
+        al256(B * p->nnp * sizeof(double)),                     // npart
         al256(B * AMAX_BLOCKS * sizeof(uint32_t)),              // amax_part
         al256(B * BAR_STRIDE * sizeof(uint32_t)),               // bar
         al256((6 * CH_MAXROW + 2) * sizeof(uint64_t)),          // stamps
@@ -3142,10 +3342,17 @@ int enqueue_borth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, 
 int spanqr_split_rows(int K, int r) {
     const int rc = check_shape(K, r);
     if (rc != SPANQR_OK) return rc;
-    const int nt = (r + TB - 1) / TB;
-    int S = 0, KS = 0;
-    split_policy(K, nt * (nt + 1) / 2, &S, &KS);
-    return KS;
+    spanqr_plan p;
+    plan_shape(&p, K, r, 1);
+    return p.KS;
+}
+
+int spanqr_norm_partials(int K, int r) {
+    const int rc = check_shape(K, r);
+    if (rc != SPANQR_OK) return rc;
+    spanqr_plan p;
+    plan_shape(&p, K, r, 1);
+    return p.nnp;
 }
 
 int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
@@ -3242,6 +3449,7 @@ long spanqr_plan_query(const spanqr_plan* p, int what) {
         case SPANQR_Q_CHOL_BATCH: return p->blk ? p->blk->chol_bmax : p->chol_bmax;
         case SPANQR_Q_BLOCKS: return p->nblk;
         case SPANQR_Q_BLOCK_WIDTH: return p->bw;
+        case SPANQR_Q_NORM_PARTIALS: return p->blk ? p->blk->nnp : p->nnp;
         case SPANQR_Q_SOLVE_ROWS: {
             const spanqr_plan* q = p->blk ? p->blk : p;
             return q->solve_rb == 0 ? 0 : (q->solve_q == 0 ? 16L * q->solve_wpg : 16L * q->solve_rb);
@@ -3314,6 +3522,8 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
     if (which < SPANQR_K_AMAX || which > SPANQR_K_CHOL_SOLVE) return fail(SPANQR_EINVAL, "unknown kernel %d", which);
     if ((which == SPANQR_K_CHOL_SOLVE_PASS1 || which == SPANQR_K_CHOL_SOLVE) && p->solve_rb == 0)
         return fail(SPANQR_EINVAL, "this plan runs the Cholesky and the solve in separate launches");
+    if (which == SPANQR_K_REDUCE && p->gram_short)
+        return fail(SPANQR_EINVAL, "this plan's Gram reduces its splits in the same launch");
     DeviceGuard dg(p->device);
     if (!dg.ok) return fail(SPANQR_EHIP, "cannot select HIP device %d", p->device);
     hipStream_t st = (hipStream_t)stream;
@@ -3325,10 +3535,16 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
     auto launch = [&]() -> int {
         switch (which) {
             case SPANQR_K_AMAX: k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(y0, r, p->K, r, p->amax_part); break;
-            case SPANQR_K_GRAM_PASS1: launch_gram(p, y0, r, 1, true, true, st); break;
-            case SPANQR_K_GRAM: launch_gram(p, y0, r, 1, false, false, st); break;
+            case SPANQR_K_GRAM_PASS1:
+                if (p->gram_short) launch_gram32_t<true, true, 0>(p, y0, r, 1, st);
+                else launch_gram(p, y0, r, 1, true, true, st);
+                break;
+            case SPANQR_K_GRAM:
+                if (p->gram_short) launch_gram32_t<false, false, 0>(p, y0, r, 1, st);
+                else launch_gram(p, y0, r, 1, false, false, st);
+                break;
             case SPANQR_K_REDUCE: launch_reduce(p, 0, p->G, 1, st); break;
-            case SPANQR_K_CHOL: return launch_chol(p, 1e-7f, 1e-8f, p->scal + 1, st, 16 * p->U, 1);
+            case SPANQR_K_CHOL: return launch_chol(p, 1e-7f, 1e-8f, p->scal + 1, st, p->nnp, 1);
             case SPANQR_K_TRSM_PASS1: launch_trsm(p, y0, r, true, 5e-7f, Dust{p->Z, r}, y1, r, 1, st); break;
             case SPANQR_K_TRSM: launch_trsm(p, y0, r, false, 0.0f, Dust{p->Z, r}, y1, r, 1, st); break;
             case SPANQR_K_NS_APPLY: launch_nsapply(p, y0, r, y1, r, 1, st); break;
@@ -3343,7 +3559,7 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
         for (int i = 0; i <= reps; ++i) {
             k_clear_words<<<1, 64, 0, st>>>(p->colcnt, CH_MAXROW, CC_STRIDE);
             HIPCHK(hipEventRecord(p->ev[0], st));
-            if ((rc = launch_chol_solve(p, 1e-7f, 1e-8f, p->scal + 1, st, 16 * p->U, 1, y0, r, p1, p1 ? 5e-7f : 0.0f,
+            if ((rc = launch_chol_solve(p, 1e-7f, 1e-8f, p->scal + 1, st, p->nnp, 1, y0, r, p1, p1 ? 5e-7f : 0.0f,
                                         Dust{p->Z, r}, y1, r)))
                 return rc;
             HIPCHK(hipEventRecord(p->ev[1], st));
@@ -3388,10 +3604,9 @@ int spanqr_stage_gram(spanqr_plan* p, const float* A, long lda, int use_scale, i
     if (!G) return fail(SPANQR_EINVAL, "G is null");
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
-    launch_gram(p, mats_in(&A, 1), lda, 1, use_scale != 0, kahan != 0, st);
-    launch_reduce(p, 0, p->G, 1, st);
+    launch_gram_g(p, mats_in(&A, 1), lda, 1, use_scale != 0, kahan != 0, 0, st, [] { return SPANQR_OK; });
     HIPCHK(hipMemcpyAsync(G, p->G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
-    if (npart) HIPCHK(hipMemcpyAsync(npart, p->npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
+    if (npart) HIPCHK(hipMemcpyAsync(npart, p->npart, (size_t)p->nnp * sizeof(double), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
@@ -3403,9 +3618,9 @@ int spanqr_stage_chol(spanqr_plan* p, const float* G, const double* npart, float
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
-    if (npart) HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
+    if (npart) HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)p->nnp * sizeof(double), hipMemcpyDeviceToDevice, st));
     k_clear_words<<<1, 64, 0, st>>>(p->bar + 2, 1, BAR_STRIDE);
-    int rc = launch_chol(p, alpha, tau, p->chscal, st, npart ? 16 * p->U : 0, 1);
+    int rc = launch_chol(p, alpha, tau, p->chscal, st, npart ? p->nnp : 0, 1);
     if (rc) return rc;
     HIPCHK(hipMemcpyAsync(L, p->L, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipMemcpyAsync(Li, p->Li, (size_t)p->r * CB * sizeof(float), hipMemcpyDeviceToDevice, st));
@@ -3440,8 +3655,7 @@ int spanqr_stage_ns(spanqr_plan* p, const float* Y, long ldy, int kahan, float* 
     if ((rc = check_mat(p, Yout, ldo, "Yout"))) return rc;
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
-    launch_gram(p, mats_in(&Y, 1), ldy, 1, false, kahan != 0, st);
-    launch_reduce(p, 1, p->G, 1, st);
+    launch_gram_g(p, mats_in(&Y, 1), ldy, 1, false, kahan != 0, 1, st, [] { return SPANQR_OK; });
     launch_nsapply(p, mats_in(&Y, 1), ldy, mats_out(&Yout, 1), ldo, 1, st);
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
@@ -3454,9 +3668,9 @@ int spanqr_profile_chol(spanqr_plan* p, const float* G, const double* npart, flo
     DeviceGuard dg(p->device);
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
-    HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)16 * p->U * sizeof(double), hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)p->nnp * sizeof(double), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipMemsetAsync(p->stamps, 0, (size_t)(6 * p->NB + 2) * sizeof(uint64_t), st));
-    int rc = launch_chol(p, alpha, tau, p->chscal, st, 16 * p->U, 1, true);
+    int rc = launch_chol(p, alpha, tau, p->chscal, st, p->nnp, 1, true);
     if (rc) return rc;
     HIPCHK(hipMemcpyAsync(stamps_out, p->stamps, (size_t)(6 * p->NB + 2) * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));

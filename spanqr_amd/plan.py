@@ -57,6 +57,16 @@ class Plan:
         return self.query(_lib.Q_SOLVE_ROWS)
 
     @property
+    def norm_partials(self):
+        return self.query(_lib.Q_NORM_PARTIALS)
+
+    @property
+    def gram_short(self):
+        """the one-launch Gram over 32x32 tiles (no separate split reduction)"""
+        nt = (self.r + 63) // 64
+        return self.norm_partials != 16 * nt * (nt + 1) // 2
+
+    @property
     def chol_batch(self):
         return self.query(_lib.Q_CHOL_BATCH)
 

@@ -24,10 +24,6 @@ def _dev(t):
     return t.device
 
 
-def _u(nt):
-    return nt * (nt + 1) // 2
-
-
 def dust_host(K, r):
     """the dust matrix as the library generates it on the host (numpy, no GPU needed)"""
     Z = np.empty((K, r), np.float32)
@@ -59,12 +55,13 @@ def amax(X):
 
 
 def gram(A, kahan, use_scale=False):
-    """(G [r, r], ||G||_F^2 partials [16 U] fp64); use_scale: scale on load by the plan's pass-1 scale"""
+    """(G [r, r], ||G||_F^2 partials fp64: 16 per upper 64x64 tile, or one per upper 32x32 tile where the plan runs
+    the one-launch Gram of short X); use_scale: scale on load by the plan's pass-1 scale"""
     A = A.contiguous()
     K, r = A.shape
     plan = get_plan(K, r, _dev(A))
     G = torch.empty(r, r, device=A.device, dtype=torch.float32)
-    npart = torch.empty(16 * _u((r + 63) // 64), device=A.device, dtype=torch.float64)
+    npart = torch.empty(plan.query(_lib.Q_NORM_PARTIALS), device=A.device, dtype=torch.float64)
     _lib.check(_lib.lib().spanqr_stage_gram(plan.handle, A.data_ptr(), A.stride(0), int(bool(use_scale)),
                                             int(bool(kahan)), G.data_ptr(), npart.data_ptr(),
                                             stream_handle(A.device)))

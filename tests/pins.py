@@ -198,8 +198,10 @@ def check_gram():
     f = []
     rng = np.random.default_rng(3)
     # ragged last split (200 = 3 x 64 + 8); r = 96 and 32: the last 64-column tile is half outside X (its columns
-    # read as 0, entries past r neither stored nor counted in the norm partials)
-    for K, r, KS in ((200, 128, 64), (200, 96, 64), (150, 32, 64)):
+    # read as 0, entries past r neither stored nor counted in the norm partials). The norm partials come in both
+    # groupings: one per upper 32x32 tile for short X with many tiles (K <= 1024, r >= 448: the last two), 16 per
+    # upper 64x64 tile otherwise
+    for K, r, KS in ((200, 128, 64), (200, 96, 64), (150, 32, 64), (600, 480, 320), (460, 448, 256)):
         X = rng.standard_normal((K, r)).astype(np.float32)
         X[:, 5] *= 1e3
         G64 = X.astype(np.float64).T @ X.astype(np.float64)
@@ -212,6 +214,10 @@ def check_gram():
             if not np.array_equal(G, G.T):
                 f.append(f"gram (r={r}) not exactly symmetric")
             fro2 = float((G.astype(np.float64) ** 2).sum())
+            nt, nb = -(-r // 64), r // 32
+            want = nb * (nb + 1) // 2 if oracle.gram_short(K, r) else 16 * nt * (nt + 1) // 2
+            if npart.size != want or oracle.gram_short(K, r) != (K <= 1024 and r >= 448):
+                f.append(f"gram({K}x{r}): {npart.size} norm partials, expected {want}")
             if not abs(npart.sum() - fro2) <= 1e-12 * fro2:
                 f.append(f"norm partials (r={r}) do not sum to ||G||_F^2")
             if not abs(float(oracle.norm(npart)) - math.sqrt(fro2)) <= 2 * U32 * math.sqrt(fro2):
@@ -503,7 +509,7 @@ def check_borth_composition():
     Z = oracle.dust(K, r)
     for b, reorth in ((256, True), (128, True), (128, False)):
         Q = oracle.borth(X, b, reorth)
-        KSb = oracle.split_rows(K, (b // 64) * (b // 64 + 1) // 2)
+        KSb = oracle.gram_rows(K, b)
         R = np.empty_like(X)
         for j in range(0, r, b):
             W = X[:, j:j + b] * s

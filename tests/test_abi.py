@@ -31,16 +31,25 @@ def test_host_dust_is_the_oracle_dust(K, r):
 
 def test_split_policy():
     f = _lib.lib().spanqr_split_rows
-    # tri.py:364-367 with 512 target workgroups: S = min(ceil(512 / U), ceil(K / 128)), KS = 32 ceil(ceil(K/S) / 32)
+    nparts = _lib.lib().spanqr_norm_partials
+    # short X with many tiles (K <= 1024, r >= 448): two splits of ceil(K / 2) rows rounded up to 32, one norm partial per upper
+    # 32x32 tile; otherwise tri.py:364-367 with 512 target workgroups: S = min(ceil(512 / U), ceil(K / 128)),
+    # KS = 32 ceil(ceil(K/S) / 32), 16 partials per upper 64x64 tile
     for K, r in [(1024, 256), (2048, 256), (3584, 256), (768, 512), (2048, 512), (5120, 256), (17408, 256),
                  (64, 64), (100, 64), (12345, 192), (1024, 96), (4100, 160), (32, 32), (9217, 224), (768, 480),
-                 (1024, 576), (2048, 768), (1100, 1024), (5000, 992)]:
+                 (1024, 576), (2048, 768), (1100, 1024), (5000, 992), (1025, 512), (1024, 416), (512, 448),
+                 (1024, 1024)]:
         nt = -(-r // 64)
         U = nt * (nt + 1) // 2
-        S = max(1, min(-(-512 // U), -(-K // 128)))
-        KS = 32 * -(-(-(-K // S)) // 32)
+        if K <= 1024 and r >= 448:
+            KS = 32 * -(-(-(-K // 2)) // 32)
+            assert nparts(K, r) == (r // 32) * (r // 32 + 1) // 2, (K, r)
+        else:
+            S = max(1, min(-(-512 // U), -(-K // 128)))
+            KS = 32 * -(-(-(-K // S)) // 32)
+            assert KS % 32 == 0 and -(-K // KS) <= S
+            assert nparts(K, r) == 16 * U, (K, r)
         assert f(K, r) == KS, (K, r)
-        assert KS % 32 == 0 and -(-K // KS) <= S
     for K, r in [(100, 128), (1024, 80), (2048, 1056), (1024, 0), (4096, 1280), (1024, 16), (10, 32), (544, 576)]:
         assert f(K, r) == -1
         assert _lib.lib().spanqr_last_error()
@@ -49,11 +58,13 @@ def test_split_policy():
 def test_split_policy_is_the_oracle_rule():
     """the library's split rule (every Gram and block projection) is the one the oracle restates"""
     f = _lib.lib().spanqr_split_rows
-    for K in (64, 100, 513, 1024, 3000, 17408, 65536):
+    nparts = _lib.lib().spanqr_norm_partials
+    for K in (64, 100, 513, 768, 1024, 1025, 2048, 3000, 17408, 65536):
         for r in range(32, 1025, 32):
             if K >= r:
-                nt = -(-r // 64)
-                assert f(K, r) == oracle.split_rows(K, nt * (nt + 1) // 2), (K, r)
+                assert f(K, r) == oracle.gram_rows(K, r), (K, r)
+                assert nparts(K, r) == oracle.npart_count(K, r), (K, r)
+                assert (nparts(K, r) != 16 * (-(-r // 64)) * (-(-r // 64) + 1) // 2) == oracle.gram_short(K, r)
 
 
 def test_column_blocked_shapes_checked_before_any_device_work():

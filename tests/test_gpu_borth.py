@@ -97,7 +97,7 @@ def test_borth_large_shape_properties(cuda):
     Xn = X.numpy()
     s = oracle.pow2_scale(oracle.amax(Xn))
     Z = oracle.dust(K, r)
-    Q0 = oracle.orth_dust(Xn[:, :256] * s, Z[:, :256], oracle.split_rows(K, 10))
+    Q0 = oracle.orth_dust(Xn[:, :256] * s, Z[:, :256], oracle.gram_rows(K, 256))
     assert_bits(Q1[:, :256], Q0, "first block vs the oracle's _kf")
 
 
@@ -142,7 +142,7 @@ def test_blocked_plan_refused_where_it_does_not_apply(cuda):
     plan = get_borth_plan(K, r, 256, True, cuda)   # spanqr_plan_create's plan at r = 768
     L = _lib.lib()
     assert L.spanqr_plan_query(plan.handle, _lib.Q_BLOCKS) == 3
-    assert L.spanqr_plan_query(plan.handle, _lib.Q_SPLIT_ROWS) == oracle.split_rows(K, 10)
+    assert L.spanqr_plan_query(plan.handle, _lib.Q_SPLIT_ROWS) == oracle.gram_rows(K, 256)
     X = torch.zeros(K, r, device=cuda)
     ptrs = (ctypes.c_void_p * 1)(X.data_ptr())
     assert L.spanqr_orth_batched_f32(plan.handle, 1, ptrs, r, ptrs, r, 5e-7, 1e-7, 1e-8, 2, stream_handle(cuda)) == -1
