@@ -104,7 +104,7 @@ def chol_steps_us(X):
     nb = r // 32
     runs = []
     for rep in range(7):
-        stamps = (ctypes.c_ulonglong * (6 * nb + 2))()
+        stamps = (ctypes.c_ulonglong * (24 * nb + 2))()
         tick = ctypes.c_double()
         _lib.check(_lib.lib().spanqr_profile_chol(plan.handle, G.data_ptr(), npart.data_ptr(), 1e-7, 1e-8, stamps,
                                                   ctypes.byref(tick), stream_handle(X.device)))

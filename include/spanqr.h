@@ -130,11 +130,17 @@ int spanqr_profile_orth(spanqr_plan* plan, const float* X, long ldx, float* Q, l
                         float tau, int ns, void* stream, float* ms, int max_n, int* n_out);
 
 /* Profiling form of the Cholesky stage (spanqr_stage_chol with npart): runs an instrumented copy of the kernel whose
- * workgroup 0 stamps the device wall clock, copies 6 r/32 + 2 stamps to host memory and waits for the stream: [0]
- * kernel start; for each 32-column diagonal step j (nb = r/32 steps), [1 + 4j] step start, [2 + 4j] tile factored and
- * the next tile row fetched (the whole workgroup), [3 + 4j] look-ahead done, [4 + 4j] the tile factor's wavefront
- * done; [1 + 4 nb] end; [2 + 4 nb + j] the next tile row's wavefronts done; [2 + 5 nb + j] the publishing wavefront
- * done; zero where a step has no such work. *tick_ns: nanoseconds per wall-clock tick. The reference keeps similar
+ * workgroup 0 stamps the device wall clock, copies 24 r/32 + 2 stamps to host memory and waits for the stream: [0]
+ * kernel start; for each 32-column diagonal step j (nb = r/32 steps), [1 + 4j] step start, [2 + 4j] step end (the
+ * whole workgroup), [3 + 4j] the look-ahead's wavefront done, [4 + 4j] the tile factor's wavefront done; [1 + 4 nb]
+ * end; [2 + 4 nb + j] tile row j+2's wavefronts done; [2 + 5 nb + j] the publishing wavefront done; [2 + 6 nb + j]
+ * the hand-over of row j+2 seen; [2 + 7 nb + j] row j+2 fetched; [2 + 8 nb + j] its panel L(j+2, j-1) formed;
+ * [2 + 9 nb + j] the second of row j+2's wavefronts done; for the owner of tile row i (its last part, at the
+ * block before it hands the row over), [2 + 10 nb + 6i + s]: s = 0 block published, 1 operands loaded, 2 its own
+ * panel published, 3 row handed over, 4 row updated, 5 hand-over stores done; for the last tile row's last part at
+ * block j, [2 + 16 nb + 8j + s]: s = 0 block published, 1 operands loaded, 2 own panel published, 3 L(j+2, j) formed,
+ * 4 early tiles updated, 5 other panels' flags seen, 6 other panels loaded, 7 block done; zero where a step has no
+ * such work. *tick_ns: nanoseconds per wall-clock tick. The reference keeps similar
  * stamps behind a debug define (candidates/cuk/chol.cu:17-23). */
 int spanqr_profile_chol(spanqr_plan* plan, const float* G, const double* npart, float alpha, float tau,
                         unsigned long long* stamps_out, double* tick_ns, void* stream);

@@ -23,7 +23,7 @@
  * one fixed sequence of IEEE operations, and the MI355X kernels produce the same sequence (an fp32 MFMA chain on
  * gfx950 rounds exactly like a sequential fmaf chain in k order), so results are compared bit for bit.
  * Where the reference leaves an order open (its Triton dots, cuBLAS GEMMs, tree reductions, CUDA rsqrtf) this file
- * fixes one, documented at each function. In three places it also departs, deliberately, from an order the
+ * fixes one, documented at each function. In four places it also departs, deliberately, from an order the
  * reference's own source does fix; each is the same mathematics, and the accumulation chosen is the one an MFMA
  * chain on gfx950 produces in a single pass (bitwise parity with the reference's Q is out of reach anyway: its
  * dust comes from CUDA Philox, its pivots from CUDA rsqrtf, its solve dots from Triton tf32x3):
@@ -36,6 +36,10 @@
  *   - in the blocked solve the off-diagonal blocks are one chain per element starting from the operand a, over the
  *     earlier column blocks in order; the reference takes each block's dot product and subtracts it
  *     (candidates/tri.py:396-399 acc - tl.dot(Yk, Ljk^T));
+ *   - the first panel below each diagonal tile, L(j+1, j), is solved from T(j+1, j) against L(j, j) by forward
+ *     substitution (one chain per element over the earlier columns, then times the pivot's reciprocal square root),
+ *     the order in which the factor's column pairs produce it beside the tile; the reference multiplies by the tile
+ *     inverse like every other panel (candidates/cuk/chol.cu:199-202, panel = A Linv^T);
  * and where it fixes an order the reference leaves open:
  *   - dot products are fmaf chains in ascending summation index, starting from +0 (or from the value being updated);
  *   - Gram output tiles are 64 wide, Cholesky tiles and TRSM column blocks 32 wide (as in the reference); products
@@ -336,8 +340,8 @@ float spqo_rsqrt(float x) {
  * (chol.cu:151-168): x_i = 0 for i < kk; otherwise acc = [i == kk], acc = fmaf(-L[i][m], x_m, acc) for
  * m = 0..i-1 in order, x_i = acc * rd_i. Li[i][kk] = x_i. D: 32x32 with row stride ld (lower part read and
  * overwritten); L gets the lower factor (upper part zero), Li the inverse (row-major 32x32). */
-void spqo_diag_factor(float* D, long ld, float tau, float* L, long ldl, float* Li) {
-    float rd[CB], lc[CB];
+static void diag_factor_rd(float* D, long ld, float tau, float* L, long ldl, float* Li, float* rd) {
+    float lc[CB];
     for (int c = 0; c < CB; ++c) {
         float piv = PLANTED(8) ? fminf(D[(size_t)c * ld + c], tau) : fmaxf(D[(size_t)c * ld + c], tau);   /* 8 */
         float q = spqo_rsqrt(piv);
@@ -359,11 +363,19 @@ void spqo_diag_factor(float* D, long ld, float tau, float* L, long ldl, float* L
     }
 }
 
+void spqo_diag_factor(float* D, long ld, float tau, float* L, long ldl, float* Li) {
+    float rd[CB];
+    diag_factor_rd(D, ld, tau, L, ldl, Li, rd);
+}
+
 /* Blocked right-looking Cholesky of A (r x r, lower tiles read; destroyed), following chol.cu:182-271: step j
- * factors tile (j, j) into L[j][j] and Li[j]; every panel tile is P_i = A[i][j] Li[j]^T (fmaf chain over
- * m < mend(b) from +0) and is stored as L[i][j]; every trailing tile (i, k), j < k <= i, becomes A[i][k] - P_i P_k^T
- * as an fmaf chain over m = 0..31 starting from A[i][k]. L: r x r (upper triangle zero). Li: r x 32, block j at
- * rows 32j.. */
+ * factors tile (j, j) into L[j][j] and Li[j]; the first panel below it, P_{j+1} = L[j+1][j], comes out of the
+ * factor by forward substitution (element (a, c): acc = A[j+1][j][a][c], acc = fmaf(-L[j][j][c][m], P[a][m], acc)
+ * for m = 0..c-1 in order, P[a][c] = acc * rd_c with the pivot's reciprocal square root rd_c), the order in which
+ * the factor's wavefront forms it column by column beside the tile; every other panel tile is P_i = A[i][j] Li[j]^T
+ * (fmaf chain over m < mend(b) from +0). Each is stored as L[i][j]; every trailing tile (i, k), j < k <= i, becomes
+ * A[i][k] - P_i P_k^T as an fmaf chain over m = 0..31 starting from A[i][k]. L: r x r (upper triangle zero).
+ * Li: r x 32, block j at rows 32j.. */
 void spqo_chol(float* A, int r, float tau, float* L, float* Li) {
     fp_env();
     const int nb = r / CB;
@@ -373,10 +385,23 @@ void spqo_chol(float* A, int r, float tau, float* L, float* Li) {
         float* Dj = A + (size_t)(j * CB) * r + j * CB;
         float* Lj = L + (size_t)(j * CB) * r + j * CB;
         float* Lij = Li + (size_t)(j * CB) * CB;
-        spqo_diag_factor(Dj, r, tau, Lj, r, Lij);
+        float rd[CB];
+        diag_factor_rd(Dj, r, tau, Lj, r, Lij, rd);
         #pragma omp parallel for schedule(static)
         for (int i = j + 1; i < nb; ++i) {
             fp_env();
+            if (i == j + 1) {
+                for (int a = 0; a < CB; ++a)
+                    for (int c = 0; c < CB; ++c) {
+                        float acc = A[(size_t)(i * CB + a) * r + j * CB + c];
+                        for (int m = 0; m < c; ++m)
+                            acc = fmaf(-Lj[(size_t)c * r + m], P[(size_t)(i * CB + a) * CB + m], acc);
+                        acc = acc * rd[c];
+                        P[(size_t)(i * CB + a) * CB + c] = acc;
+                        L[(size_t)(i * CB + a) * r + j * CB + c] = acc;
+                    }
+                continue;
+            }
             for (int a = 0; a < CB; ++a)
                 for (int b = 0; b < CB; ++b) {
                     float acc = 0.0f;

@@ -587,16 +587,16 @@ __global__ __launch_bounds__(512) void k_gram32(const MatsIn As, long lda, int K
 // ---------------------------------------------------------------------------------------------------------------
 // Clamped Cholesky (chol.cu:115-271): one persistent kernel over 32x32 tiles T(i, k), i >= k, nb = r / 32 tile rows,
 // synchronised by per-tile flags instead of grid barriers.
-//   * Workgroup 0 runs the critical chain. Step j: wave 0 factors T(j, j) and inverts the factor in one pass; at the
-//     same time waves 1-2 fetch tile row j+2 (T(j+2, j-1..j+2), handed over by its owner through column block j-2,
-//     plus the owner's panel L(j+2, j-2)) while wave 3 publishes the previous step's L tiles and Li; then wave 1
-//     forms the panel L(j+2, j-1) (the previous step's Li_{j-1}, L(j, j-1), L(j+1, j-1) are still in LDS), wave 2
-//     applies the block j-2 update of T(j+2, j+1) that the owner leaves out, and the two waves apply block j-1 to
-//     T(j+2, j) and the lower half of T(j+2, j+2) (wave 1), T(j+2, j+1) and the rest (wave 2); wave 7 forms the
-//     previous step's L(j+1, j-1), which wave 3 publishes and waves 2-3 use; wave 3, after publishing, applies block
-//     j-1 to T(j+1, j) and T(j+1, j+1). Then waves 0-3 form the panel L(j+1, j) and apply column block j to
-//     T(j+1, j+1), the tile the next step factors (look-ahead over the next two tile rows; block j on the rest of
-//     row j+2 is wave 3's work in the next step).
+//   * Workgroup 0 runs the critical chain, one step per tile row j, with T(j, j) in the registers of the wavefront
+//     that factors it (wave 0 at even j, wave 7 at odd j). Step j: that wavefront factors T(j, j) and inverts the
+//     factor in one pass, column pair by column pair, publishing each pair in LDS; the other of the two (the
+//     look-ahead) forms the previous step's L(j+1, j-1) (Li_{j-1} is still in LDS), applies block j-1 to T(j+1, j)
+//     and T(j+1, j+1), then follows the factor pair by pair: the panel L(j+1, j) by forward substitution and the
+//     block j update of T(j+1, j+1), which it keeps in its registers and factors at step j+1. At the same time waves
+//     1-2 fetch tile row j+2 (T(j+2, j-1..j+2), handed over by its owner through column block j-2, plus the owner's
+//     panel L(j+2, j-2)) while wave 3 publishes the previous step's L tiles and Li; then wave 1 forms the panel
+//     L(j+2, j-1), wave 2 applies the block j-2 update of T(j+2, j+1) that the owner leaves out, and the two waves
+//     apply block j-1 to T(j+2, j) and the lower half of T(j+2, j+2) (wave 1), T(j+2, j+1) and the rest (wave 2).
 //   * Tile row i >= 4 is owned for the whole factorisation, in LDS, by ceil((i + 1) / OWNER_W) workgroups (parts),
 //     each holding a run of its tiles. For column block j = 0..i-4 in order: panel L(i, j) = T(i, j) Li_j^T
 //     (published by the part holding T(i, j)), then T(i, k) -= L(i, j) L(k, j)^T for each part's k = j+1..i with the
@@ -798,36 +798,6 @@ __device__ __forceinline__ void panel32x2(Tile& outA, const Tile& inA, Tile& out
     __syncthreads();
 }
 
-// Two panels in place: A = A Li^T, B = B Li^T (every operand is read before the first write)
-__device__ __forceinline__ void panel32x2_inplace(Tile& A, Tile& B, const Tile& li, bool on = true) {
-    WAVE_COORDS;
-    f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
-    if (on) {
-        float xa[8], xb[8], lv[8];
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            xa[kk] = A[16 * bi + l16][4 * kk + lk];
-            xb[kk] = B[16 * bi + l16][4 * kk + lk];
-            lv[kk] = li[16 * bj + l16][4 * kk + lk];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-            if (kk < 4 * (bj + 1)) {
-                a = mfma(xa[kk], lv[kk], a);
-                c = mfma(xb[kk], lv[kk], c);
-            }
-    }
-    __syncthreads();
-    if (on)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            A[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
-            B[16 * bi + 4 * lk + v][16 * bj + l16] = c[v];
-        }
-    __syncthreads();
-}
-
 // quadrant masks: the row half h of the A operand (bi = h) and the row half of the B operand (bj = h) that a set of
 // 16x16 quadrants qd = 2 bi + bj uses
 constexpr bool qm_uses_a(int qm, int h) { return (qm >> (2 * h)) & 3; }
@@ -906,140 +876,6 @@ __device__ __forceinline__ void update32_wave_to(Tile& dst, const Tile& C, const
 template <bool LOWER>
 __device__ __forceinline__ void update32_wave(Tile& C, const Tile& Pi, const Tile& Pk) {
     update32_wave_q<LOWER ? 0xD : 0xF>(C, C, Pi, Pk);
-}
-
-// Wave 0 only: factor the 32x32 tile D (lower part) and invert the factor in one pass (chol.cu:131-168).
-// Lanes 0..31 hold row i of D; lanes 32..63 start from column kk of the identity (from the LDS tile `id`), which
-// becomes column kk of the inverse. Column c: piv = fmaxf(D_cc, tau) and q = rsqrt(piv) are uniform; every lane
-// forms own = R[c] q, which is l_i = D_ic q on a factor lane below the diagonal and x_c = acc_c q on an inverse lane
-// (exactly +0 while c < kk: those registers stay +0). The factor's diagonal entry is piv q, which differs from
-// R[c] q only when the pivot was clamped; it is used nowhere but the output, so it is recorded in pq[c] and patched
-// in at the end (a factor lane above the diagonal computes values that only its own dead upper-triangle registers
-// see). Both halves run the same rank-1 updates R[k] = fma(-own_c, l_k, R[k]), k > c: the factor's trailing update
-// D_ik -= l_i l_k and the inverse's forward substitution acc_k -= L_kc x_c, each element's chain in column order.
-//
-// Schedule (a single wavefront issues in order, so the work that does not feed the next pivot is placed in the gaps
-// of the pivot chain): each lane keeps its diagonal element also in dg (the same fmas as R[lane]: l_lane is the lane's
-// own value), so the pivot chain dn = fma(-own, own, dg) -> fmaxf -> rsqrt -> v_readlane touches no memory. Column
-// c's values reach the other lanes through LDS (96 floats per column: lane i writes at 28 - c + i, so l_{c+4} lands
-// on the aligned bl + 32, alternating between bl0 and bl1), are read back during column c+1 and applied during column
-// c+2 to the elements k >= c+5, interleaved with that column's pivot chain. Elements c+1 and c+2 are needed within two
-// columns; at column c, element c+2 takes column c-2's update (from the same LDS values), then column c-1's and
-// column c's through v_readlane, and element c+1 column c's; so every element still gets its updates in column order.
-// Writes the factor to dl (the upper triangle is left unspecified: publishers zero it) and the inverse to Li, and the
-// inverse also to global memory at gli (row stride 32; the stores are left in flight).
-__device__ __forceinline__ void factor_inv32(float* bl0, float* bl1, float* pq, const Tile& id, const Tile& D,
-                                             float tau, Tile& dl, Tile& Li, float* gli) {
-    const int lane = threadIdx.x & 63, i = lane & 31;
-    const bool fl = lane < 32;
-    const float* src = fl ? &D[i][0] : &id[i][0];
-    float R[CB];
-#pragma unroll
-    for (int k = 0; k < CB; ++k) R[k] = src[k];
-    float dg = src[i];
-    const float pl = fmaxf(R[0], tau);         // lane 0's value is the first pivot
-    float q = readlane(rsqrt_sw(pl), 0);
-    float piv = readlane(pl, 0);
-    float own_m1 = 0.0f, own_m2 = 0.0f;        // own of columns c-1 and c-2
-    float rl_m1 = 0.0f;                        // l_{c+2} of column c-1 (v_readlane of lane c+2)
-    float lbA[CB], lbB[CB];                    // LDS values of columns c-2 (in use) and c-1 (being read), by parity
-#pragma unroll
-    for (int c = 0; c < CB; ++c) {
-        float* lb = (c & 1) ? lbB : lbA;       // column c-2's l_k at lb[k - c - 2]
-        float* lbn = (c & 1) ? lbA : lbB;      // column c-1's l_k at lbn[k - c - 3]
-        const float own = R[c] * q;
-        pq[c] = piv * q;
-        R[c] = own;
-        if (c >= 1 && c + 3 < CB) {            // read column c-1's values (k >= c+3) back; used at column c+1
-            const float* src4 = ((c - 1) & 1 ? bl1 : bl0) + 32;
-#pragma unroll
-            for (int kq = 0; 4 * kq < CB - 3 - c; ++kq) {
-                const float4 l4 = *reinterpret_cast<const float4*>(&src4[4 * kq]);
-                lbn[4 * kq + 0] = l4.x;
-                lbn[4 * kq + 1] = l4.y;
-                lbn[4 * kq + 2] = l4.z;
-                lbn[4 * kq + 3] = l4.w;
-            }
-        }
-        // bulk: column c-2's update of the elements k >= c+3, spread over the pivot chain's steps
-        constexpr int NSTEP = 14;
-        auto bulk = [&](int g) {
-            if (c >= 2) {
-                const int nbk = CB - 3 - c;
-                const int per = (nbk + NSTEP - 1) / NSTEP;
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int t = g * per + u;
-                    if (u < per && t < nbk) {
-                        const int k = c + 3 + t;
-                        R[k] = __builtin_fmaf(-own_m2, lb[k - c - 2], R[k]);
-                    }
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        float qn = 0.0f, pivn = 0.0f;
-        __builtin_amdgcn_sched_barrier(0);
-        if (c + 1 < CB) {
-            // the pivot chain of column c+1, written out step by step (rsqrt_sw's operations in its order)
-            const float dn = __builtin_fmaf(-own, own, dg);
-            __builtin_amdgcn_sched_barrier(0);
-            bulk(0);
-            const float pn = fmaxf(dn, tau);
-            __builtin_amdgcn_sched_barrier(0);
-            bulk(1);
-            float y = __uint_as_float(0x5f375a86u - (__float_as_uint(pn) >> 1));
-            const float h = 0.5f * pn;
-            __builtin_amdgcn_sched_barrier(0);
-            bulk(2);
-#pragma unroll
-            for (int it = 0; it < 3; ++it) {
-                float t = h * y;
-                __builtin_amdgcn_sched_barrier(0);
-                bulk(3 + 3 * it);
-                t = __builtin_fmaf(-t, y, 1.5f);
-                __builtin_amdgcn_sched_barrier(0);
-                bulk(4 + 3 * it);
-                y = y * t;
-                __builtin_amdgcn_sched_barrier(0);
-                bulk(5 + 3 * it);
-            }
-            qn = readlane(y, c + 1);
-            pivn = readlane(pn, c + 1);
-            dg = dn;
-            __builtin_amdgcn_sched_barrier(0);
-            bulk(12);
-            bulk(13);
-        } else {
-            bulk(0);
-        }
-        // element c+2: columns c-2, c-1 and c; element c+1: column c
-        if (c + 2 < CB) {
-            if (c >= 2) R[c + 2] = __builtin_fmaf(-own_m2, lb[0], R[c + 2]);
-            if (c >= 1) R[c + 2] = __builtin_fmaf(-own_m1, rl_m1, R[c + 2]);
-            R[c + 2] = __builtin_fmaf(-own, readlane(own, c + 2), R[c + 2]);
-        }
-        if (c + 1 < CB) R[c + 1] = __builtin_fmaf(-own, readlane(own, c + 1), R[c + 1]);
-        if (c + 3 < CB) rl_m1 = readlane(own, c + 3);
-        if (c + 4 < CB) ((c & 1) ? bl1 : bl0)[28 - c + lane] = own;
-        own_m2 = own_m1;
-        own_m1 = own;
-        piv = pivn;
-        q = qn;
-    }
-    __builtin_amdgcn_wave_barrier();
-    if (!fl) {   // the inverse, row-major (row stride 32) from its column lanes, to gli for the other workgroups
-#pragma unroll
-        for (int k = 0; k < CB; ++k) gli[k * CB + i] = R[k];
-    }
-    float* dst = fl ? &dl[i][0] : &Li[0][i];
-    const int step = fl ? 1 : TS;
-#pragma unroll
-    for (int k = 0; k < CB; ++k) dst[k * step] = R[k];
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
-    if (fl) dl[i][i] = pq[i];
-    __builtin_amdgcn_wave_barrier();
 }
 
 // Poll an agent-scope flag until it holds `ep` (bounded), then acquire. Called by one lane.
@@ -1134,7 +970,167 @@ __device__ __forceinline__ void wait_lds(const uint32_t* word, uint32_t target, 
     __builtin_amdgcn_wave_barrier();
 }
 
-constexpr int CH_WG0_TILES = 24;   // workgroup 0: D[2], X1, R2[2][5], dl[2], li[2], P1[2], P2[2], C2[2], id
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// The v_mfma_f32_32x32x2_f32 accumulator layout of a 32x32 tile: lane l, register v holds element (m, n) with
+// m = 8 (v >> 2) + 4 (l >> 5) + (v & 3), n = l & 31. A symmetric tile loaded from its lower triangle, and a tile's
+// transpose:
+__device__ __forceinline__ void load_sym(f32x16& C, const Tile& T) {
+    const int lane = threadIdx.x & 63, h = lane >> 5, n = lane & 31;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int m = 8 * (v >> 2) + 4 * h + (v & 3);
+        C[v] = m >= n ? T[m][n] : T[n][m];
+    }
+}
+__device__ __forceinline__ void load_tr(f32x16& C, const Tile& T) {
+    const int lane = threadIdx.x & 63, h = lane >> 5, n = lane & 31;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) C[v] = T[n][8 * (v >> 2) + 4 * h + (v & 3)];
+}
+
+// Tile factor of diagonal step j (chol.cu:131-168), every trailing update on the matrix cores, by one wavefront. C
+// holds T(j, j) through block j-1 in the accumulator layout (kept whole and symmetric: element (m, n) and (n, m)
+// receive the same operations, so row c -- register v(c) = 4 (c >> 3) + (c & 3) on the lanes of half (c >> 2) & 1 --
+// is also column c). Columns go in pairs (c, c+1): pivot c from the diagonal element (piv = fmaxf(d, tau),
+// q = rsqrt(piv); a NaN pivot becomes tau), L's column c = row c times q; the second pivot from scalars
+// (s = L(c+1, c), d' = fma(-s, s, C(c+1, c+1)), the operations that give lane c+1 of a per-row factor its own
+// values), row c+1 takes column c's update on the VALU; the two columns become one MFMA operand (lanes 0-31 column c,
+// 32-63 column c+1: one cross-half swap) and a single 32x32x2 MFMA applies both columns to the whole tile, k = c then
+// c+1: every element receives its updates in column order (an MFMA rounds each k step like a sequential fmaf). The
+// inverse's accumulator W (from the identity) takes the same column pairs against its rows X_c = W_c q_c (W_{c+1}
+// first updated by X_c): the forward substitution x = (delta - sum_m L_im x_m) q_i, column by column. Elements of
+// finished rows and columns take further updates that nothing reads. Outputs: L(j, j) to dl (upper triangle
+// unspecified, diagonal piv q patched in at the end), the inverse to Li and to gli (row stride 32), pq[c] = piv q;
+// per pair p, for the wavefront that forms the panel below (row_pairs): L's two columns in dl, fq[4p..4p+2] =
+// q_c, q_{c+1}, L(c+1, c), and then the LDS word fcnt = base + p + 1 (a plain store after them: one wavefront's LDS
+// operations complete in issue order). Global stores are left in flight.
+__device__ __forceinline__ void factor_pairs(f32x16& C, float* pq, float* fq, uint32_t* fcnt, uint32_t base, float tau,
+                                             Tile& dl, Tile& Li, float* gli) {
+    const int lane = threadIdx.x & 63, h = lane >> 5, n = lane & 31;
+    f32x16 W;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) W[v] = (8 * (v >> 2) + 4 * h + (v & 3)) == n ? 1.0f : 0.0f;
+#pragma unroll
+    for (int p = 0; p < CB / 2; ++p) {
+        const int c = 2 * p;
+        const int v0 = 4 * (c >> 3) + (c & 3), hh = (c >> 2) & 1, lc = c + 32 * hh;   // row c: register, half, lane
+        const bool mine = h == hh;
+        const float x = readlane(C[v0], lc + 1), y = readlane(C[v0 + 1], lc + 1);
+        const float pn0 = fmaxf(readlane(C[v0], lc), tau);
+        const float q0 = rsqrt_sw(pn0);
+        const float s = x * q0;                          // L(c+1, c)
+        const float pn1 = fmaxf(__builtin_fmaf(-s, s, y), tau);
+        const float q1 = rsqrt_sw(pn1);
+        const float Lc = C[v0] * q0;
+        const float cu = __builtin_fmaf(-Lc, s, C[v0 + 1]);   // row c+1 by column c (lanes of half hh only: the
+        C[v0 + 1] = mine ? cu : C[v0 + 1];                    // other half of the register holds another row)
+        const float Lc1 = C[v0 + 1] * q1;
+        const auto la = __builtin_amdgcn_permlane32_swap(__float_as_uint(Lc), __float_as_uint(Lc1), false, false);
+        const float a = __uint_as_float(hh == 0 ? la[0] : la[1]);    // lane l: L(l & 31, c + (l >> 5))
+        C = mfma32(-a, a, C);
+        const float Xc = W[v0] * q0;
+        const float wu = __builtin_fmaf(-Xc, s, W[v0 + 1]);
+        W[v0 + 1] = mine ? wu : W[v0 + 1];
+        const float Xc1 = W[v0 + 1] * q1;
+        const auto lx = __builtin_amdgcn_permlane32_swap(__float_as_uint(Xc), __float_as_uint(Xc1), false, false);
+        const float bx = __uint_as_float(hh == 0 ? lx[0] : lx[1]);   // lane l: X(c + (l >> 5), l & 31)
+        W = mfma32(-a, bx, W);
+        dl[n][c + h] = a;
+        Li[c + h][n] = bx;
+        gli[(c + h) * CB + n] = bx;
+        if (lane == 0) {
+            pq[c] = pn0 * q0;
+            pq[c + 1] = pn1 * q1;
+            fq[4 * p] = q0;
+            fq[4 * p + 1] = q1;
+            fq[4 * p + 2] = s;
+            asm volatile("" ::: "memory");
+            __hip_atomic_store(fcnt, base + p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    if (lane < CB) dl[lane][lane] = pq[lane];
+    __builtin_amdgcn_wave_barrier();
+}
+
+// The look-ahead of step j on tile row j+1, by a second wavefront: C = T(j+1, j+1) and T2 = the transpose of
+// T(j+1, j) through block j-1 from the tiles Dt = T(j+1, j+1) (lower triangle) and Xt = T(j+1, j) through block
+// j-2 and the panels P2 = L(j+1, j-1), P1 = L(j, j-1) (chol.cu:182-271's trailing update, each element an fmaf
+// chain over the 32 columns in order: C(m, n) -= P2(m, c) P2(n, c), T2(m, n) -= P1(m, c) P2(n, c), two columns per
+// 32x32x2 MFMA).
+__device__ __forceinline__ void row_setup(f32x16& C, f32x16& T2, const Tile& Dt, const Tile& Xt, const Tile& P2,
+                                          const Tile& P1) {
+    const int lane = threadIdx.x & 63, h = lane >> 5, n = lane & 31;
+    load_sym(C, Dt);
+    load_tr(T2, Xt);
+#pragma unroll
+    for (int k = 0; k < CB / 2; ++k) {
+        const float v2 = P2[n][2 * k + h], v1 = P1[n][2 * k + h];
+        C = mfma32(-v2, v2, C);
+        T2 = mfma32(-v1, v2, T2);
+    }
+}
+
+// Then the panel L(j+1, j) by forward substitution beside the tile factor (row c of T2 times q_c after the updates
+// by columns < c: the pair's first column on the VALU, then both by one MFMA against L's column pair), and C takes
+// the panel's column pairs -- the look-ahead update T(j+1, j+1) -= L(j+1, j) L(j+1, j)^T -- so that on return C holds
+// T(j+1, j+1) through block j, the next step's tile. Pair k's operands are read one pair ahead together with the
+// factor's word fcnt (read first: the factor stores a pair's operands before raising fcnt to base + k + 1, and one
+// wavefront's LDS operations complete in issue order); if that word shows them not yet there, the wavefront polls
+// (bounded) and reads them again. Outputs: L(j+1, j) to P1 and to gP1 (row stride ldg); global stores are left in
+// flight.
+__device__ __forceinline__ void row_pairs(f32x16& C, f32x16& T2, const float* fq, const uint32_t* fcnt, uint32_t base,
+                                          const Tile& dl, Tile& P1, float* gP1, long ldg, uint32_t* err, bool& dead,
+                                          uint32_t lim) {
+    const int lane = threadIdx.x & 63, h = lane >> 5, n = lane & 31;
+    uint32_t polls = 0;
+    uint32_t got;
+    float an;
+    float4 fn;
+    auto fetch = [&](int k) {
+        got = __hip_atomic_load(fcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        asm volatile("" ::: "memory");
+        an = dl[n][2 * k + h];
+        fn = *reinterpret_cast<const float4*>(fq + 4 * k);
+    };
+    fetch(0);
+#pragma unroll
+    for (int k = 0; k < CB / 2; ++k) {
+        const int c = 2 * k, v0 = 4 * (c >> 3) + (c & 3), hh = (c >> 2) & 1;
+        const bool mine = h == hh;
+        if (__builtin_amdgcn_readfirstlane(got) < base + k + 1) {
+            while (!dead && __builtin_amdgcn_readfirstlane(__hip_atomic_load(fcnt, __ATOMIC_ACQUIRE,
+                                                                             __HIP_MEMORY_SCOPE_WORKGROUP)) <
+                                base + k + 1) {
+                if (++polls > lim) {
+                    if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    dead = true;
+                }
+            }
+            fetch(k);
+        }
+        const float a = an;                              // lane l: L(l & 31, c + (l >> 5))
+        const float q0 = fn.x, q1 = fn.y, s = fn.z;
+        if (k + 1 < CB / 2) fetch(k + 1);
+        const float l0 = T2[v0] * q0;
+        const float tu = __builtin_fmaf(-l0, s, T2[v0 + 1]);
+        T2[v0 + 1] = mine ? tu : T2[v0 + 1];
+        const float l1 = T2[v0 + 1] * q1;
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l0), __float_as_uint(l1), false, false);
+        const float b2 = __uint_as_float(hh == 0 ? sw[0] : sw[1]);   // lane l: L(j+1, j)(l & 31, c + (l >> 5))
+        T2 = mfma32(-a, b2, T2);
+        C = mfma32(-b2, b2, C);
+        P1[n][c + h] = b2;
+        gP1[(size_t)n * ldg + c + h] = b2;
+    }
+}
+
+constexpr int CH_WG0_TILES = 23;   // workgroup 0: D[2], X1, R2[2][5], dl[2], li[2], P1[2], P2[2], C2[2]
 // Owner parts: tile row i (i + 1 tiles) is split over P = ceil((i + 1) / w) workgroups, each holding a run of
 // consecutive tiles T(i, s..e-1): widths floor((i + 1) / P), the last (i + 1) % P parts one wider, so that for
 // w >= 6 the last part (which holds T(i, i-3..i) and hands them to workgroup 0) has at least 4 tiles for every row
@@ -1177,8 +1173,8 @@ struct CholWG0 {
     Tile P1[2];     // L(j+1, j)
     Tile P2[2];     // L(j+2, j)
     Tile C2[2];     // L(j+2, j-1) (the catch-up panel of row j+2)
-    Tile id;        // identity (the tile factor's inverse lanes start from it)
 };
+static_assert(sizeof(CholWG0) == CH_WG0_TILES * sizeof(Tile), "workgroup 0's tiles");
 
 size_t chol_lds_bytes(int r, int w) {
     const int owner_tiles = owner_lds_tiles(r / CB, w);
@@ -1192,11 +1188,16 @@ size_t chol_lds_bytes(int r, int w) {
 // shift = alpha * nrm added to the diagonal after the first load, tau = tau_rel * nrm + 1e-30 (kcholqr.py:107-109).
 // flags: [nb * nb] panel flags (L(i, j) published; (j, j): L(j, j) and Li_j), [nb] hand-over flags (tile row i),
 // [64] per-workgroup call counters. STAMP: workgroup 0 records wall_clock64() at 1 + 4j + s for step j: s = 0 step
-// start, 1 tile factored and row j+2 fetched, 2 look-ahead done, 3 wave 0's tile factor done; slot 0 is the kernel
-// start, 1 + 4 nb the end; 2 + 4 nb + j: wave 1's row work of step j done; 2 + 5 nb + j: wave 3's done.
-// Workgroups of eight wavefronts: waves 0-3 do the work described here (and wave 7 of workgroup 0 the L(j+1, j-1)
-// above); waves 4-7 share the owners' row update with them (two wavefronts per SIMD there, so one's LDS traffic
-// overlaps the other's MFMA chain) and otherwise only pass the same workgroup barriers.
+// start, 1 step end, 2 look-ahead done, 3 tile factor done; slot 0 is the kernel start, 1 + 4 nb the end;
+// 2 + 4 nb + j: wave 1's row work of step j done; 2 + 5 nb + j: wave 3's done; 2 + 6 nb + j: the hand-over of row j+2
+// seen; 2 + 7 nb + j: row j+2 fetched; 2 + 8 nb + j: its panel L(j+2, j-1) formed; 2 + 9 nb + j: wave 2 done;
+// 2 + 10 nb + 6 i + s: the owner of row i's last part at its last block: s = 0 block published, 1 operands loaded,
+// 2 own panel published, 3 row handed over, 4 update done, 5 hand-over stores done; 2 + 16 nb + 8 j + s: the last
+// row's last part at block j: s = 0 block published, 1 operands loaded, 2 own panel published, 3 panel L(j+2, j)
+// formed, 4 early tiles updated, 5 other panels' flags seen, 6 other panels loaded, 7 block done.
+// Workgroups of eight wavefronts: waves 0-3 do the work described here (and wave 7 of workgroup 0 its turns at the
+// tile factor and the look-ahead); waves 4-7 share the owners' row update with them (two wavefronts per SIMD there,
+// so one's LDS traffic overlaps the other's MFMA chain) and otherwise only pass the same workgroup barriers.
 // colcnt (may be null): per column block k, a counter (stride CC_STRIDE) that every producer of the packed operands
 // of column k (Li_k and L(i, k), i > k) raises once those are released, for the solve that runs in the same launch:
 // owner i credits column j-1 when it publishes L(i, j) and column i-4 when it hands its row over; workgroup 0 credits
@@ -1237,8 +1238,9 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
     bool dead = false;
     if (STAMP && b == 0 && tid == 0) stamps[0] = wall_clock64();
     const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
-    // misc: [0..2] nrm, shift, tau; [4] the waves 1-2 barrier counter; [5] the last step whose L(j+2, j) is formed; [32..63] the tile factor's diagonal;
-    // [64..159] and [160..255] tile-factor broadcast buffers
+    // misc: [0..2] nrm, shift, tau; workgroup 0's LDS words: [4] the waves 1-2 barrier counter, [5] the last step
+    // whose L(j+2, j) is formed, [7] the tile factor's pairs done; [32..63] the tile factor's diagonal (piv q),
+    // [64..127] its per-pair scalars
     float* misc = reinterpret_cast<float*>(chol_lds);
     Tile* tiles = reinterpret_cast<Tile*>(misc + 256);
     // an owner part: tile row oi, tiles T(oi, os..oe-1)
@@ -1257,10 +1259,6 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                                      [&](int q) { return A + (size_t)CB * oi * r + (size_t)CB * (os + q); });
         }
     }
-    if (w == 3 && b == 0) {
-        Tile& id = reinterpret_cast<CholWG0*>(tiles)->id;
-        for (int e = lane; e < CB * CB; e += 64) id[e >> 5][e & 31] = ((e >> 5) == (e & 31)) ? 1.0f : 0.0f;
-    }
     if (w == 0) {
         // lane sums in index order, the partials loaded eight at a time (one memory latency per eight)
         double s = 0.0;
@@ -1276,6 +1274,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         if (lane == 0) {
             reinterpret_cast<uint32_t*>(misc)[4] = 0u;
             reinterpret_cast<uint32_t*>(misc)[5] = 0u;
+            reinterpret_cast<uint32_t*>(misc)[7] = 0u;
             if (nnp > 0) {
                 const float nrm = sqrtf((float)s);
                 misc[0] = nrm;
@@ -1300,8 +1299,6 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
     }
     __syncthreads();
     float* pq = misc + 32;
-    float* bl0 = misc + 64;
-    float* bl1 = misc + 160;
 
     if (b == 0) {
         if (tid == 0 && scal != nullptr) {
@@ -1313,12 +1310,13 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         uint32_t* p2done = reinterpret_cast<uint32_t*>(misc + 5);   // L(j+2, j) of step j formed: j + 1 (zeroed above)
         uint32_t n12 = 0;
         // wave 3: publish L(j, j), Li_j, L(j+1, j), L(j+2, j) of step j (parity q = j & 1)
-        // What the owners need for column block j -- Li_j (into its place in Li), T(j+1, j) and T(j+2, j) through
-        // block j-1 (into the slots (j+1..j+2, j) of A, which nothing reads any more: rows j+1 and j+2 were fetched
-        // at steps j-1 and j; rows 1 and 2 are still the Gram's there at step 0) -- is stored by the wave that
-        // finishes it during step j (wave 0: Li_j; wave 3: T(j+1, j); wave 1: T(j+2, j)) and completed before the
-        // look-ahead's last barrier. Wave 3, at the start of step j+1: release them, then the outputs of step j
-        // (L(j, j), L(j+1, j), L(j+2, j) and the packed forms), which only later kernels read.
+        // What the owners need for column block j -- Li_j (into its place in Li), the panel L(j+1, j) (into its
+        // place in L) and T(j+2, j) through block j-1 (into the slot (j+2, j) of A, which nothing reads any more:
+        // row j+2 was fetched at step j; row 2 is still the Gram's there at step 0) -- is stored by the wave that
+        // finishes it during step j (the factor's wavefront: Li_j; the look-ahead's: L(j+1, j); wave 1: T(j+2, j))
+        // and completed before the
+        // step's last barrier. Wave 3, at the start of step j+1: release them, then the outputs of step j (L(j, j),
+        // L(j+2, j) and the packed forms), which only later kernels read.
         auto publish = [&](int j) {
             const int q = j & 1;
             const size_t o = (size_t)CB * j;
@@ -1329,20 +1327,28 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 if (j >= 1 && j < nb - 1) credit(colcnt, j - 1);
             }
             store_tile_lower(L + o * r + o, r, z.dl[q], false, lane, 64);
-            if (j + 1 < nb) store_tile(L + (o + CB) * r + o, r, z.P1[q], lane, 64);
             store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[q], lane, 64);
             if (j + 1 < nb) store_tile_op(Lp + (size_t)op_pair(j + 1, j) * CB * CB, z.P1[q], lane, 64);
             if (j + 2 < nb) {
-                wait_lds(p2done, (uint32_t)j + 1, err, dead, lim);   // L(j+2, j), formed by wave 7
+                wait_lds(p2done, (uint32_t)j + 1, err, dead, lim);   // L(j+2, j), formed by the look-ahead
                 store_tile(L + (o + 2 * CB) * r + o, r, z.P2[q], lane, 64);
                 store_tile_op(Lp + (size_t)op_pair(j + 2, j) * CB * CB, z.P2[q], lane, 64);
             }
         };
+        // Waves 0 and 7 take turns: at step j one factors T(j, j) (wave 0 at even j), the other forms tile row j+1's
+        // look-ahead beside it and so ends the step holding T(j+1, j+1) through block j -- the next step's tile, in
+        // the registers of the wavefront that factors it.
+        float* fq = misc + 64;                                      // per pair: q_c, q_{c+1}, L(c+1, c)
+        uint32_t* fcnt = reinterpret_cast<uint32_t*>(misc + 7);     // the factor's pairs done: 16 j + p + 1
+        f32x16 C;                                                   // T(j, j) (factor) or T(j+1, j+1) (look-ahead)
+        if (w == 0) load_sym(C, z.D[0]);
         for (int j = 0; j < nb; ++j) {
             const int p = j & 1, pp = p ^ 1;
+            const int wf = p ? 7 : 0, wr = 7 - wf;                  // this step's factor and look-ahead wavefronts
+            const uint32_t fbase = (uint32_t)(CB / 2) * j;
             if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
-            if (w == 0) {
-                factor_inv32(bl0, bl1, pq, z.id, z.D[p], tau, z.dl[p], z.li[p], Li + (size_t)CB * j * CB);
+            if (w == wf) {
+                factor_pairs(C, pq, fq, fcnt, fbase, tau, z.dl[p], z.li[p], Li + (size_t)CB * j * CB);
                 if (STAMP && lane == 0) stamps[4 + 4 * j] = wall_clock64();
                 if (colcnt != nullptr && j == nb - 1) {
                     // the last column of the factor is Li_{nb-1} alone: packed, released and credited at once
@@ -1350,13 +1356,29 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     release();
                     if (lane == 0) credit(colcnt, j);
                 }
+                __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this step's Li_j stored
+            } else if (w == wr && j + 1 < nb) {
+                f32x16 T2;
+                if (j == 0) {
+                    load_sym(C, z.D[1]);
+                    load_tr(T2, z.X1);
+                } else {
+                    // L(j+1, j-1) = T(j+1, j-1) Li_{j-1}^T (row j+1 as fetched at step j-1), for waves 2 and 3; then
+                    // block j-1 on T(j+1, j+1) and T(j+1, j)
+                    panel32_wave(z.P2[pp], z.R2[pp][1], z.li[pp]);
+                    if (lane == 0)
+                        __hip_atomic_store(p2done, (uint32_t)j, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    row_setup(C, T2, z.R2[pp][3], z.R2[pp][2], z.P2[pp], z.P1[pp]);
+                }
+                row_pairs(C, T2, fq, fcnt, fbase, z.dl[p], z.P1[p], L + (size_t)CB * (j + 1) * r + CB * j, r, err,
+                          dead, lim);
+                if (STAMP && lane == 0) stamps[3 + 4 * j] = wall_clock64();
+                __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this step's L(j+1, j) stored
             } else if (w < 4) {
-                // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p]. Wave 3
-                // publishes the previous step, then applies the part of the previous step's look-ahead that this
-                // step's factor does not need: block j-1 on T(j+1, j) (into X1) and T(j+1, j+1) (into D[pp]), from
-                // row j+1 as R2[pp] holds it. Waves 1-2 fetch row j+2; then L(j+2, j-1) (wave 1) and the block j-2
-                // update of T(j+2, j+1) that its owner left (wave 2); then block j-1 on T(j+2, j) and the lower
-                // half of T(j+2, j+2) (wave 1) and on T(j+2, j+1) and T(j+2, j+2)'s quadrant (0, 0) (wave 2).
+                // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p].
+                // Wave 3 publishes the previous step. Waves 1-2 fetch row j+2; then L(j+2, j-1) (wave 1) and the
+                // block j-2 update of T(j+2, j+1) that its owner left (wave 2); then block j-1 on T(j+2, j) and the
+                // lower half of T(j+2, j+2) (wave 1) and on T(j+2, j+1) and T(j+2, j+2)'s quadrant (0, 0) (wave 2).
                 Tile* R2 = z.R2[p];
                 const bool row2 = j + 2 < nb;
                 if (w == 3) {
@@ -1364,12 +1386,6 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     if (colcnt != nullptr && j == nb - 1) {   // column nb-2's operands, stored just now
                         release();
                         if (lane == 0) credit(colcnt, nb - 2);
-                    }
-                    if (j >= 1 && j + 1 < nb) {
-                        const Tile* R1 = z.R2[pp];
-                        update32_wave_to<false>(z.X1, R1[2], z.P2[pp], z.P1[pp]);      // T(j+1, j)
-                        store_tile(A + (size_t)CB * (j + 1) * r + CB * j, r, z.X1, lane, 64);
-                        update32_wave_to<true>(z.D[pp], R1[3], z.P2[pp], z.P2[pp]);    // T(j+1, j+1)
                     }
                     if (STAMP && lane == 0) stamps[2 + 5 * nb + j] = wall_clock64();
                 } else if (row2) {
@@ -1381,18 +1397,21 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                                            [&](int q) { return rowp + CB * (j - 1 + t0 + q); });
                     } else {
                         if (lane == 0) wait_flag(flagT + i2, ep, err, dead, lim);
+                        if (STAMP && w == 1 && lane == 0) stamps[2 + 6 * nb + j] = wall_clock64();
                         __builtin_amdgcn_wave_barrier();
                         const float* hp = L + (size_t)CB * i2 * r + (size_t)CB * (j - 2);     // into R2[4] = H
                         load_tiles<5, 128>(&R2[0], 5, r, 0u, 0.f, wl,
                                            [&](int q) { return q < 4 ? rowp + CB * (j - 1 + q) : hp; });
                     }
                     wave_group_barrier(bar12, 2 * ++n12, err, dead, lim);
+                    if (STAMP && w == 1 && lane == 0) stamps[2 + 7 * nb + j] = wall_clock64();
                     if (j >= 1) {
                         if (w == 1)
                             panel32_wave(z.C2[p], R2[0], z.li[pp]);                    // L(j+2, j-1)
                         else if (j >= 2)
                             update32_wave<false>(R2[2], R2[4], z.C2[pp]);      // T(j+2, j+1), block j-2 (owner skips it)
                         wave_group_barrier(bar12, 2 * ++n12, err, dead, lim);
+                        if (STAMP && w == 1 && lane == 0) stamps[2 + 8 * nb + j] = wall_clock64();
                         if (w == 1) {
                             update32_wave<false>(R2[1], z.C2[p], z.P1[pp]);            // T(j+2, j), block j-1
                             store_tile(A + (size_t)CB * (j + 2) * r + CB * j, r, R2[1], lane, 64);
@@ -1405,29 +1424,17 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                             const size_t o = (size_t)CB * (j - 1);
                             store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
                             store_tile_op(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], lane, 64);
+                            if (STAMP && lane == 0) stamps[2 + 9 * nb + j] = wall_clock64();
                         }
                     }
                     if (STAMP && w == 1 && lane == 0) stamps[2 + 4 * nb + j] = wall_clock64();
                 }
-            } else if (w == 7 && j >= 1 && j + 1 < nb) {
-                // the previous step's L(j+1, j-1) = T(j+1, j-1) Li_{j-1}^T (row j+1 as fetched at step j-1), which
-                // only this step's waves 2 and 3 use: formed here, beside the factor, not in the look-ahead
-                panel32_wave(z.P2[pp], z.R2[pp][1], z.li[pp]);
-                if (lane == 0) __hip_atomic_store(p2done, (uint32_t)j, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
             __syncthreads();
-            // start the L2 write-back of this step's stores now (wave 7 has no part in the look-ahead); the
-            // publication at the next step's start then finds the lines clean
-            if (w == 7) asm volatile("buffer_wbl2 sc1" ::: "memory");
+            // start the L2 write-back of this step's stores now; the publication at the next step's start then
+            // finds the lines clean
+            if (w == 4) asm volatile("buffer_wbl2 sc1" ::: "memory");
             if (STAMP && tid == 0) stamps[2 + 4 * j] = wall_clock64();
-            // look-ahead, the part the next factor needs: L(j+1, j), then block j on T(j+1, j+1); L(j+2, j) is formed
-            // by wave 7 and block j on tile row j+2 applied by wave 3, both in the next step
-            const bool q4 = w < 4;
-            if (j + 1 < nb) {
-                panel32(z.P1[p], z.X1, z.li[p], q4);                           // L(j+1, j)
-                update32(z.D[pp], z.D[pp], z.P1[p], z.P1[p], true, q4);
-            }
-            if (STAMP && tid == 0) stamps[3 + 4 * j] = wall_clock64();
         }
         if (w == 3) publish(nb - 1);
         if (STAMP && tid == 0) stamps[1 + 4 * nb] = wall_clock64();
@@ -1451,19 +1458,27 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
             const bool q4 = w < 4;
             const bool mine = j >= s;                               // this part forms L(i, j)
             const bool h1 = j + 1 >= s && j + 1 < e, h2 = j + 2 >= s && j + 2 < e;
-            // workgroup 0's block j: Li_j into li; T(j+1, j) and T(j+2, j) (through block j-1), where they are in
+            // workgroup 0's block j: Li_j into li; L(j+1, j) and T(j+2, j) (through block j-1), where they are in
             // the part's columns, into their panel slots
+            const bool hst = STAMP && last && j + 4 == i && tid == 0;   // the hand-over block's stamps
+            const bool bst = STAMP && last && i == nb - 1 && tid == 0;  // the last row's stamps, every block
+            uint64_t* bs = stamps + 2 + 16 * nb + 8 * j;
             if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead, lim);
+            if (hst) stamps[2 + 10 * nb + 6 * i] = wall_clock64();
+            if (bst) bs[0] = wall_clock64();
             __syncthreads();
             if (q4)
                 load_tiles_to<3, 256>(1 + (h1 ? 1 : 0) + (h2 ? 1 : 0), tid,
                                       [&](int q) -> Tile& { return q == 0 ? li : pn[j + q + (h1 ? 0 : 1) - s]; },
                                       [&](int q) {
+                                          const int k = j + q + (h1 ? 0 : 1);
                                           return q == 0 ? Li + (size_t)CB * j * CB
-                                                        : A + (size_t)CB * (j + q + (h1 ? 0 : 1)) * r + (size_t)CB * j;
+                                                        : (k == j + 1 ? L : A) + (size_t)CB * k * r + (size_t)CB * j;
                                       },
                                       [&](int q) { return q == 0 ? CB : r; });   // Li_j's rows are 32 apart
             __syncthreads();
+            if (hst) stamps[3 + 10 * nb + 6 * i] = wall_clock64();
+            if (bst) bs[1] = wall_clock64();
             const Tile& lij = mine ? rt[j - s] : pin;
             if (mine) {
                 // panel L(i, j) = T(i, j) Li_j^T, published before anything else (so no row waits on a chain of rows)
@@ -1475,17 +1490,18 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     publish_flag(flagL + i * nb + j, ep);
                     if (j > s) credit(colcnt, j - 1);   // the release covers L(i, j-1)'s packed form, stored after it
                 }
+                if (hst) stamps[4 + 10 * nb + 6 * i] = wall_clock64();
+                if (bst) bs[2] = wall_clock64();
                 store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j - s]);   // for the solve only
             }
             // block j's panels of the part's rows between: L(k, j), k = j+1..i-1, each in LDS before the tile it
-            // updates. Rows j+1 and j+2 are workgroup 0's: their panels are formed here, as workgroup 0 forms them.
+            // updates. Rows j+1 and j+2 are workgroup 0's: L(j+1, j) comes finished; L(j+2, j) is formed here, as
+            // workgroup 0 forms it.
             // Row j+3 has just been handed to workgroup 0 (before block j; row 3 never had an owner): its panel too
             // is formed here, from the handed-over T(j+3, j). Rows j+4.. publish their own. At the last part's last
             // block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed.
-            if (h1 && h2)
-                panel32x2_inplace(pn[j + 1 - s], pn[j + 2 - s], li, q4);      // L(j+1, j), L(j+2, j)
-            else if (h1 || h2)
-                panel32(pn[j + (h1 ? 1 : 2) - s], pn[j + (h1 ? 1 : 2) - s], li, q4);
+            if (h2) panel32(pn[j + 2 - s], pn[j + 2 - s], li, q4);      // L(j+2, j)
+            if (bst) bs[3] = wall_clock64();
             const int ke = last ? (j + 4 == i ? i - 1 : i) : e;     // the part's columns k < i updated: [.., ke)
             const int k3 = j + 3 > s ? j + 3 : s;                   // [k3, ke): panels from global memory
             const int nr = ke > k3 ? ke - k3 : 0;
@@ -1550,6 +1566,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 const int a0 = h1 ? j + 1 : j + 2, nh = (h1 ? 1 : 0) + (h2 ? 1 : 0);
                 update_tiles(nh + (last && !upq ? 1 : 0), [&](int t) { return t < nh ? a0 + t : i; });
             }
+            if (bst) bs[4] = wall_clock64();
             // the other rows' panels (and L(i, j) when another part forms it): flags polled together, one batch of
             // loads
             if (w == 0) {
@@ -1563,6 +1580,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 wait_flags_wave(f, ep, err, dead, lim);
             }
             __syncthreads();
+            if (bst) bs[5] = wall_clock64();
             if (q4)
                 load_tiles_to<OWNER_WMAX + 1, 256>(nr + (mine ? 0 : 1), tid,
                                                 [&](int q) -> Tile& { return q < nr ? pn[k3 + q - s] : pin; },
@@ -1572,6 +1590,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                                                 },
                                                 [&](int) { return r; });
             __syncthreads();
+            if (bst) bs[6] = wall_clock64();
             if (j + 3 >= s && j + 3 < ke) panel32(pn[j + 3 - s], pn[j + 3 - s], li, q4);     // L(j+3, j)
             if (early) {
                 update_tiles(nr, [&](int t) { return k3 + t; });
@@ -1582,16 +1601,20 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 update_tiles(n, [&](int t) { return k0 + t < ke ? k0 + t : i; });
             }
             __syncthreads();
+            if (bst) bs[7] = wall_clock64();
             if (last && j + 4 == i) {
                 // hand T(i, i-3..i) to workgroup 0
+                if (hst) stamps[6 + 10 * nb + 6 * i] = wall_clock64();
                 for (int t = 0; t < 4; ++t)
                     store_tile(A + (size_t)CB * i * r + (size_t)CB * (i - 3 + t), r, rt[i - 3 + t - s]);
                 __builtin_amdgcn_s_waitcnt(0x0F70);
                 __syncthreads();
+                if (hst) stamps[7 + 10 * nb + 6 * i] = wall_clock64();
                 if (tid == 0) {
                     publish_flag(flagT + i, ep);
                     if (mine) credit(colcnt, j);   // L(i, i-4)'s packed form
                 }
+                if (hst) stamps[5 + 10 * nb + 6 * i] = wall_clock64();
             }
         }
         if (!last) {
@@ -3210,7 +3233,7 @@ size_t plan_layout(spanqr_plan* p, char* base) {
         al256(B * p->nnp * sizeof(double)),                     // npart
         al256(B * AMAX_BLOCKS * sizeof(uint32_t)),              // amax_part
         al256(B * BAR_STRIDE * sizeof(uint32_t)),               // bar
-        al256((6 * CH_MAXROW + 2) * sizeof(uint64_t)),          // stamps
+        al256((24 * CH_MAXROW + 2) * sizeof(uint64_t)),          // stamps
         al256(B * FLAG_STRIDE * sizeof(uint32_t)),              // flags
         al256(B * CC_STRIDE * CH_MAXROW * sizeof(uint32_t)),    // colcnt
     };
@@ -3669,10 +3692,10 @@ int spanqr_profile_chol(spanqr_plan* p, const float* G, const double* npart, flo
     hipStream_t st = (hipStream_t)stream;
     HIPCHK(hipMemcpyAsync(p->G, G, (size_t)p->r * p->r * sizeof(float), hipMemcpyDeviceToDevice, st));
     HIPCHK(hipMemcpyAsync(p->npart, npart, (size_t)p->nnp * sizeof(double), hipMemcpyDeviceToDevice, st));
-    HIPCHK(hipMemsetAsync(p->stamps, 0, (size_t)(6 * p->NB + 2) * sizeof(uint64_t), st));
+    HIPCHK(hipMemsetAsync(p->stamps, 0, (size_t)(24 * p->NB + 2) * sizeof(uint64_t), st));
     int rc = launch_chol(p, alpha, tau, p->chscal, st, p->nnp, 1, true);
     if (rc) return rc;
-    HIPCHK(hipMemcpyAsync(stamps_out, p->stamps, (size_t)(6 * p->NB + 2) * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipMemcpyAsync(stamps_out, p->stamps, (size_t)(24 * p->NB + 2) * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));
     int khz = 0;
     HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, p->device));
