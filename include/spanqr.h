@@ -136,11 +136,10 @@ int spanqr_profile_orth(spanqr_plan* plan, const float* X, long ldx, float* Q, l
  * end; [2 + 4 nb + j] tile row j+2's wavefronts done; [2 + 5 nb + j] the publishing wavefront done; [2 + 6 nb + j]
  * the hand-over of row j+2 seen; [2 + 7 nb + j] row j+2 fetched; [2 + 8 nb + j] its panel L(j+2, j-1) formed;
  * [2 + 9 nb + j] the second of row j+2's wavefronts done; for the owner of tile row i (its last part, at the
- * block before it hands the row over), [2 + 10 nb + 6i + s]: s = 0 block published, 1 operands loaded, 2 its own
- * panel published, 3 row handed over, 4 row updated, 5 hand-over stores done; for the last tile row's last part at
- * block j, [2 + 16 nb + 8j + s]: s = 0 block published, 1 operands loaded, 2 own panel published, 3 L(j+2, j) formed,
- * 4 early tiles updated, 5 other panels' flags seen, 6 other panels loaded, 7 block done; zero where a step has no
- * such work. *tick_ns: nanoseconds per wall-clock tick. The reference keeps similar
+ * block before it hands the row over), [2 + 10 nb + 6i + s]: s = 0 the block's flags seen, 1 operands loaded,
+ * 2 panels formed, 3 row handed over, 4 row updated, 5 hand-over stores done; for the last tile row's last part at
+ * block j, [2 + 16 nb + 8j + s]: s = 0 flags seen, 1 operands loaded, 2 panels formed, 3 block done, 4 the next
+ * block's tile published; zero where a step has no such work. *tick_ns: nanoseconds per wall-clock tick. The reference keeps similar
  * stamps behind a debug define (candidates/cuk/chol.cu:17-23). */
 int spanqr_profile_chol(spanqr_plan* plan, const float* G, const double* npart, float alpha, float tau,
                         unsigned long long* stamps_out, double* tick_ns, void* stream);

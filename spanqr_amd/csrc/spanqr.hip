@@ -593,10 +593,10 @@ __global__ __launch_bounds__(512) void k_gram32(const MatsIn As, long lda, int K
 //     look-ahead) forms the previous step's L(j+1, j-1) (Li_{j-1} is still in LDS), applies block j-1 to T(j+1, j)
 //     and T(j+1, j+1), then follows the factor pair by pair: the panel L(j+1, j) by forward substitution and the
 //     block j update of T(j+1, j+1), which it keeps in its registers and factors at step j+1. At the same time waves
-//     1-2 fetch tile row j+2 (T(j+2, j-1..j+2), handed over by its owner through column block j-2, plus the owner's
-//     panel L(j+2, j-2)) while wave 3 publishes the previous step's L tiles and Li; then wave 1 forms the panel
-//     L(j+2, j-1), wave 2 applies the block j-2 update of T(j+2, j+1) that the owner leaves out, and the two waves
-//     apply block j-1 to T(j+2, j) and the lower half of T(j+2, j+2) (wave 1), T(j+2, j+1) and the rest (wave 2).
+//     1, 2, 5, 6 fetch tile row j+2 (T(j+2, j-1..j+2), handed over by its owner through column block j-2, plus the
+//     owner's panel L(j+2, j-2)) while wave 3 publishes the previous step's L tiles and Li; then waves 1 and 5 form
+//     the panel L(j+2, j-1), waves 2 and 6 apply the block j-2 update of T(j+2, j+1) that the owner leaves out, and
+//     the four apply block j-1 to T(j+2, j), T(j+2, j+1) and the lower quadrants of T(j+2, j+2).
 //   * Tile row i >= 4 is owned for the whole factorisation, in LDS, by ceil((i + 1) / OWNER_W) workgroups (parts),
 //     each holding a run of its tiles. For column block j = 0..i-4 in order: panel L(i, j) = T(i, j) Li_j^T
 //     (published by the part holding T(i, j)), then T(i, k) -= L(i, j) L(k, j)^T for each part's k = j+1..i with the
@@ -621,6 +621,16 @@ typedef float Tile[CB][TS];
 
 __device__ __forceinline__ void store_tile(float* dst, int ld, const Tile& src, int t = -1, int nthr = 256) {
     for (int e = (t < 0 ? (int)threadIdx.x : t); e < 256; e += nthr) {
+        const int row = e >> 3, c4 = e & 7;
+        float4 v;
+        v.x = src[row][4 * c4 + 0]; v.y = src[row][4 * c4 + 1]; v.z = src[row][4 * c4 + 2]; v.w = src[row][4 * c4 + 3];
+        *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+    }
+}
+
+// rows 16 h .. 16 h + 15 of a tile, by one wavefront
+__device__ __forceinline__ void store_tile_half(float* dst, int ld, const Tile& src, int h, int lane) {
+    for (int e = 128 * h + lane; e < 128 * (h + 1); e += 64) {
         const int row = e >> 3, c4 = e & 7;
         float4 v;
         v.x = src[row][4 * c4 + 0]; v.y = src[row][4 * c4 + 1]; v.z = src[row][4 * c4 + 2]; v.w = src[row][4 * c4 + 3];
@@ -720,6 +730,69 @@ __device__ __forceinline__ void store_tile_lower(float* dst, int ld, const Tile&
 // The four-quadrant tile helpers below are called by every wavefront of the workgroup (they contain workgroup
 // barriers); the work is done by waves 0-3 (one 16x16 quadrant each) when `on` is set, the others only pass the
 // barriers.
+
+// One wave's quadrant (bi, bj) of NT tiles tf(t0), tf(t0 + 2), ...: acc[u] = A_u Li^T over the chain m < 4 NK
+// (NK = 4 (bj + 1)), every operand read first, the NT independent chains interleaved
+template <int NT, int NK, class TF>
+__device__ __forceinline__ void panel_chains(TF tf, int t0, const float (&bv)[8], f32x4 (&acc)[4], int bi, int l16,
+                                             int lk) {
+    float a[NT][NK];
+#pragma unroll
+    for (int u = 0; u < NT; ++u)
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) a[u][kk] = tf(t0 + 2 * u)[16 * bi + l16][4 * kk + lk];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+        for (int u = 0; u < NT; ++u) acc[u] = mfma(a[u][kk], bv[kk], acc[u]);
+}
+
+// In place, n tiles tf(q) = tf(q) Li^T, each element a chain over m < 16 (bj + 1) from +0 (Li is lower triangular,
+// chol.cu panel), by the eight wavefronts in chunks of up to eight tiles: wave w takes quadrant (bi, bj) = (w & 3) of
+// the chunk's tiles w >> 2, (w >> 2) + 2, ...; every wave reads its operands and runs its chains, then, after a
+// workgroup barrier, writes the results.
+template <class TF>
+__device__ __forceinline__ void panels_inplace(int n, TF tf, const Tile& li) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, l16 = lane & 15,
+              lk = lane >> 4, qd = w & 3, bi = qd >> 1, bj = qd & 1, half = w >> 2;
+    float bv[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) bv[kk] = li[16 * bj + l16][4 * kk + lk];   // (bj = 0 uses kk < 4)
+    for (int c0 = 0; c0 < n; c0 += 8) {
+        const int nc = n - c0 < 8 ? n - c0 : 8;
+        const int nt = (nc - half + 1) / 2;
+        auto tfc = [&](int t) -> Tile& { return tf(c0 + t); };
+        f32x4 acc[4];
+        if (bj == 0) {
+            switch (nt) {
+                case 1: panel_chains<1, 4>(tfc, half, bv, acc, bi, l16, lk); break;
+                case 2: panel_chains<2, 4>(tfc, half, bv, acc, bi, l16, lk); break;
+                case 3: panel_chains<3, 4>(tfc, half, bv, acc, bi, l16, lk); break;
+                case 4: panel_chains<4, 4>(tfc, half, bv, acc, bi, l16, lk); break;
+                default: break;
+            }
+        } else {
+            switch (nt) {
+                case 1: panel_chains<1, 8>(tfc, half, bv, acc, bi, l16, lk); break;
+                case 2: panel_chains<2, 8>(tfc, half, bv, acc, bi, l16, lk); break;
+                case 3: panel_chains<3, 8>(tfc, half, bv, acc, bi, l16, lk); break;
+                case 4: panel_chains<4, 8>(tfc, half, bv, acc, bi, l16, lk); break;
+                default: break;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (u < nt) {
+                Tile& t = tfc(half + 2 * u);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) t[16 * bi + 4 * lk + v][16 * bj + l16] = acc[u][v];
+            }
+        __syncthreads();
+    }
+}
 
 // out = in Li^T; chain over m < 16 (bj + 1) (Li is lower triangular, chol.cu panel). out may alias in.
 __device__ __forceinline__ void panel32(Tile& out, const Tile& in, const Tile& li, bool on = true) {
@@ -1191,10 +1264,9 @@ size_t chol_lds_bytes(int r, int w) {
 // start, 1 step end, 2 look-ahead done, 3 tile factor done; slot 0 is the kernel start, 1 + 4 nb the end;
 // 2 + 4 nb + j: wave 1's row work of step j done; 2 + 5 nb + j: wave 3's done; 2 + 6 nb + j: the hand-over of row j+2
 // seen; 2 + 7 nb + j: row j+2 fetched; 2 + 8 nb + j: its panel L(j+2, j-1) formed; 2 + 9 nb + j: wave 2 done;
-// 2 + 10 nb + 6 i + s: the owner of row i's last part at its last block: s = 0 block published, 1 operands loaded,
-// 2 own panel published, 3 row handed over, 4 update done, 5 hand-over stores done; 2 + 16 nb + 8 j + s: the last
-// row's last part at block j: s = 0 block published, 1 operands loaded, 2 own panel published, 3 panel L(j+2, j)
-// formed, 4 early tiles updated, 5 other panels' flags seen, 6 other panels loaded, 7 block done.
+// 2 + 10 nb + 6 i + s: the owner of row i's last part at its last block: s = 0 flags seen, 1 operands loaded,
+// 2 panels formed, 3 row handed over, 4 update done, 5 hand-over stores done; 2 + 16 nb + 8 j + s: the last row's
+// last part at block j: s = 0 flags seen, 1 operands loaded, 2 panels formed, 3 block done, 4 T(i, j+1) published.
 // Workgroups of eight wavefronts: waves 0-3 do the work described here (and wave 7 of workgroup 0 its turns at the
 // tile factor and the look-ahead); waves 4-7 share the owners' row update with them (two wavefronts per SIMD there,
 // so one's LDS traffic overlaps the other's MFMA chain) and otherwise only pass the same workgroup barriers.
@@ -1238,7 +1310,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
     bool dead = false;
     if (STAMP && b == 0 && tid == 0) stamps[0] = wall_clock64();
     const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
-    // misc: [0..2] nrm, shift, tau; workgroup 0's LDS words: [4] the waves 1-2 barrier counter, [5] the last step
+    // misc: [0..2] nrm, shift, tau; workgroup 0's LDS words: [4] the row wavefronts' barrier counter, [5] the last step
     // whose L(j+2, j) is formed, [7] the tile factor's pairs done; [32..63] the tile factor's diagonal (piv q),
     // [64..127] its per-pair scalars
     float* misc = reinterpret_cast<float*>(chol_lds);
@@ -1306,14 +1378,15 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
             scal[1] = tau;
         }
         CholWG0& z = *reinterpret_cast<CholWG0*>(tiles);
-        uint32_t* bar12 = reinterpret_cast<uint32_t*>(misc + 4);    // waves 1-2 barrier counter (zeroed above)
+        uint32_t* bar12 = reinterpret_cast<uint32_t*>(misc + 4);    // waves 1, 2, 5, 6 barrier counter (zeroed above)
         uint32_t* p2done = reinterpret_cast<uint32_t*>(misc + 5);   // L(j+2, j) of step j formed: j + 1 (zeroed above)
         uint32_t n12 = 0;
         // wave 3: publish L(j, j), Li_j, L(j+1, j), L(j+2, j) of step j (parity q = j & 1)
         // What the owners need for column block j -- Li_j (into its place in Li), the panel L(j+1, j) (into its
         // place in L) and T(j+2, j) through block j-1 (into the slot (j+2, j) of A, which nothing reads any more:
         // row j+2 was fetched at step j; row 2 is still the Gram's there at step 0) -- is stored by the wave that
-        // finishes it during step j (the factor's wavefront: Li_j; the look-ahead's: L(j+1, j); wave 1: T(j+2, j))
+        // finishes it during step j (the factor's wavefront: Li_j; the look-ahead's: L(j+1, j); waves 1 and 5:
+        // T(j+2, j))
         // and completed before the
         // step's last barrier. Wave 3, at the start of step j+1: release them, then the outputs of step j (L(j, j),
         // L(j+2, j) and the packed forms), which only later kernels read.
@@ -1374,61 +1447,76 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                           dead, lim);
                 if (STAMP && lane == 0) stamps[3 + 4 * j] = wall_clock64();
                 __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this step's L(j+1, j) stored
-            } else if (w < 4) {
-                // waves 1-3: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p].
-                // Wave 3 publishes the previous step. Waves 1-2 fetch row j+2; then L(j+2, j-1) (wave 1) and the
-                // block j-2 update of T(j+2, j+1) that its owner left (wave 2); then block j-1 on T(j+2, j) and the
-                // lower half of T(j+2, j+2) (wave 1) and on T(j+2, j+1) and T(j+2, j+2)'s quadrant (0, 0) (wave 2).
+            } else if (w == 3) {
+                // wave 3 publishes the previous step
+                if (j >= 1) publish(j - 1);
+                if (colcnt != nullptr && j == nb - 1) {   // column nb-2's operands, stored just now
+                    release();
+                    if (lane == 0) credit(colcnt, nb - 2);
+                }
+                if (STAMP && lane == 0) stamps[2 + 5 * nb + j] = wall_clock64();
+            } else if ((w == 1 || w == 2 || w == 5 || w == 6) && j + 2 < nb) {
+                // waves 1, 2, 5, 6: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p].
+                // The four fetch row j+2; then L(j+2, j-1) (waves 1 and 5, a row half each) and the block j-2 update
+                // of T(j+2, j+1) that its owner left (waves 2 and 6); then block j-1 on T(j+2, j) (waves 1 and 5),
+                // T(j+2, j+1) (waves 2 and 6) and the lower quadrants of T(j+2, j+2) (waves 1, 5 and 2).
                 Tile* R2 = z.R2[p];
-                const bool row2 = j + 2 < nb;
-                if (w == 3) {
-                    if (j >= 1) publish(j - 1);
-                    if (colcnt != nullptr && j == nb - 1) {   // column nb-2's operands, stored just now
-                        release();
-                        if (lane == 0) credit(colcnt, nb - 2);
+                const int hf = w >> 2;                                   // row half (waves 5 and 6)
+                const bool side2 = (w & 3) == 2;                         // waves 2 and 6
+                const int i2 = j + 2, wl = ((w & 3) - 1 + 2 * hf) * 64 + lane;
+                const float* rowp = A + (size_t)CB * i2 * r;
+                if (j <= 1) {
+                    const int t0 = (j == 0) ? 1 : 0;     // row 2: T(2, 0..2) into R2[1..3]; row 3: T(3, 0..3)
+                    load_tiles<4, 256>(&R2[t0], 4 - t0, r, 1u << (3 - t0), shift, wl,
+                                       [&](int q) { return rowp + CB * (j - 1 + t0 + q); });
+                } else {
+                    if (lane == 0) wait_flag(flagT + i2, ep, err, dead, lim);
+                    if (STAMP && w == 1 && lane == 0) stamps[2 + 6 * nb + j] = wall_clock64();
+                    __builtin_amdgcn_wave_barrier();
+                    const float* hp = L + (size_t)CB * i2 * r + (size_t)CB * (j - 2);     // into R2[4] = H
+                    load_tiles<5, 256>(&R2[0], 5, r, 0u, 0.f, wl,
+                                       [&](int q) { return q < 4 ? rowp + CB * (j - 1 + q) : hp; });
+                }
+                wave_group_barrier(bar12, 4 * ++n12, err, dead, lim);
+                if (STAMP && w == 1 && lane == 0) stamps[2 + 7 * nb + j] = wall_clock64();
+                if (j >= 1) {
+                    if (!side2) {
+                        if (hf) panel32_wave<0xC>(z.C2[p], R2[0], z.li[pp]);          // L(j+2, j-1)
+                        else panel32_wave<0x3>(z.C2[p], R2[0], z.li[pp]);
+                    } else if (j >= 2) {                                               // T(j+2, j+1), block j-2
+                        if (hf) update32_wave_q<0xC>(R2[2], R2[2], R2[4], z.C2[pp]);
+                        else update32_wave_q<0x3>(R2[2], R2[2], R2[4], z.C2[pp]);
                     }
-                    if (STAMP && lane == 0) stamps[2 + 5 * nb + j] = wall_clock64();
-                } else if (row2) {
-                    const int i2 = j + 2, wl = (w - 1) * 64 + lane;
-                    const float* rowp = A + (size_t)CB * i2 * r;
-                    if (j <= 1) {
-                        const int t0 = (j == 0) ? 1 : 0;     // row 2: T(2, 0..2) into R2[1..3]; row 3: T(3, 0..3)
-                        load_tiles<4, 128>(&R2[t0], 4 - t0, r, 1u << (3 - t0), shift, wl,
-                                           [&](int q) { return rowp + CB * (j - 1 + t0 + q); });
-                    } else {
-                        if (lane == 0) wait_flag(flagT + i2, ep, err, dead, lim);
-                        if (STAMP && w == 1 && lane == 0) stamps[2 + 6 * nb + j] = wall_clock64();
-                        __builtin_amdgcn_wave_barrier();
-                        const float* hp = L + (size_t)CB * i2 * r + (size_t)CB * (j - 2);     // into R2[4] = H
-                        load_tiles<5, 128>(&R2[0], 5, r, 0u, 0.f, wl,
-                                           [&](int q) { return q < 4 ? rowp + CB * (j - 1 + q) : hp; });
-                    }
-                    wave_group_barrier(bar12, 2 * ++n12, err, dead, lim);
-                    if (STAMP && w == 1 && lane == 0) stamps[2 + 7 * nb + j] = wall_clock64();
-                    if (j >= 1) {
-                        if (w == 1)
-                            panel32_wave(z.C2[p], R2[0], z.li[pp]);                    // L(j+2, j-1)
-                        else if (j >= 2)
-                            update32_wave<false>(R2[2], R2[4], z.C2[pp]);      // T(j+2, j+1), block j-2 (owner skips it)
-                        wave_group_barrier(bar12, 2 * ++n12, err, dead, lim);
-                        if (STAMP && w == 1 && lane == 0) stamps[2 + 8 * nb + j] = wall_clock64();
-                        if (w == 1) {
-                            update32_wave<false>(R2[1], z.C2[p], z.P1[pp]);            // T(j+2, j), block j-1
-                            store_tile(A + (size_t)CB * (j + 2) * r + CB * j, r, R2[1], lane, 64);
-                            update32_wave_q<0xC>(R2[3], R2[3], z.C2[p], z.C2[p]);      // T(j+2, j+2), lower half
+                    wave_group_barrier(bar12, 4 * ++n12, err, dead, lim);
+                    if (STAMP && w == 1 && lane == 0) stamps[2 + 8 * nb + j] = wall_clock64();
+                    if (!side2) {
+                        // T(j+2, j), block j-1 (for the owners, in the slot of A that nothing reads any more), then
+                        // quadrant (0, 0) or (1, 1) of T(j+2, j+2)
+                        if (hf) {
+                            update32_wave_q<0xC>(R2[1], R2[1], z.C2[p], z.P1[pp]);
+                            store_tile_half(A + (size_t)CB * (j + 2) * r + CB * j, r, R2[1], 1, lane);
+                            update32_wave_q<0x8>(R2[3], R2[3], z.C2[p], z.C2[p]);
                         } else {
-                            wait_lds(p2done, (uint32_t)j, err, dead, lim);             // L(j+1, j-1) formed
-                            update32_wave<false>(R2[2], z.C2[p], z.P2[pp]);            // T(j+2, j+1)
-                            update32_wave_q<0x1>(R2[3], R2[3], z.C2[p], z.C2[p]);      // T(j+2, j+2), quadrant (0, 0)
+                            update32_wave_q<0x3>(R2[1], R2[1], z.C2[p], z.P1[pp]);
+                            store_tile_half(A + (size_t)CB * (j + 2) * r + CB * j, r, R2[1], 0, lane);
+                            update32_wave_q<0x1>(R2[3], R2[3], z.C2[p], z.C2[p]);
+                        }
+                    } else {
+                        wait_lds(p2done, (uint32_t)j, err, dead, lim);                 // L(j+1, j-1) formed
+                        if (hf) {
+                            update32_wave_q<0xC>(R2[2], R2[2], z.C2[p], z.P2[pp]);     // T(j+2, j+1)
                             // L(j+2, j-1) for the output and the later kernels (the owners form their own copy)
                             const size_t o = (size_t)CB * (j - 1);
                             store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
                             store_tile_op(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], lane, 64);
                             if (STAMP && lane == 0) stamps[2 + 9 * nb + j] = wall_clock64();
+                        } else {
+                            update32_wave_q<0x3>(R2[2], R2[2], z.C2[p], z.P2[pp]);
+                            update32_wave_q<0x4>(R2[3], R2[3], z.C2[p], z.C2[p]);      // T(j+2, j+2), (1, 0)
                         }
                     }
-                    if (STAMP && w == 1 && lane == 0) stamps[2 + 4 * nb + j] = wall_clock64();
                 }
+                if (STAMP && w == 1 && lane == 0) stamps[2 + 4 * nb + j] = wall_clock64();
             }
             __syncthreads();
             // start the L2 write-back of this step's stores now; the publication at the next step's start then
@@ -1440,10 +1528,14 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         if (STAMP && tid == 0) stamps[1 + 4 * nb] = wall_clock64();
     } else {
         // Owner part: tile row i, tiles T(i, s..e-1) in LDS. rt[k - s] = T(i, k); pn[k - s] = L(k, j) of the current
-        // column block for the part's columns k < i; li = Li_j; pin = L(i, j) when another part of the row forms it
-        // (the part that holds T(i, j)). Each part runs blocks j until its tiles are done: the last part (which holds
-        // T(i, i)) to block i-4, after which it hands T(i, i-3..i) to workgroup 0; an earlier part to block e-1, its
-        // last panel.
+        // column block for the part's columns k < i; li = Li_j; pin = L(i, j) when another part of the row holds
+        // T(i, j). Each part runs blocks j until its tiles are done: the last part (which holds T(i, i)) to block
+        // i-4, after which it hands T(i, i-3..i) to workgroup 0; an earlier part to block e-1, its last panel.
+        // Every panel a block needs is formed here from its tile through block j-1 -- L(k, j) = T(k, j) Li_j^T --
+        // and those tiles are published a block ahead: the part holding T(i, j+1) stores it (in its slot of A) and
+        // raises flag (i, j+1) as soon as block j has updated it. So a block waits on one round of flags: workgroup
+        // 0's block j (Li_j, the finished L(j+1, j), T(j+2, j)), the hand-over of row j+3 (T(j+3, j)) and the tiles
+        // T(k, j) of rows k >= j+4 and, when another part holds it, T(i, j), all published during block j-1.
         const int i = oi, s = os, e = oe;
         const bool last = e == i + 1;
         const int jl = last ? i - 4 : e - 1;
@@ -1456,61 +1548,67 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         const bool upq = (bi == 0 && bj == 1);
         for (int j = 0; j <= jl; ++j) {
             const bool q4 = w < 4;
-            const bool mine = j >= s;                               // this part forms L(i, j)
-            const bool h1 = j + 1 >= s && j + 1 < e, h2 = j + 2 >= s && j + 2 < e;
-            // workgroup 0's block j: Li_j into li; L(j+1, j) and T(j+2, j) (through block j-1), where they are in
-            // the part's columns, into their panel slots
-            const bool hst = STAMP && last && j + 4 == i && tid == 0;   // the hand-over block's stamps
+            const bool mine = j >= s;                               // this part holds T(i, j): L(i, j) is its output
+            const bool hand = last && j + 4 == i;                   // the block after which row i is handed over
+            // the part's columns k < i updated by block j: [k0, ke) (at the hand-over block T(i, i-1) is left to
+            // workgroup 0, so L(i-1, j) is not needed)
+            const int k0 = j + 1 > s ? j + 1 : s;
+            const int ke = last ? (hand ? i - 1 : i) : e;
+            const int nk = ke > k0 ? ke - k0 : 0;
+            const bool hst = STAMP && hand && tid == 0;             // the hand-over block's stamps
             const bool bst = STAMP && last && i == nb - 1 && tid == 0;  // the last row's stamps, every block
             uint64_t* bs = stamps + 2 + 16 * nb + 8 * j;
-            if (tid == 0) wait_flag(flagL + j * nb + j, ep, err, dead, lim);
+            if (w == 0) {
+                const uint32_t* f = nullptr;
+                if (lane == 0) {
+                    f = flagL + j * nb + j;
+                } else if (lane <= nk) {
+                    const int k = k0 + lane - 1;
+                    if (k == j + 3) f = k >= 4 ? flagT + k : nullptr;             // row 3 never had an owner
+                    else if (k >= j + 4 && j >= 1) f = flagL + k * nb + j;         // (block 0: the Gram's tiles)
+                } else if (lane == nk + 1 && !mine && j >= 1) {
+                    f = flagL + i * nb + j;
+                }
+                wait_flags_wave(f, ep, err, dead, lim);
+            }
+            __syncthreads();
             if (hst) stamps[2 + 10 * nb + 6 * i] = wall_clock64();
             if (bst) bs[0] = wall_clock64();
-            __syncthreads();
+            // one batch: Li_j; per column k, the finished L(j+1, j) or T(k, j) through block j-1; T(i, j) into pin
             if (q4)
-                load_tiles_to<3, 256>(1 + (h1 ? 1 : 0) + (h2 ? 1 : 0), tid,
-                                      [&](int q) -> Tile& { return q == 0 ? li : pn[j + q + (h1 ? 0 : 1) - s]; },
-                                      [&](int q) {
-                                          const int k = j + q + (h1 ? 0 : 1);
-                                          return q == 0 ? Li + (size_t)CB * j * CB
-                                                        : (k == j + 1 ? L : A) + (size_t)CB * k * r + (size_t)CB * j;
-                                      },
-                                      [&](int q) { return q == 0 ? CB : r; });   // Li_j's rows are 32 apart
+                load_tiles_to<OWNER_WMAX + 2, 256>(1 + nk + (mine ? 0 : 1), tid,
+                                                [&](int q) -> Tile& { return q == 0 ? li : q <= nk ? pn[k0 + q - 1 - s] : pin; },
+                                                [&](int q) {
+                                                    if (q == 0) return (const float*)(Li + (size_t)CB * j * CB);
+                                                    const int k = q <= nk ? k0 + q - 1 : i;
+                                                    return (const float*)((k == j + 1 ? L : A) + (size_t)CB * k * r +
+                                                                          (size_t)CB * j);
+                                                },
+                                                [&](int q) { return q == 0 ? CB : r; });   // Li_j's rows are 32 apart
             __syncthreads();
             if (hst) stamps[3 + 10 * nb + 6 * i] = wall_clock64();
             if (bst) bs[1] = wall_clock64();
-            const Tile& lij = mine ? rt[j - s] : pin;
+            // the panels: L(i, j) (in place in rt[j - s] or pin) and L(k, j) for the columns k >= j+2
+            Tile& lij = mine ? rt[j - s] : pin;
+            const int kp = k0 > j + 2 ? k0 : j + 2;
+            const int np = 1 + (ke > kp ? ke - kp : 0);
+            panels_inplace(np, [&](int q) -> Tile& { return q == 0 ? lij : pn[kp + q - 1 - s]; }, li);
+            if (hst) stamps[4 + 10 * nb + 6 * i] = wall_clock64();
+            if (bst) bs[2] = wall_clock64();
             if (mine) {
-                // panel L(i, j) = T(i, j) Li_j^T, published before anything else (so no row waits on a chain of rows)
-                panel32(rt[j - s], rt[j - s], li, q4);
-                store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, rt[j - s]);   // threads 0-255
-                __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-                __syncthreads();
-                if (tid == 0) {
-                    publish_flag(flagL + i * nb + j, ep);
-                    if (j > s) credit(colcnt, j - 1);   // the release covers L(i, j-1)'s packed form, stored after it
-                }
-                if (hst) stamps[4 + 10 * nb + 6 * i] = wall_clock64();
-                if (bst) bs[2] = wall_clock64();
-                store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, rt[j - s]);   // for the solve only
+                // L(i, j): the output, and its packed form for the solve (released below, with the column credit)
+                if (q4) store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, lij);
+                else store_tile_op(Lp + (size_t)op_pair(i, j) * CB * CB, lij, tid - 256, 256);
+            } else if (hand && q4) {
+                // workgroup 0 reads L(i, i-4) with the handed-over row: this part's own copy (the same bits as the
+                // holder's), stored before the hand-over
+                store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, lij);
             }
-            // block j's panels of the part's rows between: L(k, j), k = j+1..i-1, each in LDS before the tile it
-            // updates. Rows j+1 and j+2 are workgroup 0's: L(j+1, j) comes finished; L(j+2, j) is formed here, as
-            // workgroup 0 forms it.
-            // Row j+3 has just been handed to workgroup 0 (before block j; row 3 never had an owner): its panel too
-            // is formed here, from the handed-over T(j+3, j). Rows j+4.. publish their own. At the last part's last
-            // block (j = i-4) T(i, i-1) is left to workgroup 0, so L(i-1, j) is not needed.
-            if (h2) panel32(pn[j + 2 - s], pn[j + 2 - s], li, q4);      // L(j+2, j)
-            if (bst) bs[3] = wall_clock64();
-            const int ke = last ? (j + 4 == i ? i - 1 : i) : e;     // the part's columns k < i updated: [.., ke)
-            const int k3 = j + 3 > s ? j + 3 : s;                   // [k3, ke): panels from global memory
-            const int nr = ke > k3 ? ke - k3 : 0;
             // Row i's update by block j, every tile's quadrant chain in one phase (the tiles are independent): waves
             // w and w + 4 take quadrant (bi, bj) = (w & 3) of alternate tiles of a sequence (without the upper
             // quadrant of T(i, i)); the panel's A operands stay in registers, and the next tile's B operands and
-            // accumulator are read while this tile's chain runs. For long rows, when the part forms L(i, j), first
-            // the tiles whose panels it has formed -- T(i, j+1), T(i, j+2) and T(i, i) -- while the other rows'
-            // panel flags are in flight; then, once those are loaded, the rest.
+            // accumulator are read while this tile's chain runs. T(i, j+1), which the next block's consumers wait
+            // for, comes first.
             auto update_tiles = [&](int n, auto kof) {
                 float an[8];
 #pragma unroll
@@ -1559,52 +1657,14 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     t = tn;
                 }
             };
-            // with at most 8 tiles per row the flags arrive before the early tiles would finish, and the part runs
-            // as one sequence after them
-            const bool early = mine && nb > 8;
-            if (early) {
-                const int a0 = h1 ? j + 1 : j + 2, nh = (h1 ? 1 : 0) + (h2 ? 1 : 0);
-                update_tiles(nh + (last && !upq ? 1 : 0), [&](int t) { return t < nh ? a0 + t : i; });
-            }
-            if (bst) bs[4] = wall_clock64();
-            // the other rows' panels (and L(i, j) when another part forms it): flags polled together, one batch of
-            // loads
-            if (w == 0) {
-                const uint32_t* f = nullptr;
-                if (lane < nr) {
-                    const int k = k3 + lane;
-                    f = (k != j + 3) ? flagL + k * nb + j : (k >= 4 ? flagT + k : nullptr);
-                } else if (lane == nr && !mine) {
-                    f = flagL + i * nb + j;
-                }
-                wait_flags_wave(f, ep, err, dead, lim);
-            }
+            // T(i, k0..ke-1), then T(i, i)
+            update_tiles(nk + (last && !upq ? 1 : 0), [&](int t) { return k0 + t < ke ? k0 + t : i; });
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this block's stores are complete before the barrier
             __syncthreads();
-            if (bst) bs[5] = wall_clock64();
-            if (q4)
-                load_tiles_to<OWNER_WMAX + 1, 256>(nr + (mine ? 0 : 1), tid,
-                                                [&](int q) -> Tile& { return q < nr ? pn[k3 + q - s] : pin; },
-                                                [&](int q) {
-                                                    const int k = q < nr ? k3 + q : i;
-                                                    return (k == j + 3 ? A : L) + (size_t)CB * k * r + (size_t)CB * j;
-                                                },
-                                                [&](int) { return r; });
-            __syncthreads();
-            if (bst) bs[6] = wall_clock64();
-            if (j + 3 >= s && j + 3 < ke) panel32(pn[j + 3 - s], pn[j + 3 - s], li, q4);     // L(j+3, j)
-            if (early) {
-                update_tiles(nr, [&](int t) { return k3 + t; });
-            } else {
-                // T(i, k0..ke-1), then T(i, i)
-                const int k0 = j + 1 > s ? j + 1 : s;
-                const int n = (ke > k0 ? ke - k0 : 0) + (last && !upq ? 1 : 0);
-                update_tiles(n, [&](int t) { return k0 + t < ke ? k0 + t : i; });
-            }
-            __syncthreads();
-            if (bst) bs[7] = wall_clock64();
-            if (last && j + 4 == i) {
+            if (hst) stamps[6 + 10 * nb + 6 * i] = wall_clock64();
+            if (bst) bs[3] = wall_clock64();
+            if (hand) {
                 // hand T(i, i-3..i) to workgroup 0
-                if (hst) stamps[6 + 10 * nb + 6 * i] = wall_clock64();
                 for (int t = 0; t < 4; ++t)
                     store_tile(A + (size_t)CB * i * r + (size_t)CB * (i - 3 + t), r, rt[i - 3 + t - s]);
                 __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -1615,15 +1675,19 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     if (mine) credit(colcnt, j);   // L(i, i-4)'s packed form
                 }
                 if (hst) stamps[5 + 10 * nb + 6 * i] = wall_clock64();
-            }
-        }
-        if (!last) {
-            // the packed form of the part's last panel, L(i, e-1), stored after its publication: released and credited
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-            __syncthreads();
-            if (tid == 0) {
-                release();
-                credit(colcnt, e - 1);
+            } else if (w == 7) {
+                // T(i, j+1) through block j for the next block's consumers, and the column credit for L(i, j);
+                // the other waves go on to the next block's wait meanwhile
+                const bool pub = j + 1 >= s && j + 1 < e && j + 1 <= i - 4;
+                if (pub) store_tile(A + (size_t)CB * i * r + (size_t)CB * (j + 1), r, rt[j + 1 - s], lane, 64);
+                if (pub || mine) {
+                    release();
+                    if (lane == 0) {
+                        if (pub) set_flag(flagL + i * nb + j + 1, ep);
+                        if (mine) credit(colcnt, j);
+                    }
+                }
+                if (STAMP && last && i == nb - 1 && lane == 0) bs[4] = wall_clock64();
             }
         }
     }
