@@ -137,6 +137,10 @@ __device__ float block_scale128(const uint32_t* __restrict__ part) {
 // Pivot reciprocal square root (the reference uses CUDA rsqrtf, chol.cu:45): the published fast inverse square root
 // start 0x5f375a86 - (bits >> 1) (C. Lomont, "Fast Inverse Square Root", 2003) and three Newton steps
 // y <- y * (1.5 - (0.5x * y) * y), each bracket one fma, so the result is a fixed function of x.
+// the 100 MHz wall clock for the instrumented Cholesky's stamps (the s_memrealtime counter, read without waiting for
+// outstanding memory operations, so a stamp does not change when stores complete)
+__device__ __forceinline__ uint64_t stamp_clock() { return __builtin_amdgcn_s_memrealtime(); }
+
 __device__ __forceinline__ float rsqrt_sw(float x) {
     float y = __uint_as_float(0x5f375a86u - (__float_as_uint(x) >> 1));
     const float h = 0.5f * x;
@@ -625,6 +629,20 @@ __device__ __forceinline__ void store_tile(float* dst, int ld, const Tile& src, 
         float4 v;
         v.x = src[row][4 * c4 + 0]; v.y = src[row][4 * c4 + 1]; v.z = src[row][4 * c4 + 2]; v.w = src[row][4 * c4 + 3];
         *reinterpret_cast<float4*>(dst + (size_t)row * ld + 4 * c4) = v;
+    }
+}
+
+// the half of store_tile_op's packed layout that holds rows 16 h .. 16 h + 15, by one wavefront
+__device__ __forceinline__ void store_tile_op_half(float* dst, const Tile& src, int h, int lane) {
+    for (int u = 0; u < 2; ++u) {
+        const int e = 4 * (32 * u + (lane >> 1)) + 2 * h + (lane & 1);   // e & 3 = 2 h + (0 or 1): cb = h
+        const int ln = e >> 2, kk0 = 4 * (e & 1), l16 = ln & 15, lk = ln >> 4;
+        float4 v;
+        v.x = src[16 * h + l16][4 * (kk0 + 0) + lk];
+        v.y = src[16 * h + l16][4 * (kk0 + 1) + lk];
+        v.z = src[16 * h + l16][4 * (kk0 + 2) + lk];
+        v.w = src[16 * h + l16][4 * (kk0 + 3) + lk];
+        *reinterpret_cast<float4*>(dst + 4 * e) = v;
     }
 }
 
@@ -1260,7 +1278,7 @@ size_t chol_lds_bytes(int r, int w) {
 // npart[l], npart[l + 64], ... in order, then a shift-down tree over the 64 lane sums; nrm = sqrtf(fp32(sum)),
 // shift = alpha * nrm added to the diagonal after the first load, tau = tau_rel * nrm + 1e-30 (kcholqr.py:107-109).
 // flags: [nb * nb] panel flags (L(i, j) published; (j, j): L(j, j) and Li_j), [nb] hand-over flags (tile row i),
-// [64] per-workgroup call counters. STAMP: workgroup 0 records wall_clock64() at 1 + 4j + s for step j: s = 0 step
+// [64] per-workgroup call counters. STAMP: workgroup 0 records the wall clock at 1 + 4j + s for step j: s = 0 step
 // start, 1 step end, 2 look-ahead done, 3 tile factor done; slot 0 is the kernel start, 1 + 4 nb the end;
 // 2 + 4 nb + j: wave 1's row work of step j done; 2 + 5 nb + j: wave 3's done; 2 + 6 nb + j: the hand-over of row j+2
 // seen; 2 + 7 nb + j: row j+2 fetched; 2 + 8 nb + j: its panel L(j+2, j-1) formed; 2 + 9 nb + j: wave 2 done;
@@ -1308,7 +1326,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
     uint32_t* flagT = flags + nb * nb;
     uint32_t* cnt = flags + nb * nb + nb;
     bool dead = false;
-    if (STAMP && b == 0 && tid == 0) stamps[0] = wall_clock64();
+    if (STAMP && b == 0 && tid == 0) stamps[0] = stamp_clock();
     const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
     // misc: [0..2] nrm, shift, tau; workgroup 0's LDS words: [4] the row wavefronts' barrier counter, [5] the last step
     // whose L(j+2, j) is formed, [7] the tile factor's pairs done; [32..63] the tile factor's diagonal (piv q),
@@ -1419,10 +1437,10 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
             const int p = j & 1, pp = p ^ 1;
             const int wf = p ? 7 : 0, wr = 7 - wf;                  // this step's factor and look-ahead wavefronts
             const uint32_t fbase = (uint32_t)(CB / 2) * j;
-            if (STAMP && tid == 0) stamps[1 + 4 * j] = wall_clock64();
+            if (STAMP && tid == 0) stamps[1 + 4 * j] = stamp_clock();
             if (w == wf) {
                 factor_pairs(C, pq, fq, fcnt, fbase, tau, z.dl[p], z.li[p], Li + (size_t)CB * j * CB);
-                if (STAMP && lane == 0) stamps[4 + 4 * j] = wall_clock64();
+                if (STAMP && lane == 0) stamps[4 + 4 * j] = stamp_clock();
                 if (colcnt != nullptr && j == nb - 1) {
                     // the last column of the factor is Li_{nb-1} alone: packed, released and credited at once
                     store_tile_op(Lp + (size_t)op_pair(j, j) * CB * CB, z.li[p], lane, 64);
@@ -1445,7 +1463,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 }
                 row_pairs(C, T2, fq, fcnt, fbase, z.dl[p], z.P1[p], L + (size_t)CB * (j + 1) * r + CB * j, r, err,
                           dead, lim);
-                if (STAMP && lane == 0) stamps[3 + 4 * j] = wall_clock64();
+                if (STAMP && lane == 0) stamps[3 + 4 * j] = stamp_clock();
                 __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this step's L(j+1, j) stored
             } else if (w == 3) {
                 // wave 3 publishes the previous step
@@ -1454,7 +1472,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     release();
                     if (lane == 0) credit(colcnt, nb - 2);
                 }
-                if (STAMP && lane == 0) stamps[2 + 5 * nb + j] = wall_clock64();
+                if (STAMP && lane == 0) stamps[2 + 5 * nb + j] = stamp_clock();
             } else if ((w == 1 || w == 2 || w == 5 || w == 6) && j + 2 < nb) {
                 // waves 1, 2, 5, 6: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p].
                 // The four fetch row j+2; then L(j+2, j-1) (waves 1 and 5, a row half each) and the block j-2 update
@@ -1471,24 +1489,28 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                                        [&](int q) { return rowp + CB * (j - 1 + t0 + q); });
                 } else {
                     if (lane == 0) wait_flag(flagT + i2, ep, err, dead, lim);
-                    if (STAMP && w == 1 && lane == 0) stamps[2 + 6 * nb + j] = wall_clock64();
+                    if (STAMP && w == 1 && lane == 0) stamps[2 + 6 * nb + j] = stamp_clock();
                     __builtin_amdgcn_wave_barrier();
                     const float* hp = L + (size_t)CB * i2 * r + (size_t)CB * (j - 2);     // into R2[4] = H
                     load_tiles<5, 256>(&R2[0], 5, r, 0u, 0.f, wl,
                                        [&](int q) { return q < 4 ? rowp + CB * (j - 1 + q) : hp; });
                 }
                 wave_group_barrier(bar12, 4 * ++n12, err, dead, lim);
-                if (STAMP && w == 1 && lane == 0) stamps[2 + 7 * nb + j] = wall_clock64();
+                if (STAMP && w == 1 && lane == 0) stamps[2 + 7 * nb + j] = stamp_clock();
                 if (j >= 1) {
                     if (!side2) {
                         if (hf) panel32_wave<0xC>(z.C2[p], R2[0], z.li[pp]);          // L(j+2, j-1)
                         else panel32_wave<0x3>(z.C2[p], R2[0], z.li[pp]);
+                        // its half for the output and the later kernels (the owners form their own copy)
+                        const size_t o = (size_t)CB * (j - 1);
+                        store_tile_half(L + (o + 3 * CB) * r + o, r, z.C2[p], hf, lane);
+                        store_tile_op_half(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], hf, lane);
                     } else if (j >= 2) {                                               // T(j+2, j+1), block j-2
                         if (hf) update32_wave_q<0xC>(R2[2], R2[2], R2[4], z.C2[pp]);
                         else update32_wave_q<0x3>(R2[2], R2[2], R2[4], z.C2[pp]);
                     }
                     wave_group_barrier(bar12, 4 * ++n12, err, dead, lim);
-                    if (STAMP && w == 1 && lane == 0) stamps[2 + 8 * nb + j] = wall_clock64();
+                    if (STAMP && w == 1 && lane == 0) stamps[2 + 8 * nb + j] = stamp_clock();
                     if (!side2) {
                         // T(j+2, j), block j-1 (for the owners, in the slot of A that nothing reads any more), then
                         // quadrant (0, 0) or (1, 1) of T(j+2, j+2)
@@ -1505,27 +1527,23 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                         wait_lds(p2done, (uint32_t)j, err, dead, lim);                 // L(j+1, j-1) formed
                         if (hf) {
                             update32_wave_q<0xC>(R2[2], R2[2], z.C2[p], z.P2[pp]);     // T(j+2, j+1)
-                            // L(j+2, j-1) for the output and the later kernels (the owners form their own copy)
-                            const size_t o = (size_t)CB * (j - 1);
-                            store_tile(L + (o + 3 * CB) * r + o, r, z.C2[p], lane, 64);
-                            store_tile_op(Lp + (size_t)op_pair(j + 2, j - 1) * CB * CB, z.C2[p], lane, 64);
-                            if (STAMP && lane == 0) stamps[2 + 9 * nb + j] = wall_clock64();
+                            if (STAMP && lane == 0) stamps[2 + 9 * nb + j] = stamp_clock();
                         } else {
                             update32_wave_q<0x3>(R2[2], R2[2], z.C2[p], z.P2[pp]);
                             update32_wave_q<0x4>(R2[3], R2[3], z.C2[p], z.C2[p]);      // T(j+2, j+2), (1, 0)
                         }
                     }
                 }
-                if (STAMP && w == 1 && lane == 0) stamps[2 + 4 * nb + j] = wall_clock64();
+                if (STAMP && w == 1 && lane == 0) stamps[2 + 4 * nb + j] = stamp_clock();
             }
             __syncthreads();
             // start the L2 write-back of this step's stores now; the publication at the next step's start then
             // finds the lines clean
             if (w == 4) asm volatile("buffer_wbl2 sc1" ::: "memory");
-            if (STAMP && tid == 0) stamps[2 + 4 * j] = wall_clock64();
+            if (STAMP && tid == 0) stamps[2 + 4 * j] = stamp_clock();
         }
         if (w == 3) publish(nb - 1);
-        if (STAMP && tid == 0) stamps[1 + 4 * nb] = wall_clock64();
+        if (STAMP && tid == 0) stamps[1 + 4 * nb] = stamp_clock();
     } else {
         // Owner part: tile row i, tiles T(i, s..e-1) in LDS. rt[k - s] = T(i, k); pn[k - s] = L(k, j) of the current
         // column block for the part's columns k < i; li = Li_j; pin = L(i, j) when another part of the row holds
@@ -1572,8 +1590,8 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 wait_flags_wave(f, ep, err, dead, lim);
             }
             __syncthreads();
-            if (hst) stamps[2 + 10 * nb + 6 * i] = wall_clock64();
-            if (bst) bs[0] = wall_clock64();
+            if (hst) stamps[2 + 10 * nb + 6 * i] = stamp_clock();
+            if (bst) bs[0] = stamp_clock();
             // one batch: Li_j; per column k, the finished L(j+1, j) or T(k, j) through block j-1; T(i, j) into pin
             if (q4)
                 load_tiles_to<OWNER_WMAX + 2, 256>(1 + nk + (mine ? 0 : 1), tid,
@@ -1586,15 +1604,15 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                                                 },
                                                 [&](int q) { return q == 0 ? CB : r; });   // Li_j's rows are 32 apart
             __syncthreads();
-            if (hst) stamps[3 + 10 * nb + 6 * i] = wall_clock64();
-            if (bst) bs[1] = wall_clock64();
+            if (hst) stamps[3 + 10 * nb + 6 * i] = stamp_clock();
+            if (bst) bs[1] = stamp_clock();
             // the panels: L(i, j) (in place in rt[j - s] or pin) and L(k, j) for the columns k >= j+2
             Tile& lij = mine ? rt[j - s] : pin;
             const int kp = k0 > j + 2 ? k0 : j + 2;
             const int np = 1 + (ke > kp ? ke - kp : 0);
             panels_inplace(np, [&](int q) -> Tile& { return q == 0 ? lij : pn[kp + q - 1 - s]; }, li);
-            if (hst) stamps[4 + 10 * nb + 6 * i] = wall_clock64();
-            if (bst) bs[2] = wall_clock64();
+            if (hst) stamps[4 + 10 * nb + 6 * i] = stamp_clock();
+            if (bst) bs[2] = stamp_clock();
             if (mine) {
                 // L(i, j): the output, and its packed form for the solve (released below, with the column credit)
                 if (q4) store_tile(L + (size_t)CB * i * r + (size_t)CB * j, r, lij);
@@ -1659,22 +1677,24 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
             };
             // T(i, k0..ke-1), then T(i, i)
             update_tiles(nk + (last && !upq ? 1 : 0), [&](int t) { return k0 + t < ke ? k0 + t : i; });
-            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this block's stores are complete before the barrier
+            // this block's stores complete before the barrier, so that wave 7's release covers them (at the
+            // hand-over the hand-over's own wait does)
+            if (!hand) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
             __syncthreads();
-            if (hst) stamps[6 + 10 * nb + 6 * i] = wall_clock64();
-            if (bst) bs[3] = wall_clock64();
+            if (hst) stamps[6 + 10 * nb + 6 * i] = stamp_clock();
+            if (bst) bs[3] = stamp_clock();
             if (hand) {
                 // hand T(i, i-3..i) to workgroup 0
                 for (int t = 0; t < 4; ++t)
                     store_tile(A + (size_t)CB * i * r + (size_t)CB * (i - 3 + t), r, rt[i - 3 + t - s]);
                 __builtin_amdgcn_s_waitcnt(0x0F70);
                 __syncthreads();
-                if (hst) stamps[7 + 10 * nb + 6 * i] = wall_clock64();
+                if (hst) stamps[7 + 10 * nb + 6 * i] = stamp_clock();
                 if (tid == 0) {
                     publish_flag(flagT + i, ep);
                     if (mine) credit(colcnt, j);   // L(i, i-4)'s packed form
                 }
-                if (hst) stamps[5 + 10 * nb + 6 * i] = wall_clock64();
+                if (hst) stamps[5 + 10 * nb + 6 * i] = stamp_clock();
             } else if (w == 7) {
                 // T(i, j+1) through block j for the next block's consumers, and the column credit for L(i, j);
                 // the other waves go on to the next block's wait meanwhile
@@ -1687,7 +1707,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                         if (mine) credit(colcnt, j);
                     }
                 }
-                if (STAMP && last && i == nb - 1 && lane == 0) bs[4] = wall_clock64();
+                if (STAMP && last && i == nb - 1 && lane == 0) bs[4] = stamp_clock();
             }
         }
     }

@@ -103,9 +103,10 @@ def traffic(fetch_csv, write_csv, shapes, copy_bytes=4 << 27):
     return out
 
 
-def mfma(csv_path, trace_csv, shapes, simds=1024, clock_ghz=2.4, cycles_per_mfma=32):
+def mfma(csv_path, trace_csv, shapes, simds=1024, clock_ghz=2.4):
     """per shape and family: SQ_INSTS_MFMA per launch and the MFMA pipes' busy fraction over the kernel's duration
-    (from a kernel trace of the same program): MFMAs x cycles per fp32 16x16x4 MFMA / (SIMDs x duration cycles)"""
+    (from a kernel trace of the same program): SQ_VALU_MFMA_BUSY_CYCLES (matrix-pipe cycles summed over the SIMDs:
+    32 per fp32 16x16x4 MFMA, 64 per fp32 32x32x2) / (SIMDs x duration cycles)"""
     counts = {}
     for counter in ("SQ_INSTS_MFMA", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES"):
         _, calls = _calls(csv_path, counter)
@@ -129,11 +130,12 @@ def mfma(csv_path, trace_csv, shapes, simds=1024, clock_ghz=2.4, cycles_per_mfma
     for shape, d in counts.items():
         for fam, c in d.items():
             n = statistics.mean(c.get("SQ_INSTS_MFMA", [0.0]))
+            busy = statistics.mean(c.get("SQ_VALU_MFMA_BUSY_CYCLES", [0.0]))
             us = statistics.mean(durs.get(shape, {}).get(fam, [float("nan")]))
             out.setdefault(shape, {})[fam] = {
                 "mfma_per_launch": n, "us": us,
-                "mfma_busy_frac": n * cycles_per_mfma / (simds * us * 1e-6 * clock_ghz * 1e9) if us == us else None,
-                "valu_mfma_busy_cycles": statistics.mean(c.get("SQ_VALU_MFMA_BUSY_CYCLES", [0.0])),
+                "mfma_busy_frac": busy / (simds * us * 1e-6 * clock_ghz * 1e9) if us == us else None,
+                "valu_mfma_busy_cycles": busy,
                 "sq_busy_cycles": statistics.mean(c.get("SQ_BUSY_CYCLES", [0.0]))}
     return out
 
