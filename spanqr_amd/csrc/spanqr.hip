@@ -1285,12 +1285,16 @@ size_t chol_lds_bytes(int r, int w) {
 // 2 + 10 nb + 6 i + s: the owner of row i's last part at its last block: s = 0 flags seen, 1 operands loaded,
 // 2 panels formed, 3 row handed over, 4 update done, 5 hand-over stores done; 2 + 16 nb + 8 j + s: the last row's
 // last part at block j: s = 0 flags seen, 1 operands loaded, 2 panels formed, 3 block done, 4 T(i, j+1) published.
-// Workgroups of eight wavefronts: waves 0-3 do the work described here (and wave 7 of workgroup 0 its turns at the
-// tile factor and the look-ahead); waves 4-7 share the owners' row update with them (two wavefronts per SIMD there,
-// so one's LDS traffic overlaps the other's MFMA chain) and otherwise only pass the same workgroup barriers.
+// Workgroups of eight wavefronts (workgroup 0: waves 0 and 7 the tile factor and the look-ahead in turn, waves 1, 2,
+// 5, 6 the row of step j+2, wave 3 the publication, wave 4 the early write-back; owners: all eight on the panels
+// and the row update, two wavefronts per SIMD so that one's LDS traffic overlaps the other's MFMA chain).
+// Flags: (j, j) workgroup 0's column j (L(j, j), Li_j, L(j+1, j), T(j+2, j)); (i, j), i > j, the tile T(i, j)
+// through block j-1 in its slot of A (an owner part, a block ahead); hand-over flag i, T(i, i-3..i) through block
+// i-4 (the last part of row i).
 // colcnt (may be null): per column block k, a counter (stride CC_STRIDE) that every producer of the packed operands
 // of column k (Li_k and L(i, k), i > k) raises once those are released, for the solve that runs in the same launch:
-// owner i credits column j-1 when it publishes L(i, j) and column i-4 when it hands its row over; workgroup 0 credits
+// the owner part holding T(i, j) credits column j at the release that ends block j (the last part's hand-over
+// release at its last block); workgroup 0 credits
 // column k at the release that opens step k+2 (its stores of column k's operands completed during step k+1), column
 // nb-2 at a release of its own in the last step, and column nb-1 (Li_{nb-1} alone) right after the last tile factor.
 // Column k is complete at 1 + max(0, nb - 4 - k) credits; the counters start at zero.
