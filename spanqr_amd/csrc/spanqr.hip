@@ -3891,39 +3891,53 @@ __global__ __launch_bounds__(256) void k_dust_raw(float* Z, int K, int r, const 
     }
 }
 
-// column norms of the raw draws: sqrt of the squares summed in double in ascending k (one thread per column, 64
-// columns per workgroup). The sum is one dependent chain per column; the loads are not: each thread keeps the rows
-// of the next 32-row group in flight while it adds the current group, so the chain, not the memory latency per
-// row, sets the time.
-constexpr int DUST_NORM_ROWS = 32;
-__global__ __launch_bounds__(64) void k_dust_norm(const float* Z, int K, int r, double* nrm, const uint64_t* tag,
-                                                  uint64_t want) {
+// column norms of the raw draws: sqrt of the squares summed in double in ascending k, one dependent chain per column.
+// A workgroup takes 32 columns: its four wavefronts stream 128-row chunks of them into a ring of three LDS buffers,
+// two chunks ahead, while lanes 0-31 of wave 0 run the chains over the chunk in LDS -- so the chains, not the memory
+// latency of a few wavefronts' loads, set the time.
+constexpr int DN_COLS = 32, DN_ROWS = 128, DN_BUF = 3;
+__global__ __launch_bounds__(256) void k_dust_norm(const float* Z, int K, int r, double* nrm, const uint64_t* tag,
+                                                   uint64_t want) {
     if (*tag == want) return;
-    const int c = blockIdx.x * 64 + threadIdx.x;
-    if (c >= r) return;
-    constexpr int U = DUST_NORM_ROWS;
-    float a[U], b[U];
-    auto load = [&](float (&v)[U], int k0) {
+    __shared__ float buf[DN_BUF][DN_ROWS][DN_COLS];
+    const int c0 = blockIdx.x * DN_COLS, tid = threadIdx.x;
+    const int nch = (K + DN_ROWS - 1) / DN_ROWS;
+    float4 v[4];   // this thread's part of a chunk: rows (tid >> 3) + 32 u, columns 4 (tid & 7) .. + 3
+    auto load = [&](int t) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = (k0 + u < K) ? Z[(size_t)(k0 + u) * r + c] : 0.0f;
+        for (int u = 0; u < 4; ++u) {
+            const int row = t * DN_ROWS + (tid >> 3) + 32 * u;
+            v[u] = row < K ? *reinterpret_cast<const float4*>(Z + (size_t)row * r + c0 + 4 * (tid & 7))
+                           : float4{0.f, 0.f, 0.f, 0.f};
+        }
     };
-    auto add = [&](const float (&v)[U], int k0, double& acc) {
+    auto store = [&](int t) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (k0 + u < K) {
-                const double z = (double)v[u];
+        for (int u = 0; u < 4; ++u)
+            *reinterpret_cast<float4*>(&buf[t % DN_BUF][(tid >> 3) + 32 * u][4 * (tid & 7)]) = v[u];
+    };
+    load(0);
+    store(0);
+    if (nch > 1) {
+        load(1);
+        store(1);
+    }
+    __syncthreads();
+    double acc = 0.0;
+    for (int t = 0; t < nch; ++t) {
+        if (t + 2 < nch) load(t + 2);
+        if (tid < DN_COLS) {
+            const int rows = K - t * DN_ROWS < DN_ROWS ? K - t * DN_ROWS : DN_ROWS;
+            for (int k = 0; k < rows; ++k) {
+                const double z = (double)buf[t % DN_BUF][k][tid];
                 acc += z * z;
             }
-    };
-    double acc = 0.0;
-    load(a, 0);
-    for (int k0 = 0; k0 < K; k0 += 2 * U) {
-        load(b, k0 + U);
-        add(a, k0, acc);
-        load(a, k0 + 2 * U);
-        add(b, k0 + U, acc);
+        }
+        // buffer (t + 2) % 3 was last read in the previous iteration, before its barrier
+        if (t + 2 < nch) store(t + 2);
+        __syncthreads();
     }
-    nrm[c] = sqrt(acc);
+    if (tid < DN_COLS) nrm[c0 + tid] = sqrt(acc);
 }
 
 __global__ __launch_bounds__(256) void k_dust_scale(float* Z, int K, int r, const double* nrm, const uint64_t* tag,
@@ -4007,7 +4021,7 @@ int spanqr_orth_f32_noalloc(int K, int r, const float* X, long ldx, float* Q, lo
     hipStream_t st = (hipStream_t)stream;
     const int eblocks = (int)(((size_t)K * r + 255) / 256 < 2048 ? ((size_t)K * r + 255) / 256 : 2048);
     k_dust_raw<<<eblocks, 256, 0, st>>>(p.Z, K, r, tag, want);
-    k_dust_norm<<<(r + 63) / 64, 64, 0, st>>>(p.Z, K, r, nrm, tag, want);
+    k_dust_norm<<<r / DN_COLS, 256, 0, st>>>(p.Z, K, r, nrm, tag, want);   // r is a multiple of 32
     k_dust_scale<<<eblocks, 256, 0, st>>>(p.Z, K, r, nrm, tag, want);
     k_noalloc_prep<<<1, 256, 0, st>>>(p.flags, FLAG_STRIDE, tag, want);
     HIPCHK(hipGetLastError());
