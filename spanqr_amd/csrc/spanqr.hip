@@ -602,11 +602,13 @@ __global__ __launch_bounds__(512) void k_gram32(const MatsIn As, long lda, int K
 //     the panel L(j+2, j-1), waves 2 and 6 apply the block j-2 update of T(j+2, j+1) that the owner leaves out, and
 //     the four apply block j-1 to T(j+2, j), T(j+2, j+1) and the lower quadrants of T(j+2, j+2).
 //   * Tile row i >= 4 is owned for the whole factorisation, in LDS, by ceil((i + 1) / OWNER_W) workgroups (parts),
-//     each holding a run of its tiles. For column block j = 0..i-4 in order: panel L(i, j) = T(i, j) Li_j^T
-//     (published by the part holding T(i, j)), then T(i, k) -= L(i, j) L(k, j)^T for each part's k = j+1..i with the
-//     other rows' panels of block j fetched together (at the last block, j = i-4, T(i, i-1) is left to workgroup 0);
-//     after block i-4 the last part hands T(i, i-3..i) to workgroup 0, two steps before workgroup 0 factors T(i, i).
-//     The panel L(j+3, j) of the row just handed over a part forms itself from the handed-over T(j+3, j).
+//     each holding a run of its tiles. For column block j = 0..i-4 in order, a part waits for one round of flags
+//     (workgroup 0's column j, and the tiles T(k, j) through block j-1 that other parts published a block ahead),
+//     loads Li_j and those tiles, forms every panel it needs itself -- L(k, j) = T(k, j) Li_j^T, its own L(i, j)
+//     included -- and applies T(i, k) -= L(i, j) L(k, j)^T to its tiles k = j+1..i (at the last block, j = i-4,
+//     T(i, i-1) is left to workgroup 0); then it publishes T(i, j+1) through block j for the next block's
+//     consumers. After block i-4 the last part hands T(i, i-3..i) to workgroup 0, two steps before workgroup 0
+//     factors T(i, i).
 // Every element keeps the reference order: updates by column block in increasing order, each one MFMA chain over the
 // block's 32 columns. A producer publishes with an agent-scope release after its stores; a consumer polls with
 // bounded waits (after `lim` polls it records an error and stops waiting, so the kernel always ends). Each
