@@ -7,7 +7,7 @@
  *
  * Conventions
  *   - Matrices are row-major fp32 in device memory; X and Q need 16-byte alignment and a leading dimension that is a
- *     multiple of 4 (the contiguous [K, r] case always qualifies). X is never written.
+ *     multiple of 4 and below 2^24 (the contiguous [K, r] case always qualifies). X is never written.
  *   - r must be a multiple of 32 with 32 <= r <= 1024 (kcholf at full width), or a multiple of 256 with
  *     512 < r <= 4096 (the column-blocked path: block Gram-Schmidt over 256-column blocks, as the reference's orth
  *     does above 512 columns; spanqr_plan_create picks it for those r); K >= r.

@@ -44,6 +44,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int TB = 64;            // Gram output tile (tri.py:362 bt = 64)
 constexpr int CB = 32;            // Cholesky tile, TRSM column block (chol.cu:15, tri.py:406)
 constexpr int BK = 32;            // rows per Kahan chunk (tri.py:352-355)
+constexpr int BUF_RSRC_WORD3 = 0x00020000;   // buffer resource word 3 for raw 32-bit loads (CDNA)
 constexpr int AMAX_BLOCKS = 256;  // partial maxima written by k_amax (one per workgroup)
 constexpr int TS = 33;            // row stride of 32x32 LDS tiles
 constexpr uint32_t SPIN_LIMIT = 1u << 20;
@@ -66,6 +67,14 @@ struct MatsIn {
 struct MatsOut {
     float* p[SPANQR_MAX_BATCH];
 };
+
+// a wave-uniform address held in scalar registers (a buffer resource built from a value the compiler keeps in vector
+// registers would be wrapped in a loop over its distinct values)
+__device__ __forceinline__ void* uniform_ptr(const void* p) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 
 __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -436,8 +445,9 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 // Gram of a short X in one launch, the split reduction inside the workgroup (tri.py:255-297, 324-375 with the sum
 // over splits of tri.py:297/375): workgroup u computes the upper 32x32 tile u = (ti, tj) of G = A^T A over all K rows
 // as two row splits of KS rows, one per group of four wavefronts (waves 0-3 rows [0, KS), waves 4-7 [KS, K)), each
-// wavefront a 16x16 quadrant of the tile. The 32-row chunks of both splits are staged through LDS together (two
-// buffers, one barrier per chunk), G32_DEPTH chunks fetched into registers ahead of the one being multiplied.
+// wavefront a 16x16 quadrant of the tile. Each wavefront reads its two 16-column operand strips of every 32-row
+// chunk straight into registers in the MFMA layout, G32_DEPTH chunks ahead of the one being multiplied, and runs on
+// its own (no LDS staging and no workgroup barrier until the splits are summed).
 // KAHAN: each chunk's MFMA chain starts from 0 and is added with Kahan compensation; otherwise one chain runs over the
 // split. SCALE: operands are s * a (the pass-1 power-of-2 scale). The splits are summed in fp64 in split order,
 // rounded once, and the tile and its mirror stored in G. MODE 0 also writes the tile's ||G||_F^2 partial npart[u]
@@ -448,8 +458,7 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
 // it measured faster than the split Gram, its reduction launch and the gap between them: short X with many tiles
 // (the plan's rule).
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int G32_LD = 48;   // LDS row stride of a chunk panel: a quadrant read's four row groups hit distinct banks
-constexpr int G32_DEPTH = 6; // chunks of each split in flight (in registers) ahead of the one being multiplied
+constexpr int G32_DEPTH = 4; // chunks in flight per wavefront (16 loads each; vmcnt counts at most 63 outstanding)
 template <bool KAHAN, bool SCALE, int MODE>
 __global__ __launch_bounds__(512) void k_gram32(const MatsIn As, long lda, int K, int nb, int KS,
                                                 const uint32_t* __restrict__ amax_part, float* __restrict__ G,
@@ -464,33 +473,41 @@ __global__ __launch_bounds__(512) void k_gram32(const MatsIn As, long lda, int K
     int ti, tj;
     upper_tile(u, nb, ti, tj);
     const bool diag = ti == tj;
-    __shared__ float sA[2][2][BK][G32_LD];   // [buffer][split][row of the chunk][column of tile ti]
-    __shared__ float sB[2][2][BK][G32_LD];   // the same for tile column tj
     __shared__ float xch[4][4][64];          // split 1's accumulators, per quadrant
     __shared__ double qn[4];
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = w >> 2, q = w & 3, qi = q >> 1, qj = q & 1, l16 = lane & 15, lk = lane >> 4;
-    // the split of this thread's group and its float4 of each 32 x 32 chunk panel
-    const int gt = tid & 255, grow = gt >> 3, gc4 = gt & 7;
     const int k0 = g * KS, k1 = (k0 + KS < K) ? k0 + KS : K;
     const int nch = k1 > k0 ? (k1 - k0 + BK - 1) / BK : 0;       // this split's chunks
-    const int nch0 = ((KS < K ? KS : K) + BK - 1) / BK;          // split 0's chunks (the longer split)
-    // stages: a multiple of G32_DEPTH, every one unconditional (a stage past the chunks stores zeros and skips the
-    // MFMAs), so no load sits under a branch and each stage waits only for its own slot
-    const int nst = (nch0 + G32_DEPTH - 1) / G32_DEPTH * G32_DEPTH;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f}, comp = {0.f, 0.f, 0.f, 0.f};
-    // Slot d holds chunk c with c % G32_DEPTH == d. Loads are unconditional: a chunk past split 0's last reads that
-    // one again (unused); rows past the split read row k1 - 1 (in bounds -- the second split's k1 - 1 >= 0 even when
-    // it is empty -- and zeroed), so the compiler keeps them where they are issued.
-    float4 ra[G32_DEPTH], rb[G32_DEPTH];
-    const float* __restrict__ pa = A + ti * CB + 4 * gc4;
-    const float* __restrict__ pb = A + tj * CB + 4 * gc4;   // (a diagonal tile reads its panel twice: cache hits)
-    auto gload = [&](int c, float4& xa, float4& xb) {
-        const int cc = c < nch0 ? c : nch0 - 1;
-        const int k = k0 + cc * BK + grow;
-        const size_t off = (size_t)(k < k1 ? k : k1 - 1) * lda;
-        xa = *reinterpret_cast<const float4*>(pa + off);
-        xb = *reinterpret_cast<const float4*>(pb + off);
+    // Each wavefront reads its own operands straight into the MFMA layout: lane (l16, lk) takes column 16 qi + l16 of
+    // tile column ti and 16 qj + l16 of tj, rows 4 kk + lk (kk = 0..7) of each 32-row chunk, through a buffer
+    // resource per chunk and strip whose range ends at the split's last row: rows past the split read as 0 without a
+    // mask (the hardware's range check), and the per-lane byte offsets are the same for every chunk. Slot d holds
+    // chunk c with c % G32_DEPTH == d. Loads are unconditional: a chunk past the split's last reads that one again
+    // (unused; an empty split's range is empty, so nothing is read).
+    float ra[G32_DEPTH][BK / 4], rb[G32_DEPTH][BK / 4];
+    const char* baseA = reinterpret_cast<const char*>(A + ti * CB + 16 * qi);
+    const char* baseB = reinterpret_cast<const char*>(A + tj * CB + 16 * qj);
+    uint32_t off[BK / 4];   // lda < 2^24 (checked by the host): 32 rows of bytes fit 31 bits
+#pragma unroll
+    for (int kk = 0; kk < BK / 4; ++kk) off[kk] = ((uint32_t)(4 * kk + lk) * (uint32_t)lda + (uint32_t)l16) * 4u;
+    const int last = nch > 0 ? nch - 1 : 0;
+    auto gload = [&](int c, float* xa, float* xb) {
+        const int kr = k0 + (c < last ? c : last) * BK;
+        int nv = k1 - kr;
+        nv = nv < 0 ? 0 : (nv > BK ? BK : nv);
+        const int num = __builtin_amdgcn_readfirstlane(nv * (int)lda * 4);
+        const size_t rowb = (size_t)(kr < K ? kr : 0) * (size_t)lda * 4;
+        const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(baseA + rowb), (short)0, num,
+                                                                            BUF_RSRC_WORD3);
+        const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(baseB + rowb), (short)0, num,
+                                                                            BUF_RSRC_WORD3);
+#pragma unroll
+        for (int kk = 0; kk < BK / 4; ++kk) {
+            xa[kk] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rA, (int)off[kk], 0, 0));
+            xb[kk] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rB, (int)off[kk], 0, 0));
+        }
     };
 #pragma unroll
     for (int d = 0; d < G32_DEPTH; ++d) {
@@ -499,56 +516,41 @@ __global__ __launch_bounds__(512) void k_gram32(const MatsIn As, long lda, int K
     }
     float sc = 1.0f;
     if (SCALE) sc = block_scale512(amax_part);   // (its reduction's barriers wait behind the first loads)
-    for (int c0 = 0; c0 < nst; c0 += G32_DEPTH) {
+    // chunk c (in slot d) into the sum; REFILL: then load chunk c + G32_DEPTH into the slot, after the MFMAs have
+    // read it, so the loads reuse the slot's registers (no copies, and no wait, where the loop closes)
+    auto stage = [&](int d, int c, bool refill) {
+        float xa[BK / 4], yb[BK / 4];
 #pragma unroll
-        for (int d = 0; d < G32_DEPTH; ++d) {
-            const int c = c0 + d;
-            const int bf = c & 1;            // LDS buffers alternate: one barrier per stage
-            // rows past the split are zeroed with a bit mask (no branch: a branch that overwrites a loaded register
-            // waits for every load in flight)
-            const uint32_t keep = k0 + c * BK + grow < k1 ? 0xffffffffu : 0u;
-            float4 va = ra[d], vb = rb[d];
-            if (SCALE) {
-                va.x = sc * va.x; va.y = sc * va.y; va.z = sc * va.z; va.w = sc * va.w;
-                vb.x = sc * vb.x; vb.y = sc * vb.y; vb.z = sc * vb.z; vb.w = sc * vb.w;
-            }
-            va.x = __uint_as_float(__float_as_uint(va.x) & keep);
-            va.y = __uint_as_float(__float_as_uint(va.y) & keep);
-            va.z = __uint_as_float(__float_as_uint(va.z) & keep);
-            va.w = __uint_as_float(__float_as_uint(va.w) & keep);
-            vb.x = __uint_as_float(__float_as_uint(vb.x) & keep);
-            vb.y = __uint_as_float(__float_as_uint(vb.y) & keep);
-            vb.z = __uint_as_float(__float_as_uint(vb.z) & keep);
-            vb.w = __uint_as_float(__float_as_uint(vb.w) & keep);
-            *reinterpret_cast<float4*>(&sA[bf][g][grow][4 * gc4]) = va;
-            *reinterpret_cast<float4*>(&sB[bf][g][grow][4 * gc4]) = vb;
-            __syncthreads();
-            gload(c + G32_DEPTH, ra[d], rb[d]);   // refill the slot just stored
-            __builtin_amdgcn_sched_barrier(0);     // the loads go out before the MFMAs
-            if (c < nch) {                         // a chunk wholly past the split is not part of the sum
-                f32x4 part = KAHAN ? f32x4{0.f, 0.f, 0.f, 0.f} : acc;
-                float xa[BK / 4], yb[BK / 4];
-#pragma unroll
-                for (int kk = 0; kk < BK / 4; ++kk) {
-                    xa[kk] = sA[bf][g][4 * kk + lk][16 * qi + l16];
-                    yb[kk] = sB[bf][g][4 * kk + lk][16 * qj + l16];
-                }
-#pragma unroll
-                for (int kk = 0; kk < BK / 4; ++kk) part = mfma(xa[kk], yb[kk], part);
-                if (KAHAN) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const float y = part[v] - comp[v];
-                        const float t = acc[v] + y;
-                        comp[v] = (t - acc[v]) - y;
-                        acc[v] = t;
-                    }
-                } else {
-                    acc = part;
-                }
-            }
+        for (int kk = 0; kk < BK / 4; ++kk) {
+            xa[kk] = SCALE ? sc * ra[d][kk] : ra[d][kk];
+            yb[kk] = SCALE ? sc * rb[d][kk] : rb[d][kk];
         }
+        f32x4 part = KAHAN ? f32x4{0.f, 0.f, 0.f, 0.f} : acc;
+#pragma unroll
+        for (int kk = 0; kk < BK / 4; ++kk) part = mfma(xa[kk], yb[kk], part);
+        if (refill) gload(c + G32_DEPTH, ra[d], rb[d]);
+        if (KAHAN) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float y = part[v] - comp[v];
+                const float t = acc[v] + y;
+                comp[v] = (t - acc[v]) - y;
+                acc[v] = t;
+            }
+        } else {
+            acc = part;
+        }
+    };
+    // whole rounds of G32_DEPTH chunks with refills (the last round's refills read chunks past the split: unused),
+    // then the remaining chunks from the slots as they stand
+    const int nfull = nch / G32_DEPTH * G32_DEPTH;
+    for (int c0 = 0; c0 < nfull; c0 += G32_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < G32_DEPTH; ++d) stage(d, c0 + d, true);
     }
+#pragma unroll
+    for (int d = 0; d < G32_DEPTH - 1; ++d)
+        if (nfull + d < nch) stage(d, nfull + d, false);
     __syncthreads();
     if (g == 1)
 #pragma unroll
@@ -2724,12 +2726,15 @@ bool gram_short_rule(int K, int r) { return K <= GRAM_SHORT_KMAX && r >= GRAM_SH
 int gram_short_rows(int K) { return ((K + 1) / 2 + BK - 1) / BK * BK; }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+// the kernels address 32 rows of a matrix with 32-bit byte offsets (the short Gram's buffer loads)
+constexpr long LD_LIMIT = 1L << 24;
 
 int check_mat(const spanqr_plan* p, const float* M, long ld, const char* name) {
     if (M == nullptr) return fail(SPANQR_EINVAL, "%s is null", name);
     if (!aligned16(M)) return fail(SPANQR_EINVAL, "%s must be 16-byte aligned", name);
-    if (ld < p->r || (ld & 3)) return fail(SPANQR_EINVAL, "leading dimension of %s (%ld) must be >= r and a multiple of 4",
-                                           name, ld);
+    if (ld < p->r || (ld & 3) || ld >= LD_LIMIT)
+        return fail(SPANQR_EINVAL, "leading dimension of %s (%ld) must be >= r, below 2^24 and a multiple of 4", name,
+                    ld);
     return SPANQR_OK;
 }
 

@@ -117,6 +117,7 @@ def test_abi_rejects_bad_operands(cuda):
     assert f(plan.handle, X.data_ptr() + 4, r, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2, st) == -1   # alignment
     assert f(plan.handle, None, r, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2, st) == -1
     assert f(plan.handle, X.data_ptr(), r, Q.data_ptr(), r - 4, 5e-7, 1e-7, 1e-8, 2, st) == -1   # ldq < r
+    assert f(plan.handle, X.data_ptr(), 1 << 24, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2, st) == -1  # ldx >= 2^24
     assert _lib.lib().spanqr_last_error()
 
 
