@@ -3486,7 +3486,8 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
 int spanqr_plan_create_borth(int K, int r, int b, int reorth, int device, spanqr_plan** out) {
     if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
     *out = nullptr;
-    if (b < 64 || b > 512 || b % 64 != 0) return fail(SPANQR_EINVAL, "b = %d: must be a multiple of 64 in [64, 512]", b);
+    if (b < 64 || b > KCH_MAX_R || b % 64 != 0)
+        return fail(SPANQR_EINVAL, "b = %d: must be a multiple of 64 in [64, %d]", b, KCH_MAX_R);
     if (r <= b || r % b != 0 || r > SPANQR_MAX_R)
         return fail(SPANQR_EINVAL, "r = %d: must be a multiple of b = %d above it, at most %d", r, b, SPANQR_MAX_R);
     if (K < r) return fail(SPANQR_EINVAL, "K = %d < r = %d", K, r);

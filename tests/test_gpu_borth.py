@@ -62,7 +62,8 @@ def test_borth_block_width_and_dispatch(cuda):
 # single projection without the reorthogonalisation
 OPTION_CASES = [(1024, 1024, 512, True, "mixed_c4"), (1000, 768, 128, True, "rank_half"),
                 (1000, 768, 128, False, "mixed_c4"), (1400, 640, 64, True, "zero"), (2048, 1536, 512, False, "dup_cols"),
-                (1200, 1024, 256, False, "ttf_cu4_t1e-2")]
+                (1200, 1024, 256, False, "ttf_cu4_t1e-2"), (1600, 1536, 768, True, "mixed_c4"),
+                (2100, 2048, 1024, True, "rank_half"), (1100, 960, 320, False, "mixed_c4")]
 
 
 @pytest.mark.parametrize("K,r,b,reorth,name", OPTION_CASES)
