@@ -143,13 +143,12 @@ __device__ float block_scale128(const uint32_t* __restrict__ part) {
     return pow2_scale_bits(t);
 }
 
+// The 100 MHz wall clock (the s_memrealtime counter) for the instrumented Cholesky's stamps
+__device__ __forceinline__ uint64_t stamp_clock() { return __builtin_amdgcn_s_memrealtime(); }
+
 // Pivot reciprocal square root (the reference uses CUDA rsqrtf, chol.cu:45): the published fast inverse square root
 // start 0x5f375a86 - (bits >> 1) (C. Lomont, "Fast Inverse Square Root", 2003) and three Newton steps
 // y <- y * (1.5 - (0.5x * y) * y), each bracket one fma, so the result is a fixed function of x.
-// the 100 MHz wall clock for the instrumented Cholesky's stamps (the s_memrealtime counter, read without waiting for
-// outstanding memory operations, so a stamp does not change when stores complete)
-__device__ __forceinline__ uint64_t stamp_clock() { return __builtin_amdgcn_s_memrealtime(); }
-
 __device__ __forceinline__ float rsqrt_sw(float x) {
     float y = __uint_as_float(0x5f375a86u - (__float_as_uint(x) >> 1));
     const float h = 0.5f * x;
