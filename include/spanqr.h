@@ -83,7 +83,7 @@ int spanqr_plan_create_batched(int K, int r, int batch, int device, spanqr_plan*
 /* Column-blocked plan for borth(X, b, reorth) (candidates/kbig.py:69-95, whose parameters these are): block
  * Gram-Schmidt over b-column blocks, each block projected twice against the finished ones and orthonormalised by
  * kcholf at width b with its column slice of the K x r dust; with reorth != 0 projected and orthonormalised once more
- * (kbig.py:91-92). b a multiple of 64 in [64, 1024], r > b a multiple of b up to 4096, K >= r (the reference runs
+ * (kbig.py:91-92). b a multiple of 32 in [32, 1024], r > b a multiple of b up to 4096, K >= r (the reference runs
  * kcholf at full width when r <= b or r % b != 0: the caller's choice, kbig.py:77-78). spanqr_orth_f32 on the plan
  * runs it (eps, alpha, tau, ns apply to every block's kcholf); spanqr_plan_create for r > 512 is b = 256 with reorth,
  * the call orth.py:19 makes. */

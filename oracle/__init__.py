@@ -298,11 +298,11 @@ def project(P, C, KS):
 
 
 def borth(X, b=BW, reorth=True, eps=5e-7, alpha=1e-7, tau=1e-8, ns=2):
-    """Q = borth(X, b, reorth) (kbig.py:69-95), b a multiple of 64, r > b a multiple of b; the default b is the 256
+    """Q = borth(X, b, reorth) (kbig.py:69-95), b a multiple of 32, r > b a multiple of b; the default b is the 256
     orth.py:19 passes"""
     X = _c32(X)
     K, r = X.shape
-    assert b % 64 == 0 and r % b == 0 and r > b
+    assert b % 32 == 0 and r % b == 0 and r > b
     Q = np.empty((K, r), np.float32)
     lib().spqo_borth(X, r, K, r, b, int(bool(reorth)), float(np.float32(eps)), float(np.float32(alpha)),
                      float(np.float32(tau)), ns, Q, r)

@@ -633,7 +633,7 @@ void spqo_project(const float* P, long ldp, int K, int j, const float* C, long l
 /* it. Per block j: W = fp32(s * X[:, j:j+b]); for j > 0 W = project(W) twice; Q_j = orth_z(W, dust slice) (_kf = */
 /* kcholqr_f with the dust given, kbig.py:48-63); with reorth, for j > 0 W = project(Q_j), Q_j = orth_z(W, dust   */
 /* slice). P = Q[:, :j], the finished blocks. Every orth_z uses the b-column split rule; every projection the rule */
-/* for its (j / 64) (b / 64) tiles. b a multiple of 64, r a multiple of b.                                       */
+/* for its ceil(j / 64) ceil(b / 64) tiles. b a multiple of 32, r a multiple of b.                               */
 /* ------------------------------------------------------------------------------------------------------------ */
 void spqo_borth(const float* X, long ldx, int K, int r, int b, int reorth, float eps, float alpha, float tau_rel,
                 int ns, float* Q, long ldq) {
@@ -644,7 +644,7 @@ void spqo_borth(const float* X, long ldx, int K, int r, int b, int reorth, float
     spqo_dust(K, r, Zf);
     const int KSb = spqo_gram_rows(K, b);   /* the block's kcholf: the Gram of a K x b block, either form */
     for (int j = 0; j < r; j += b) {
-        const int KSp = j > 0 ? spqo_split_rows(K, (j / TB) * (b / TB)) : 0;
+        const int KSp = j > 0 ? spqo_split_rows(K, ((j + TB - 1) / TB) * ((b + TB - 1) / TB)) : 0;
         float* Qj = Q + j;
         const float* Zj = Zf + (PLANTED(13) ? 0 : j);   /* 13: every block gets the first dust slice */
         for (int k = 0; k < K; ++k)

@@ -229,13 +229,13 @@ __device__ __forceinline__ void upper_tile(int u, int nt, int& ti, int& tj) {
 
 // CROSS: partials of A^T B instead (the block projection of the column-blocked path, kbig.py:88-89): every tile
 // u = ti * ntb + tj of the (columns of A) x (ntb * 64 columns of B) product, A's panel ti against B's panel tj.
-// rc: the columns of A; when r % 64 == 32 the last tile column is half outside A and those columns read as 0 (they
-// only feed outputs past r, which are never read).
+// rc: the columns of A (rcb: of B, CROSS); when they end at a multiple of 32 but not of 64 the last tile column is
+// half outside and those columns read as 0 (they only feed outputs past the bound, which are never read).
 template <bool KAHAN, bool SCALE, bool CROSS = false, int NCH = 1>
 __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, int nt, int KS,
                                               const uint32_t* __restrict__ amax_part, float* __restrict__ P,
                                               const float* __restrict__ Bx = nullptr, long ldb = 0, int ntb = 0,
-                                              int rc = 1 << 30) {
+                                              int rc = 1 << 30, int rcb = 1 << 30) {
     const int u = blockIdx.x, sp = blockIdx.y, U = gridDim.x;
     const float* __restrict__ A = As.p[blockIdx.z];
     amax_part += (size_t)blockIdx.z * AMAX_BLOCKS;
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
     // multiplied; rows past the split read row k1 - 1 (in bounds) and are zeroed, so the loads are unconditional
     float4 ra[NCH], rb[NCH];
     const int grow = tid >> 4, gc4 = tid & 15;   // this thread's float4 of each 32 x 64 chunk
-    const bool ina = ti * TB + 4 * gc4 < rc, inb = CROSS || tj * TB + 4 * gc4 < rc;
+    const bool ina = ti * TB + 4 * gc4 < rc, inb = tj * TB + 4 * gc4 < (CROSS ? rcb : rc);
     auto gload = [&](int kc) {
 #pragma unroll
         for (int h = 0; h < NCH; ++h) {
@@ -413,8 +413,9 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
     for (; s < S; ++s) sum = sum + (double)p[(size_t)s * stride];
     const float g = (float)sum;
     const int gi = ti * TB + row, gj = tj * TB + col;
-    // a tile past r (r % 64 == 32) holds entries outside G: neither written nor counted in the norm
-    const bool in = MODE == 2 || (gi < r && gj < r);
+    // a tile past r (r % 64 == 32) holds entries outside G: neither written nor counted in the norm; MODE 2's rows
+    // past P's columns are written (the product has room for them, and nothing reads them), its columns past r not
+    const bool in = MODE == 2 ? gj < r : (gi < r && gj < r);
     if (MODE == 0) {
         if (in) {
             G[(size_t)gi * r + gj] = g;
@@ -435,7 +436,7 @@ __global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ P, int
             G[(size_t)gi * r + gj] = d;
             if (ti != tj) G[(size_t)gj * r + gi] = d;
         }
-    } else {
+    } else if (in) {
         G[(size_t)gi * r + gj] = g;
     }
 }
@@ -2329,7 +2330,8 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
         for (int q = 0; q < MS / 16; ++q) {
             const int idx = tid + 256 * q, row = idx >> 4, c4 = idx & 15;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (SUB || col0 + 4 * c4 < r)   // columns past r (r % 64 == 32) feed only outputs that are not written
+            // columns past r (SUB: past ldd, B's columns; a multiple of 32) feed only outputs that are not written
+            if (col0 + 4 * c4 < (SUB ? ldd : r))
                 v = *reinterpret_cast<const float4*>(D + (size_t)(m0 + row) * ldD + col0 + 4 * c4);
             *reinterpret_cast<float4*>(&sD[row][4 * c4]) = v;
         }
@@ -2347,7 +2349,7 @@ __global__ __launch_bounds__(256) void k_nsapply(const MatsIn Ys, long ldy, int 
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int row = row0 + 16 * rb + 4 * lk + v, col = col0 + 16 * (cbase + c) + l16;
-            if (row < K && (SUB || col < r)) {
+            if (row < K && col < (SUB ? ldd : r)) {
                 const float cv = Cin[(size_t)row * ldC + col];
                 Out[(size_t)row * ldo + col] = failed ? __builtin_nanf("") : SUB ? cv - acc[c][v] : cv + acc[c][v];
             }
@@ -3347,6 +3349,10 @@ size_t plan_layout(spanqr_plan* p, char* base) {
 
 namespace {
 
+// 64x64 tiles of a projection's P^T C, P with j columns and C with bw (the last tile row and column half used where
+// either is an odd multiple of 32); the split rule takes this count
+int proj_tiles(int j, int bw) { return ((j + TB - 1) / TB) * ((bw + TB - 1) / TB); }
+
 // Column-blocked plan: a bw-column block plan plus the blocked path's own buffers (no Gram or Cholesky of its own).
 int create_blocked(int K, int r, int bw, bool reorth, int device, spanqr_plan** out) {
     spanqr_plan* p = new spanqr_plan;
@@ -3359,7 +3365,7 @@ int create_blocked(int K, int r, int bw, bool reorth, int device, spanqr_plan** 
     size_t maxp = 0;   // split partials of the largest projection (U = (j / 64) (bw / 64) tiles for j = r - bw)
     for (int jb = 1; jb < p->nblk; ++jb) {
         int S = 0, KS = 0;
-        const int U = (bw * jb / TB) * (bw / TB);
+        const int U = proj_tiles(bw * jb, bw);
         split_policy(K, U, &S, &KS);
         if ((size_t)S * U > maxp) maxp = (size_t)S * U;
     }
@@ -3402,18 +3408,24 @@ int create_blocked(int K, int r, int bw, bool reorth, int device, spanqr_plan** 
 // order, tri.py's Gram rule for the split count), then one MFMA chain per element of P T, subtracted once.
 void project(const spanqr_plan* p, const float* Q, long ldq, int j, const float* Cin, long ldc, float* Out,
              hipStream_t st) {
-    const int BW = p->bw;
-    const int U = (j / TB) * (BW / TB);
+    const int BW = p->bw, ntb = (BW + TB - 1) / TB;
+    const int U = proj_tiles(j, BW);
     int S = 0, KS = 0;
     split_policy(p->K, U, &S, &KS);
     const MatsIn P = mats_in(&Q, 1);
     if (KS <= GRAM_DEEP_KS)
-        k_gram<false, false, true, 2><<<dim3(U, S), 512, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, BW / TB);
+        k_gram<false, false, true, 2><<<dim3(U, S), 512, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, ntb,
+                                                                 j, BW);
     else
-        k_gram<false, false, true, 1><<<dim3(U, S), 512, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, BW / TB);
-    k_reduce<2><<<dim3(16, U), 256, 0, st>>>(p->Tp, S, BW / TB, BW, p->T, nullptr);
-    k_nsapply<true, 64><<<dim3((p->K + 31) / 32, BW / 64), 256, 0, st>>>(P, ldq, p->K, j, p->T, mats_out(&Out, 1), BW, Cin,
-                                                                    ldc, BW);
+        k_gram<false, false, true, 1><<<dim3(U, S), 512, 0, st>>>(P, ldq, p->K, 0, KS, p->bamax, p->Tp, Cin, ldc, ntb,
+                                                                 j, BW);
+    k_reduce<2><<<dim3(16, U), 256, 0, st>>>(p->Tp, S, ntb, BW, p->T, nullptr);
+    // the chain over P's j columns in 64-column steps, or 32 where j is an odd multiple of 32 (no step past j)
+    const dim3 ag((p->K + 31) / 32, ntb);
+    if (j % 64 == 0)
+        k_nsapply<true, 64><<<ag, 256, 0, st>>>(P, ldq, p->K, j, p->T, mats_out(&Out, 1), BW, Cin, ldc, BW);
+    else
+        k_nsapply<true, 32><<<ag, 256, 0, st>>>(P, ldq, p->K, j, p->T, mats_out(&Out, 1), BW, Cin, ldc, BW);
 }
 
 // borth (kbig.py:69-95, BCGS2 over bw-column blocks; orth.py:18-19 calls it with 256): per block, W = s X_blk,
@@ -3485,8 +3497,8 @@ int spanqr_plan_create(int K, int r, int device, spanqr_plan** out) {
 int spanqr_plan_create_borth(int K, int r, int b, int reorth, int device, spanqr_plan** out) {
     if (out == nullptr) return fail(SPANQR_EINVAL, "out is null");
     *out = nullptr;
-    if (b < 64 || b > KCH_MAX_R || b % 64 != 0)
-        return fail(SPANQR_EINVAL, "b = %d: must be a multiple of 64 in [64, %d]", b, KCH_MAX_R);
+    if (b < CB || b > KCH_MAX_R || b % CB != 0)
+        return fail(SPANQR_EINVAL, "b = %d: must be a multiple of 32 in [32, %d]", b, KCH_MAX_R);
     if (r <= b || r % b != 0 || r > SPANQR_MAX_R)
         return fail(SPANQR_EINVAL, "r = %d: must be a multiple of b = %d above it, at most %d", r, b, SPANQR_MAX_R);
     if (K < r) return fail(SPANQR_EINVAL, "K = %d < r = %d", K, r);

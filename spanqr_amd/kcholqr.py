@@ -158,8 +158,8 @@ def borth(X, b=512, reorth=True):
     reorth it is projected and orthonormalised once more. One native call for the whole X, no host synchronisation.
 
     As kbig.py:77-78, r <= b or r not a multiple of b is one kcholf call at full width instead (here for r a multiple
-    of 32 up to 1024; other such shapes use torch.linalg.qr). Natively b is a multiple of 64 in
-    [64, 1024] (orth passes 256, the reference's default is 512); other b raise ValueError, as does r above 4096.
+    of 32 up to 1024; other such shapes use torch.linalg.qr). Natively b is a multiple of 32 in
+    [32, 1024] (orth passes 256, the reference's default is 512); other b raise ValueError, as does r above 4096.
     """
     _check_input(X)
     K, r = X.shape
@@ -167,8 +167,9 @@ def borth(X, b=512, reorth=True):
         if _full_width(K, r):
             return kcholqr_f(X)
         return torch.linalg.qr(X)[0]
-    if b % 64 or not 64 <= b <= KCHOLF_MAX_R:
-        raise ValueError(f"borth: b = {b}: the native block width must be a multiple of 64 in [64, {KCHOLF_MAX_R}]")
+    if b % TILE or not TILE <= b <= KCHOLF_MAX_R:
+        raise ValueError(f"borth: b = {b}: the native block width must be a multiple of {TILE} in [{TILE}, "
+                         f"{KCHOLF_MAX_R}]")
     if r > _lib.MAX_R or K < r:
         raise ValueError(f"borth: shape [{K}, {r}] needs r <= {_lib.MAX_R} and K >= r")
     X = _prepare(X)

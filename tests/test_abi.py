@@ -94,12 +94,13 @@ def test_plan_create_without_gpu_fails_cleanly():
 
 
 def test_borth_plan_arguments_checked_before_any_device_work():
-    """spanqr_plan_create_borth (kbig.py:69's b and reorth): b a multiple of 64 in [64, 1024], r > b a multiple of b up
+    """spanqr_plan_create_borth (kbig.py:69's b and reorth): b a multiple of 32 in [32, 1024], r > b a multiple of b up
     to 4096, K >= r -- refused with SPANQR_EINVAL and no plan before any device call"""
     h = ctypes.c_void_p()
     f = _lib.lib().spanqr_plan_create_borth
-    for K, r, b in [(1024, 1024, 96), (1024, 1024, 32), (1024, 1024, 576), (1024, 512, 512), (1024, 768, 512),
-                    (1000, 1024, 256), (8192, 8192, 512), (2048, 1024, 0), (4096, 2304, 1152), (2048, 2048, 2048)]:
+    for K, r, b in [(1024, 1024, 96), (1024, 1024, 48), (1024, 1024, 16), (1024, 1024, 576), (1024, 512, 512),
+                    (1024, 768, 512), (1000, 1024, 256), (8192, 8192, 512), (2048, 1024, 0), (4096, 2304, 1152),
+                    (2048, 2048, 2048)]:
         assert f(K, r, b, 1, 0, ctypes.byref(h)) == -1 and not h.value, (K, r, b)
         assert _lib.lib().spanqr_last_error()
     assert f(1024, 1024, 256, 1, 0, None) == -1

@@ -50,8 +50,8 @@ def test_borth_block_width_and_dispatch(cuda):
     Q = orth(X)
     E = Q.double().T @ Q.double() - torch.eye(576, device=cuda, dtype=torch.float64)
     assert E.abs().max().item() < 1e-5
-    with pytest.raises(ValueError):                              # b not a multiple of 64: not built natively
-        borth(torch.randn(1024, 960, device=cuda), b=96)
+    with pytest.raises(ValueError):                              # b not a multiple of 32: not built natively
+        borth(torch.randn(1024, 960, device=cuda), b=80)
     X = torch.randn(1024, 768, generator=g).to(cuda)             # r % b != 0 above 512: full width -> torch.linalg.qr
     Q = borth(X, b=512)
     E = Q.double().T @ Q.double() - torch.eye(768, device=cuda, dtype=torch.float64)
@@ -63,7 +63,11 @@ def test_borth_block_width_and_dispatch(cuda):
 OPTION_CASES = [(1024, 1024, 512, True, "mixed_c4"), (1000, 768, 128, True, "rank_half"),
                 (1000, 768, 128, False, "mixed_c4"), (1400, 640, 64, True, "zero"), (2048, 1536, 512, False, "dup_cols"),
                 (1200, 1024, 256, False, "ttf_cu4_t1e-2"), (1600, 1536, 768, True, "mixed_c4"),
-                (2100, 2048, 1024, True, "rank_half"), (1100, 960, 320, False, "mixed_c4")]
+                (2100, 2048, 1024, True, "rank_half"), (1100, 960, 320, False, "mixed_c4"),
+                # block widths that are odd multiples of 32: the projection's last 64-wide tile row or column is half
+                # used (and every other block starts at an odd multiple of 32)
+                (700, 640, 160, True, "mixed_c4"), (600, 576, 96, True, "rank_half"), (400, 256, 32, True, "zero"),
+                (1000, 960, 480, True, "mixed_c4"), (900, 864, 288, True, "dup_cols")]
 
 
 @pytest.mark.parametrize("K,r,b,reorth,name", OPTION_CASES)
