@@ -354,6 +354,99 @@ __global__ __launch_bounds__(512) void k_gram(const MatsIn As, long lda, int K, 
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Plain Gram partials with the operands read straight into registers: k_gram<false, false>'s partials, element for
+// element, without LDS staging or barriers (taken for long splits, where it measured faster). Workgroup (u, sp) of
+// four wavefronts computes upper 64x64 tile u over the split's rows, wavefront w the 32x32 block (qi, qj) =
+// (w >> 1, w & 1) as four 16x16 MFMA quadrants. Lane (l16, lk) reads columns 2 l16 and 2 l16 + 1 of the block's 32
+// columns of each operand strip with one 8-byte load per row 4 kk + lk of a 32-row chunk, so quadrant (a, b) holds
+// the tile entries (32 qi + 2 m + a, 32 qj + 2 n + b) -- each element's chain still runs over the split's rows in
+// order, four per MFMA. A buffer resource per chunk and strip whose range ends at the split's last row makes rows
+// past it read as 0; a strip past the columns rc (r % 64 == 32) has an empty range. GR_DEPTH chunks are in flight
+// per wavefront.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int GR_DEPTH = 3;   // chunks in flight per wavefront (16 loads each; vmcnt counts at most 63 outstanding)
+__global__ __launch_bounds__(256) void k_gramr(const MatsIn As, long lda, int K, int nt, int KS, float* __restrict__ P,
+                                               int rc) {
+    const int u = blockIdx.x, sp = blockIdx.y, U = gridDim.x;
+    const float* __restrict__ A = As.p[blockIdx.z];
+    P += (size_t)blockIdx.z * gridDim.y * U * TB * TB;
+    int ti, tj;
+    upper_tile(u, nt, ti, tj);
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int qi = w >> 1, qj = w & 1, l16 = lane & 15, lk = lane >> 4;
+    const int ca = ti * TB + 32 * qi, cb = tj * TB + 32 * qj;   // the block's first column in each strip
+    const int k0 = sp * KS, k1 = (k0 + KS < K) ? k0 + KS : K;
+    const int nch = k1 > k0 ? (k1 - k0 + BK - 1) / BK : 0;
+    const char* baseA = reinterpret_cast<const char*>(A + ca);
+    const char* baseB = reinterpret_cast<const char*>(A + cb);
+    uint32_t off[BK / 4];   // lda < 2^24 (checked by the host): 32 rows of bytes fit 31 bits
+#pragma unroll
+    for (int kk = 0; kk < BK / 4; ++kk) off[kk] = ((uint32_t)(4 * kk + lk) * (uint32_t)lda + 2u * (uint32_t)l16) * 4u;
+    const int last = nch > 0 ? nch - 1 : 0;
+    // bytes per row of each strip's range (0: the strip is past rc and reads as 0)
+    const int rowa = __builtin_amdgcn_readfirstlane(ca < rc ? (int)lda * 4 : 0);
+    const int rowbb = __builtin_amdgcn_readfirstlane(cb < rc ? (int)lda * 4 : 0);
+    // slot d holds chunk c with c % GR_DEPTH == d; a chunk past the split's last reads that one again (unused)
+    float ra[GR_DEPTH][BK / 4][2], rb[GR_DEPTH][BK / 4][2];
+    auto gload = [&](int c, float (*xa)[2], float (*xb)[2]) {
+        const int kr = k0 + (c < last ? c : last) * BK;
+        int nv = k1 - kr;
+        nv = nv < 0 ? 0 : (nv > BK ? BK : nv);
+        const int numa = __builtin_amdgcn_readfirstlane(nv * rowa);
+        const int numb = __builtin_amdgcn_readfirstlane(nv * rowbb);
+        const size_t rowb = (size_t)(kr < K ? kr : 0) * (size_t)lda * 4;
+        const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(baseA + rowb), (short)0, numa,
+                                                                            BUF_RSRC_WORD3);
+        const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(baseB + rowb), (short)0, numb,
+                                                                            BUF_RSRC_WORD3);
+#pragma unroll
+        for (int kk = 0; kk < BK / 4; ++kk) {
+            const auto va = __builtin_amdgcn_raw_buffer_load_b64(rA, (int)off[kk], 0, 0);
+            const auto vb = __builtin_amdgcn_raw_buffer_load_b64(rB, (int)off[kk], 0, 0);
+            xa[kk][0] = __uint_as_float(va[0]);
+            xa[kk][1] = __uint_as_float(va[1]);
+            xb[kk][0] = __uint_as_float(vb[0]);
+            xb[kk][1] = __uint_as_float(vb[1]);
+        }
+    };
+#pragma unroll
+    for (int d = 0; d < GR_DEPTH; ++d) {
+        gload(d, ra[d], rb[d]);
+        __builtin_amdgcn_sched_barrier(0);   // issued in slot order, so each stage waits only for its own slot
+    }
+    f32x4 acc[4];   // quadrant q = 2 a + b
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // chunk c (in slot d) into the sums; REFILL: then load chunk c + GR_DEPTH into the slot, after the MFMAs have read
+    // it (the loads reuse the slot's registers: no copies, and no wait where the loop closes)
+    auto stage = [&](int d, int c, bool refill) {
+#pragma unroll
+        for (int kk = 0; kk < BK / 4; ++kk)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[q] = mfma(ra[d][kk][q >> 1], rb[d][kk][q & 1], acc[q]);
+        if (refill) gload(c + GR_DEPTH, ra[d], rb[d]);
+        __builtin_amdgcn_sched_barrier(0);   // the refill goes out here, before the next chunk's MFMAs
+    };
+    const int nfull = nch / GR_DEPTH * GR_DEPTH;
+    for (int c0 = 0; c0 < nfull; c0 += GR_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < GR_DEPTH; ++d) stage(d, c0 + d, true);
+    }
+#pragma unroll
+    for (int d = 0; d < GR_DEPTH - 1; ++d)
+        if (nfull + d < nch) stage(d, nfull + d, false);
+    // entry (32 qi + 2 (4 lk + v) + a, 32 qj + 2 l16 + b) of quadrant (a, b): quadrants (a, 0) and (a, 1) side by side
+    float* Pt = P + ((size_t)sp * U + u) * TB * TB;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int i = 32 * qi + 2 * (4 * lk + v) + a, j = 32 * qj + 2 * l16;
+            *reinterpret_cast<float2*>(Pt + i * TB + j) = make_float2(acc[2 * a][v], acc[2 * a + 1][v]);
+        }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // Split reduction (tri.py:297/375): G = fp32(sum_s fp64(P_s)) in split order, mirrored into the lower triangle.
 // MODE 0 also writes ||G||_F^2 partials: per tile u and row quad b, squares are reduced per 64-wide row by a
 // shift-down tree, the four rows added in order, off-diagonal tiles doubled. MODE 1 writes D = fp32(I - G) * 0.5
@@ -2766,6 +2859,11 @@ MatsOut buf_out(const spanqr_plan* p, float* base) {
 // Chunks per Gram stage: two for splits of at most GRAM_DEEP_KS rows (more loads in flight: 0.2-0.5 us faster at
 // 128-row splits), one for longer splits (the two-chunk stage measured ~1 us slower at 352-row splits).
 constexpr int GRAM_DEEP_KS = 8 * BK;
+// The plain Gram reads its operands straight into registers (k_gramr) for splits of at least GRAMR_MIN_KS rows: per
+// launch 19.8 -> 18.2 us at 17408x256 and 20.0 -> 18.3 at 8192x384 (352-row splits), 64.8 -> 56.6 at 16384x512,
+// 24.3 -> 23.2 at 65536x128; slower for shorter splits (4096x512, 288 rows: 18.0 -> 20.3; 6144x256, 128 rows:
+// 8.7 -> 9.9). Its Kahan and scaled forms measured slower than k_gram's at every shape but 32768x256 and are not kept.
+constexpr int GRAMR_MIN_KS = 320;
 
 template <int NCH>
 void launch_gram_n(const spanqr_plan* p, const MatsIn& A, long lda, dim3 grid, bool scale, bool kahan, hipStream_t st) {
@@ -2782,7 +2880,9 @@ void launch_gram_n(const spanqr_plan* p, const MatsIn& A, long lda, dim3 grid, b
 
 void launch_gram(const spanqr_plan* p, const MatsIn& A, long lda, int n, bool scale, bool kahan, hipStream_t st) {
     const dim3 grid(p->U, p->S, n);
-    if (p->KS <= GRAM_DEEP_KS)
+    if (!kahan && !scale && p->KS >= GRAMR_MIN_KS)
+        k_gramr<<<grid, 256, 0, st>>>(A, lda, p->K, p->nt, p->KS, p->P, p->r);
+    else if (p->KS <= GRAM_DEEP_KS)
         launch_gram_n<2>(p, A, lda, grid, scale, kahan, st);
     else
         launch_gram_n<1>(p, A, lda, grid, scale, kahan, st);

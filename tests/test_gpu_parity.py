@@ -42,6 +42,8 @@ SHAPES32 = [(100, 32), (300, 96), (512, 160), (640, 224), (1000, 480)]
 # kcholf at full width above 512 columns (orth.py:20 for r not a multiple of 256; kcholqr_f at any multiple of 32):
 # tile rows of up to 32 tiles over up to six owner workgroups each, four column blocks per solve wavefront
 SHAPESW = [(600, 544), (1100, 640), (2000, 800), (1024, 992), (1100, 1024)]
+# splits of 352 rows (the plain Gram's register-operand kernel), one with a ragged last chunk and r % 64 == 32
+SHAPESL = [(8192, 384), (8100, 352), (16700, 224)]
 
 
 @pytest.mark.parametrize("K,r", SHAPES)
@@ -51,7 +53,7 @@ def test_dust_on_device(cuda, K, r):
     assert_bits(Z, oracle.dust(K, r), "dust")
 
 
-@pytest.mark.parametrize("K,r", SHAPES + SHAPES32 + SHAPESW)
+@pytest.mark.parametrize("K,r", SHAPES + SHAPES32 + SHAPESW + SHAPESL)
 @pytest.mark.parametrize("kahan", [True, False])
 def test_gram(cuda, K, r, kahan):
     print(f"gram {K}x{r} kahan={kahan}", flush=True)
