@@ -1569,7 +1569,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
             } else if (w == 3) {
                 // wave 3 publishes the previous step
                 if (j >= 1) publish(j - 1);
-                if (colcnt != nullptr && j == nb - 1) {   // column nb-2's operands, stored just now
+                if (colcnt != nullptr && j == nb - 1 && nb >= 2) {   // column nb-2's operands, stored just now
                     release();
                     if (lane == 0) credit(colcnt, nb - 2);
                 }
