@@ -154,3 +154,18 @@ def test_batched_ns_apply_forms_agree(cuda):
     for i in (0, 5, n - 1):
         assert_bits(Qs[i], kcholqr_f(Xs[i].to(cuda)), f"batch element {i} vs single call")
     assert_bits(Qs[n - 1], oracle.orth(Xs[n - 1].numpy(), get_plan(K, r, cuda).split_rows), "last element vs oracle")
+
+
+def test_batched_long_splits(cuda):
+    """3 x 8192x384: 352-row Gram splits, so every matrix's plain Grams go through the register-operand kernel in
+    one launch per pass; each Q bit-identical to its single call, one to the oracle"""
+    K, r, n = 8192, 384, 3
+    plan = get_plan(K, r, cuda, n)
+    assert plan.split_rows >= 320
+    g = torch.Generator().manual_seed(17)
+    Xs = [torch.randn(K, r, generator=g) * torch.logspace(0, -4, r) for _ in range(n)]
+    print(f"batched {n} x {K}x{r}", flush=True)
+    Qs = kcholqr_f_many([X.to(cuda) for X in Xs])
+    for i in range(n):
+        assert_bits(Qs[i], kcholqr_f(Xs[i].to(cuda)), f"batch element {i} vs single call")
+    assert_bits(Qs[1], oracle.orth(Xs[1].numpy(), plan.split_rows), "element 1 vs oracle")
