@@ -27,8 +27,9 @@ def noalloc(X, Q=None):
 
 
 def test_noalloc_matches_plan_calls(cuda):
-    # the second call smaller than the first; then the first shape again (its dust regenerated) and once more
-    for K, r, seed in [(2048, 512, 1), (768, 256, 2), (2048, 512, 3), (2048, 512, 4)]:
+    # the second call smaller than the first; then the first shape again (its dust regenerated) and once more; then
+    # a tall shape whose Gram splits are 352 rows (the plain Grams' register-operand kernel)
+    for K, r, seed in [(2048, 512, 1), (768, 256, 2), (2048, 512, 3), (2048, 512, 4), (8192, 384, 5)]:
         X = gen.ttf_uu(K, r, N=K, seed=seed).to(cuda)
         print(f"noalloc {K}x{r} seed {seed}", flush=True)
         Qn = noalloc(X)
