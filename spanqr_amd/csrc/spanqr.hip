@@ -166,15 +166,17 @@ __device__ __forceinline__ float rsqrt_sw(float x) {
 // NaN patterns sort above +inf, so NaN propagates as in torch. As the first kernel of a call it also clears the
 // matrix's wait-error word (bar[2], set by a bounded wait of this call's Cholesky that gave up).
 // ---------------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, int r, uint32_t* __restrict__ part,
+template <int NT>
+__global__ __launch_bounds__(NT) void k_amax(const MatsIn Xs, long ldx, int K, int r, uint32_t* __restrict__ part,
                                               uint32_t* bar = nullptr) {
+    // the maximum is exact in any order, so the block size (and with it the order) leaves the result unchanged
     const float* __restrict__ X = Xs.p[blockIdx.z];
     part += (size_t)blockIdx.z * AMAX_BLOCKS;
     if (bar != nullptr && blockIdx.x == 0 && threadIdx.x == 0) bar[(size_t)blockIdx.z * BAR_STRIDE + 2] = 0u;
     uint32_t m = 0;
     const int r4 = r >> 2;
     const int n4 = K * r4;
-    const int stride = gridDim.x * 256;
+    const int stride = gridDim.x * NT;
     auto amax4 = [](const float4 v) {
         const uint32_t a = __float_as_uint(v.x) & 0x7fffffffu, b = __float_as_uint(v.y) & 0x7fffffffu;
         const uint32_t c = __float_as_uint(v.z) & 0x7fffffffu, d = __float_as_uint(v.w) & 0x7fffffffu;
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, 
         return ab > cd ? ab : cd;
     };
     // four independent loads in flight per thread (one memory latency per four strides, not one per stride)
-    for (int e0 = blockIdx.x * 256 + threadIdx.x; e0 < n4; e0 += 4 * stride) {
+    for (int e0 = blockIdx.x * NT + threadIdx.x; e0 < n4; e0 += 4 * stride) {
         float4 v[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -203,12 +205,12 @@ __global__ __launch_bounds__(256) void k_amax(const MatsIn Xs, long ldx, int K, 
         const uint32_t o = (uint32_t)__shfl_xor((int)m, off);
         m = o > m ? o : m;
     }
-    __shared__ uint32_t sm[4];
+    __shared__ uint32_t sm[NT / 64];
     if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = m;
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t t = sm[0];
-        for (int i = 1; i < 4; ++i) t = sm[i] > t ? sm[i] : t;
+        for (int i = 1; i < NT / 64; ++i) t = sm[i] > t ? sm[i] : t;
         part[blockIdx.x] = t;
     }
 }
@@ -2668,6 +2670,17 @@ __global__ __launch_bounds__(256, 2) void k_nsapply_res(const MatsIn Ys, long ld
     }
 }
 
+// k_amax's block size: 1024 threads for X of at least AMAX_BIG elements (four times the loads in flight: 5.1 -> 3.8 us
+// at 17408x256, 9.8 -> 5.5 at 32768x256), 256 below (0.1 us faster at 768x512 and 2048x256); AMAX_BLOCKS
+// partial maxima either way
+constexpr long AMAX_BIG = 1L << 20;
+void launch_amax(const MatsIn& X, long ldx, int K, int r, uint32_t* part, uint32_t* bar, int n, hipStream_t st) {
+    if ((long)K * r >= AMAX_BIG)
+        k_amax<1024><<<dim3(AMAX_BLOCKS, 1, n), 1024, 0, st>>>(X, ldx, K, r, part, bar);
+    else
+        k_amax<256><<<dim3(AMAX_BLOCKS, 1, n), 256, 0, st>>>(X, ldx, K, r, part, bar);
+}
+
 // word[i * stride] = 0 for i < n (clears wait-error words where no k_amax runs first)
 __global__ void k_clear_words(uint32_t* word, int n, int stride) {
     if ((int)threadIdx.x < n) word[(size_t)threadIdx.x * stride] = 0u;
@@ -3206,7 +3219,7 @@ int enqueue_orth(spanqr_plan* p, int n, const MatsIn& X, long ldx, const MatsOut
         }
         return SPANQR_OK;
     };
-    k_amax<<<dim3(AMAX_BLOCKS, 1, n), 256, 0, st>>>(X, ldx, p->K, p->r, p->amax_part, p->bar);
+    launch_amax(X, ldx, p->K, p->r, p->amax_part, p->bar, n, st);
     if ((rc = mark())) return rc;
     const MatsIn bin[2] = {buf_in(p, p->Y0), buf_in(p, p->Y1)};
     const MatsOut bout[2] = {buf_out(p, p->Y0), buf_out(p, p->Y1)};
@@ -3537,7 +3550,7 @@ int enqueue_borth(spanqr_plan* p, const float* X, long ldx, float* Q, long ldq, 
     const int K = p->K, BW = p->bw;
     p->last_n = 1;
     k_clear_words<<<1, 64, 0, st>>>(p->blk->bar + 3, 1, BAR_STRIDE);
-    k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(mats_in(&X, 1), ldx, K, p->r, p->bamax);
+    launch_amax(mats_in(&X, 1), ldx, K, p->r, p->bamax, nullptr, 1, st);
     const int sgrid = (K * (BW / 4) + 255) / 256 < 1024 ? (K * (BW / 4) + 255) / 256 : 1024;
     int rc;
     for (int jb = 0; jb < p->nblk; ++jb) {
@@ -3764,7 +3777,7 @@ int spanqr_profile_kernel(spanqr_plan* p, int which, int reps, float* avg_ms, vo
     const MatsOut y1 = buf_out(p, p->Y1);
     auto launch = [&]() -> int {
         switch (which) {
-            case SPANQR_K_AMAX: k_amax<<<AMAX_BLOCKS, 256, 0, st>>>(y0, r, p->K, r, p->amax_part); break;
+            case SPANQR_K_AMAX: launch_amax(y0, r, p->K, r, p->amax_part, nullptr, 1, st); break;
             case SPANQR_K_GRAM_PASS1:
                 if (p->gram_short) launch_gram32_t<true, true, 0>(p, y0, r, 1, st);
                 else launch_gram(p, y0, r, 1, true, true, st);
@@ -3820,7 +3833,7 @@ int spanqr_stage_amax(spanqr_plan* p, const float* X, long ldx, void* stream) {
     int rc = check_mat(p, X, ldx, "X");
     if (rc) return rc;
     DeviceGuard dg(p->device);
-    k_amax<<<AMAX_BLOCKS, 256, 0, (hipStream_t)stream>>>(mats_in(&X, 1), ldx, p->K, p->r, p->amax_part);
+    launch_amax(mats_in(&X, 1), ldx, p->K, p->r, p->amax_part, nullptr, 1, (hipStream_t)stream);
     HIPCHK(hipGetLastError());
     return SPANQR_OK;
 }
