@@ -1326,7 +1326,7 @@ constexpr int CH_WG0_TILES = 23;   // workgroup 0: D[2], X1, R2[2][5], dl[2], li
 // w >= 6 the last part (which holds T(i, i-3..i) and hands them to workgroup 0) has at least 4 tiles for every row
 // i >= 4. A part's work per column block shrinks with its width, so long rows keep up with workgroup 0's steps; the
 // plan picks w (a single matrix: OWNER_W; a batch: wider parts where that puts it in fewer co-resident launches).
-constexpr int OWNER_W = 6;       // (6: the best of 6, 7, 8 and 16 measured at r = 512 for one matrix)
+constexpr int OWNER_W = 6;       // (6: the best of 6, 7, 8 and 16 at r = 512 and of 6, 8 and 16 at r = 256)
 constexpr int OWNER_WMAX = 16;   // widest parts (one part per row up to r = 512)
 __host__ __device__ constexpr int row_parts(int i, int w) { return (i + w) / w; }
 __host__ __device__ inline void part_range(int i, int q, int w, int& s, int& e) {
