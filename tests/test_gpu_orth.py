@@ -91,6 +91,28 @@ def test_pow2_scale_edges(cuda):
         assert_bits(Q, oracle.orth(X, get_plan(K, r, cuda).split_rows), f"Q at max {m!r}")
 
 
+@pytest.mark.parametrize("where", ["first", "last", "middle", "strided"])
+def test_scale_of_tall_x(cuda, where):
+    """X of 2^20 elements and more (the amax's 1024-thread workgroups): the maximum is found wherever it sits, and a
+    row stride wider than r hides the columns past r (filled with 1e30 here)"""
+    K, r = 8192, 128
+    rng = np.random.default_rng(1)
+    X = rng.uniform(-1, 1, (K, r)).astype(np.float32)
+    i, j = {"first": (0, 0), "last": (K - 1, r - 1), "middle": (4099, 77), "strided": (K - 1, r - 1)}[where]
+    X[i, j] = np.float32(-3.0e4)
+    print(f"scale of {K}x{r}, maximum at {where}", flush=True)
+    plan = get_plan(K, r, cuda)
+    pad = 4 if where == "strided" else 0
+    Xp = torch.full((K, r + pad), 1e30, device=cuda)
+    Xp[:, :r] = torch.from_numpy(X).to(cuda)
+    Q = torch.empty(K, r, device=cuda)
+    _lib.check(_lib.lib().spanqr_orth_f32(plan.handle, Xp.data_ptr(), r + pad, Q.data_ptr(), r, 5e-7, 1e-7, 1e-8, 2,
+                                          stream_handle(cuda)))
+    torch.cuda.synchronize()
+    s = stages.scalars(K, r, cuda)[0].item()
+    assert np.float32(s) == oracle.pow2_scale(np.float32(3.0e4)) == np.float32(2.0 ** -15), f"scale {s}"
+
+
 def test_strided_operands(cuda):
     """ldx > r and ldq > r through the C ABI (the reference copies to contiguous first, kcholqr.py:100)"""
     K, r, pad = 1024, 256, 12
