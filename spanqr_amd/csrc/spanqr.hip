@@ -1432,7 +1432,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
     if (STAMP && b == 0 && tid == 0) stamps[0] = stamp_clock();
     const uint32_t ep = cnt[b] + 1;        // this call's number (every workgroup runs every call)
     // misc: [0..2] nrm, shift, tau; workgroup 0's LDS words: [4] the row wavefronts' barrier counter, [5] the last step
-    // whose L(j+2, j) is formed, [7] the tile factor's pairs done; [32..63] the tile factor's diagonal (piv q),
+    // whose L(j+2, j) is formed, [6] the halves of L(j+2, j-1) formed, [7] the tile factor's pairs done; [32..63] the tile factor's diagonal (piv q),
     // [64..127] its per-pair scalars
     float* misc = reinterpret_cast<float*>(chol_lds);
     Tile* tiles = reinterpret_cast<Tile*>(misc + 256);
@@ -1467,6 +1467,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         if (lane == 0) {
             reinterpret_cast<uint32_t*>(misc)[4] = 0u;
             reinterpret_cast<uint32_t*>(misc)[5] = 0u;
+            reinterpret_cast<uint32_t*>(misc)[6] = 0u;
             reinterpret_cast<uint32_t*>(misc)[7] = 0u;
             if (nnp > 0) {
                 const float nrm = sqrtf((float)s);
@@ -1501,6 +1502,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
         CholWG0& z = *reinterpret_cast<CholWG0*>(tiles);
         uint32_t* bar12 = reinterpret_cast<uint32_t*>(misc + 4);    // waves 1, 2, 5, 6 barrier counter (zeroed above)
         uint32_t* p2done = reinterpret_cast<uint32_t*>(misc + 5);   // L(j+2, j) of step j formed: j + 1 (zeroed above)
+        uint32_t* c2cnt = reinterpret_cast<uint32_t*>(misc + 6);    // halves of L(j+2, j-1) in C2: 2 j after step j
         uint32_t n12 = 0;
         // wave 3: publish L(j, j), Li_j, L(j+1, j), L(j+2, j) of step j (parity q = j & 1)
         // What the owners need for column block j -- Li_j (into its place in Li), the panel L(j+1, j) (into its
@@ -1578,9 +1580,10 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                 if (STAMP && lane == 0) stamps[2 + 5 * nb + j] = stamp_clock();
             } else if ((w == 1 || w == 2 || w == 5 || w == 6) && j + 2 < nb) {
                 // waves 1, 2, 5, 6: tile row j+2 through block j-1 (rows 2 and 3 straight from the Gram), into R2[p].
-                // The four fetch row j+2; then L(j+2, j-1) (waves 1 and 5, a row half each) and the block j-2 update
-                // of T(j+2, j+1) that its owner left (waves 2 and 6); then block j-1 on T(j+2, j) (waves 1 and 5),
-                // T(j+2, j+1) (waves 2 and 6) and the lower quadrants of T(j+2, j+2) (waves 1, 5 and 2).
+                // The four fetch row j+2 (from step 2 on each its own parts, without a barrier); then L(j+2, j-1)
+                // (waves 1 and 5, a row half each) and the block j-2 update of T(j+2, j+1) that its owner left
+                // (waves 2 and 6); then block j-1 on T(j+2, j) (waves 1 and 5), T(j+2, j+1) (waves 2 and 6, once
+                // both halves of L(j+2, j-1) are there) and the lower quadrants of T(j+2, j+2) (waves 1, 5 and 2).
                 Tile* R2 = z.R2[p];
                 const int hf = w >> 2;                                   // row half (waves 5 and 6)
                 const bool side2 = (w & 3) == 2;                         // waves 2 and 6
@@ -1594,16 +1597,48 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                     if (lane == 0) wait_flag(flagT + i2, ep, err, dead, lim);
                     if (STAMP && w == 1 && lane == 0) stamps[2 + 6 * nb + j] = stamp_clock();
                     __builtin_amdgcn_wave_barrier();
-                    const float* hp = L + (size_t)CB * i2 * r + (size_t)CB * (j - 2);     // into R2[4] = H
-                    load_tiles<5, 256>(&R2[0], 5, r, 0u, 0.f, wl,
-                                       [&](int q) { return q < 4 ? rowp + CB * (j - 1 + q) : hp; });
+                    // each wavefront fetches the parts of row j+2 that it alone reads and updates below: waves 1 and
+                    // 5 their halves of T(j+2, j-1) and T(j+2, j) and quadrant (hf, hf) of T(j+2, j+2); waves 2 and 6
+                    // their halves of T(j+2, j+1) and of H = L(j+2, j-2), wave 2 quadrant (1, 0) of T(j+2, j+2)
+                    const float* hp = L + (size_t)CB * i2 * r + (size_t)CB * (j - 2);
+                    const int t0 = side2 ? 2 : 0, t1 = side2 ? 4 : 1;
+                    const float* s0 = rowp + CB * (j - 1 + t0);
+                    const float* s1 = side2 ? hp : rowp + CB * (j - 1 + t1);
+                    const float* s3 = rowp + CB * (j + 2);
+                    const bool quad = !side2 || hf == 0;
+                    const int qa = side2 ? 1 : hf, qb = side2 ? 0 : hf;
+                    float4 v[5];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int e = lane + 64 * u, row = 16 * hf + (e >> 3), c4 = e & 7;
+                        v[u] = *reinterpret_cast<const float4*>(s0 + (size_t)row * r + 4 * c4);
+                        v[2 + u] = *reinterpret_cast<const float4*>(s1 + (size_t)row * r + 4 * c4);
+                    }
+                    const int qrow = 16 * qa + (lane >> 2), qc4 = 4 * qb + (lane & 3);
+                    if (quad) v[4] = *reinterpret_cast<const float4*>(s3 + (size_t)qrow * r + 4 * qc4);
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int e = lane + 64 * u, row = 16 * hf + (e >> 3), c4 = e & 7;
+                        float* d0 = &R2[t0][row][4 * c4];
+                        float* d1 = &R2[t1][row][4 * c4];
+                        d0[0] = v[u].x; d0[1] = v[u].y; d0[2] = v[u].z; d0[3] = v[u].w;
+                        d1[0] = v[2 + u].x; d1[1] = v[2 + u].y; d1[2] = v[2 + u].z; d1[3] = v[2 + u].w;
+                    }
+                    if (quad) {
+                        float* d3 = &R2[3][qrow][4 * qc4];
+                        d3[0] = v[4].x; d3[1] = v[4].y; d3[2] = v[4].z; d3[3] = v[4].w;
+                    }
+                    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wavefront's parts are in LDS
+                    __builtin_amdgcn_wave_barrier();
                 }
-                wave_group_barrier(bar12, 4 * ++n12, err, dead, lim);
+                if (j <= 1) wave_group_barrier(bar12, 4 * ++n12, err, dead, lim);
                 if (STAMP && w == 1 && lane == 0) stamps[2 + 7 * nb + j] = stamp_clock();
                 if (j >= 1) {
                     if (!side2) {
                         if (hf) panel32_wave<0xC>(z.C2[p], R2[0], z.li[pp]);          // L(j+2, j-1)
                         else panel32_wave<0x3>(z.C2[p], R2[0], z.li[pp]);
+                        // this half of L(j+2, j-1) is in LDS for waves 2 and 6 (two per step from step 1)
+                        if (lane == 0) __hip_atomic_fetch_add(c2cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
                         // its half for the output and the later kernels (the owners form their own copy)
                         const size_t o = (size_t)CB * (j - 1);
                         store_tile_half(L + (o + 3 * CB) * r + o, r, z.C2[p], hf, lane);
@@ -1612,7 +1647,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                         if (hf) update32_wave_q<0xC>(R2[2], R2[2], R2[4], z.C2[pp]);
                         else update32_wave_q<0x3>(R2[2], R2[2], R2[4], z.C2[pp]);
                     }
-                    wave_group_barrier(bar12, 4 * ++n12, err, dead, lim);
+                    if (j <= 1) wave_group_barrier(bar12, 4 * ++n12, err, dead, lim);
                     if (STAMP && w == 1 && lane == 0) stamps[2 + 8 * nb + j] = stamp_clock();
                     if (!side2) {
                         // T(j+2, j), block j-1 (for the owners, in the slot of A that nothing reads any more), then
@@ -1627,6 +1662,7 @@ __device__ __forceinline__ void chol_body(const int b, const size_t z, float* A,
                             update32_wave_q<0x1>(R2[3], R2[3], z.C2[p], z.C2[p]);
                         }
                     } else {
+                        if (j >= 2) wait_lds(c2cnt, 2u * (uint32_t)j, err, dead, lim);  // L(j+2, j-1), both halves
                         wait_lds(p2done, (uint32_t)j, err, dead, lim);                 // L(j+1, j-1) formed
                         if (hf) {
                             update32_wave_q<0xC>(R2[2], R2[2], z.C2[p], z.P2[pp]);     // T(j+2, j+1)
