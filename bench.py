@@ -15,8 +15,9 @@ launch duration (HIP events around back-to-back launches on the call's stream) w
 as fractions of the MFMA and HBM peaks, the roofline of the dominant kernel, the Cholesky's per-step critical path
 (device wall clock) and the gap between the graph replay and the summed kernel times.
 
-Secondary lines: the 0.8B layer shapes (1024x256, 2048x256, 3584x256, two seeds each), 2048x512, 5120x256,
-6144x256, the 27B layers wider than 512 (block Gram-Schmidt), the batched layer set (12 x 768x512 + 12 x 2048x512,
+Secondary lines: the 0.8B layer shapes (1024x256, 2048x256, 3584x256, two seeds each), 2048x512, 5120x256 and
+6144x256 (the 27B layer shapes with the algorithmic GB/s of each pass's Gram and Cholesky + solve, `pass_gbs`), the
+27B layers wider than 512 (block Gram-Schmidt), the batched layer set (12 x 768x512 + 12 x 2048x512,
 one hipGraph per shape group, against 24 single-call graphs) and a CPU baseline on a bounded sample at the two
 headline shapes (the C restatement in oracle/ with OpenMP on the host, and CPU torch.linalg.qr).
 
@@ -377,6 +378,11 @@ def main(argv=None):
         X = gen.bench_input(K, r, seed=0).to(dev)
         g, q = runner(X, graphs)
         others[f"{K}x{r}"] = {"thr_us": round(thr_us(g), 2), "lat_us": round(lat_us(g), 2), "orth": orth_error(q)}
+        if r == 256:
+            # the 27B layer shapes: the algorithmic GB/s of each pass's Gram (SYRK) and Cholesky + solve (TRSM)
+            ks = kernels_at(X, a.kernel_reps)
+            kern[f"{K}x{r}"] = ks
+            others[f"{K}x{r}"]["pass_gbs"] = {fam: v["gbs"] for fam, v in ks.items()}
         del g, q, X
     blocked = {}
     for K, r in BLOCKED_SHAPES:
