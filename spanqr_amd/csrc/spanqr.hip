@@ -714,12 +714,6 @@ __global__ __launch_bounds__(512) void k_gram32(const MatsIn As, long lda, int K
 // own counter, so nothing is reset between calls.
 // ---------------------------------------------------------------------------------------------------------------
 
-// wave w computes the 16x16 block (w >> 1, w & 1) of a 32x32 tile; lane (l16, lk) holds rows 16bi + 4lk + v
-#define WAVE_COORDS                                                                  \
-    const int w_ = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane_ = threadIdx.x & 63; \
-    const int bi = w_ >> 1, bj = w_ & 1, l16 = lane_ & 15, lk = lane_ >> 4;          \
-    (void)bi; (void)bj; (void)l16; (void)lk
-
 typedef float Tile[CB][TS];
 
 __device__ __forceinline__ void store_tile(float* dst, int ld, const Tile& src, int t = -1, int nthr = 256) {
@@ -909,83 +903,6 @@ __device__ __forceinline__ void panels_inplace(int n, TF tf, const Tile& li) {
             }
         __syncthreads();
     }
-}
-
-// out = in Li^T; chain over m < 16 (bj + 1) (Li is lower triangular, chol.cu panel). out may alias in.
-__device__ __forceinline__ void panel32(Tile& out, const Tile& in, const Tile& li, bool on = true) {
-    WAVE_COORDS;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (on) {
-        float a[8], b[8];
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            a[kk] = in[16 * bi + l16][4 * kk + lk];
-            b[kk] = li[16 * bj + l16][4 * kk + lk];
-        }
-        __builtin_amdgcn_sched_barrier(0);   // every operand read issued before the chain
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-            if (kk < 4 * (bj + 1)) acc = mfma(a[kk], b[kk], acc);
-    }
-    __syncthreads();
-    if (on)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) out[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
-    __syncthreads();
-}
-
-// dst = C - Pi Pk^T (chain over m = 0..31 starting from C); lower: skip the upper 16x16 block. dst may alias C.
-// Every wave's global stores have completed when it returns (they are covered by a release made after it).
-__device__ __forceinline__ void update32(Tile& dst, const Tile& C, const Tile& Pi, const Tile& Pk, bool lower,
-                                         bool on = true) {
-    WAVE_COORDS;
-    if (on && !(lower && bi == 0 && bj == 1)) {
-        f32x4 acc;
-        float a[8], b[8];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[v] = C[16 * bi + 4 * lk + v][16 * bj + l16];
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            a[kk] = Pi[16 * bi + l16][4 * kk + lk];
-            b[kk] = Pk[16 * bj + l16][4 * kk + lk];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) acc = mfma(-a[kk], b[kk], acc);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) dst[16 * bi + 4 * lk + v][16 * bj + l16] = acc[v];
-    }
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-    __syncthreads();
-}
-
-// Two panels in one phase: outA = inA Li^T, outB = inB Li^T (outputs must not alias the inputs)
-__device__ __forceinline__ void panel32x2(Tile& outA, const Tile& inA, Tile& outB, const Tile& inB, const Tile& li,
-                                          bool on = true) {
-    WAVE_COORDS;
-    if (on) {
-        float xa[8], xb[8], lv[8];
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            xa[kk] = inA[16 * bi + l16][4 * kk + lk];
-            xb[kk] = inB[16 * bi + l16][4 * kk + lk];
-            lv[kk] = li[16 * bj + l16][4 * kk + lk];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-            if (kk < 4 * (bj + 1)) {
-                a = mfma(xa[kk], lv[kk], a);
-                c = mfma(xb[kk], lv[kk], c);
-            }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            outA[16 * bi + 4 * lk + v][16 * bj + l16] = a[v];
-            outB[16 * bi + 4 * lk + v][16 * bj + l16] = c[v];
-        }
-    }
-    __syncthreads();
 }
 
 // quadrant masks: the row half h of the A operand (bi = h) and the row half of the B operand (bj = h) that a set of
@@ -1293,9 +1210,9 @@ __device__ __forceinline__ void row_pairs(f32x16& C, f32x16& T2, const float* fq
     for (int k = 0; k < CB / 2; ++k) {
         const int c = 2 * k, v0 = 4 * (c >> 3) + (c & 3), hh = (c >> 2) & 1;
         const bool mine = h == hh;
-        if (__builtin_amdgcn_readfirstlane(got) < base + k + 1) {
-            while (!dead && __builtin_amdgcn_readfirstlane(__hip_atomic_load(fcnt, __ATOMIC_ACQUIRE,
-                                                                             __HIP_MEMORY_SCOPE_WORKGROUP)) <
+        if ((uint32_t)__builtin_amdgcn_readfirstlane(got) < base + k + 1) {
+            while (!dead && (uint32_t)__builtin_amdgcn_readfirstlane(__hip_atomic_load(fcnt, __ATOMIC_ACQUIRE,
+                                                                                       __HIP_MEMORY_SCOPE_WORKGROUP)) <
                                 base + k + 1) {
                 if (++polls > lim) {
                     if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2134,7 +2051,6 @@ __device__ __forceinline__ void trsm_wave_body(const int g, const int z, const M
                                                long ldy, float* scal, const uint32_t* colcnt, uint32_t* err,
                                                uint32_t lim) {
     extern __shared__ float smem[];
-    constexpr int r = NBC * CB;
     const float* __restrict__ A = As.p[z];
     float* __restrict__ Y = Ys.p[z];
     amax_part += (size_t)z * AMAX_BLOCKS;
